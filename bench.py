@@ -1,0 +1,249 @@
+"""Benchmark of the MI355X MatMulNBits path (one JSON line on stdout).
+
+Workload: the Phi-3.5-mini decode layer set at M=1, int4,
+block_size 32, packed uint8 zero points — qkv (K=3072, N=9216), o (3072 -> 3072), gate_up
+(3072 -> 16384), down (8192 -> 3072).  One step = those four MatMulNBits launches over one
+layer's weights.  The weights of L layer copies (>= 2 x the 256 MB Infinity Cache) are rotated
+step by step so every step streams its weights from HBM, as a real decode does.  Inputs are
+synthetic (seeded), resident in HBM before the timed region.
+
+value = algorithmic bytes of the layer set (65,568,768 B) per step / step time, in GB/s.
+The line also carries, measured in the same run:
+  roofline      the dominant decode kernel's algorithmic bytes / its HIP-event launch time vs 8 TB/s
+  prefill       MatMulNBits M=2048, K=3072, N=8192 in TFLOP/s vs 2.5 PFLOP/s fp16
+  cpu_baseline  the C restatement in oracle/ (kind "port"; stock ORT is not installed in this
+                image) on the host's cores, on a bounded sample of the same layer set
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "onnxruntime-ep-vulkan_amd"
+for _p in (str(ROOT), str(PKG)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 * 1024 * 1024
+
+LAYER = [  # (name, K, N)
+    ("qkv_proj", 3072, 9216),
+    ("o_proj", 3072, 3072),
+    ("gate_up_proj", 3072, 16384),
+    ("down_proj", 8192, 3072),
+]
+BITS, BS = 4, 32
+
+
+def node_bytes(m: int, k: int, n: int, bs: int = BS, zp: bool = True) -> int:
+    bpc = k // bs
+    b = n * k // 2 + 2 * n * bpc + (n * ((bpc * 4 + 7) // 8) if zp else 0)
+    return b + 2 * m * k + 2 * m * n
+
+
+def make_weights(torch, dev, k, n, gen, bs=BS, zp=True):
+    bpc = k // bs
+    B = torch.randint(0, 256, (n, bpc, bs // 2), dtype=torch.uint8, device=dev, generator=gen)
+    S = (torch.randn(n * bpc, device=dev, generator=gen).abs() * 0.02).to(torch.float16)
+    Z = torch.randint(0, 256, (n, (bpc * 4 + 7) // 8), dtype=torch.uint8, device=dev,
+                      generator=gen) if zp else None
+    return B, S, Z
+
+
+def cpu_baseline(seconds: float = 10.0) -> dict:
+    """The oracle's C restatement on the host cores, over the same layer set at M=1."""
+    import numpy as np
+
+    so = ROOT / "oracle" / "build" / "libmnb_oracle.so"
+    lib = C.CDLL(str(so))
+    lib.mnb_oracle_matmul.argtypes = [C.c_void_p] * 5 + [C.c_int64] * 3 + [C.c_int] * 4
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+    rng = np.random.default_rng(20260801)
+    nodes = []
+    for _, k, n in LAYER:
+        bpc = k // BS
+        nodes.append((k, n,
+                      rng.standard_normal(k).astype(np.float16),
+                      rng.integers(0, 256, size=n * k // 2, dtype=np.uint8),
+                      (np.abs(rng.standard_normal(n * bpc)) * 0.02).astype(np.float16),
+                      rng.integers(0, 256, size=n * ((bpc * 4 + 7) // 8), dtype=np.uint8),
+                      np.zeros(n, dtype=np.float16)))
+    per_set = sum(node_bytes(1, k, n) for _, k, n in LAYER)
+    iters, t0 = 0, time.perf_counter()
+    while True:
+        for k, n, a, b, s, z, y in nodes:
+            rc = lib.mnb_oracle_matmul(a.ctypes.data, b.ctypes.data, s.ctypes.data, z.ctypes.data,
+                                       y.ctypes.data, 1, n, k, 4, BS, 1, cores)
+            assert rc == 0
+        iters += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or iters >= 2000:
+            break
+    return {"value": round(per_set * iters / el / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{iters} passes of the 4-node Phi-3.5 decode layer set (M=1, int4 bs32, zp) "
+                      f"in {el:.1f} s; stock ORT CPUExecutionProvider is not installed in this "
+                      f"image, so the oracle's C restatement (fp32 accumulate, OpenMP) stands in"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              f"(MatMulNBits shards along N with no collective in the hot path)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import mnb
+
+    mnb.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260801)
+
+    per_layer = sum(node_bytes(1, k, n) for _, k, n in LAYER)
+    copies = max(2, -(-2 * MALL_BYTES // per_layer))
+    layers = [[make_weights(torch, dev, k, n, gen) for _, k, n in LAYER] for _ in range(copies)]
+    acts = [torch.randn(1, k, device=dev, generator=gen).to(torch.float16) for _, k, _ in LAYER]
+    outs = [torch.empty(1, n, dtype=torch.float16, device=dev) for _, _, n in LAYER]
+    probs = [mnb.problem(1, n, k, BITS, BS, True) for _, k, n in LAYER]
+    lib = mnb.load()
+    sptr = int(stream.cuda_stream)
+
+    def launch(i, layer):
+        B, S, Z = layers[layer][i]
+        rc = lib.mnb_matmul_nbits(C.byref(probs[i]), acts[i].data_ptr(), B.data_ptr(),
+                                  S.data_ptr(), Z.data_ptr(), outs[i].data_ptr(), None, 0, sptr)
+        if rc:
+            mnb.check(rc)
+
+    def step(s):
+        for i in range(len(LAYER)):
+            launch(i, s % copies)
+
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+
+    # Timed region: exactly `steps` steps; HIP events bracket every launch on the launch stream.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(LAYER) + 1)]
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        e = evs[s]
+        for i in range(len(LAYER)):
+            e[i].record(stream)
+            launch(i, s % copies)
+        e[len(LAYER)].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall * 1e3 / args.steps
+    kern_ms = [0.0] * len(LAYER)
+    for e in evs:
+        for i in range(len(LAYER)):
+            kern_ms[i] += e[i].elapsed_time(e[i + 1])
+    kern_us = [1e3 * t / args.steps for t in kern_ms]
+    value = per_layer / (ms_step * 1e-3) / 1e9
+
+    per_kernel = []
+    for (name, k, n), us in zip(LAYER, kern_us):
+        nb = node_bytes(1, k, n)
+        per_kernel.append({"node": name, "K": k, "N": n, "bytes": nb, "us": round(us, 3),
+                           "GB/s": round(nb / (us * 1e-6) / 1e9, 1)})
+    dom = max(range(len(LAYER)), key=lambda i: kern_us[i])
+    dom_bytes = node_bytes(1, LAYER[dom][1], LAYER[dom][2])
+    achieved = dom_bytes / (kern_us[dom] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"MatMulNBits {LAYER[dom][0]} M=1 K={LAYER[dom][1]} N={LAYER[dom][2]}",
+                "per_launch_bytes": dom_bytes}
+
+    # Prefill, BASELINE configs[2] at M=2048 (not part of `value`).
+    pk, pn, pm = 3072, 8192, 2048
+    pB, pS, _ = make_weights(torch, dev, pk, pn, gen, zp=False)
+    pA = torch.randn(pm, pk, device=dev, generator=gen).to(torch.float16)
+    pY = torch.empty(pm, pn, dtype=torch.float16, device=dev)
+    pprob = mnb.problem(pm, pn, pk, BITS, BS, False)
+    pinfo = mnb.plan(pprob)
+
+    def plaunch():
+        rc = lib.mnb_matmul_nbits(C.byref(pprob), pA.data_ptr(), pB.data_ptr(), pS.data_ptr(),
+                                  None, pY.data_ptr(), None, 0, sptr)
+        if rc:
+            mnb.check(rc)
+
+    for _ in range(3):
+        plaunch()
+    torch.cuda.synchronize()
+    reps = 10
+    pe = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    for a, b in pe:
+        a.record(stream)
+        plaunch()
+        b.record(stream)
+    torch.cuda.synchronize()
+    pus = 1e3 * sum(a.elapsed_time(b) for a, b in pe) / reps
+    pflops = 2.0 * pm * pn * pk
+    ptf = pflops / (pus * 1e-6) / 1e12
+    prefill = {"metric": "MatMulNBits prefill TFLOP/s", "M": pm, "K": pk, "N": pn,
+               "us": round(pus, 2), "TFLOP/s": round(ptf, 2),
+               "kernel": mnb.KERNEL_NAMES.get(pinfo.kernel, "?"),
+               "roofline": {"bound": "mfma", "achieved": round(ptf, 2),
+                            "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(ptf / F16_MFMA_PEAK_TFLOPS, 4)}}
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": "MatMulNBits int4 decode GB/s (% HBM peak) at M=1; prefill TFLOP/s at M=2048",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 activations x int4 weights, fp32 accumulate",
+        "data": "synthetic (seeded): A ~ N(0,1), uniform nibbles and zero points, scales |N(0,1)|*0.02",
+        "config": {"workload": "Phi-3.5-mini decode layer set, M=1, int4 block_size=32 with "
+                               "zero_points (qkv 3072->9216, o 3072->3072, gate_up 3072->16384, "
+                               "down 8192->3072)",
+                   "bytes_per_step": per_layer, "weight_copies_rotated": copies,
+                   "rotated_bytes": per_layer * copies},
+        "roofline": roofline,
+        "per_kernel": per_kernel,
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

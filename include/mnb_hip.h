@@ -1,0 +1,163 @@
+/*
+ * mnb_hip.h — C ABI of the MI355X (gfx950) MatMulNBits HIP shim.
+ *
+ * This is the device layer that the ORT plugin EP (include/onnxruntime_mi355x_ep.h) calls from
+ * its Compute, and that any other host (ctypes, cgo, a C++ engine) can bind directly.  It
+ * replaces the reference's Vulkan session and dispatch plumbing for this op:
+ *
+ *   mnb_matmul_nbits        replaces the q_gemv dispatch recorded by matmul_nbits_gemv
+ *                           (rust/src/ops/quant.rs:521-651) and executed by
+ *                           VulkanSession::dispatch_ort (rust/src/vk/session.rs:1036, :2540)
+ *   mnb_session_* /         replace the per-session device, queue and the constant-input
+ *   mnb_weights_*           weight cache keyed by (host ptr, bytes) that uploads B / scales /
+ *                           zero_points once (rust/src/vk/session.rs:1633-1700)
+ *   mnb_session_run_host    the host-I/O Compute path: stage A in, one launch, Y out, fence
+ *                           (rust/src/vk/session.rs:1077-1134, :2635-2736, :2791)
+ *   mnb_dequantize_f16      the Regime-1 dequant the reference checks bit-exact
+ *                           (docs/OP_COVERAGE.md:5648-5651; tests/ops/test_matmulnbits.py:94-175)
+ *   mnb_moe_grouped         expert-grouped MatMulNBits (no reference kernel: rust/src/ops/moe.rs:92-94,118)
+ *   mnb_quantize_a_int8     the accuracy_level=4 activation quantiser (no reference kernel:
+ *                           rust/src/ops/quant.rs:191-200 declines the level)
+ *
+ * Conventions
+ *   - Every function returns MNB_OK (0) or an MNB_ERR_* code; mnb_last_error() returns the
+ *     calling thread's last message.  No function aborts the process.
+ *   - Device pointers are plain addresses from hipMalloc (or any allocator of the same device).
+ *   - `stream` is a hipStream_t passed as void*; NULL means the legacy default stream.
+ *     Device-pointer entry points are stream-ordered and do not synchronise.
+ *   - Layouts are ORT's MatMulNBits layouts: A [M, K] row-major; B [N][K/bs][bs*bits/8] bytes;
+ *     scales [N * K/bs]; zero_points [N][ceil((K/bs)*bits/8)] bytes (4-bit: two blocks per byte,
+ *     low nibble first); Y [M, N] row-major.  A, scales and Y share one dtype (fp16 or fp32).
+ */
+#ifndef MNB_HIP_H_
+#define MNB_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MNB_OK 0
+#define MNB_ERR_INVALID 1     /* bad argument or shape */
+#define MNB_ERR_UNSUPPORTED 2 /* well-formed, but a form this library does not implement */
+#define MNB_ERR_HIP 3         /* a HIP runtime call failed */
+#define MNB_ERR_NOMEM 4       /* device or host allocation failed */
+
+#define MNB_DTYPE_F16 1
+#define MNB_DTYPE_F32 2
+
+/* Kernel families the planner can select (reported by mnb_plan, forced by MNB_FORCE_KERNEL). */
+#define MNB_KERNEL_GEMV_MFMA 1   /* fp16, M <= 64: streaming GEMV on 16x16x32 f16 MFMA */
+#define MNB_KERNEL_GEMM_MFMA 2   /* fp16, M > 64: dequantise-into-LDS f16 MFMA GEMM */
+#define MNB_KERNEL_GENERIC 3     /* any dtype/bits/block: per-block fp32 partial, scaled once */
+#define MNB_KERNEL_ACC4_I8 4     /* accuracy_level 4: int8 A, int8 MFMA, int32 block dots */
+
+/* One MatMulNBits node: the attributes plus the row count of this call. */
+typedef struct mnb_problem {
+    int64_t m;              /* rows: product of A's leading dimensions (may be 0) */
+    int64_t n;              /* attribute N */
+    int64_t k;              /* attribute K */
+    int32_t bits;           /* attribute bits: 4 or 8 */
+    int32_t block_size;     /* attribute block_size: 16, 32, 64 or 128 */
+    int32_t has_zero_points;/* 1 when input 3 (uint8 zero_points) is present */
+    int32_t dtype;          /* MNB_DTYPE_F16 or MNB_DTYPE_F32 for A, scales and Y */
+    int32_t accuracy_level; /* attribute accuracy_level (0 when absent) */
+    int32_t reserved;
+} mnb_problem;
+
+/* The launch the planner chose for a problem (host-only; no device work). */
+typedef struct mnb_plan_info {
+    int32_t kernel;         /* MNB_KERNEL_* */
+    int32_t waves_per_group;/* wavefronts per workgroup */
+    int32_t tile_n;         /* output columns per workgroup */
+    int32_t tile_m;         /* output rows per workgroup */
+    int64_t grid_x;
+    int64_t grid_y;
+    int64_t workspace_bytes;/* device scratch the launch needs (0 for all but accuracy_level 4) */
+} mnb_plan_info;
+
+const char* mnb_last_error(void);
+int mnb_version(void);
+
+/* Validates a problem against the claim domain (bits, block_size, K % block_size, dtype). */
+int mnb_check_problem(const mnb_problem* p);
+/* Fills `out` with the launch the planner would make for `p`. */
+int mnb_plan(const mnb_problem* p, mnb_plan_info* out);
+/* Device scratch in bytes that mnb_matmul_nbits needs for `p` (0 except accuracy_level 4). */
+int mnb_workspace_bytes(const mnb_problem* p, size_t* bytes);
+
+/* Y = A @ dequant(B)^T on device pointers.  `workspace` may be NULL when
+ * mnb_workspace_bytes() reports 0; otherwise it must hold at least that many bytes. */
+int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, const void* scales,
+                     const uint8_t* zero_points, void* y, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* W[n][k] = fp16_rne(fp32(q - zp) * fp32(scale)), written as fp16 [N][K]. */
+int mnb_dequantize_f16(int64_t n, int64_t k, int32_t bits, int32_t block_size,
+                       const uint8_t* b, const void* scales_f16, const uint8_t* zero_points,
+                       void* w_out_f16, void* stream);
+
+/* accuracy_level=4 activation quantiser: per (row, block) amax, scale = amax/127,
+ * qa = clamp(rint(a * (127/amax)), -127, 127).  a is fp16 [m][k] (dtype MNB_DTYPE_F16) or
+ * fp32; writes qa int8 [m][k], scale fp32 [m][k/bs], qsum int32 [m][k/bs]. */
+int mnb_quantize_a_int8(int64_t m, int64_t k, int32_t block_size, int32_t dtype, const void* a,
+                        int8_t* qa, float* a_scale, int32_t* qsum, void* stream);
+
+/* Expert-grouped MatMulNBits.  For expert e, rows i in [offsets[e], offsets[e+1]):
+ *   Y[i, :] = A[row_index[i], :] @ dequant(B_e)^T
+ * B/scales/zero_points hold `num_experts` consecutive per-expert tensors of one node's layout.
+ * offsets is int32 [num_experts+1] and row_index int32 [offsets[num_experts]] on the device;
+ * `total_rows` must equal offsets[num_experts] and `max_rows_per_expert` bound every group. */
+typedef struct mnb_moe_problem {
+    int64_t num_experts;
+    int64_t total_rows;         /* rows of Y (= assignments) */
+    int64_t max_rows_per_expert;
+    int64_t a_rows;             /* rows of A (tokens) */
+    int64_t n;
+    int64_t k;
+    int32_t bits;
+    int32_t block_size;
+    int32_t has_zero_points;
+    int32_t dtype;              /* MNB_DTYPE_F16 only */
+} mnb_moe_problem;
+
+int mnb_moe_grouped(const mnb_moe_problem* p, const void* a, const int32_t* row_index,
+                    const int32_t* offsets, const uint8_t* b, const void* scales,
+                    const uint8_t* zero_points, void* y, void* stream);
+
+/* ---- session layer: one device, one stream, weights uploaded once ---------------------- */
+
+typedef struct mnb_session mnb_session;
+typedef struct mnb_weights mnb_weights;
+
+int mnb_device_count(int* count);
+int mnb_session_create(int device_index, mnb_session** out);
+int mnb_session_destroy(mnb_session* s);
+/* The session's hipStream_t (as void*). */
+void* mnb_session_stream(mnb_session* s);
+int mnb_session_synchronize(mnb_session* s);
+
+/* Uploads one node's constant inputs to HBM (hipMalloc + copy), once.  Byte sizes are checked
+ * against the problem's layout.  zero_points may be NULL (implied zero point). */
+int mnb_weights_upload(mnb_session* s, const mnb_problem* node, const void* b_host,
+                       size_t b_bytes, const void* scales_host, size_t scales_bytes,
+                       const void* zp_host, size_t zp_bytes, mnb_weights** out);
+int mnb_weights_release(mnb_weights* w);
+
+/* Compute with device-resident A and Y (stream-ordered on the session stream, no sync). */
+int mnb_session_run_device(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_dev,
+                           void* y_dev);
+/* Compute with host A and Y: stage A in, launch, copy Y out, synchronise (ORT host I/O). */
+int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,
+                         void* y_host);
+
+/* Number of MatMulNBits-family kernel launches made by this process (proves the GPU ran). */
+uint64_t mnb_launch_count(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MNB_HIP_H_ */

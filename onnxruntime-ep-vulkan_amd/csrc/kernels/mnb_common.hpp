@@ -1,0 +1,123 @@
+// Shared device helpers for the gfx950 MatMulNBits kernels.
+//
+// Unpacking follows ORT's MatMulNBits layout (reference: docs/OP_COVERAGE.md:4210-4230,
+// rust/shaders/glsl/templates/q_gemv.comp:284-338): 4-bit weights low nibble first, zero points
+// packed like B with per-column byte padding, implied zero point 1 << (bits-1).
+//
+// The fp16 dequantisation is exact by construction: a nibble or byte q is placed in the low
+// mantissa bits of the fp16 value 1024 (0x6400), which makes the half 1024 + q (or 1024 + 16q for
+// a high nibble kept in place); one packed FMA with (1, 1/16) and -(1024 + z, 64 + z) then yields
+// the small integer q - z with no rounding, and a single packed multiply by the fp16 scale rounds
+// once to nearest even: fp16_rne((q - z) * s), the bit-exact dequant definition.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mnb {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// (a & m) | o in one v_and_or_b32.  gfx9 VOP3 cannot encode a literal and may read one SGPR,
+// so the two constants are passed in VGPRs; left to itself the compiler emits v_and + v_or.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+    return r;
+}
+
+// Byte `i` of `w` copied into bits 0-7 and 16-23; bits 8-15 and 24-31 zero (v_perm_b32,
+// selector 0x0c yields a zero byte).
+template <int I>
+__device__ __forceinline__ uint32_t dup_byte(uint32_t w) {
+    constexpr uint32_t sel = (uint32_t)I | (0x0Cu << 8) | ((uint32_t)I << 16) | (0x0Cu << 24);
+    return __builtin_amdgcn_perm(w, w, sel);
+}
+
+// The constant pair (1024 + z, 64 + z) that turns 4-bit magic halves into q - z.
+__device__ __forceinline__ f16x2 zoff4(int z) {
+    f16x2 r;
+    r.x = (f16)(-(1024 + z));
+    r.y = (f16)(-(64 + z));
+    return r;
+}
+
+// Four exact (q - z) pairs from one dword of eight 4-bit weights, natural element order:
+// out[i] = (q[2i] - z, q[2i+1] - z).
+template <int I>
+__device__ __forceinline__ f16x2 nib_pair(uint32_t w, f16x2 zo) {
+    const uint32_t t = and_or(dup_byte<I>(w), 0x00F0000Fu, 0x64006400u);
+    const f16x2 mul = {(f16)1.0f, (f16)0.0625f};
+    return __builtin_elementwise_fma(as_h2(t), mul, zo);
+}
+
+// Eight fp16 dequantised weights (natural order) from one dword of 4-bit weights.
+__device__ __forceinline__ f16x8 dequant8_4b(uint32_t w, f16x2 zo, f16x2 s2) {
+    const f16x2 p0 = nib_pair<0>(w, zo) * s2;
+    const f16x2 p1 = nib_pair<1>(w, zo) * s2;
+    const f16x2 p2 = nib_pair<2>(w, zo) * s2;
+    const f16x2 p3 = nib_pair<3>(w, zo) * s2;
+    f16x8 r;
+    r.s01 = p0;
+    r.s23 = p1;
+    r.s45 = p2;
+    r.s67 = p3;
+    return r;
+}
+
+// Two exact (q - z) pairs from one dword of four 8-bit weights: (q0-z, q1-z), (q2-z, q3-z).
+__device__ __forceinline__ f16x2 byte_pair_lo(uint32_t w, f16x2 zo) {
+    // bytes [b0, 0x64, b1, 0x64]
+    const uint32_t t = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);
+    return as_h2(t) + zo;
+}
+__device__ __forceinline__ f16x2 byte_pair_hi(uint32_t w, f16x2 zo) {
+    // bytes [b2, 0x64, b3, 0x64]
+    const uint32_t t = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);
+    return as_h2(t) + zo;
+}
+__device__ __forceinline__ f16x2 zoff8(int z) {
+    f16x2 r;
+    r.x = (f16)(-(1024 + z));
+    r.y = r.x;
+    return r;
+}
+
+// Eight fp16 dequantised weights from two dwords of 8-bit weights.
+__device__ __forceinline__ f16x8 dequant8_8b(uint32_t w0, uint32_t w1, f16x2 zo, f16x2 s2) {
+    f16x8 r;
+    r.s01 = byte_pair_lo(w0, zo) * s2;
+    r.s23 = byte_pair_hi(w0, zo) * s2;
+    r.s45 = byte_pair_lo(w1, zo) * s2;
+    r.s67 = byte_pair_hi(w1, zo) * s2;
+    return r;
+}
+
+// Zero point of (column n, block blk); implied 1 << (bits-1) when Z is null.
+template <int BITS, bool HAS_ZP>
+__device__ __forceinline__ int load_zp(const uint8_t* __restrict__ Z, int64_t n, int blk, int zpb) {
+    if constexpr (!HAS_ZP) {
+        return 1 << (BITS - 1);
+    } else if constexpr (BITS == 4) {
+        const uint32_t byte = Z[n * zpb + (blk >> 1)];
+        return (int)((byte >> ((blk & 1) * 4)) & 0xFu);
+    } else {
+        return (int)Z[n * zpb + blk];
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace mnb

@@ -1,0 +1,400 @@
+// C ABI of the MatMulNBits HIP shim (declared in include/mnb_hip.h).
+//
+// Replaces, for this one op, the reference's Vulkan session: the dispatch translation of
+// rust/src/ops/quant.rs:521-651 becomes mnb_plan + one kernel launch; the constant-input weight
+// cache of rust/src/vk/session.rs:1633-1700 becomes mnb_weights_upload (hipMalloc + copy once);
+// the submit/fence/readback of rust/src/vk/session.rs:2635-2736,2791 becomes
+// mnb_session_run_host on one hipStream_t per session.  Errors never abort: every entry point
+// returns a code and leaves a message for mnb_last_error().
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+
+#include "../../../include/mnb_hip.h"
+#include "../kernels/mnb_launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+std::atomic<uint64_t> g_launches{0};
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(MNB_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int64_t bpc_of(const mnb_problem* p) { return p->k / p->block_size; }
+int64_t b_bytes_of(const mnb_problem* p) { return p->n * (p->k * p->bits / 8); }
+int64_t zp_bytes_per_col(const mnb_problem* p) { return (bpc_of(p) * p->bits + 7) / 8; }
+int64_t elem_bytes(int32_t dtype) { return dtype == MNB_DTYPE_F16 ? 2 : 4; }
+
+// Environment override of the planner, the counterpart of the reference's A/B controls
+// (ONNXRUNTIME_EP_VULKAN_GEMV_PACKED / _GEMV_MAX_ROWS, rust/src/ops/quant.rs:373-449).
+int forced_kernel() {
+    const char* v = std::getenv("MNB_FORCE_KERNEL");
+    if (!v || !*v) return 0;
+    if (!std::strcmp(v, "gemv")) return MNB_KERNEL_GEMV_MFMA;
+    if (!std::strcmp(v, "gemm")) return MNB_KERNEL_GEMM_MFMA;
+    if (!std::strcmp(v, "generic")) return MNB_KERNEL_GENERIC;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mnb_last_error(void) { return g_last_error.c_str(); }
+
+int mnb_version(void) { return 1; }
+
+uint64_t mnb_launch_count(void) { return g_launches.load(); }
+
+int mnb_check_problem(const mnb_problem* p) {
+    if (!p) return fail(MNB_ERR_INVALID, "problem is NULL");
+    if (p->bits != 4 && p->bits != 8)
+        return fail(MNB_ERR_UNSUPPORTED, "bits = %d; this library implements 4 and 8", p->bits);
+    if (p->block_size != 16 && p->block_size != 32 && p->block_size != 64 && p->block_size != 128)
+        return fail(MNB_ERR_UNSUPPORTED, "block_size = %d; this library implements 16/32/64/128",
+                    p->block_size);
+    if (p->k <= 0 || p->n <= 0)
+        return fail(MNB_ERR_INVALID, "K = %lld, N = %lld; both must be positive",
+                    (long long)p->k, (long long)p->n);
+    if (p->m < 0) return fail(MNB_ERR_INVALID, "M = %lld is negative", (long long)p->m);
+    if (p->k % p->block_size)
+        return fail(MNB_ERR_UNSUPPORTED, "K = %lld is not a multiple of block_size = %d",
+                    (long long)p->k, p->block_size);
+    if (p->dtype != MNB_DTYPE_F16 && p->dtype != MNB_DTYPE_F32)
+        return fail(MNB_ERR_UNSUPPORTED, "dtype %d; A/scales/Y must be fp16 or fp32", p->dtype);
+    if (p->accuracy_level < 0 || p->accuracy_level > 4)
+        return fail(MNB_ERR_INVALID, "accuracy_level = %d is outside 0..4", p->accuracy_level);
+    const int64_t lim = (int64_t)1 << 31;
+    if (p->k >= lim || p->n >= lim || p->m >= lim || p->m * p->k >= ((int64_t)1 << 40))
+        return fail(MNB_ERR_UNSUPPORTED, "extent too large (M=%lld N=%lld K=%lld)",
+                    (long long)p->m, (long long)p->n, (long long)p->k);
+    return MNB_OK;
+}
+
+int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
+    int rc = mnb_check_problem(p);
+    if (rc) return rc;
+    if (!out) return fail(MNB_ERR_INVALID, "plan output is NULL");
+    std::memset(out, 0, sizeof(*out));
+    if (p->accuracy_level == 4)
+        return fail(MNB_ERR_UNSUPPORTED, "accuracy_level 4 (int8 activations) is not built yet");
+    int kern = MNB_KERNEL_GENERIC;
+    const bool fast = p->dtype == MNB_DTYPE_F16 && mnb::gemv_supported(p->k, p->bits, p->block_size);
+    if (fast) kern = MNB_KERNEL_GEMV_MFMA;
+    const int forced = forced_kernel();
+    if (forced == MNB_KERNEL_GENERIC) kern = MNB_KERNEL_GENERIC;
+    if (forced == MNB_KERNEL_GEMV_MFMA && fast) kern = MNB_KERNEL_GEMV_MFMA;
+    out->kernel = kern;
+    if (kern == MNB_KERNEL_GEMV_MFMA) {
+        const mnb::GemvGeom g = mnb::gemv_geometry(p->m, p->n, p->k, p->bits, p->block_size);
+        out->waves_per_group = g.waves;
+        out->tile_n = 16;
+        out->tile_m = 16 * g.mt;
+        out->grid_x = g.gx;
+        out->grid_y = g.gy;
+    } else {
+        out->waves_per_group = 4;
+        out->tile_n = 4;
+        out->tile_m = 4;
+        out->grid_x = (p->n + 3) / 4;
+        out->grid_y = (p->m + 3) / 4;
+    }
+    out->workspace_bytes = 0;
+    return MNB_OK;
+}
+
+int mnb_workspace_bytes(const mnb_problem* p, size_t* bytes) {
+    mnb_plan_info info;
+    int rc = mnb_plan(p, &info);
+    if (rc) return rc;
+    if (!bytes) return fail(MNB_ERR_INVALID, "bytes is NULL");
+    *bytes = (size_t)info.workspace_bytes;
+    return MNB_OK;
+}
+
+int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, const void* scales,
+                     const uint8_t* zero_points, void* y, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+    mnb_plan_info info;
+    int rc = mnb_plan(p, &info);
+    if (rc) return rc;
+    if (p->m == 0) return MNB_OK;
+    if (!a || !b || !scales || !y) return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    if (p->has_zero_points && !zero_points)
+        return fail(MNB_ERR_INVALID, "has_zero_points is set but zero_points is NULL");
+    if (!p->has_zero_points) zero_points = nullptr;
+    if ((size_t)info.workspace_bytes > workspace_bytes ||
+        (info.workspace_bytes > 0 && !workspace))
+        return fail(MNB_ERR_INVALID, "workspace of %zu bytes is smaller than the %lld needed",
+                    workspace_bytes, (long long)info.workspace_bytes);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    int kern = info.kernel;
+    // The MFMA path loads A in 16-byte and B in 16-byte units; fall back when a caller hands
+    // over a sub-aligned view.
+    if (kern == MNB_KERNEL_GEMV_MFMA && (!aligned(a, 16) || !aligned(b, 16)))
+        kern = MNB_KERNEL_GENERIC;
+    if (kern == MNB_KERNEL_GEMV_MFMA) {
+        e = mnb::launch_gemv_f16(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
+                                 p->block_size, st);
+    } else {
+        if (!aligned(b, 4)) return fail(MNB_ERR_INVALID, "B must be 4-byte aligned");
+        e = mnb::launch_generic(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
+                                p->block_size, p->dtype == MNB_DTYPE_F16, st);
+    }
+    if (e != hipSuccess) return hip_fail(e, "MatMulNBits kernel launch");
+    g_launches.fetch_add(1);
+    return MNB_OK;
+}
+
+int mnb_dequantize_f16(int64_t n, int64_t k, int32_t bits, int32_t block_size,
+                       const uint8_t* b, const void* scales_f16, const uint8_t* zero_points,
+                       void* w_out_f16, void* stream) {
+    mnb_problem p{};
+    p.m = 1;
+    p.n = n;
+    p.k = k;
+    p.bits = bits;
+    p.block_size = block_size;
+    p.dtype = MNB_DTYPE_F16;
+    int rc = mnb_check_problem(&p);
+    if (rc) return rc;
+    if (!b || !scales_f16 || !w_out_f16) return fail(MNB_ERR_INVALID, "a NULL pointer was passed");
+    if (!aligned(b, 4) || !aligned(w_out_f16, 16))
+        return fail(MNB_ERR_INVALID, "B must be 4-byte and W 16-byte aligned");
+    hipError_t e = mnb::launch_dequant_f16(b, scales_f16, zero_points, w_out_f16, n, k, bits,
+                                           block_size, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    g_launches.fetch_add(1);
+    return MNB_OK;
+}
+
+int mnb_quantize_a_int8(int64_t, int64_t, int32_t, int32_t, const void*, int8_t*, float*,
+                        int32_t*, void*) {
+    return fail(MNB_ERR_UNSUPPORTED, "accuracy_level 4 quantiser is not built yet");
+}
+
+int mnb_moe_grouped(const mnb_moe_problem*, const void*, const int32_t*, const int32_t*,
+                    const uint8_t*, const void*, const uint8_t*, void*, void*) {
+    return fail(MNB_ERR_UNSUPPORTED, "expert-grouped MatMulNBits is not built yet");
+}
+
+// ---- session layer ------------------------------------------------------------------------
+
+struct mnb_session {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+    void* a_dev = nullptr;
+    size_t a_cap = 0;
+    void* y_dev = nullptr;
+    size_t y_cap = 0;
+    void* ws = nullptr;
+    size_t ws_cap = 0;
+};
+
+struct mnb_weights {
+    mnb_session* s = nullptr;
+    mnb_problem node{};
+    uint8_t* b = nullptr;
+    void* scales = nullptr;
+    uint8_t* zp = nullptr;
+};
+
+int mnb_device_count(int* count) {
+    if (!count) return fail(MNB_ERR_INVALID, "count is NULL");
+    int c = 0;
+    hipError_t e = hipGetDeviceCount(&c);
+    if (e != hipSuccess) {
+        *count = 0;
+        return hip_fail(e, "hipGetDeviceCount");
+    }
+    *count = c;
+    return MNB_OK;
+}
+
+int mnb_session_create(int device_index, mnb_session** out) {
+    if (!out) return fail(MNB_ERR_INVALID, "out is NULL");
+    *out = nullptr;
+    int c = 0;
+    int rc = mnb_device_count(&c);
+    if (rc) return rc;
+    if (device_index < 0 || device_index >= c)
+        return fail(MNB_ERR_INVALID, "device index %d outside [0, %d)", device_index, c);
+    hipError_t e = hipSetDevice(device_index);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    mnb_session* s = new (std::nothrow) mnb_session();
+    if (!s) return fail(MNB_ERR_NOMEM, "session allocation failed");
+    s->device = device_index;
+    e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete s;
+        return hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    *out = s;
+    return MNB_OK;
+}
+
+int mnb_session_destroy(mnb_session* s) {
+    if (!s) return MNB_OK;
+    (void)hipSetDevice(s->device);
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    if (s->a_dev) (void)hipFree(s->a_dev);
+    if (s->y_dev) (void)hipFree(s->y_dev);
+    if (s->ws) (void)hipFree(s->ws);
+    if (s->stream) (void)hipStreamDestroy(s->stream);
+    delete s;
+    return MNB_OK;
+}
+
+void* mnb_session_stream(mnb_session* s) { return s ? static_cast<void*>(s->stream) : nullptr; }
+
+int mnb_session_synchronize(mnb_session* s) {
+    if (!s) return fail(MNB_ERR_INVALID, "session is NULL");
+    (void)hipSetDevice(s->device);
+    hipError_t e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+static int grow(void** p, size_t* cap, size_t need) {
+    if (need <= *cap) return MNB_OK;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    hipError_t e = hipMalloc(p, need);
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return fail(MNB_ERR_NOMEM, "hipMalloc(%zu): %s", need, hipGetErrorString(e));
+    }
+    *cap = need;
+    return MNB_OK;
+}
+
+int mnb_weights_upload(mnb_session* s, const mnb_problem* node, const void* b_host,
+                       size_t b_bytes, const void* scales_host, size_t scales_bytes,
+                       const void* zp_host, size_t zp_bytes, mnb_weights** out) {
+    if (!s || !node || !out) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    *out = nullptr;
+    mnb_problem p = *node;
+    p.m = 0;
+    int rc = mnb_check_problem(&p);
+    if (rc) return rc;
+    const size_t want_b = (size_t)b_bytes_of(&p);
+    const size_t want_s = (size_t)(p.n * bpc_of(&p) * elem_bytes(p.dtype));
+    const size_t want_z = (size_t)(p.n * zp_bytes_per_col(&p));
+    if (!b_host || b_bytes != want_b)
+        return fail(MNB_ERR_INVALID, "B holds %zu bytes, the layout needs %zu", b_bytes, want_b);
+    if (!scales_host || scales_bytes != want_s)
+        return fail(MNB_ERR_INVALID, "scales hold %zu bytes, the layout needs %zu", scales_bytes,
+                    want_s);
+    if (p.has_zero_points && (!zp_host || zp_bytes != want_z))
+        return fail(MNB_ERR_INVALID, "zero_points hold %zu bytes, the layout needs %zu", zp_bytes,
+                    want_z);
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    mnb_weights* w = new (std::nothrow) mnb_weights();
+    if (!w) return fail(MNB_ERR_NOMEM, "weights allocation failed");
+    w->s = s;
+    w->node = p;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->b), want_b);
+    if (e == hipSuccess) e = hipMalloc(&w->scales, want_s);
+    if (e == hipSuccess && p.has_zero_points) e = hipMalloc(reinterpret_cast<void**>(&w->zp), want_z);
+    if (e == hipSuccess) e = hipMemcpyAsync(w->b, b_host, want_b, hipMemcpyHostToDevice, s->stream);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(w->scales, scales_host, want_s, hipMemcpyHostToDevice, s->stream);
+    if (e == hipSuccess && p.has_zero_points)
+        e = hipMemcpyAsync(w->zp, zp_host, want_z, hipMemcpyHostToDevice, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) {
+        if (w->b) (void)hipFree(w->b);
+        if (w->scales) (void)hipFree(w->scales);
+        if (w->zp) (void)hipFree(w->zp);
+        delete w;
+        return hip_fail(e, "weight upload");
+    }
+    *out = w;
+    return MNB_OK;
+}
+
+int mnb_weights_release(mnb_weights* w) {
+    if (!w) return MNB_OK;
+    (void)hipSetDevice(w->s->device);
+    (void)hipStreamSynchronize(w->s->stream);
+    if (w->b) (void)hipFree(w->b);
+    if (w->scales) (void)hipFree(w->scales);
+    if (w->zp) (void)hipFree(w->zp);
+    delete w;
+    return MNB_OK;
+}
+
+static int run_locked(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_dev,
+                      void* y_dev) {
+    mnb_problem p = w->node;
+    p.m = m;
+    size_t ws = 0;
+    int rc = mnb_workspace_bytes(&p, &ws);
+    if (rc) return rc;
+    if (ws) {
+        rc = grow(&s->ws, &s->ws_cap, ws);
+        if (rc) return rc;
+    }
+    return mnb_matmul_nbits(&p, a_dev, w->b, w->scales, w->zp, y_dev, s->ws, s->ws_cap,
+                            s->stream);
+}
+
+int mnb_session_run_device(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_dev,
+                           void* y_dev) {
+    if (!s || !w) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    return run_locked(s, w, m, a_dev, y_dev);
+}
+
+int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,
+                         void* y_host) {
+    if (!s || !w) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    if (m < 0) return fail(MNB_ERR_INVALID, "M = %lld is negative", (long long)m);
+    if (m == 0) return MNB_OK;
+    if (!a_host || !y_host) return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    const size_t eb = (size_t)elem_bytes(w->node.dtype);
+    const size_t a_bytes = (size_t)m * (size_t)w->node.k * eb;
+    const size_t y_bytes = (size_t)m * (size_t)w->node.n * eb;
+    int rc = grow(&s->a_dev, &s->a_cap, a_bytes);
+    if (rc) return rc;
+    rc = grow(&s->y_dev, &s->y_cap, y_bytes);
+    if (rc) return rc;
+    hipError_t e = hipMemcpyAsync(s->a_dev, a_host, a_bytes, hipMemcpyHostToDevice, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "A upload");
+    rc = run_locked(s, w, m, s->a_dev, s->y_dev);
+    if (rc) return rc;
+    e = hipMemcpyAsync(y_host, s->y_dev, y_bytes, hipMemcpyDeviceToHost, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "Y download");
+    e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    return MNB_OK;
+}
+
+}  // extern "C"

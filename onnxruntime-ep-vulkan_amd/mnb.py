@@ -1,0 +1,178 @@
+"""ctypes binding of ``libmnb_hip.so`` (the C ABI in ``include/mnb_hip.h``).
+
+This is the Python host's view of the MI355X MatMulNBits library: tests and ``bench.py`` call
+the HIP kernels through exactly the C entry points an ORT plugin or any other FFI host binds.
+PyTorch is used only as device-memory and stream plumbing (``tensor.data_ptr()``,
+``torch.cuda.current_stream().cuda_stream``).  Loading fails loudly when the library has not
+been built; there is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_DIR = PKG / "lib"
+HIP_LIB = LIB_DIR / "libmnb_hip.so"
+EP_LIB = LIB_DIR / "libonnxruntime_mi355x_ep.so"
+
+MNB_OK = 0
+MNB_ERR_INVALID = 1
+MNB_ERR_UNSUPPORTED = 2
+MNB_ERR_HIP = 3
+MNB_ERR_NOMEM = 4
+
+DTYPE_F16 = 1
+DTYPE_F32 = 2
+
+KERNEL_GEMV_MFMA = 1
+KERNEL_GEMM_MFMA = 2
+KERNEL_GENERIC = 3
+KERNEL_ACC4_I8 = 4
+KERNEL_NAMES = {1: "gemv_mfma", 2: "gemm_mfma", 3: "generic", 4: "acc4_i8"}
+
+
+class Problem(C.Structure):
+    _fields_ = [
+        ("m", C.c_int64), ("n", C.c_int64), ("k", C.c_int64),
+        ("bits", C.c_int32), ("block_size", C.c_int32), ("has_zero_points", C.c_int32),
+        ("dtype", C.c_int32), ("accuracy_level", C.c_int32), ("reserved", C.c_int32),
+    ]
+
+
+class PlanInfo(C.Structure):
+    _fields_ = [
+        ("kernel", C.c_int32), ("waves_per_group", C.c_int32), ("tile_n", C.c_int32),
+        ("tile_m", C.c_int32), ("grid_x", C.c_int64), ("grid_y", C.c_int64),
+        ("workspace_bytes", C.c_int64),
+    ]
+
+
+class MoeProblem(C.Structure):
+    _fields_ = [
+        ("num_experts", C.c_int64), ("total_rows", C.c_int64), ("max_rows_per_expert", C.c_int64),
+        ("a_rows", C.c_int64), ("n", C.c_int64), ("k", C.c_int64),
+        ("bits", C.c_int32), ("block_size", C.c_int32), ("has_zero_points", C.c_int32),
+        ("dtype", C.c_int32),
+    ]
+
+
+class MnbError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"mnb error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Load ``libmnb_hip.so`` (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not HIP_LIB.exists():
+        raise FileNotFoundError(
+            f"{HIP_LIB} is missing: build it with `python onnxruntime-ep-vulkan_amd/build.py`")
+    lib = C.CDLL(str(HIP_LIB), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+    vp, i64, i32, sz = C.c_void_p, C.c_int64, C.c_int32, C.c_size_t
+    sig = {
+        "mnb_last_error": (C.c_char_p, []),
+        "mnb_version": (C.c_int, []),
+        "mnb_check_problem": (C.c_int, [C.POINTER(Problem)]),
+        "mnb_plan": (C.c_int, [C.POINTER(Problem), C.POINTER(PlanInfo)]),
+        "mnb_workspace_bytes": (C.c_int, [C.POINTER(Problem), C.POINTER(sz)]),
+        "mnb_matmul_nbits": (C.c_int, [C.POINTER(Problem), vp, vp, vp, vp, vp, vp, sz, vp]),
+        "mnb_dequantize_f16": (C.c_int, [i64, i64, i32, i32, vp, vp, vp, vp, vp]),
+        "mnb_quantize_a_int8": (C.c_int, [i64, i64, i32, i32, vp, vp, vp, vp, vp]),
+        "mnb_moe_grouped": (C.c_int, [C.POINTER(MoeProblem), vp, vp, vp, vp, vp, vp, vp, vp]),
+        "mnb_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+        "mnb_session_create": (C.c_int, [C.c_int, C.POINTER(vp)]),
+        "mnb_session_destroy": (C.c_int, [vp]),
+        "mnb_session_stream": (vp, [vp]),
+        "mnb_session_synchronize": (C.c_int, [vp]),
+        "mnb_weights_upload": (C.c_int, [vp, C.POINTER(Problem), vp, sz, vp, sz, vp, sz,
+                                         C.POINTER(vp)]),
+        "mnb_weights_release": (C.c_int, [vp]),
+        "mnb_session_run_device": (C.c_int, [vp, vp, i64, vp, vp]),
+        "mnb_session_run_host": (C.c_int, [vp, vp, i64, vp, vp]),
+        "mnb_launch_count": (C.c_uint64, []),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != MNB_OK:
+        raise MnbError(rc, load().mnb_last_error().decode(errors="replace"))
+
+
+def problem(m, n, k, bits=4, block_size=32, has_zp=False, dtype=DTYPE_F16,
+            accuracy_level=0) -> Problem:
+    return Problem(int(m), int(n), int(k), int(bits), int(block_size), int(bool(has_zp)),
+                   int(dtype), int(accuracy_level), 0)
+
+
+def plan(p: Problem) -> PlanInfo:
+    info = PlanInfo()
+    check(load().mnb_plan(C.byref(p), C.byref(info)))
+    return info
+
+
+def workspace_bytes(p: Problem) -> int:
+    v = C.c_size_t(0)
+    check(load().mnb_workspace_bytes(C.byref(p), C.byref(v)))
+    return int(v.value)
+
+
+# ---- torch conveniences (device-pointer plumbing only) ---------------------------------------
+
+def _ptr(t) -> int | None:
+    return None if t is None else int(t.data_ptr())
+
+
+def _stream(stream) -> int | None:
+    if stream is not None:
+        return int(stream)
+    import torch
+    return int(torch.cuda.current_stream().cuda_stream)
+
+
+def matmul_nbits(A, B, scales, zp, N: int, K: int, bits: int = 4, block_size: int = 32,
+                 accuracy_level: int = 0, out=None, workspace=None, stream=None):
+    """Run MatMulNBits on CUDA tensors through the C ABI; returns ``out`` ``[.., N]``."""
+    import torch
+    lead = tuple(A.shape[:-1])
+    m = 1
+    for d in lead:
+        m *= int(d)
+    dtype = DTYPE_F16 if A.dtype == torch.float16 else DTYPE_F32
+    p = problem(m, N, K, bits, block_size, zp is not None, dtype, accuracy_level)
+    if out is None:
+        out = torch.empty(*lead, N, dtype=A.dtype, device=A.device)
+    ws = workspace_bytes(p)
+    if ws and workspace is None:
+        workspace = torch.empty(ws, dtype=torch.uint8, device=A.device)
+    check(load().mnb_matmul_nbits(C.byref(p), _ptr(A), _ptr(B), _ptr(scales), _ptr(zp),
+                                  _ptr(out), _ptr(workspace), ws, _stream(stream)))
+    return out
+
+
+def dequantize_f16(B, scales, zp, N: int, K: int, bits: int = 4, block_size: int = 32,
+                   out=None, stream=None):
+    import torch
+    if out is None:
+        out = torch.empty(N, K, dtype=torch.float16, device=B.device)
+    check(load().mnb_dequantize_f16(N, K, bits, block_size, _ptr(B), _ptr(scales), _ptr(zp),
+                                    _ptr(out), _stream(stream)))
+    return out
+
+
+def launch_count() -> int:
+    return int(load().mnb_launch_count())

@@ -1,0 +1,221 @@
+"""GPU parity of the MatMulNBits HIP kernels against the CPU oracle, through the C ABI.
+
+Bars (stated per test): dequant is bit-exact in fp16; integer-exact known answers are exact;
+fp16 outputs are within max relative error 2e-3 over significant elements (|y_ref| >= 0.1 RMS,
+the reference's own denominator, docs/PERF.md:4350-4372) of the fp64-accumulated oracle, and
+within 2e-3 of it when normalised by max(|y_ref|, RMS) over every element; fp32 outputs within
+1e-5.  fp16 output rounding alone contributes up to 4.9e-4.
+"""
+
+from __future__ import annotations
+
+import os
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import matmul_nbits as orc
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+F16_TOL = 2e-3
+F32_TOL = 1e-5
+
+
+def _load(name):
+    d = np.load(GOLDEN / name)
+    return {k: d[k] for k in d.files}
+
+
+def _dev(x, device):
+    import torch
+    return None if x is None else torch.from_numpy(np.ascontiguousarray(x)).to(device)
+
+
+def _run(inp, N, K, bits, bs, device, kernel=None, acc=0):
+    import mnb
+    import torch
+    old = os.environ.get("MNB_FORCE_KERNEL")
+    try:
+        if kernel:
+            os.environ["MNB_FORCE_KERNEL"] = kernel
+        else:
+            os.environ.pop("MNB_FORCE_KERNEL", None)
+        y = mnb.matmul_nbits(_dev(inp["A"], device), _dev(inp["B"], device),
+                             _dev(inp["scales"], device), _dev(inp.get("zp"), device), N, K,
+                             bits, bs, accuracy_level=acc)
+        torch.cuda.synchronize()
+    finally:
+        if old is None:
+            os.environ.pop("MNB_FORCE_KERNEL", None)
+        else:
+            os.environ["MNB_FORCE_KERNEL"] = old
+    return y.cpu().numpy()
+
+
+def _check_f16(y, ref, what):
+    e1 = orc.max_rel_err_significant(y, ref)
+    e2 = orc.max_err_rms_normalised(y, ref)
+    assert np.isfinite(y).all(), what
+    assert e1 <= F16_TOL and e2 <= F16_TOL, f"{what}: rel_sig={e1:.3e} rms_norm={e2:.3e}"
+
+
+KATS = sorted(p.name for p in GOLDEN.glob("kat_*.npz"))
+DEQUANTS = sorted(p.name for p in GOLDEN.glob("dequant_*.npz"))
+
+
+@pytest.mark.parametrize("name", DEQUANTS)
+def test_dequant_bit_exact(cuda, name):
+    import mnb
+    import torch
+    d = _load(name)
+    N, K, bits, bs, hz = (int(v) for v in d["meta"])
+    print(f"[gpu] dequant {name}", flush=True)
+    W = mnb.dequantize_f16(_dev(d["B"], cuda), _dev(d["scales"], cuda), _dev(d.get("zp"), cuda),
+                           N, K, bits, bs)
+    torch.cuda.synchronize()
+    got = W.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, d["W_bits"]), f"{np.count_nonzero(got != d['W_bits'])} mismatches"
+
+
+@pytest.mark.parametrize("kernel", ["gemv", "generic"])
+@pytest.mark.parametrize("name", KATS)
+def test_integer_exact_kat(cuda, name, kernel):
+    d = _load(name)
+    M, N, K, bits, bs, hz = (int(v) for v in d["meta"])
+    print(f"[gpu] kat {name} {kernel}", flush=True)
+    y = _run(d, N, K, bits, bs, cuda, kernel)
+    assert np.array_equal(y.view(np.uint16), d["Y"].view(np.uint16)), \
+        f"max |diff| = {np.abs(y.astype(np.float64) - d['Y_exact']).max()}"
+
+
+SHAPES = [
+    # (M, N, K, bits, bs, zp)
+    (1, 64, 256, 4, 32, False),
+    (1, 33, 256, 4, 32, True),         # odd N, partial column tile
+    (1, 47, 512, 4, 16, False),
+    (1, 65, 1024, 4, 64, True),
+    (1, 96, 2048, 4, 128, True),
+    (2, 128, 3072, 4, 32, False),
+    (3, 48, 2880, 4, 32, True),        # K not a multiple of the 128-weight wave step
+    (4, 80, 640, 8, 32, True),
+    (5, 64, 512, 8, 16, False),
+    (7, 32, 256, 8, 64, True),
+    (8, 160, 1024, 8, 128, False),
+    (9, 64, 4096, 4, 32, True),
+    (16, 128, 3072, 4, 32, False),
+    (17, 64, 512, 4, 32, True),        # two 16-row MFMA tiles
+    (32, 96, 1024, 4, 64, False),
+    (33, 64, 512, 4, 16, True),        # four-tile path
+    (64, 64, 256, 8, 32, True),
+    (100, 48, 256, 4, 32, False),      # several row groups
+]
+
+
+@pytest.mark.parametrize("kernel", ["gemv", "generic"])
+@pytest.mark.parametrize("M,N,K,bits,bs,zp", SHAPES)
+def test_random_parity_f16(cuda, M, N, K, bits, bs, zp, kernel):
+    inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=M * 1000 + N + K)
+    print(f"[gpu] parity M={M} N={N} K={K} bits={bits} bs={bs} zp={zp} {kernel}", flush=True)
+    y = _run(inp, N, K, bits, bs, cuda, kernel)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
+    _check_f16(y, ref, f"{kernel} M={M} N={N} K={K} b{bits} bs{bs} zp={zp}")
+
+
+@pytest.mark.parametrize("M,N,K,bits,bs,zp", [(1, 40, 256, 4, 32, True), (6, 24, 512, 8, 64, False),
+                                              (3, 17, 128, 4, 16, True), (9, 50, 1024, 4, 128, False)])
+def test_random_parity_f32(cuda, M, N, K, bits, bs, zp):
+    inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=7 + M, a_dtype=np.float32)
+    print(f"[gpu] parity f32 M={M} N={N} K={K}", flush=True)
+    y = _run(inp, N, K, bits, bs, cuda)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
+    assert orc.max_rel_err_significant(y, ref) <= F32_TOL
+    assert orc.max_err_rms_normalised(y, ref) <= F32_TOL
+
+
+# BASELINE configs 1 and 2 (Phi-3.5 decode layer set), full size, through the default planner.
+CONFIGS = [
+    ("cfg1", 1, 3072, 3072, False),
+    ("cfg2_qkv", 1, 9216, 3072, True),
+    ("cfg2_o", 1, 3072, 3072, True),
+    ("cfg2_gate_up", 1, 16384, 3072, True),
+    ("cfg2_down", 1, 3072, 8192, True),
+    ("cfg5_shape_fp", 16, 3072, 8192, True),
+]
+
+
+@pytest.mark.parametrize("name,M,N,K,zp", CONFIGS)
+def test_baseline_configs_full_size(cuda, name, M, N, K, zp):
+    bs = 32 if name != "cfg5_shape_fp" else 128
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=20260801)
+    print(f"[gpu] {name} M={M} N={N} K={K}", flush=True)
+    y = _run(inp, N, K, 4, bs, cuda)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
+    _check_f16(y, ref, name)
+
+
+def test_three_runs_bit_identical(cuda):
+    # tests/ops/test_matmulnbits.py:558-653: repeated runs in one session are bit-identical
+    inp = orc.make_inputs(4, 1000, 3072, bits=4, block_size=32, with_zp=True, seed=42)
+    print("[gpu] determinism", flush=True)
+    ys = [_run(inp, 1000, 3072, 4, 32, cuda) for _ in range(3)]
+    assert all(np.array_equal(ys[0].view(np.uint16), y.view(np.uint16)) for y in ys[1:])
+    # negative control: the rows are distinct (tests/ops/test_matmulnbits.py:454-478)
+    assert not np.array_equal(ys[0][0], ys[0][1])
+
+
+def test_m_zero_is_a_no_op(cuda):
+    import mnb
+    import torch
+    A = torch.empty(0, 256, dtype=torch.float16, device=cuda)
+    inp = orc.make_inputs(1, 32, 256, seed=1)
+    y = mnb.matmul_nbits(A, _dev(inp["B"], cuda), _dev(inp["scales"], cuda), None, 32, 256, 4, 32)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (0, 32)
+
+
+def test_unaligned_activation_view_falls_back(cuda):
+    import mnb
+    import torch
+    inp = orc.make_inputs(2, 64, 256, seed=3)
+    flat = torch.zeros(2 * 256 + 1, dtype=torch.float16, device=cuda)
+    flat[1:] = torch.from_numpy(inp["A"].reshape(-1)).to(cuda)
+    A = flat[1:].view(2, 256)                       # 2-byte aligned, not 16
+    y = mnb.matmul_nbits(A, _dev(inp["B"], cuda), _dev(inp["scales"], cuda), None, 64, 256, 4, 32)
+    torch.cuda.synchronize()
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], None, 64, 256, 4, 32)
+    _check_f16(y.cpu().numpy(), ref, "unaligned")
+
+
+def test_session_host_io_path(cuda):
+    """Weights uploaded once, then host A in / host Y out (the reference's Compute data flow)."""
+    import ctypes as C
+    import mnb
+    lib = mnb.load()
+    inp = orc.make_inputs(3, 96, 512, bits=4, block_size=32, with_zp=True, seed=77)
+    s = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(s)))
+    try:
+        p = mnb.problem(0, 96, 512, 4, 32, True)
+        w = C.c_void_p()
+        B, S, Z = inp["B"], inp["scales"], inp["zp"]
+        mnb.check(lib.mnb_weights_upload(s, C.byref(p), B.ctypes.data, B.nbytes, S.ctypes.data,
+                                         S.nbytes, Z.ctypes.data, Z.nbytes, C.byref(w)))
+        before = mnb.launch_count()
+        for _ in range(2):
+            Y = np.zeros((3, 96), dtype=np.float16)
+            A = np.ascontiguousarray(inp["A"])
+            mnb.check(lib.mnb_session_run_host(s, w, 3, A.ctypes.data, Y.ctypes.data))
+            ref = orc.matmul_nbits(A, B, S, Z, 96, 512, 4, 32)
+            _check_f16(Y, ref, "session")
+        assert mnb.launch_count() == before + 2
+        # a wrong byte count is rejected, not read past
+        w2 = C.c_void_p()
+        rc = lib.mnb_weights_upload(s, C.byref(p), B.ctypes.data, B.nbytes - 1, S.ctypes.data,
+                                    S.nbytes, Z.ctypes.data, Z.nbytes, C.byref(w2))
+        assert rc == mnb.MNB_ERR_INVALID
+        mnb.check(lib.mnb_weights_release(w))
+    finally:
+        lib.mnb_session_destroy(s)
