@@ -53,6 +53,7 @@ extern "C" {
 #define MNB_KERNEL_GEMM_MFMA 2   /* fp16, M > 64: dequantise-into-LDS f16 MFMA GEMM */
 #define MNB_KERNEL_GENERIC 3     /* any dtype/bits/block: per-block fp32 partial, scaled once */
 #define MNB_KERNEL_ACC4_I8 4     /* accuracy_level 4: int8 A, int8 MFMA, int32 block dots */
+#define MNB_KERNEL_GEMV_STREAM 5 /* fp16, M <= 4: coalesced 16-byte-chunk streaming GEMV */
 
 /* One MatMulNBits node: the attributes plus the row count of this call. */
 typedef struct mnb_problem {

@@ -47,6 +47,7 @@ HIP_FLAGS = [
 
 HIP_SOURCES = [
     CSRC / "kernels" / "mnb_gemv.hip",
+    CSRC / "kernels" / "mnb_gemv_stream.hip",
     CSRC / "shim" / "mnb_shim.hip",
 ]
 EP_SOURCES: list[Path] = sorted((CSRC / "ep").glob("*.cpp"))

@@ -15,6 +15,27 @@ struct GemvGeom {
     size_t lds;    // dynamic LDS bytes
 };
 
+// Launch shape of the streaming decode GEMV (mnb_gemv_stream.hip).
+struct StreamConfig {
+    int mr;              // rows of A per workgroup row-tile (1..4)
+    int g;               // lanes per column (16, 32, 64)
+    int cpl;             // 16-byte chunks per lane (ceil(chunks per column / g))
+    int u;               // columns per lane group per pass (1 or 2)
+    int waves_per_group; // wavefronts per workgroup
+    int nontemporal;     // stream weights with non-temporal loads
+    int64_t tasks;       // passes over (64/g)*u columns
+    int64_t total_waves; // wavefronts launched (<= tasks; waves loop over tasks)
+};
+
+bool gemv_stream_supported(int64_t m, int64_t k, int bits, int bs);
+StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int bs);
+hipError_t launch_gemv_stream(const void* a, const uint8_t* b, const void* s, const uint8_t* z,
+                              void* y, int64_t m, int64_t n, int64_t k, int bits, int bs,
+                              hipStream_t stream);
+hipError_t launch_gemv_stream_cfg(const StreamConfig& c, const void* a, const uint8_t* b,
+                                  const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
+                                  int64_t k, int bits, int bs, hipStream_t stream);
+
 GemvGeom gemv_geometry(int64_t m, int64_t n, int64_t k, int bits, int bs);
 bool gemv_supported(int64_t k, int bits, int block_size);
 

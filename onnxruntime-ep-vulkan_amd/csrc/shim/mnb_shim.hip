@@ -54,6 +54,7 @@ int forced_kernel() {
     if (!std::strcmp(v, "gemv")) return MNB_KERNEL_GEMV_MFMA;
     if (!std::strcmp(v, "gemm")) return MNB_KERNEL_GEMM_MFMA;
     if (!std::strcmp(v, "generic")) return MNB_KERNEL_GENERIC;
+    if (!std::strcmp(v, "stream")) return MNB_KERNEL_GEMV_STREAM;
     return 0;
 }
 
@@ -101,12 +102,24 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
         return fail(MNB_ERR_UNSUPPORTED, "accuracy_level 4 (int8 activations) is not built yet");
     int kern = MNB_KERNEL_GENERIC;
     const bool fast = p->dtype == MNB_DTYPE_F16 && mnb::gemv_supported(p->k, p->bits, p->block_size);
+    const bool stream = p->dtype == MNB_DTYPE_F16 &&
+                        mnb::gemv_stream_supported(p->m, p->k, p->bits, p->block_size);
     if (fast) kern = MNB_KERNEL_GEMV_MFMA;
+    if (stream) kern = MNB_KERNEL_GEMV_STREAM;
     const int forced = forced_kernel();
     if (forced == MNB_KERNEL_GENERIC) kern = MNB_KERNEL_GENERIC;
     if (forced == MNB_KERNEL_GEMV_MFMA && fast) kern = MNB_KERNEL_GEMV_MFMA;
+    if (forced == MNB_KERNEL_GEMV_STREAM && stream) kern = MNB_KERNEL_GEMV_STREAM;
     out->kernel = kern;
-    if (kern == MNB_KERNEL_GEMV_MFMA) {
+    if (kern == MNB_KERNEL_GEMV_STREAM) {
+        const mnb::StreamConfig c =
+            mnb::gemv_stream_config(p->m, p->n, p->k, p->bits, p->block_size);
+        out->waves_per_group = c.waves_per_group;
+        out->tile_n = (64 / c.g) * c.u;
+        out->tile_m = c.mr;
+        out->grid_x = (c.total_waves + c.waves_per_group - 1) / c.waves_per_group;
+        out->grid_y = (p->m + c.mr - 1) / c.mr;
+    } else if (kern == MNB_KERNEL_GEMV_MFMA) {
         const mnb::GemvGeom g = mnb::gemv_geometry(p->m, p->n, p->k, p->bits, p->block_size);
         out->waves_per_group = g.waves;
         out->tile_n = 16;
@@ -153,9 +166,13 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
     int kern = info.kernel;
     // The MFMA path loads A in 16-byte and B in 16-byte units; fall back when a caller hands
     // over a sub-aligned view.
-    if (kern == MNB_KERNEL_GEMV_MFMA && (!aligned(a, 16) || !aligned(b, 16)))
+    if ((kern == MNB_KERNEL_GEMV_MFMA || kern == MNB_KERNEL_GEMV_STREAM) &&
+        (!aligned(a, 16) || !aligned(b, 16)))
         kern = MNB_KERNEL_GENERIC;
-    if (kern == MNB_KERNEL_GEMV_MFMA) {
+    if (kern == MNB_KERNEL_GEMV_STREAM) {
+        e = mnb::launch_gemv_stream(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
+                                    p->block_size, st);
+    } else if (kern == MNB_KERNEL_GEMV_MFMA) {
         e = mnb::launch_gemv_f16(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
                                  p->block_size, st);
     } else {

@@ -31,7 +31,8 @@ KERNEL_GEMV_MFMA = 1
 KERNEL_GEMM_MFMA = 2
 KERNEL_GENERIC = 3
 KERNEL_ACC4_I8 = 4
-KERNEL_NAMES = {1: "gemv_mfma", 2: "gemm_mfma", 3: "generic", 4: "acc4_i8"}
+KERNEL_GEMV_STREAM = 5
+KERNEL_NAMES = {1: "gemv_mfma", 2: "gemm_mfma", 3: "generic", 4: "acc4_i8", 5: "gemv_stream"}
 
 
 class Problem(C.Structure):

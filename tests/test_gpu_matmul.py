@@ -80,7 +80,7 @@ def test_dequant_bit_exact(cuda, name):
     assert np.array_equal(got, d["W_bits"]), f"{np.count_nonzero(got != d['W_bits'])} mismatches"
 
 
-@pytest.mark.parametrize("kernel", ["gemv", "generic"])
+@pytest.mark.parametrize("kernel", ["stream", "gemv", "generic"])
 @pytest.mark.parametrize("name", KATS)
 def test_integer_exact_kat(cuda, name, kernel):
     d = _load(name)
@@ -94,6 +94,11 @@ def test_integer_exact_kat(cuda, name, kernel):
 SHAPES = [
     # (M, N, K, bits, bs, zp)
     (1, 64, 256, 4, 32, False),
+    (1, 4096, 16384, 4, 32, True),     # 512 chunks per column: the widest register budget
+    (1, 100, 8192, 8, 64, True),
+    (2, 77, 4096, 8, 16, True),
+    (3, 50, 2048, 4, 16, True),
+    (4, 64, 4096, 4, 128, False),
     (1, 33, 256, 4, 32, True),         # odd N, partial column tile
     (1, 47, 512, 4, 16, False),
     (1, 65, 1024, 4, 64, True),
@@ -114,7 +119,7 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("kernel", ["gemv", "generic"])
+@pytest.mark.parametrize("kernel", ["stream", "gemv", "generic"])
 @pytest.mark.parametrize("M,N,K,bits,bs,zp", SHAPES)
 def test_random_parity_f16(cuda, M, N, K, bits, bs, zp, kernel):
     inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=M * 1000 + N + K)
