@@ -147,39 +147,52 @@ def main() -> int:
         step(s)
     torch.cuda.synchronize()
 
-    # Timed region: exactly `steps` steps; HIP events bracket every launch on the launch stream.
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(LAYER) + 1)]
-           for _ in range(args.steps)]
+    # Timed region: exactly `steps` steps of the four launches, bracketed by a synchronize on
+    # both sides (wall clock) and by two HIP events on the launch stream (device time).
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record(stream)
     for s in range(args.steps):
-        e = evs[s]
-        for i in range(len(LAYER)):
-            e[i].record(stream)
-            launch(i, s % copies)
-        e[len(LAYER)].record(stream)
+        step(s)
+    ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
-    kern_ms = [0.0] * len(LAYER)
-    for e in evs:
-        for i in range(len(LAYER)):
-            kern_ms[i] += e[i].elapsed_time(e[i + 1])
-    kern_us = [1e3 * t / args.steps for t in kern_ms]
+    dev_ms_step = ev0.elapsed_time(ev1) / args.steps
     value = per_layer / (ms_step * 1e-3) / 1e9
 
+    # Per-node launch duration: HIP events around `reps` back-to-back launches of one node on
+    # the launch stream (weights rotated as in the step), divided by `reps`.  This is each
+    # launch's device time including the gap to the next launch on the stream.
+    reps = max(20, copies * 4)
+    kern_us = []
+    for i in range(len(LAYER)):
+        for r in range(copies):
+            launch(i, r)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for r in range(reps):
+            launch(i, r % copies)
+        b.record(stream)
+        torch.cuda.synchronize()
+        kern_us.append(1e3 * a.elapsed_time(b) / reps)
+
     per_kernel = []
-    for (name, k, n), us in zip(LAYER, kern_us):
+    for i, ((name, k, n), us) in enumerate(zip(LAYER, kern_us)):
         nb = node_bytes(1, k, n)
         per_kernel.append({"node": name, "K": k, "N": n, "bytes": nb, "us": round(us, 3),
-                           "GB/s": round(nb / (us * 1e-6) / 1e9, 1)})
+                           "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
+                           "kernel": mnb.KERNEL_NAMES.get(mnb.plan(probs[i]).kernel, "?")})
     dom = max(range(len(LAYER)), key=lambda i: kern_us[i])
     dom_bytes = node_bytes(1, LAYER[dom][1], LAYER[dom][2])
     achieved = dom_bytes / (kern_us[dom] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                 "kernel": f"MatMulNBits {LAYER[dom][0]} M=1 K={LAYER[dom][1]} N={LAYER[dom][2]}",
-                "per_launch_bytes": dom_bytes}
+                "per_launch_bytes": dom_bytes, "launch_us": round(kern_us[dom], 3)}
 
     # Prefill, BASELINE configs[2] at M=2048 (not part of `value`).
     pk, pn, pm = 3072, 8192, 2048
@@ -226,6 +239,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
+        "device_ms_per_step": round(dev_ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -134,6 +134,8 @@ typedef struct mnb_session mnb_session;
 typedef struct mnb_weights mnb_weights;
 
 int mnb_device_count(int* count);
+/* The device's architecture name (hipDeviceProp_t::gcnArchName, e.g. "gfx950:sramecc+:xnack-"). */
+int mnb_device_arch(int device_index, char* buf, size_t len);
 int mnb_session_create(int device_index, mnb_session** out);
 int mnb_session_destroy(mnb_session* s);
 /* The session's hipStream_t (as void*). */

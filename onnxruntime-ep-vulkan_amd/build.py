@@ -48,6 +48,8 @@ HIP_FLAGS = [
 HIP_SOURCES = [
     CSRC / "kernels" / "mnb_gemv.hip",
     CSRC / "kernels" / "mnb_gemv_stream.hip",
+    CSRC / "kernels" / "mnb_gemv_stream_b4.hip",
+    CSRC / "kernels" / "mnb_gemv_stream_b8.hip",
     CSRC / "shim" / "mnb_shim.hip",
 ]
 EP_SOURCES: list[Path] = sorted((CSRC / "ep").glob("*.cpp"))

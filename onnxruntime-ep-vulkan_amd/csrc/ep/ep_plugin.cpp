@@ -1,0 +1,819 @@
+// ONNX Runtime plugin execution provider for com.microsoft::MatMulNBits on MI355X (gfx950).
+//
+// The exported surface is the plugin-EP ABI a stock ORT resolves by name (include/
+// onnxruntime_mi355x_ep.h): CreateEpFactories / ReleaseEpFactory.  Behind it:
+//   factory   OrtEpFactory: advertises each gfx950 GPU as an OrtEpDevice, creates one OrtEp per
+//             session bound to exactly one device (reference: rust/src/factory.rs:57-118,
+//             :189-480, :835-940).
+//   ep        OrtEp: GetCapability claims MatMulNBits nodes (predicate in claim.hpp, reference
+//             rust/src/ops/quant.rs:110-203; fused one node per island, reference
+//             rust/src/ep.rs:1514-1537), Compile builds one compute info per island and uploads
+//             constant B / scales / zero_points to HBM once (the reference uploads them at the
+//             first Compute, keyed by host pointer, rust/src/vk/session.rs:1633-1700), and
+//             Compute stages A in, launches one HIP kernel and copies Y out
+//             (rust/src/ep.rs:2538-2716, rust/src/vk/session.rs:1036).
+// Every vtable entry is wrapped so that a C++ exception becomes an OrtStatus and never unwinds
+// into ORT (the reference's guard_ffi_*, rust/src/lib.rs:99-206).  A Compute failure is always
+// reported as a status; nothing is recomputed on the CPU.
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "onnxruntime_c_api.h"   // also declares the plugin-EP ABI (onnxruntime_ep_c_api.h)
+
+#include "claim.hpp"
+#include "mnb_hip.h"
+#include "onnxruntime_mi355x_ep.h"
+
+#define MI355X_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace mi355x_ep {
+namespace {
+
+constexpr uint32_t kVersionBuilt = ORT_API_VERSION;
+constexpr uint32_t kVersionMin = MI355X_EP_ORT_API_VERSION_MIN;
+static_assert(ORT_API_VERSION == MI355X_EP_ORT_API_VERSION_BUILT,
+              "ORT headers declare a different ORT_API_VERSION than this EP was written for");
+constexpr uint32_t kAmdVendorId = 0x1002;
+const char* const kEpName = MI355X_EP_NAME;
+const char* const kEpVendor = "onnxruntime-ep-mi355x";
+const char* const kEpVersion = "0.28.0";
+const char* const kMetaDeviceIndex = "mi355x.hip_device_index";
+
+std::atomic<uint64_t> g_compute_count{0};
+
+// ---- errors ------------------------------------------------------------------------------
+
+struct EpError : std::runtime_error {
+    OrtErrorCode code;
+    EpError(OrtErrorCode c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+[[noreturn]] void fail(OrtErrorCode code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    throw EpError(code, buf);
+}
+
+std::string status_text(const OrtApi* api, OrtStatus* st) {
+    const char* m = api->GetErrorMessage(st);
+    std::string s = m ? m : "<null message>";
+    api->ReleaseStatus(st);
+    return s;
+}
+
+// Turns an ORT call's status into an exception (releasing the status exactly once).
+void ort_check(const OrtApi* api, OrtStatus* st, const char* what) {
+    if (!st) return;
+    const OrtErrorCode code = api->GetErrorCode(st);
+    const std::string msg = status_text(api, st);
+    throw EpError(code, std::string(what) + ": " + msg);
+}
+#define ORT_OK(api, call) ort_check((api), (api)->call, #call)
+
+void mnb_ok(int rc, const char* what) {
+    if (rc == MNB_OK) return;
+    const OrtErrorCode code = rc == MNB_ERR_INVALID ? ORT_INVALID_ARGUMENT : ORT_EP_FAIL;
+    throw EpError(code, std::string(what) + ": " + mnb_last_error());
+}
+
+OrtStatus* to_status(const OrtApi* api, OrtErrorCode code, const std::string& msg) {
+    if (!api) return nullptr;
+    return api->CreateStatus(code, msg.c_str());
+}
+
+// Runs `f`, converting any exception into an OrtStatus for ORT.
+template <typename F>
+OrtStatus* guarded(const OrtApi* api, const char* where, F&& f) {
+    try {
+        f();
+        return nullptr;
+    } catch (const EpError& e) {
+        return to_status(api, e.code, std::string(kEpName) + " " + where + ": " + e.what());
+    } catch (const std::bad_alloc&) {
+        return to_status(api, ORT_EP_FAIL, std::string(kEpName) + " " + where + ": out of memory");
+    } catch (const std::exception& e) {
+        return to_status(api, ORT_EP_FAIL, std::string(kEpName) + " " + where + ": " + e.what());
+    } catch (...) {
+        return to_status(api, ORT_EP_FAIL, std::string(kEpName) + " " + where + ": unknown error");
+    }
+}
+
+bool env_flag(const char* name) {
+    const char* v = std::getenv(name);
+    return v && *v && std::strcmp(v, "0") != 0;
+}
+
+void claim_log(const char* fmt, ...) {
+    if (!env_flag("MI355X_EP_CLAIM_DEBUG")) return;
+    va_list ap;
+    va_start(ap, fmt);
+    std::fprintf(stderr, "[mi355x-ep] ");
+    std::vfprintf(stderr, fmt, ap);
+    std::fprintf(stderr, "\n");
+    va_end(ap);
+}
+
+// ---- reading the ORT graph ------------------------------------------------------------------
+
+std::string node_string(const OrtApi* api, const OrtNode* node,
+                        OrtStatus* (*getter)(const OrtNode*, const char**)) {
+    const char* s = nullptr;
+    OrtStatus* st = getter(node, &s);
+    if (st) {
+        api->ReleaseStatus(st);
+        return {};
+    }
+    return s ? s : "";
+}
+
+std::string value_name(const OrtApi* api, const OrtValueInfo* vi) {
+    if (!vi) return {};
+    const char* s = nullptr;
+    ORT_OK(api, GetValueInfoName(vi, &s));
+    return s ? s : "";
+}
+
+std::vector<const OrtValueInfo*> node_inputs(const OrtApi* api, const OrtNode* node) {
+    size_t n = 0;
+    ORT_OK(api, Node_GetNumInputs(node, &n));
+    std::vector<const OrtValueInfo*> v(n, nullptr);
+    if (n) ORT_OK(api, Node_GetInputs(node, v.data(), n));
+    return v;
+}
+
+std::vector<const OrtValueInfo*> node_outputs(const OrtApi* api, const OrtNode* node) {
+    size_t n = 0;
+    ORT_OK(api, Node_GetNumOutputs(node, &n));
+    std::vector<const OrtValueInfo*> v(n, nullptr);
+    if (n) ORT_OK(api, Node_GetOutputs(node, v.data(), n));
+    return v;
+}
+
+InputFacts input_facts(const OrtApi* api, const OrtValueInfo* vi) {
+    InputFacts f;
+    if (!vi) return f;
+    f.present = true;
+    const OrtTypeInfo* ti = nullptr;
+    ORT_OK(api, GetValueInfoTypeInfo(vi, &ti));
+    if (ti) {
+        const OrtTensorTypeAndShapeInfo* tsi = nullptr;
+        ORT_OK(api, CastTypeInfoToTensorInfo(ti, &tsi));
+        if (tsi) {
+            ONNXTensorElementDataType et = ONNX_TENSOR_ELEMENT_DATA_TYPE_UNDEFINED;
+            ORT_OK(api, GetTensorElementType(tsi, &et));
+            f.elem_type = (int32_t)et;
+            size_t rank = 0;
+            ORT_OK(api, GetDimensionsCount(tsi, &rank));
+            f.dims.assign(rank, 0);
+            if (rank) ORT_OK(api, GetDimensions(tsi, f.dims.data(), rank));
+            f.has_shape = true;
+        }
+    }
+    bool is_const = false;
+    OrtStatus* st = api->ValueInfo_IsConstantInitializer(vi, &is_const);
+    if (st) {
+        api->ReleaseStatus(st);
+        is_const = false;
+    }
+    f.constant = is_const;
+    return f;
+}
+
+bool int_attr(const OrtApi* api, const OrtNode* node, const char* name, int64_t* out) {
+    const OrtOpAttr* attr = nullptr;
+    OrtStatus* st = api->Node_GetAttributeByName(node, name, &attr);
+    if (st) {
+        api->ReleaseStatus(st);
+        return false;
+    }
+    if (!attr) return false;
+    int64_t v = 0;
+    size_t got = 0;
+    st = api->ReadOpAttr(attr, ORT_OP_ATTR_INT, &v, sizeof(v), &got);
+    if (st) {
+        api->ReleaseStatus(st);
+        return false;
+    }
+    *out = v;
+    return true;
+}
+
+NodeFacts node_facts(const OrtApi* api, const OrtNode* node) {
+    NodeFacts f;
+    f.op_type = node_string(api, node, api->Node_GetOperatorType);
+    f.domain = node_string(api, node, api->Node_GetDomain);
+    if (!is_matmul_nbits(f)) return f;
+    for (const OrtValueInfo* vi : node_inputs(api, node)) f.inputs.push_back(input_facts(api, vi));
+    f.num_outputs = node_outputs(api, node).size();
+    f.has_k = int_attr(api, node, "K", &f.k);
+    f.has_n = int_attr(api, node, "N", &f.n);
+    f.has_bits = int_attr(api, node, "bits", &f.bits);
+    f.has_block_size = int_attr(api, node, "block_size", &f.block_size);
+    f.has_accuracy_level = int_attr(api, node, "accuracy_level", &f.accuracy_level);
+    return f;
+}
+
+// Session option `key` (ORT prefixes EP options with "ep.<name>."; both spellings are read).
+bool session_option(const OrtApi* api, const OrtSessionOptions* so, const std::string& key,
+                    std::string* value) {
+    if (!so) return false;
+    for (const std::string& k : {key, "ep." + std::string(kEpName) + "." + key.substr(3)}) {
+        int has = 0;
+        OrtStatus* st = api->HasSessionConfigEntry(so, k.c_str(), &has);
+        if (st) {
+            api->ReleaseStatus(st);
+            continue;
+        }
+        if (!has) continue;
+        size_t size = 0;
+        st = api->GetSessionConfigEntry(so, k.c_str(), nullptr, &size);
+        if (st) {
+            api->ReleaseStatus(st);
+            continue;
+        }
+        std::string buf(size, '\0');
+        st = api->GetSessionConfigEntry(so, k.c_str(), &buf[0], &size);
+        if (st) {
+            api->ReleaseStatus(st);
+            continue;
+        }
+        buf.resize(std::strlen(buf.c_str()));
+        *value = buf;
+        return true;
+    }
+    return false;
+}
+
+// ---- objects ORT holds ------------------------------------------------------------------------
+
+struct Factory;
+struct Ep;
+
+// One claimed MatMulNBits node after Compile.
+struct NodeKernel {
+    mnb_problem prob{};             // m filled per call
+    size_t fused_a = 0;             // fused-node input index of A
+    // Fused-node input index of B / scales / zero_points, or SIZE_MAX when they were dropped
+    // (constant initializers uploaded at Compile).
+    size_t fused_w[3] = {SIZE_MAX, SIZE_MAX, SIZE_MAX};
+    bool resident = false;          // weights uploaded at Compile
+    mnb_weights* weights = nullptr; // resident weights, or the last per-call upload
+    std::mutex mu;
+    std::string name;
+};
+
+struct ComputeInfo {
+    OrtNodeComputeInfo base;        // first member: ORT's pointer is this object's pointer
+    Ep* ep = nullptr;
+    std::unique_ptr<NodeKernel> kernel;
+};
+
+struct Ep {
+    OrtEp base;                     // first member
+    Factory* factory = nullptr;
+    const OrtApi* api = nullptr;
+    const OrtEpApi* ep_api = nullptr;
+    int device = 0;
+    mnb_session* session = nullptr;
+    bool keep_constant_initializers = false;
+    bool claim_enabled = true;
+    std::mutex mu;
+};
+
+struct Factory {
+    OrtEpFactory base;              // first member
+    const OrtApi* api = nullptr;
+    const OrtEpApi* ep_api = nullptr;
+    uint32_t version = 0;
+    std::string registered_name;
+};
+
+Factory* as_factory(const OrtEpFactory* p) {
+    return reinterpret_cast<Factory*>(const_cast<OrtEpFactory*>(p));
+}
+Ep* as_ep(const OrtEp* p) { return reinterpret_cast<Ep*>(const_cast<OrtEp*>(p)); }
+ComputeInfo* as_info(OrtNodeComputeInfo* p) { return reinterpret_cast<ComputeInfo*>(p); }
+
+// ---- OrtNodeComputeInfo -------------------------------------------------------------------------
+
+OrtStatus* ORT_API_CALL ci_create_state(OrtNodeComputeInfo* self, OrtNodeComputeContext*,
+                                        void** state) noexcept {
+    if (state) *state = self;
+    return nullptr;
+}
+
+void ORT_API_CALL ci_release_state(OrtNodeComputeInfo*, void*) noexcept {}
+
+const void* tensor_data(const OrtApi* api, const OrtValue* v) {
+    const void* p = nullptr;
+    ORT_OK(api, GetTensorData(v, &p));
+    return p;
+}
+
+size_t tensor_bytes(const OrtApi* api, const OrtValue* v) {
+    size_t n = 0;
+    ORT_OK(api, GetTensorSizeInBytes(v, &n));
+    return n;
+}
+
+int32_t tensor_elem_type(const OrtApi* api, const OrtValue* v, std::vector<int64_t>* dims) {
+    OrtTensorTypeAndShapeInfo* info = nullptr;
+    ORT_OK(api, GetTensorTypeAndShape(v, &info));
+    ONNXTensorElementDataType et = ONNX_TENSOR_ELEMENT_DATA_TYPE_UNDEFINED;
+    size_t rank = 0;
+    OrtStatus* st = api->GetTensorElementType(info, &et);
+    if (!st) st = api->GetDimensionsCount(info, &rank);
+    if (!st && dims) {
+        dims->assign(rank, 0);
+        if (rank) st = api->GetDimensions(info, dims->data(), rank);
+    }
+    api->ReleaseTensorTypeAndShapeInfo(info);
+    ort_check(api, st, "reading a tensor's type and shape");
+    return (int32_t)et;
+}
+
+void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
+    const OrtApi* api = ep->api;
+    if (env_flag("MI355X_EP_FORCE_COMPUTE_FAILURE"))
+        fail(ORT_EP_FAIL, "forced Compute failure (MI355X_EP_FORCE_COMPUTE_FAILURE is set)");
+    size_t nin = 0;
+    ORT_OK(api, KernelContext_GetInputCount(ctx, &nin));
+    if (k.fused_a >= nin) fail(ORT_EP_FAIL, "fused node has %zu inputs; A expected at %zu", nin, k.fused_a);
+    const OrtValue* a = nullptr;
+    ORT_OK(api, KernelContext_GetInput(ctx, k.fused_a, &a));
+    if (!a) fail(ORT_INVALID_ARGUMENT, "input A is missing");
+    std::vector<int64_t> adims;
+    const int32_t at = tensor_elem_type(api, a, &adims);
+    const int32_t want = k.prob.dtype == MNB_DTYPE_F16 ? kElemFloat16 : kElemFloat;
+    if (at != want) fail(ORT_INVALID_ARGUMENT, "A has element type %d, the node was compiled for %d", at, want);
+    if (adims.empty() || adims.back() != k.prob.k)
+        fail(ORT_INVALID_ARGUMENT, "A's last dimension is not K = %lld", (long long)k.prob.k);
+    int64_t m = 1;
+    for (size_t i = 0; i + 1 < adims.size(); ++i) {
+        if (adims[i] < 0) fail(ORT_INVALID_ARGUMENT, "A has a negative extent");
+        m *= adims[i];
+    }
+    std::vector<int64_t> ydims(adims.begin(), adims.end() - 1);
+    ydims.push_back(k.prob.n);
+    OrtValue* y = nullptr;
+    ORT_OK(api, KernelContext_GetOutput(ctx, 0, ydims.data(), ydims.size(), &y));
+    if (!y) fail(ORT_EP_FAIL, "ORT returned no output tensor");
+    if (m == 0) return;
+    void* ydata = nullptr;
+    ORT_OK(api, GetTensorMutableData(y, &ydata));
+    const void* adata = tensor_data(api, a);
+
+    std::lock_guard<std::mutex> lk(k.mu);
+    if (!k.resident) {
+        // Weights that are not constant initializers arrive with every call: upload them.
+        const void* host[3] = {nullptr, nullptr, nullptr};
+        size_t bytes[3] = {0, 0, 0};
+        for (int r = 0; r < 3; ++r) {
+            if (k.fused_w[r] == SIZE_MAX) continue;
+            if (k.fused_w[r] >= nin) fail(ORT_EP_FAIL, "weight input %d is missing", r + 1);
+            const OrtValue* v = nullptr;
+            ORT_OK(api, KernelContext_GetInput(ctx, k.fused_w[r], &v));
+            if (!v) continue;
+            host[r] = tensor_data(api, v);
+            bytes[r] = tensor_bytes(api, v);
+        }
+        if (k.weights) {
+            mnb_weights_release(k.weights);
+            k.weights = nullptr;
+        }
+        mnb_ok(mnb_weights_upload(ep->session, &k.prob, host[0], bytes[0], host[1], bytes[1],
+                                  host[2], bytes[2], &k.weights),
+               "uploading MatMulNBits weights");
+    }
+    mnb_ok(mnb_session_run_host(ep->session, k.weights, m, adata, ydata), "MatMulNBits kernel");
+    g_compute_count.fetch_add(1);
+}
+
+OrtStatus* ORT_API_CALL ci_compute(OrtNodeComputeInfo* self, void*, OrtKernelContext* ctx) noexcept {
+    ComputeInfo* ci = as_info(self);
+    const OrtApi* api = ci && ci->ep ? ci->ep->api : nullptr;
+    return guarded(api, "Compute", [&] {
+        if (!ci || !ci->kernel || !ctx) fail(ORT_INVALID_ARGUMENT, "null compute arguments");
+        compute_node(ci->ep, *ci->kernel, ctx);
+    });
+}
+
+// ---- OrtEp ----------------------------------------------------------------------------------
+
+const char* ORT_API_CALL ep_get_name(const OrtEp*) noexcept { return kEpName; }
+
+void get_capability(Ep* ep, const OrtGraph* graph, OrtEpGraphSupportInfo* support) {
+    const OrtApi* api = ep->api;
+    size_t n = 0;
+    ORT_OK(api, Graph_GetNumNodes(graph, &n));
+    std::vector<const OrtNode*> nodes(n, nullptr);
+    if (n) ORT_OK(api, Graph_GetNodes(graph, nodes.data(), n));
+    // Nodes inside control-flow bodies are declined (reference: rust/src/ep.rs:650-664).
+    const OrtNode* parent = nullptr;
+    ORT_OK(api, Graph_GetParentNode(graph, &parent));
+    if (parent) {
+        claim_log("declining %zu node(s) of a nested subgraph", n);
+        return;
+    }
+    if (!ep->claim_enabled) return;
+    for (const OrtNode* node : nodes) {
+        if (!node) continue;
+        const NodeFacts f = node_facts(api, node);
+        if (!is_matmul_nbits(f)) continue;
+        const std::string name = node_string(api, node, api->Node_GetName);
+        const ClaimDecision d = claim_matmul_nbits(f, /*int8_path=*/true);
+        if (!d.claim) {
+            claim_log("decline %s: %s", name.c_str(), d.reason.c_str());
+            continue;
+        }
+        bool all_const = true;
+        for (size_t i = 1; i <= 3 && i < f.inputs.size(); ++i)
+            if (f.inputs[i].present && !f.inputs[i].constant) all_const = false;
+        OrtNodeFusionOptions opts{};
+        opts.ort_version_supported = ep->factory->version;
+        opts.drop_constant_initializers = all_const && !ep->keep_constant_initializers;
+        ort_check(api, ep->ep_api->EpGraphSupportInfo_AddNodesToFuse(support, &node, 1, &opts),
+                  "EpGraphSupportInfo_AddNodesToFuse");
+        claim_log("claim %s (K=%lld N=%lld bits=%lld bs=%lld acc=%lld, weights %s)", name.c_str(),
+                  (long long)f.k, (long long)f.n, (long long)f.bits, (long long)f.block_size,
+                  (long long)f.accuracy_level, opts.drop_constant_initializers ? "dropped" : "kept");
+    }
+}
+
+OrtStatus* ORT_API_CALL ep_get_capability(OrtEp* self, const OrtGraph* graph,
+                                          OrtEpGraphSupportInfo* support) noexcept {
+    Ep* ep = as_ep(self);
+    return guarded(ep ? ep->api : nullptr, "GetCapability", [&] {
+        if (!ep || !graph || !support) fail(ORT_INVALID_ARGUMENT, "null GetCapability argument");
+        get_capability(ep, graph, support);
+    });
+}
+
+// Opens the EP's HIP session on first use.
+mnb_session* ep_session(Ep* ep) {
+    std::lock_guard<std::mutex> lk(ep->mu);
+    if (!ep->session) mnb_ok(mnb_session_create(ep->device, &ep->session), "opening the HIP device");
+    return ep->session;
+}
+
+std::unique_ptr<NodeKernel> compile_one(Ep* ep, const OrtGraph* graph, const OrtNode* fused) {
+    const OrtApi* api = ep->api;
+    size_t n = 0;
+    ORT_OK(api, Graph_GetNumNodes(graph, &n));
+    if (n != 1) fail(ORT_EP_FAIL, "a fused MatMulNBits island holds %zu nodes, expected 1", n);
+    const OrtNode* node = nullptr;
+    ORT_OK(api, Graph_GetNodes(graph, &node, 1));
+    const NodeFacts f = node_facts(api, node);
+    const ClaimDecision d = claim_matmul_nbits(f, true);
+    if (!d.claim) fail(ORT_EP_FAIL, "compiled node fails the claim predicate: %s", d.reason.c_str());
+
+    auto k = std::make_unique<NodeKernel>();
+    k->name = node_string(api, node, api->Node_GetName);
+    k->prob.n = f.n;
+    k->prob.k = f.k;
+    k->prob.bits = (int32_t)f.bits;
+    k->prob.block_size = (int32_t)f.block_size;
+    k->prob.dtype = f.inputs[0].elem_type == kElemFloat16 ? MNB_DTYPE_F16 : MNB_DTYPE_F32;
+    k->prob.accuracy_level = f.has_accuracy_level ? (int32_t)f.accuracy_level : 0;
+    k->prob.has_zero_points = f.inputs.size() > 3 && f.inputs[3].present;
+    mnb_ok(mnb_check_problem(&k->prob), "MatMulNBits attributes");
+
+    // Map the body node's inputs to the fused node's inputs by value name.
+    const std::vector<const OrtValueInfo*> body_in = node_inputs(api, node);
+    const std::vector<const OrtValueInfo*> fused_in = node_inputs(api, fused);
+    std::vector<std::string> fused_names;
+    for (const OrtValueInfo* vi : fused_in) fused_names.push_back(value_name(api, vi));
+    auto fused_index = [&](size_t body_i) -> size_t {
+        if (body_i >= body_in.size() || !body_in[body_i]) return SIZE_MAX;
+        const std::string nm = value_name(api, body_in[body_i]);
+        for (size_t j = 0; j < fused_names.size(); ++j)
+            if (fused_names[j] == nm) return j;
+        return SIZE_MAX;
+    };
+    k->fused_a = fused_index(0);
+    if (k->fused_a == SIZE_MAX) fail(ORT_EP_FAIL, "input A is not an input of the fused node");
+
+    // Constant weights are read from the graph now and uploaded once.
+    bool all_const = true;
+    const void* host[3] = {nullptr, nullptr, nullptr};
+    size_t bytes[3] = {0, 0, 0};
+    for (int r = 0; r < 3; ++r) {
+        const size_t bi = (size_t)r + 1;
+        k->fused_w[r] = fused_index(bi);
+        if (bi >= f.inputs.size() || !f.inputs[bi].present) continue;
+        const OrtValue* v = nullptr;
+        if (f.inputs[bi].constant) ORT_OK(api, ValueInfo_GetInitializerValue(body_in[bi], &v));
+        if (!v) {
+            all_const = false;
+            continue;
+        }
+        host[r] = tensor_data(api, v);
+        bytes[r] = tensor_bytes(api, v);
+    }
+    mnb_session* sess = ep_session(ep);
+    if (all_const) {
+        mnb_ok(mnb_weights_upload(sess, &k->prob, host[0], bytes[0], host[1], bytes[1],
+                                  host[2], bytes[2], &k->weights),
+               "uploading MatMulNBits weights at Compile");
+        k->resident = true;
+    } else {
+        for (int r = 0; r < 3; ++r) {
+            const size_t bi = (size_t)r + 1;
+            if (bi < f.inputs.size() && f.inputs[bi].present && k->fused_w[r] == SIZE_MAX)
+                fail(ORT_EP_FAIL, "weight input %d is neither constant nor a fused-node input", r + 1);
+        }
+    }
+    return k;
+}
+
+OrtStatus* ORT_API_CALL ep_compile(OrtEp* self, const OrtGraph** graphs, const OrtNode** fused,
+                                   size_t count, OrtNodeComputeInfo** infos,
+                                   OrtNode** ep_context_nodes) noexcept {
+    Ep* ep = as_ep(self);
+    // Every out-slot is defined before anything can fail (reference: rust/src/ep.rs:1906-1913).
+    for (size_t i = 0; infos && i < count; ++i) infos[i] = nullptr;
+    for (size_t i = 0; ep_context_nodes && i < count; ++i) ep_context_nodes[i] = nullptr;
+    std::vector<ComputeInfo*> made;
+    OrtStatus* st = guarded(ep ? ep->api : nullptr, "Compile", [&] {
+        if (!ep || !graphs || !fused || !infos) fail(ORT_INVALID_ARGUMENT, "null Compile argument");
+        for (size_t i = 0; i < count; ++i) {
+            auto ci = std::make_unique<ComputeInfo>();
+            std::memset(&ci->base, 0, sizeof(ci->base));
+            ci->base.ort_version_supported = ep->factory->version;
+            ci->base.CreateState = ci_create_state;
+            ci->base.Compute = ci_compute;
+            ci->base.ReleaseState = ci_release_state;
+            ci->ep = ep;
+            ci->kernel = compile_one(ep, graphs[i], fused[i]);
+            made.push_back(ci.release());
+        }
+    });
+    if (st) {
+        for (ComputeInfo* ci : made) {
+            if (ci->kernel && ci->kernel->weights) mnb_weights_release(ci->kernel->weights);
+            delete ci;
+        }
+        return st;
+    }
+    for (size_t i = 0; i < count; ++i) infos[i] = &made[i]->base;
+    return nullptr;
+}
+
+void ORT_API_CALL ep_release_infos(OrtEp*, OrtNodeComputeInfo** infos, size_t n) noexcept {
+    for (size_t i = 0; infos && i < n; ++i) {
+        ComputeInfo* ci = as_info(infos[i]);
+        if (!ci) continue;
+        if (ci->kernel && ci->kernel->weights) mnb_weights_release(ci->kernel->weights);
+        delete ci;
+    }
+}
+
+// ---- OrtEpFactory ---------------------------------------------------------------------------
+
+const char* ORT_API_CALL f_get_name(const OrtEpFactory*) noexcept { return kEpName; }
+const char* ORT_API_CALL f_get_vendor(const OrtEpFactory*) noexcept { return kEpVendor; }
+uint32_t ORT_API_CALL f_get_vendor_id(const OrtEpFactory*) noexcept { return kAmdVendorId; }
+const char* ORT_API_CALL f_get_version(const OrtEpFactory*) noexcept { return kEpVersion; }
+bool ORT_API_CALL f_is_stream_aware(const OrtEpFactory*) noexcept { return false; }
+
+// HIP devices this library can run on (gfx950), in HIP ordinal order.
+std::vector<int> usable_hip_devices() {
+    std::vector<int> out;
+    int count = 0;
+    if (mnb_device_count(&count) != MNB_OK) return out;
+    for (int i = 0; i < count; ++i) {
+        char arch[64] = {0};
+        if (mnb_device_arch(i, arch, sizeof(arch)) != MNB_OK) continue;
+        if (std::strncmp(arch, "gfx950", 6) == 0) out.push_back(i);
+    }
+    return out;
+}
+
+void get_supported_devices(Factory* f, const OrtHardwareDevice* const* devices, size_t num,
+                           OrtEpDevice** ep_devices, size_t max_ep_devices, size_t* num_out) {
+    const OrtApi* api = f->api;
+    *num_out = 0;
+    const std::vector<int> hip = usable_hip_devices();
+    if (hip.empty()) {
+        claim_log("no gfx950 device is visible; advertising none (models run on the CPU EP)");
+        return;
+    }
+    if (!ep_devices || max_ep_devices == 0) return;
+    // Correlate the k-th AMD GPU hardware device with the k-th gfx950 HIP device; fall back to
+    // any GPU-typed device (reference: rust/src/factory.rs:~290-330).
+    std::vector<const OrtHardwareDevice*> amd, gpus;
+    for (size_t i = 0; devices && i < num; ++i) {
+        const OrtHardwareDevice* d = devices[i];
+        if (!d || api->HardwareDevice_Type(d) != OrtHardwareDeviceType_GPU) continue;
+        gpus.push_back(d);
+        if (api->HardwareDevice_VendorId(d) == kAmdVendorId) amd.push_back(d);
+    }
+    const std::vector<const OrtHardwareDevice*>& pool = amd.empty() ? gpus : amd;
+    size_t written = 0;
+    for (size_t i = 0; i < hip.size() && i < pool.size() && written < max_ep_devices; ++i) {
+        OrtKeyValuePairs* meta = nullptr;
+        api->CreateKeyValuePairs(&meta);
+        const std::string idx = std::to_string(hip[i]);
+        char arch[64] = {0};
+        mnb_device_arch(hip[i], arch, sizeof(arch));
+        if (meta) {
+            api->AddKeyValuePair(meta, kMetaDeviceIndex, idx.c_str());
+            api->AddKeyValuePair(meta, "mi355x.arch", arch);
+            api->AddKeyValuePair(meta, "mi355x.correlation", amd.empty() ? "device_type" : "vendor_id");
+        }
+        OrtEpDevice* epd = nullptr;
+        OrtStatus* st = f->ep_api->CreateEpDevice(&f->base, pool[i], meta, nullptr, &epd);
+        if (meta) api->ReleaseKeyValuePairs(meta);
+        ort_check(api, st, "CreateEpDevice");
+        ep_devices[written++] = epd;
+    }
+    *num_out = written;
+}
+
+OrtStatus* ORT_API_CALL f_get_supported_devices(OrtEpFactory* self,
+                                                const OrtHardwareDevice* const* devices,
+                                                size_t num, OrtEpDevice** ep_devices,
+                                                size_t max_ep_devices, size_t* num_out) noexcept {
+    Factory* f = as_factory(self);
+    return guarded(f ? f->api : nullptr, "GetSupportedDevices", [&] {
+        if (!f || !num_out) fail(ORT_INVALID_ARGUMENT, "null GetSupportedDevices argument");
+        get_supported_devices(f, devices, num, ep_devices, max_ep_devices, num_out);
+    });
+}
+
+OrtStatus* ORT_API_CALL f_create_ep(OrtEpFactory* self, const OrtHardwareDevice* const*,
+                                    const OrtKeyValuePairs* const* metadata, size_t num_devices,
+                                    const OrtSessionOptions* so, const OrtLogger*, OrtEp** out) noexcept {
+    Factory* f = as_factory(self);
+    if (out) *out = nullptr;
+    return guarded(f ? f->api : nullptr, "CreateEp", [&] {
+        if (!f || !out) fail(ORT_INVALID_ARGUMENT, "null CreateEp argument");
+        if (num_devices != 1)
+            fail(ORT_INVALID_ARGUMENT, "one device per session is supported, %zu were selected",
+                 num_devices);
+        const OrtApi* api = f->api;
+        int device = -1;
+        if (metadata && metadata[0]) {
+            const char* v = api->GetKeyValue(metadata[0], kMetaDeviceIndex);
+            if (v && *v) device = std::atoi(v);
+        }
+        std::string opt;
+        if (device < 0 && session_option(api, so, "ep.device_index", &opt)) device = std::atoi(opt.c_str());
+        if (device < 0) device = 0;
+        auto ep = std::make_unique<Ep>();
+        std::memset(&ep->base, 0, sizeof(ep->base));
+        ep->base.ort_version_supported = f->version;
+        ep->base.GetName = ep_get_name;
+        ep->base.GetCapability = ep_get_capability;
+        ep->base.Compile = ep_compile;
+        ep->base.ReleaseNodeComputeInfos = ep_release_infos;
+        ep->factory = f;
+        ep->api = api;
+        ep->ep_api = f->ep_api;
+        ep->device = device;
+        if (session_option(api, so, "ep.keep_constant_initializers", &opt))
+            ep->keep_constant_initializers = opt == "1" || opt == "true";
+        // ep.max_claim_ops: comma-separated allowlist (reference: rust/src/ep.rs:39-160);
+        // claiming is on only when MatMulNBits is listed.
+        if (session_option(api, so, "ep.max_claim_ops", &opt))
+            ep->claim_enabled = opt.find("MatMulNBits") != std::string::npos;
+        // The HIP device is opened by the first Compile, so creating a session (and claiming
+        // nodes) costs no device work.
+        *out = &ep.release()->base;
+    });
+}
+
+void ORT_API_CALL f_release_ep(OrtEpFactory*, OrtEp* p) noexcept {
+    Ep* ep = as_ep(p);
+    if (!ep) return;
+    if (ep->session) mnb_session_destroy(ep->session);
+    delete ep;
+}
+
+OrtStatus* ORT_API_CALL f_create_allocator(OrtEpFactory*, const OrtMemoryInfo*,
+                                           const OrtKeyValuePairs*, OrtAllocator** out) noexcept {
+    if (out) *out = nullptr;   // host I/O: ORT's CPU allocator serves every tensor
+    return nullptr;
+}
+
+void ORT_API_CALL f_release_allocator(OrtEpFactory*, OrtAllocator*) noexcept {}
+
+OrtStatus* ORT_API_CALL f_create_data_transfer(OrtEpFactory*, OrtDataTransferImpl** out) noexcept {
+    if (out) *out = nullptr;
+    return nullptr;
+}
+
+OrtStatus* ORT_API_CALL f_create_sync_stream(OrtEpFactory*, const OrtMemoryDevice*,
+                                             const OrtKeyValuePairs*, OrtSyncStreamImpl** out) noexcept {
+    if (out) *out = nullptr;
+    return nullptr;
+}
+
+// ---- ABI negotiation --------------------------------------------------------------------------
+
+struct Negotiated {
+    const OrtApi* api = nullptr;
+    const OrtEpApi* ep_api = nullptr;
+    uint32_t version = 0;
+};
+
+// Asks the host for the newest OrtApi from the built version down to the minimum (reference:
+// rust/src/sys.rs:193-277).  Older tables are prefixes of newer ones, and ORT reads our vtables
+// only up to the version we report.
+Negotiated negotiate(const OrtApiBase* base, std::string* err) {
+    Negotiated n;
+    if (!base || !base->GetApi) {
+        *err = "ONNX Runtime passed no usable OrtApiBase";
+        return n;
+    }
+    for (uint32_t v = kVersionBuilt; v >= kVersionMin; --v) {
+        const OrtApi* api = base->GetApi(v);
+        if (api) {
+            n.api = api;
+            n.version = v;
+            break;
+        }
+    }
+    if (!n.api) {
+        const char* hv = base->GetVersionString ? base->GetVersionString() : nullptr;
+        char buf[256];
+        std::snprintf(buf, sizeof(buf),
+                      "%s requires ONNX Runtime with ORT_API_VERSION >= %u (built against %u); "
+                      "this host (%s) offered none of them",
+                      kEpName, kVersionMin, kVersionBuilt, hv ? hv : "unknown version");
+        *err = buf;
+        return n;
+    }
+    n.ep_api = n.api->GetEpApi ? n.api->GetEpApi() : nullptr;
+    if (!n.ep_api) {
+        *err = "the host's OrtApi has no OrtEpApi (plugin EPs unsupported)";
+        n.api = nullptr;
+    }
+    return n;
+}
+
+}  // namespace
+}  // namespace mi355x_ep
+
+using namespace mi355x_ep;
+
+MI355X_EXPORT OrtStatus* CreateEpFactories(const char* registered_name,
+                                           const OrtApiBase* ort_api_base, const OrtLogger*,
+                                           OrtEpFactory** factories, size_t max_factories,
+                                           size_t* num_factories) {
+    std::string err;
+    const Negotiated n = negotiate(ort_api_base, &err);
+    if (!n.api) {
+        // Build the error status from the oldest table, whose CreateStatus slot never moved.
+        const OrtApi* any = ort_api_base && ort_api_base->GetApi ? ort_api_base->GetApi(1) : nullptr;
+        return to_status(any, ORT_INVALID_ARGUMENT, err);
+    }
+    return guarded(n.api, "CreateEpFactories", [&] {
+        if (!factories || !num_factories) fail(ORT_INVALID_ARGUMENT, "null factory out-parameters");
+        *num_factories = 0;
+        if (max_factories < 1) fail(ORT_INVALID_ARGUMENT, "ORT allowed room for no factory");
+        auto f = std::make_unique<Factory>();
+        std::memset(&f->base, 0, sizeof(f->base));
+        f->api = n.api;
+        f->ep_api = n.ep_api;
+        f->version = n.version;
+        f->registered_name = registered_name ? registered_name : kEpName;
+        OrtEpFactory& b = f->base;
+        b.ort_version_supported = n.version;
+        b.GetName = f_get_name;
+        b.GetVendor = f_get_vendor;
+        b.GetSupportedDevices = f_get_supported_devices;
+        b.CreateEp = f_create_ep;
+        b.ReleaseEp = f_release_ep;
+        b.GetVendorId = f_get_vendor_id;
+        b.GetVersion = f_get_version;
+        b.CreateAllocator = f_create_allocator;
+        b.ReleaseAllocator = f_release_allocator;
+        b.CreateDataTransfer = f_create_data_transfer;
+        b.IsStreamAware = f_is_stream_aware;
+        b.CreateSyncStreamForDevice = f_create_sync_stream;
+        factories[0] = &f.release()->base;
+        *num_factories = 1;
+    });
+}
+
+MI355X_EXPORT OrtStatus* ReleaseEpFactory(OrtEpFactory* factory) {
+    delete as_factory(factory);
+    return nullptr;
+}
+
+MI355X_EXPORT uint64_t OrtEpMi355xGetComputeCount(void) { return g_compute_count.load(); }
+
+MI355X_EXPORT void OrtEpMi355xResetComputeCount(void) { g_compute_count.store(0); }

@@ -115,6 +115,36 @@ __device__ __forceinline__ int load_zp(const uint8_t* __restrict__ Z, int64_t n,
     }
 }
 
+// DPP lane permutation of a float (gfx9 dpp_ctrl encodings: quad_perm 0x00-0xFF,
+// row_mirror 0x140, row_half_mirror 0x141).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL,
+                                                                0xF, 0xF, false));
+}
+
+// Sum over aligned groups of G lanes (G = 1, 2, 4, ..., 64); every lane of a group receives the
+// group's sum.  Quad permutes and row mirrors are DPP modifiers on the add; the 16- and 32-lane
+// steps exchange rows / half-waves with v_permlane16_swap / v_permlane32_swap.  The pairing is
+// fixed, so the result is deterministic.
+__device__ __forceinline__ float group_sum(float v, int G) {
+    if (G >= 2) v += dpp_f<0xB1>(v);     // quad_perm [1,0,3,2]: lane ^ 1
+    if (G >= 4) v += dpp_f<0x4E>(v);     // quad_perm [2,3,0,1]: lane ^ 2
+    if (G >= 8) v += dpp_f<0x141>(v);    // row_half_mirror: lane i <-> 7 - i within 8
+    if (G >= 16) v += dpp_f<0x140>(v);   // row_mirror: lane i <-> 15 - i within 16
+    if (G >= 32) {
+        const uint32_t x = __builtin_bit_cast(uint32_t, v);
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        v = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+    }
+    if (G >= 64) {
+        const uint32_t x = __builtin_bit_cast(uint32_t, v);
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        v = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+    }
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;

@@ -251,6 +251,16 @@ int mnb_device_count(int* count) {
     return MNB_OK;
 }
 
+int mnb_device_arch(int device_index, char* buf, size_t len) {
+    if (!buf || len == 0) return fail(MNB_ERR_INVALID, "buffer is NULL or empty");
+    buf[0] = '\0';
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device_index);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    std::snprintf(buf, len, "%s", prop.gcnArchName);
+    return MNB_OK;
+}
+
 int mnb_session_create(int device_index, mnb_session** out) {
     if (!out) return fail(MNB_ERR_INVALID, "out is NULL");
     *out = nullptr;

@@ -90,6 +90,7 @@ def load() -> C.CDLL:
         "mnb_quantize_a_int8": (C.c_int, [i64, i64, i32, i32, vp, vp, vp, vp, vp]),
         "mnb_moe_grouped": (C.c_int, [C.POINTER(MoeProblem), vp, vp, vp, vp, vp, vp, vp, vp]),
         "mnb_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+        "mnb_device_arch": (C.c_int, [C.c_int, C.c_char_p, sz]),
         "mnb_session_create": (C.c_int, [C.c_int, C.POINTER(vp)]),
         "mnb_session_destroy": (C.c_int, [vp]),
         "mnb_session_stream": (vp, [vp]),

@@ -1,0 +1,191 @@
+"""ctypes driver for the mock ONNX Runtime host (tests/mock_ort/mock_ort.cpp) — test helper.
+
+The mock host dlopens the plugin EP and plays ORT's side of the plugin-EP ABI over an in-memory
+graph.  This module wraps it so a test can build a one-node (or larger) graph of MatMulNBits
+nodes, run GetCapability / Compile / Compute, and read the output tensors.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+MOCK_SO = Path(__file__).resolve().parent / "mock_ort" / "build" / "libmock_ort.so"
+EP_SO = ROOT / "onnxruntime-ep-vulkan_amd" / "lib" / "libonnxruntime_mi355x_ep.so"
+
+FLOAT, UINT8, INT32, FLOAT16 = 1, 2, 6, 10
+NP_ELEM = {np.dtype(np.float32): FLOAT, np.dtype(np.uint8): UINT8, np.dtype(np.int32): INT32,
+           np.dtype(np.float16): FLOAT16}
+ORT_INVALID_ARGUMENT = 2
+ORT_EP_FAIL = 11   # onnxruntime_error_code.h: OK=0, FAIL, INVALID_ARGUMENT, ..., INVALID_GRAPH=10, EP_FAIL=11
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not MOCK_SO.exists():
+            raise FileNotFoundError(f"{MOCK_SO} is missing: run `make -C tests/mock_ort`")
+        L = C.CDLL(str(MOCK_SO))
+        i64p = C.POINTER(C.c_int64)
+        sig = {
+            "mock_last_error": (C.c_char_p, []),
+            "mock_live_statuses": (C.c_long, []),
+            "mock_created_statuses": (C.c_long, []),
+            "mock_bad_status_release": (C.c_int, []),
+            "mock_init": (C.c_int, [C.c_char_p, C.c_uint]),
+            "mock_factory_info": (C.c_int, [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t,
+                                            C.POINTER(C.c_uint), C.POINTER(C.c_uint)]),
+            "mock_supported_devices": (C.c_int, [C.c_int, C.c_int]),
+            "mock_device_meta": (C.c_char_p, [C.c_int, C.c_char_p]),
+            "mock_session_option": (None, [C.c_char_p, C.c_char_p]),
+            "mock_create_ep": (C.c_int, [C.c_int]),
+            "mock_create_ep_n": (C.c_int, [C.c_int]),
+            "mock_ep_name": (C.c_char_p, []),
+            "mock_graph_reset": (None, []),
+            "mock_add_value": (C.c_int, [C.c_char_p, C.c_int, C.c_int, i64p, C.c_void_p, C.c_size_t]),
+            "mock_add_node": (C.c_int, [C.c_char_p] * 6),
+            "mock_get_capability": (C.c_int, [C.c_int, C.c_char_p, C.c_size_t]),
+            "mock_compile": (C.c_int, []),
+            "mock_feed": (C.c_int, [C.c_char_p, C.c_int, C.c_int, i64p, C.c_void_p, C.c_size_t]),
+            "mock_compute": (C.c_int, [C.c_int]),
+            "mock_fetch": (C.c_int, [C.c_char_p, C.c_void_p, C.c_size_t, i64p, C.c_int]),
+            "mock_shutdown": (C.c_int, []),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def EP_COUNT() -> int:
+    """OrtEpMi355xGetComputeCount of the EP library (MatMulNBits Computes that launched)."""
+    import ctypes
+    f = ctypes.CDLL(str(EP_SO)).OrtEpMi355xGetComputeCount
+    f.restype = ctypes.c_uint64
+    return int(f())
+
+
+def err() -> str:
+    return lib().mock_last_error().decode(errors="replace")
+
+
+def _dims(shape):
+    arr = (C.c_int64 * max(1, len(shape)))(*[int(d) for d in shape])
+    return arr
+
+
+class Host:
+    """One mock ORT process-level environment with the EP library loaded."""
+
+    def __init__(self, api_version: int = 28, ep_path: Path = EP_SO):
+        self.L = lib()
+        self._keep = []
+        rc = self.L.mock_init(str(ep_path).encode(), api_version)
+        self.init_rc = rc
+        if rc:
+            self.init_error = err()
+
+    def close(self):
+        rc = self.L.mock_shutdown()
+        self._keep.clear()
+        return rc
+
+    # ---- factory / device ----
+    def factory_info(self):
+        name = C.create_string_buffer(128)
+        vendor = C.create_string_buffer(128)
+        vid, ver = C.c_uint(), C.c_uint()
+        assert self.L.mock_factory_info(name, 128, vendor, 128, C.byref(vid), C.byref(ver)) == 0
+        return name.value.decode(), vendor.value.decode(), vid.value, ver.value
+
+    def supported_devices(self, n_amd=1, n_other=0) -> int:
+        return self.L.mock_supported_devices(n_amd, n_other)
+
+    def device_meta(self, i, key):
+        v = self.L.mock_device_meta(i, key.encode())
+        return None if v is None else v.decode()
+
+    def option(self, key, value):
+        self.L.mock_session_option(key.encode(), str(value).encode())
+
+    def create_ep(self, device: int = 0) -> int:
+        return self.L.mock_create_ep(device)
+
+    # ---- graph ----
+    def reset(self):
+        self.L.mock_graph_reset()
+        self._keep.clear()
+
+    def value(self, name, elem, shape, data: np.ndarray | None = None):
+        ptr, nbytes = None, 0
+        if data is not None:
+            data = np.ascontiguousarray(data)
+            self._keep.append(data)
+            ptr, nbytes = data.ctypes.data, data.nbytes
+        assert self.L.mock_add_value(name.encode(), elem, len(shape), _dims(shape), ptr, nbytes) == 0
+
+    def node(self, op, domain, name, inputs, outputs, attrs: dict):
+        a = ",".join(f"{k}={int(v)}" for k, v in attrs.items())
+        rc = self.L.mock_add_node(op.encode(), domain.encode(), name.encode(),
+                                  ",".join(inputs).encode(), ",".join(outputs).encode(), a.encode())
+        assert rc == 0, err()
+
+    def get_capability(self, nested=False):
+        buf = C.create_string_buffer(4096)
+        n = self.L.mock_get_capability(int(nested), buf, 4096)
+        claimed = [s for s in buf.value.decode().split(";") if s]
+        return n, claimed
+
+    def compile(self) -> int:
+        return self.L.mock_compile()
+
+    def feed(self, name, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        self._keep.append(arr)
+        assert self.L.mock_feed(name.encode(), NP_ELEM[arr.dtype], arr.ndim, _dims(arr.shape),
+                                arr.ctypes.data, arr.nbytes) == 0
+
+    def compute(self, group=0) -> int:
+        return self.L.mock_compute(group)
+
+    def fetch(self, name, dtype, max_elems):
+        out = np.empty(max_elems, dtype=dtype)
+        dims = (C.c_int64 * 8)()
+        r = self.L.mock_fetch(name.encode(), out.ctypes.data, out.nbytes, dims, 8)
+        assert r >= 0, err()
+        shape = tuple(dims[i] for i in range(r))
+        n = int(np.prod(shape)) if shape else 1
+        return out[:n].reshape(shape)
+
+
+def add_matmul_nbits(h: Host, name: str, inp: dict, N: int, K: int, bits: int, bs: int,
+                     a_shape, a_dtype=np.float16, const_weights=True, acc_level=None,
+                     extra_inputs=(), y_name=None):
+    """Adds one MatMulNBits node with inputs from an oracle make_inputs() dict."""
+    el = FLOAT16 if np.dtype(a_dtype) == np.float16 else FLOAT
+    a_name, y_name = f"{name}_A", y_name or f"{name}_Y"
+    h.value(a_name, el, a_shape)
+    h.value(y_name, el, tuple(a_shape[:-1]) + (N,))
+    ins = [a_name]
+    for role, arr, elem in (("B", inp["B"], UINT8), ("scales", inp["scales"], el),
+                            ("zp", inp.get("zp"), UINT8)):
+        if arr is None:
+            if role == "zp" and extra_inputs:
+                ins.append("")
+            continue
+        vn = f"{name}_{role}"
+        h.value(vn, elem, arr.shape, arr if const_weights else None)
+        ins.append(vn)
+    ins.extend(extra_inputs)
+    attrs = {"K": K, "N": N, "bits": bits, "block_size": bs}
+    if acc_level is not None:
+        attrs["accuracy_level"] = acc_level
+    h.node("MatMulNBits", "com.microsoft", name, ins, [y_name], attrs)
+    return a_name, y_name

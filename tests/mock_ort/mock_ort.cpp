@@ -1,0 +1,836 @@
+// A mock ONNX Runtime host for the MI355X plugin EP — TEST INFRASTRUCTURE.
+//
+// It plays ORT's side of the plugin-EP ABI the way the reference's Rust mock host does
+// (rust/tests/mock_ort/mod.rs:1-60, driven through dlopen in rust/tests/cdylib_load.rs:1-50):
+// an OrtApiBase whose OrtApi / OrtEpApi implement only the calls an EP may make, over an
+// in-memory graph, so the library is loaded by `dlopen` and driven through CreateEpFactories ->
+// GetSupportedDevices -> CreateEp -> GetCapability -> Compile -> Compute exactly as ORT would.
+// Every slot the mock does not implement is NULL, so an EP that calls outside the contract
+// crashes the test instead of passing it.  Contract checks recorded for the tests:
+//   * every OrtStatus the mock creates is released exactly once (live count returns to 0);
+//   * out-parameters are written before any failure (Compile's infos are NULL or valid);
+//   * the EP only fuses nodes of the graph it was handed.
+// The API version the mock offers is selectable, to exercise ABI negotiation.
+//
+// Exposed to Python (ctypes) through the mock_* functions at the end of this file.
+#include <dlfcn.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "onnxruntime_c_api.h"
+
+// ---- the opaque ORT objects, as this host defines them ----------------------------------------
+
+struct OrtStatus {
+    OrtErrorCode code;
+    std::string msg;
+};
+struct OrtTensorTypeAndShapeInfo {
+    int32_t elem = 0;
+    std::vector<int64_t> dims;
+};
+struct OrtTypeInfo {
+    OrtTensorTypeAndShapeInfo tensor;
+};
+struct OrtValueInfo {
+    std::string name;
+    OrtTypeInfo type;
+    bool constant = false;
+    std::vector<uint8_t> init;       // initializer bytes when constant
+};
+struct OrtValue {
+    int32_t elem = 0;
+    std::vector<int64_t> dims;
+    const void* data = nullptr;      // borrowed (inputs, initializers) or owned (outputs)
+    std::vector<uint8_t> owned;
+    size_t bytes = 0;
+};
+struct OrtOpAttr {
+    std::string name;
+    int64_t value = 0;
+};
+struct OrtNode {
+    std::string op_type, domain, name;
+    std::vector<OrtValueInfo*> inputs;   // nullptr for an absent optional input
+    std::vector<OrtValueInfo*> outputs;
+    std::vector<OrtOpAttr> attrs;
+};
+struct OrtGraph {
+    std::vector<OrtNode*> nodes;
+    OrtNode* parent = nullptr;
+};
+struct OrtKeyValuePairs {
+    std::map<std::string, std::string> kv;
+    std::vector<const char*> keys, values;
+};
+struct OrtHardwareDevice {
+    OrtHardwareDeviceType type;
+    uint32_t vendor_id, device_id;
+};
+struct OrtEpDevice {
+    OrtEpFactory* factory;
+    const OrtHardwareDevice* hw;
+    OrtKeyValuePairs meta;
+};
+struct OrtEpGraphSupportInfo {
+    const OrtGraph* graph;
+    std::vector<std::vector<const OrtNode*>> groups;
+    std::vector<bool> drop;
+};
+struct OrtSessionOptions {
+    std::map<std::string, std::string> config;
+};
+struct OrtKernelContext {
+    std::vector<OrtValue*> inputs;
+    std::vector<std::unique_ptr<OrtValue>> outputs;
+    std::vector<int32_t> out_elem;
+};
+struct OrtLogger {};
+struct OrtNodeComputeContext {};
+
+namespace {
+
+std::string g_err;
+long g_live_status = 0;
+long g_created_status = 0;
+std::set<const OrtStatus*> g_status_set;
+bool g_bad_release = false;
+
+void set_err(const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+}
+
+OrtStatus* mk_status(OrtErrorCode code, const std::string& msg) {
+    OrtStatus* s = new OrtStatus{code, msg};
+    ++g_live_status;
+    ++g_created_status;
+    g_status_set.insert(s);
+    return s;
+}
+
+// ---- OrtApi implementation -----------------------------------------------------------------
+
+#define NX noexcept
+
+OrtStatus* ORT_API_CALL m_CreateStatus(OrtErrorCode code, const char* msg) NX {
+    return mk_status(code, msg ? msg : "");
+}
+OrtErrorCode ORT_API_CALL m_GetErrorCode(const OrtStatus* s) NX { return s->code; }
+const char* ORT_API_CALL m_GetErrorMessage(const OrtStatus* s) NX { return s->msg.c_str(); }
+void ORT_API_CALL m_ReleaseStatus(OrtStatus* s) NX {
+    if (!s) return;
+    if (!g_status_set.count(s)) {
+        g_bad_release = true;   // double release or a foreign pointer
+        return;
+    }
+    g_status_set.erase(s);
+    --g_live_status;
+    delete s;
+}
+
+OrtStatus* ORT_API_CALL m_Graph_GetNumNodes(const OrtGraph* g, size_t* n) NX {
+    *n = g->nodes.size();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Graph_GetNodes(const OrtGraph* g, const OrtNode** out, size_t n) NX {
+    if (n < g->nodes.size()) return mk_status(ORT_INVALID_ARGUMENT, "node array too small");
+    for (size_t i = 0; i < g->nodes.size(); ++i) out[i] = g->nodes[i];
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Graph_GetParentNode(const OrtGraph* g, const OrtNode** out) NX {
+    *out = g->parent;
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Node_GetName(const OrtNode* n, const char** out) NX {
+    *out = n->name.c_str();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Node_GetOperatorType(const OrtNode* n, const char** out) NX {
+    *out = n->op_type.c_str();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Node_GetDomain(const OrtNode* n, const char** out) NX {
+    *out = n->domain.c_str();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Node_GetNumInputs(const OrtNode* n, size_t* out) NX {
+    *out = n->inputs.size();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Node_GetInputs(const OrtNode* n, const OrtValueInfo** out, size_t k) NX {
+    if (k < n->inputs.size()) return mk_status(ORT_INVALID_ARGUMENT, "input array too small");
+    for (size_t i = 0; i < n->inputs.size(); ++i) out[i] = n->inputs[i];
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Node_GetNumOutputs(const OrtNode* n, size_t* out) NX {
+    *out = n->outputs.size();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Node_GetOutputs(const OrtNode* n, const OrtValueInfo** out, size_t k) NX {
+    if (k < n->outputs.size()) return mk_status(ORT_INVALID_ARGUMENT, "output array too small");
+    for (size_t i = 0; i < n->outputs.size(); ++i) out[i] = n->outputs[i];
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_Node_GetAttributeByName(const OrtNode* n, const char* name,
+                                                  const OrtOpAttr** out) NX {
+    *out = nullptr;
+    for (const OrtOpAttr& a : n->attrs)
+        if (a.name == name) {
+            *out = &a;
+            return nullptr;
+        }
+    static const char* known[] = {"K", "N", "bits", "block_size", "accuracy_level", "weight_prepacked"};
+    for (const char* k : known)
+        if (!std::strcmp(k, name)) return nullptr;     // unset optional attribute
+    return mk_status(ORT_NOT_FOUND, std::string("no attribute ") + name);
+}
+OrtStatus* ORT_API_CALL m_ReadOpAttr(const OrtOpAttr* a, OrtOpAttrType type, void* data, size_t len,
+                                     size_t* out) NX {
+    if (type != ORT_OP_ATTR_INT) return mk_status(ORT_INVALID_ARGUMENT, "mock holds INT attributes only");
+    *out = sizeof(int64_t);
+    if (len < sizeof(int64_t)) return mk_status(ORT_INVALID_ARGUMENT, "buffer too small");
+    std::memcpy(data, &a->value, sizeof(int64_t));
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetValueInfoName(const OrtValueInfo* v, const char** out) NX {
+    *out = v->name.c_str();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetValueInfoTypeInfo(const OrtValueInfo* v, const OrtTypeInfo** out) NX {
+    *out = &v->type;
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_CastTypeInfoToTensorInfo(const OrtTypeInfo* t,
+                                                   const OrtTensorTypeAndShapeInfo** out) NX {
+    *out = &t->tensor;
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetTensorElementType(const OrtTensorTypeAndShapeInfo* t,
+                                               ONNXTensorElementDataType* out) NX {
+    *out = (ONNXTensorElementDataType)t->elem;
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetDimensionsCount(const OrtTensorTypeAndShapeInfo* t, size_t* out) NX {
+    *out = t->dims.size();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetDimensions(const OrtTensorTypeAndShapeInfo* t, int64_t* d, size_t n) NX {
+    for (size_t i = 0; i < n && i < t->dims.size(); ++i) d[i] = t->dims[i];
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_ValueInfo_IsConstantInitializer(const OrtValueInfo* v, bool* out) NX {
+    *out = v->constant;
+    return nullptr;
+}
+
+size_t elem_size(int32_t e) {
+    switch (e) {
+        case 1: return 4;
+        case 2: return 1;
+        case 10: return 2;
+        default: return 1;
+    }
+}
+
+// Initializer OrtValues handed out by ValueInfo_GetInitializerValue (owned by the host).
+std::vector<std::unique_ptr<OrtValue>> g_init_values;
+
+OrtStatus* ORT_API_CALL m_ValueInfo_GetInitializerValue(const OrtValueInfo* v, const OrtValue** out) NX {
+    *out = nullptr;
+    if (!v->constant) return nullptr;
+    auto val = std::make_unique<OrtValue>();
+    val->elem = v->type.tensor.elem;
+    val->dims = v->type.tensor.dims;
+    val->data = v->init.data();
+    val->bytes = v->init.size();
+    *out = val.get();
+    g_init_values.push_back(std::move(val));
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetTensorData(const OrtValue* v, const void** out) NX {
+    *out = v->data;
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetTensorMutableData(OrtValue* v, void** out) NX {
+    *out = const_cast<void*>(v->data);
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetTensorSizeInBytes(const OrtValue* v, size_t* out) NX {
+    *out = v->bytes;
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetTensorTypeAndShape(const OrtValue* v, OrtTensorTypeAndShapeInfo** out) NX {
+    *out = new OrtTensorTypeAndShapeInfo{v->elem, v->dims};
+    return nullptr;
+}
+void ORT_API_CALL m_ReleaseTensorTypeAndShapeInfo(OrtTensorTypeAndShapeInfo* t) NX { delete t; }
+
+OrtStatus* ORT_API_CALL m_KernelContext_GetInputCount(const OrtKernelContext* c, size_t* out) NX {
+    *out = c->inputs.size();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_KernelContext_GetOutputCount(const OrtKernelContext* c, size_t* out) NX {
+    *out = c->out_elem.size();
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_KernelContext_GetInput(const OrtKernelContext* c, size_t i, const OrtValue** out) NX {
+    if (i >= c->inputs.size()) return mk_status(ORT_INVALID_ARGUMENT, "input index out of range");
+    *out = c->inputs[i];
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_KernelContext_GetOutput(OrtKernelContext* c, size_t i, const int64_t* dims,
+                                                  size_t rank, OrtValue** out) NX {
+    if (i >= c->out_elem.size()) return mk_status(ORT_INVALID_ARGUMENT, "output index out of range");
+    auto v = std::make_unique<OrtValue>();
+    v->elem = c->out_elem[i];
+    v->dims.assign(dims, dims + rank);
+    size_t n = 1;
+    for (int64_t d : v->dims) n *= (size_t)d;
+    v->bytes = n * elem_size(v->elem);
+    v->owned.assign(v->bytes + 16, 0xCD);   // poison: unwritten output is detectable
+    v->data = v->owned.data();
+    *out = v.get();
+    if (c->outputs.size() <= i) c->outputs.resize(i + 1);
+    c->outputs[i] = std::move(v);
+    return nullptr;
+}
+
+OrtHardwareDeviceType ORT_API_CALL m_HardwareDevice_Type(const OrtHardwareDevice* d) NX { return d->type; }
+uint32_t ORT_API_CALL m_HardwareDevice_VendorId(const OrtHardwareDevice* d) NX { return d->vendor_id; }
+uint32_t ORT_API_CALL m_HardwareDevice_DeviceId(const OrtHardwareDevice* d) NX { return d->device_id; }
+
+void ORT_API_CALL m_CreateKeyValuePairs(OrtKeyValuePairs** out) NX { *out = new OrtKeyValuePairs(); }
+void ORT_API_CALL m_AddKeyValuePair(OrtKeyValuePairs* kv, const char* k, const char* v) NX { kv->kv[k] = v; }
+const char* ORT_API_CALL m_GetKeyValue(const OrtKeyValuePairs* kv, const char* k) NX {
+    auto it = kv->kv.find(k);
+    return it == kv->kv.end() ? nullptr : it->second.c_str();
+}
+void ORT_API_CALL m_ReleaseKeyValuePairs(OrtKeyValuePairs* kv) NX { delete kv; }
+
+OrtStatus* ORT_API_CALL m_HasSessionConfigEntry(const OrtSessionOptions* so, const char* k, int* out) NX {
+    *out = so->config.count(k) ? 1 : 0;
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_GetSessionConfigEntry(const OrtSessionOptions* so, const char* k, char* v,
+                                                size_t* size) NX {
+    auto it = so->config.find(k);
+    if (it == so->config.end()) return mk_status(ORT_INVALID_ARGUMENT, "no such config entry");
+    const size_t need = it->second.size() + 1;
+    if (!v) {
+        *size = need;
+        return nullptr;
+    }
+    if (*size < need) {
+        *size = need;
+        return mk_status(ORT_INVALID_ARGUMENT, "buffer too small");
+    }
+    std::memcpy(v, it->second.c_str(), need);
+    *size = need;
+    return nullptr;
+}
+
+// ---- OrtEpApi implementation ------------------------------------------------------------------
+
+std::vector<std::unique_ptr<OrtEpDevice>> g_ep_devices;
+
+OrtStatus* ORT_API_CALL m_CreateEpDevice(OrtEpFactory* f, const OrtHardwareDevice* hw,
+                                         const OrtKeyValuePairs* meta, const OrtKeyValuePairs*,
+                                         OrtEpDevice** out) NX {
+    auto d = std::make_unique<OrtEpDevice>();
+    d->factory = f;
+    d->hw = hw;
+    if (meta) d->meta.kv = meta->kv;   // ORT copies the metadata
+    *out = d.get();
+    g_ep_devices.push_back(std::move(d));
+    return nullptr;
+}
+OrtStatus* ORT_API_CALL m_AddNodesToFuse(OrtEpGraphSupportInfo* info, const OrtNode* const* nodes,
+                                         size_t n, const OrtNodeFusionOptions* opts) NX {
+    std::vector<const OrtNode*> group;
+    for (size_t i = 0; i < n; ++i) {
+        bool found = false;
+        for (const OrtNode* g : info->graph->nodes) found = found || g == nodes[i];
+        if (!found) return mk_status(ORT_INVALID_ARGUMENT, "node is not in the graph");
+        group.push_back(nodes[i]);
+    }
+    info->groups.push_back(group);
+    info->drop.push_back(opts ? opts->drop_constant_initializers : false);
+    return nullptr;
+}
+
+OrtApi g_api;
+OrtEpApi g_ep_api;
+uint32_t g_offered_version = ORT_API_VERSION;
+
+const OrtEpApi* ORT_API_CALL m_GetEpApi() NX { return &g_ep_api; }
+
+const OrtApi* ORT_API_CALL m_GetApi(uint32_t v) NX {
+    return (v >= 1 && v <= g_offered_version) ? &g_api : nullptr;
+}
+const char* ORT_API_CALL m_GetVersionString() NX { return "mock-1.28.0"; }
+OrtApiBase g_base = {m_GetApi, m_GetVersionString};
+
+void init_api() {
+    std::memset(&g_api, 0, sizeof(g_api));
+    std::memset(&g_ep_api, 0, sizeof(g_ep_api));
+    g_api.CreateStatus = m_CreateStatus;
+    g_api.GetErrorCode = m_GetErrorCode;
+    g_api.GetErrorMessage = m_GetErrorMessage;
+    g_api.ReleaseStatus = m_ReleaseStatus;
+    g_api.Graph_GetNumNodes = m_Graph_GetNumNodes;
+    g_api.Graph_GetNodes = m_Graph_GetNodes;
+    g_api.Graph_GetParentNode = m_Graph_GetParentNode;
+    g_api.Node_GetName = m_Node_GetName;
+    g_api.Node_GetOperatorType = m_Node_GetOperatorType;
+    g_api.Node_GetDomain = m_Node_GetDomain;
+    g_api.Node_GetNumInputs = m_Node_GetNumInputs;
+    g_api.Node_GetInputs = m_Node_GetInputs;
+    g_api.Node_GetNumOutputs = m_Node_GetNumOutputs;
+    g_api.Node_GetOutputs = m_Node_GetOutputs;
+    g_api.Node_GetAttributeByName = m_Node_GetAttributeByName;
+    g_api.ReadOpAttr = m_ReadOpAttr;
+    g_api.GetValueInfoName = m_GetValueInfoName;
+    g_api.GetValueInfoTypeInfo = m_GetValueInfoTypeInfo;
+    g_api.CastTypeInfoToTensorInfo = m_CastTypeInfoToTensorInfo;
+    g_api.GetTensorElementType = m_GetTensorElementType;
+    g_api.GetDimensionsCount = m_GetDimensionsCount;
+    g_api.GetDimensions = m_GetDimensions;
+    g_api.ValueInfo_IsConstantInitializer = m_ValueInfo_IsConstantInitializer;
+    g_api.ValueInfo_GetInitializerValue = m_ValueInfo_GetInitializerValue;
+    g_api.GetTensorData = m_GetTensorData;
+    g_api.GetTensorMutableData = m_GetTensorMutableData;
+    g_api.GetTensorSizeInBytes = m_GetTensorSizeInBytes;
+    g_api.GetTensorTypeAndShape = m_GetTensorTypeAndShape;
+    g_api.ReleaseTensorTypeAndShapeInfo = m_ReleaseTensorTypeAndShapeInfo;
+    g_api.KernelContext_GetInputCount = m_KernelContext_GetInputCount;
+    g_api.KernelContext_GetOutputCount = m_KernelContext_GetOutputCount;
+    g_api.KernelContext_GetInput = m_KernelContext_GetInput;
+    g_api.KernelContext_GetOutput = m_KernelContext_GetOutput;
+    g_api.HardwareDevice_Type = m_HardwareDevice_Type;
+    g_api.HardwareDevice_VendorId = m_HardwareDevice_VendorId;
+    g_api.HardwareDevice_DeviceId = m_HardwareDevice_DeviceId;
+    g_api.CreateKeyValuePairs = m_CreateKeyValuePairs;
+    g_api.AddKeyValuePair = m_AddKeyValuePair;
+    g_api.GetKeyValue = m_GetKeyValue;
+    g_api.ReleaseKeyValuePairs = m_ReleaseKeyValuePairs;
+    g_api.HasSessionConfigEntry = m_HasSessionConfigEntry;
+    g_api.GetSessionConfigEntry = m_GetSessionConfigEntry;
+    g_api.GetEpApi = m_GetEpApi;
+    g_ep_api.CreateEpDevice = m_CreateEpDevice;
+    g_ep_api.EpGraphSupportInfo_AddNodesToFuse = m_AddNodesToFuse;
+}
+
+// ---- host state ---------------------------------------------------------------------------------
+
+using CreateFn = OrtStatus* (*)(const char*, const OrtApiBase*, const OrtLogger*, OrtEpFactory**,
+                                size_t, size_t*);
+using ReleaseFn = OrtStatus* (*)(OrtEpFactory*);
+
+struct Group {
+    std::unique_ptr<OrtGraph> graph;      // the island as its own graph
+    std::unique_ptr<OrtNode> fused;       // the fused node ORT would create
+    OrtNodeComputeInfo* info = nullptr;
+};
+
+struct Host {
+    void* lib = nullptr;
+    CreateFn create = nullptr;
+    ReleaseFn release = nullptr;
+    OrtEpFactory* factory = nullptr;
+    std::vector<std::unique_ptr<OrtHardwareDevice>> hw;
+    std::vector<OrtEpDevice*> ep_devices;
+    OrtEp* ep = nullptr;
+    OrtSessionOptions so;
+    OrtLogger logger;
+    std::map<std::string, std::unique_ptr<OrtValueInfo>> values;
+    std::vector<std::unique_ptr<OrtNode>> nodes;
+    OrtGraph graph;
+    std::vector<Group> groups;
+    std::vector<bool> drop;
+    // host tensors for compute
+    std::map<std::string, OrtValue> feeds;
+    std::map<std::string, OrtValue> fetches;
+};
+Host* g = nullptr;
+
+int status_rc(OrtStatus* st) {
+    if (!st) return 0;
+    set_err("%s", st->msg.c_str());
+    const int code = (int)st->code;
+    m_ReleaseStatus(st);
+    return code ? code : -1;
+}
+
+std::vector<std::string> split(const char* s, char sep) {
+    std::vector<std::string> out;
+    if (!s) return out;
+    std::string cur;
+    for (const char* p = s;; ++p) {
+        if (*p == sep || *p == '\0') {
+            out.push_back(cur);
+            cur.clear();
+            if (!*p) break;
+        } else {
+            cur += *p;
+        }
+    }
+    return out;
+}
+
+}  // namespace
+
+// ---- the C surface the tests drive -----------------------------------------------------------------
+
+extern "C" {
+
+const char* mock_last_error(void) { return g_err.c_str(); }
+long mock_live_statuses(void) { return g_live_status; }
+long mock_created_statuses(void) { return g_created_status; }
+int mock_bad_status_release(void) { return g_bad_release ? 1 : 0; }
+
+// dlopen the EP and call CreateEpFactories with an OrtApiBase offering versions <= api_version.
+int mock_init(const char* ep_path, unsigned api_version) {
+    init_api();
+    g_offered_version = api_version;
+    delete g;
+    g = new Host();
+    g->lib = dlopen(ep_path, RTLD_NOW | RTLD_LOCAL);
+    if (!g->lib) {
+        set_err("dlopen: %s", dlerror());
+        return -1;
+    }
+    g->create = (CreateFn)dlsym(g->lib, "CreateEpFactories");
+    g->release = (ReleaseFn)dlsym(g->lib, "ReleaseEpFactory");
+    if (!g->create || !g->release) {
+        set_err("the library does not export CreateEpFactories / ReleaseEpFactory");
+        return -1;
+    }
+    OrtEpFactory* fs[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t n = 0;
+    int rc = status_rc(g->create("MI355XExecutionProvider", &g_base, &g->logger, fs, 4, &n));
+    if (rc) return rc;
+    if (n != 1 || !fs[0]) {
+        set_err("expected one factory, got %zu", n);
+        return -1;
+    }
+    g->factory = fs[0];
+    return 0;
+}
+
+// Factory identity: returns the negotiated version the factory reports.
+int mock_factory_info(char* name, size_t nlen, char* vendor, size_t vlen, unsigned* vendor_id,
+                      unsigned* version) {
+    if (!g || !g->factory) return -1;
+    std::snprintf(name, nlen, "%s", g->factory->GetName(g->factory));
+    std::snprintf(vendor, vlen, "%s", g->factory->GetVendor(g->factory));
+    *vendor_id = g->factory->GetVendorId(g->factory);
+    *version = g->factory->ort_version_supported;
+    return 0;
+}
+
+// Offers `n_amd` AMD GPUs and `n_other` other GPUs; returns the number of EP devices advertised.
+int mock_supported_devices(int n_amd, int n_other) {
+    if (!g || !g->factory) return -1;
+    g->hw.clear();
+    for (int i = 0; i < n_amd; ++i)
+        g->hw.push_back(std::make_unique<OrtHardwareDevice>(OrtHardwareDevice{OrtHardwareDeviceType_GPU, 0x1002, 0x75a3}));
+    for (int i = 0; i < n_other; ++i)
+        g->hw.push_back(std::make_unique<OrtHardwareDevice>(OrtHardwareDevice{OrtHardwareDeviceType_GPU, 0x10de, 0x2900}));
+    g->hw.push_back(std::make_unique<OrtHardwareDevice>(OrtHardwareDevice{OrtHardwareDeviceType_CPU, 0x1022, 0}));
+    std::vector<const OrtHardwareDevice*> hw;
+    for (auto& h : g->hw) hw.push_back(h.get());
+    OrtEpDevice* out[8] = {nullptr};
+    size_t n = 99;
+    int rc = status_rc(g->factory->GetSupportedDevices(g->factory, hw.data(), hw.size(), out, 8, &n));
+    if (rc) return -rc;
+    g->ep_devices.assign(out, out + n);
+    return (int)n;
+}
+
+const char* mock_device_meta(int i, const char* key) {
+    if (!g || i < 0 || i >= (int)g->ep_devices.size()) return nullptr;
+    auto it = g->ep_devices[i]->meta.kv.find(key);
+    return it == g->ep_devices[i]->meta.kv.end() ? nullptr : it->second.c_str();
+}
+
+void mock_session_option(const char* key, const char* value) {
+    if (g) g->so.config[key] = value;
+}
+
+// CreateEp on advertised device `i` (or, with i < 0, on no metadata at all).
+int mock_create_ep(int i) {
+    if (!g || !g->factory) return -1;
+    const OrtHardwareDevice* hw[1] = {g->hw.empty() ? nullptr : g->hw[0].get()};
+    const OrtKeyValuePairs* meta[1] = {nullptr};
+    if (i >= 0 && i < (int)g->ep_devices.size()) {
+        hw[0] = g->ep_devices[i]->hw;
+        meta[0] = &g->ep_devices[i]->meta;
+    }
+    OrtEp* ep = nullptr;
+    int rc = status_rc(g->factory->CreateEp(g->factory, hw, meta, 1, &g->so, &g->logger, &ep));
+    if (rc) return rc;
+    if (!ep) {
+        set_err("CreateEp returned success and no EP");
+        return -1;
+    }
+    g->ep = ep;
+    return 0;
+}
+
+int mock_create_ep_n(int num_devices) {
+    if (!g || !g->factory) return -1;
+    std::vector<const OrtHardwareDevice*> hw(num_devices, g->hw.empty() ? nullptr : g->hw[0].get());
+    std::vector<const OrtKeyValuePairs*> meta(num_devices, nullptr);
+    OrtEp* ep = nullptr;
+    int rc = status_rc(g->factory->CreateEp(g->factory, hw.data(), meta.data(), num_devices, &g->so,
+                                            &g->logger, &ep));
+    if (!rc && ep) g->ep = ep;
+    return rc;
+}
+
+const char* mock_ep_name(void) { return g && g->ep ? g->ep->GetName(g->ep) : nullptr; }
+
+void mock_graph_reset(void) {
+    if (!g) return;
+    g->values.clear();
+    g->nodes.clear();
+    g->graph = OrtGraph();
+    g->groups.clear();
+    g->drop.clear();
+    g->feeds.clear();
+    g->fetches.clear();
+}
+
+// A graph value; `data` non-NULL makes it a constant initializer (its bytes are copied).
+int mock_add_value(const char* name, int elem, int rank, const int64_t* dims, const void* data,
+                   size_t bytes) {
+    auto v = std::make_unique<OrtValueInfo>();
+    v->name = name;
+    v->type.tensor.elem = elem;
+    v->type.tensor.dims.assign(dims, dims + rank);
+    if (data) {
+        v->constant = true;
+        v->init.assign((const uint8_t*)data, (const uint8_t*)data + bytes);
+    }
+    g->values[name] = std::move(v);
+    return 0;
+}
+
+// A node: inputs/outputs are comma-separated value names ("" = absent optional input);
+// int_attrs is "K=64,N=32,bits=4".
+int mock_add_node(const char* op, const char* domain, const char* name, const char* inputs,
+                  const char* outputs, const char* int_attrs) {
+    auto n = std::make_unique<OrtNode>();
+    n->op_type = op;
+    n->domain = domain;
+    n->name = name;
+    for (const std::string& s : split(inputs, ',')) {
+        if (s.empty()) {
+            n->inputs.push_back(nullptr);
+            continue;
+        }
+        auto it = g->values.find(s);
+        if (it == g->values.end()) {
+            set_err("unknown value %s", s.c_str());
+            return -1;
+        }
+        n->inputs.push_back(it->second.get());
+    }
+    for (const std::string& s : split(outputs, ',')) {
+        auto it = g->values.find(s);
+        if (it == g->values.end()) {
+            set_err("unknown value %s", s.c_str());
+            return -1;
+        }
+        n->outputs.push_back(it->second.get());
+    }
+    for (const std::string& kv : split(int_attrs, ',')) {
+        if (kv.empty()) continue;
+        const size_t eq = kv.find('=');
+        n->attrs.push_back(OrtOpAttr{kv.substr(0, eq), std::atoll(kv.c_str() + eq + 1)});
+    }
+    g->graph.nodes.push_back(n.get());
+    g->nodes.push_back(std::move(n));
+    return 0;
+}
+
+// GetCapability on the whole graph (nested=1 pretends it is a control-flow body).  Returns the
+// number of fused groups; `out` receives "node[:drop|:keep];..." for the claimed nodes.
+int mock_get_capability(int nested, char* out, size_t len) {
+    if (!g || !g->ep) return -1;
+    OrtNode parent_stub;
+    g->graph.parent = nested ? &parent_stub : nullptr;
+    OrtEpGraphSupportInfo info{&g->graph, {}, {}};
+    int rc = status_rc(g->ep->GetCapability(g->ep, &g->graph, &info));
+    g->graph.parent = nullptr;
+    if (rc) return -rc;
+    std::string s;
+    g->groups.clear();
+    g->drop = info.drop;
+    for (size_t i = 0; i < info.groups.size(); ++i) {
+        Group gr;
+        gr.graph = std::make_unique<OrtGraph>();
+        gr.fused = std::make_unique<OrtNode>();
+        gr.fused->op_type = "MI355X_fused";
+        gr.fused->domain = "";
+        std::set<std::string> seen;
+        for (const OrtNode* n : info.groups[i]) {
+            gr.graph->nodes.push_back(const_cast<OrtNode*>(n));
+            if (!s.empty()) s += ';';
+            s += n->name + (info.drop[i] ? ":drop" : ":keep");
+            gr.fused->name += n->name;
+            for (OrtValueInfo* v : n->inputs) {
+                if (!v || seen.count(v->name)) continue;
+                if (v->constant && info.drop[i]) continue;   // ORT drops constant initializers
+                seen.insert(v->name);
+                gr.fused->inputs.push_back(v);
+            }
+            for (OrtValueInfo* v : n->outputs) gr.fused->outputs.push_back(v);
+        }
+        g->groups.push_back(std::move(gr));
+    }
+    std::snprintf(out, len, "%s", s.c_str());
+    return (int)info.groups.size();
+}
+
+// Compile every group; returns 0 or an error code.
+int mock_compile(void) {
+    if (!g || !g->ep) return -1;
+    const size_t n = g->groups.size();
+    std::vector<const OrtGraph*> graphs;
+    std::vector<const OrtNode*> fused;
+    for (auto& gr : g->groups) {
+        graphs.push_back(gr.graph.get());
+        fused.push_back(gr.fused.get());
+    }
+    std::vector<OrtNodeComputeInfo*> infos(n, reinterpret_cast<OrtNodeComputeInfo*>(0x1));
+    std::vector<OrtNode*> ctx_nodes(n, reinterpret_cast<OrtNode*>(0x1));
+    int rc = status_rc(g->ep->Compile(g->ep, graphs.data(), fused.data(), n, infos.data(), ctx_nodes.data()));
+    for (size_t i = 0; i < n; ++i) {
+        // On failure every slot must have been reset; on success every slot is a compute info.
+        if (infos[i] == reinterpret_cast<OrtNodeComputeInfo*>(0x1)) {
+            set_err("Compile left compute-info slot %zu unwritten", i);
+            return -2;
+        }
+        if (ctx_nodes[i] == reinterpret_cast<OrtNode*>(0x1)) {
+            set_err("Compile left EPContext slot %zu unwritten", i);
+            return -2;
+        }
+        if (rc && infos[i]) {
+            set_err("Compile failed but left compute info %zu set", i);
+            return -2;
+        }
+        if (!rc) g->groups[i].info = infos[i];
+    }
+    return rc;
+}
+
+// Host tensor for a graph input (borrowed: the caller keeps `data` alive until compute ends).
+int mock_feed(const char* name, int elem, int rank, const int64_t* dims, const void* data, size_t bytes) {
+    OrtValue v;
+    v.elem = elem;
+    v.dims.assign(dims, dims + rank);
+    v.data = data;
+    v.bytes = bytes;
+    g->feeds[name] = v;
+    return 0;
+}
+
+// Runs group `i`'s compute (CreateState / Compute / ReleaseState); outputs go to fetches.
+int mock_compute(int i) {
+    if (!g || i < 0 || i >= (int)g->groups.size() || !g->groups[i].info) return -1;
+    Group& gr = g->groups[i];
+    OrtKernelContext ctx;
+    std::vector<std::unique_ptr<OrtValue>> init_vals;
+    for (OrtValueInfo* v : gr.fused->inputs) {
+        auto it = g->feeds.find(v->name);
+        if (it != g->feeds.end()) {
+            ctx.inputs.push_back(&it->second);
+        } else if (v->constant) {
+            auto val = std::make_unique<OrtValue>();
+            val->elem = v->type.tensor.elem;
+            val->dims = v->type.tensor.dims;
+            val->data = v->init.data();
+            val->bytes = v->init.size();
+            ctx.inputs.push_back(val.get());
+            init_vals.push_back(std::move(val));
+        } else {
+            set_err("no feed for %s", v->name.c_str());
+            return -1;
+        }
+    }
+    for (OrtValueInfo* v : gr.fused->outputs) ctx.out_elem.push_back(v->type.tensor.elem);
+    OrtNodeComputeInfo* info = gr.info;
+    void* state = nullptr;
+    int rc = 0;
+    if (info->CreateState) rc = status_rc(info->CreateState(info, nullptr, &state));
+    if (rc) return rc;
+    rc = status_rc(info->Compute(info, state, &ctx));
+    if (info->ReleaseState) info->ReleaseState(info, state);
+    if (rc) return rc;
+    for (size_t o = 0; o < ctx.outputs.size() && o < gr.fused->outputs.size(); ++o) {
+        if (!ctx.outputs[o]) continue;
+        OrtValue& dst = g->fetches[gr.fused->outputs[o]->name];
+        dst.elem = ctx.outputs[o]->elem;
+        dst.dims = ctx.outputs[o]->dims;
+        dst.owned = ctx.outputs[o]->owned;
+        dst.bytes = ctx.outputs[o]->bytes;
+        dst.data = dst.owned.data();
+    }
+    return 0;
+}
+
+// Copies a fetched output; returns its rank (dims written to `dims`), or -1.
+int mock_fetch(const char* name, void* dst, size_t bytes, int64_t* dims, int max_rank) {
+    auto it = g->fetches.find(name);
+    if (it == g->fetches.end()) {
+        set_err("no output %s", name);
+        return -1;
+    }
+    const OrtValue& v = it->second;
+    if (bytes < v.bytes) {
+        set_err("destination holds %zu bytes, output has %zu", bytes, v.bytes);
+        return -1;
+    }
+    std::memcpy(dst, v.data, v.bytes);
+    for (int d = 0; d < (int)v.dims.size() && d < max_rank; ++d) dims[d] = v.dims[d];
+    return (int)v.dims.size();
+}
+
+// Releases compute infos, the EP and the factory (in ORT's order) and unloads the library.
+int mock_shutdown(void) {
+    if (!g) return 0;
+    if (g->ep) {
+        std::vector<OrtNodeComputeInfo*> infos;
+        for (auto& gr : g->groups)
+            if (gr.info) infos.push_back(gr.info);
+        if (!infos.empty()) g->ep->ReleaseNodeComputeInfos(g->ep, infos.data(), infos.size());
+        g->factory->ReleaseEp(g->factory, g->ep);
+        g->ep = nullptr;
+    }
+    int rc = 0;
+    if (g->factory) rc = status_rc(g->release(g->factory));
+    g->factory = nullptr;
+    g_init_values.clear();
+    g_ep_devices.clear();
+    // The library stays loaded: HIP's runtime does not support being unloaded mid-process.
+    delete g;
+    g = nullptr;
+    return rc;
+}
+
+}  // extern "C"

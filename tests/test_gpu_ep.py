@@ -1,0 +1,151 @@
+"""The plugin EP end to end on the GPU, driven through the mock ORT host.
+
+CreateEpFactories -> GetSupportedDevices (the MI355X is advertised) -> CreateEp -> GetCapability
+-> Compile (constant weights uploaded to HBM once) -> Compute (host A in, one HIP launch, host Y
+out), checked against the oracle at the fp16 bar (max rel err 2e-3 over significant elements and
+RMS-normalised), with the reference's own Compute behaviours: leading dims of A fold into rows
+(tests/ops/test_matmulnbits.py:510-551), repeated runs are bit-identical (:558-653), weights that
+are graph inputs are re-read on every call, and a forced failure surfaces as a status
+(rust/src/ep.rs:2409-2424).
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+import mock_host as mh
+from oracle import matmul_nbits as orc
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.fixture
+def host(cuda):
+    h = mh.Host(28)
+    assert h.init_rc == 0, mh.err()
+    n = h.supported_devices(n_amd=1)
+    assert n == 1, "the MI355X was not advertised"
+    assert h.device_meta(0, "mi355x.arch").startswith("gfx950")
+    assert h.create_ep(0) == 0, mh.err()
+    yield h
+    assert h.close() == 0
+    assert mh.lib().mock_live_statuses() == 0
+    assert mh.lib().mock_bad_status_release() == 0
+
+
+def _check(y, ref, what):
+    e1 = orc.max_rel_err_significant(y, ref)
+    e2 = orc.max_err_rms_normalised(y, ref)
+    assert e1 <= TOL and e2 <= TOL, f"{what}: {e1:.3e} {e2:.3e}"
+
+
+@pytest.mark.parametrize("lead,N,K,bits,bs,zp", [
+    ((1,), 3072, 3072, 4, 32, False),
+    ((1,), 9216, 3072, 4, 32, True),           # configs[1] qkv
+    ((2, 3), 160, 1024, 4, 64, True),          # leading dims fold into M = 6
+    ((7,), 48, 256, 8, 16, False),
+    ((33,), 96, 512, 4, 128, True),            # MFMA GEMV row tiles
+])
+def test_compute_matches_oracle(host, lead, N, K, bits, bs, zp):
+    print(f"[gpu] ep lead={lead} N={N} K={K} bits={bits} bs={bs} zp={zp}", flush=True)
+    M = int(np.prod(lead))
+    inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=M + N)
+    host.reset()
+    a_name, y_name = mh.add_matmul_nbits(host, "mm", inp, N, K, bits, bs, lead + (K,))
+    assert host.get_capability() == (1, ["mm:drop"])
+    assert host.compile() == 0, mh.err()
+    before = mh.EP_COUNT()
+    A = inp["A"].reshape(lead + (K,))
+    host.feed(a_name, A)
+    assert host.compute(0) == 0, mh.err()
+    assert mh.EP_COUNT() == before + 1
+    y = host.fetch(y_name, np.float16, M * N)
+    assert y.shape == lead + (N,)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
+    _check(y.reshape(M, N), ref, "ep")
+
+
+def test_three_runs_bit_identical_and_row_count_changes(host):
+    N, K = 512, 2048
+    inp = orc.make_inputs(4, N, K, with_zp=True, seed=5)
+    host.reset()
+    a_name, y_name = mh.add_matmul_nbits(host, "mm", inp, N, K, 4, 32, (-1, K))
+    host.get_capability()
+    assert host.compile() == 0, mh.err()
+    outs = []
+    for _ in range(3):
+        host.feed(a_name, inp["A"])
+        assert host.compute(0) == 0, mh.err()
+        outs.append(host.fetch(y_name, np.float16, 4 * N).copy())
+    assert all(np.array_equal(outs[0].view(np.uint16), o.view(np.uint16)) for o in outs[1:])
+    assert not np.array_equal(outs[0][0], outs[0][1])
+    # a different row count through the same compiled node (symbolic batch)
+    host.feed(a_name, inp["A"][:1])
+    assert host.compute(0) == 0, mh.err()
+    y1 = host.fetch(y_name, np.float16, N)
+    assert np.array_equal(y1.reshape(-1).view(np.uint16), outs[0][0].view(np.uint16))
+    # zero rows: an empty output, no launch
+    host.feed(a_name, inp["A"][:0])
+    assert host.compute(0) == 0, mh.err()
+
+
+def test_weights_as_graph_inputs_are_read_every_call(host):
+    N, K = 64, 256
+    inp = orc.make_inputs(2, N, K, with_zp=True, seed=9)
+    inp2 = orc.make_inputs(2, N, K, with_zp=True, seed=10)
+    host.reset()
+    a_name, y_name = mh.add_matmul_nbits(host, "mm", inp, N, K, 4, 32, (2, K), const_weights=False)
+    assert host.get_capability()[1] == ["mm:keep"]
+    assert host.compile() == 0, mh.err()
+    for d in (inp, inp2):
+        host.feed(a_name, inp["A"])
+        host.feed("mm_B", d["B"])
+        host.feed("mm_scales", d["scales"])
+        host.feed("mm_zp", d["zp"])
+        assert host.compute(0) == 0, mh.err()
+        y = host.fetch(y_name, np.float16, 2 * N)
+        _check(y, orc.matmul_nbits(inp["A"], d["B"], d["scales"], d["zp"], N, K, 4, 32), "inputs")
+
+
+def test_fp32_node(host):
+    N, K = 40, 512
+    inp = orc.make_inputs(3, N, K, with_zp=True, seed=11, a_dtype=np.float32)
+    host.reset()
+    a_name, y_name = mh.add_matmul_nbits(host, "mm", inp, N, K, 4, 32, (3, K), a_dtype=np.float32)
+    host.get_capability()
+    assert host.compile() == 0, mh.err()
+    host.feed(a_name, inp["A"])
+    assert host.compute(0) == 0, mh.err()
+    y = host.fetch(y_name, np.float32, 3 * N)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, 32)
+    assert orc.max_rel_err_significant(y, ref) <= 1e-5
+
+
+def test_forced_compute_failure_is_a_status(host):
+    inp = orc.make_inputs(1, 32, 64, seed=2)
+    host.reset()
+    a_name, _ = mh.add_matmul_nbits(host, "mm", inp, 32, 64, 4, 32, (1, 64))
+    host.get_capability()
+    assert host.compile() == 0, mh.err()
+    host.feed(a_name, inp["A"])
+    os.environ["MI355X_EP_FORCE_COMPUTE_FAILURE"] = "1"
+    try:
+        assert host.compute(0) == mh.ORT_EP_FAIL
+        assert "forced Compute failure" in mh.err()
+    finally:
+        del os.environ["MI355X_EP_FORCE_COMPUTE_FAILURE"]
+    assert host.compute(0) == 0, mh.err()
+
+
+def test_wrong_activation_width_is_rejected(host):
+    inp = orc.make_inputs(1, 32, 64, seed=2)
+    host.reset()
+    a_name, _ = mh.add_matmul_nbits(host, "mm", inp, 32, 64, 4, 32, (1, -1))
+    host.get_capability()
+    assert host.compile() == 0, mh.err()
+    host.feed(a_name, np.zeros((1, 128), np.float16))
+    assert host.compute(0) == mh.ORT_INVALID_ARGUMENT
