@@ -5,7 +5,9 @@ block_size 32, packed uint8 zero points — qkv (K=3072, N=9216), o (3072 -> 307
 (3072 -> 16384), down (8192 -> 3072).  One step = those four MatMulNBits launches over one
 layer's weights.  The weights of L layer copies (>= 2 x the 256 MB Infinity Cache) are rotated
 step by step so every step streams its weights from HBM, as a real decode does.  Inputs are
-synthetic (seeded), resident in HBM before the timed region.
+synthetic (seeded), resident in HBM before the timed region.  The timed steps are recorded once
+into a HIP graph and replayed, so the figure is the device's, not Python's launch overhead
+(the same steps launched one by one from Python are reported as eager_ms_per_step).
 
 value = algorithmic bytes of the layer set (65,568,768 B) per step / step time, in GB/s.
 The line also carries, measured in the same run:
@@ -132,30 +134,56 @@ def main() -> int:
     lib = mnb.load()
     sptr = int(stream.cuda_stream)
 
-    def launch(i, layer):
+    def launch(i, layer, sp=sptr):
         B, S, Z = layers[layer][i]
         rc = lib.mnb_matmul_nbits(C.byref(probs[i]), acts[i].data_ptr(), B.data_ptr(),
-                                  S.data_ptr(), Z.data_ptr(), outs[i].data_ptr(), None, 0, sptr)
+                                  S.data_ptr(), Z.data_ptr(), outs[i].data_ptr(), None, 0, sp)
         if rc:
             mnb.check(rc)
 
-    def step(s):
+    def step(s, sp=sptr):
         for i in range(len(LAYER)):
-            launch(i, s % copies)
+            launch(i, s % copies, sp)
 
     for s in range(args.warmup):
         step(s)
     torch.cuda.synchronize()
+    eager_out = [o.clone() for o in outs]          # outputs of step warmup-1
 
-    # Timed region: exactly `steps` steps of the four launches, bracketed by a synchronize on
-    # both sides (wall clock) and by two HIP events on the launch stream (device time).
+    # The step's launches are recorded once into a HIP graph (stream capture on a side stream)
+    # so that the timed region measures the device, not Python's per-launch overhead.
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        cs = torch.cuda.Stream()
+        cs.wait_stream(stream)
+        with torch.cuda.graph(g, stream=cs):
+            fn(int(torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        return g
+
+    graph = capture(lambda sp: [step(s, sp) for s in range(args.steps)])
+    graph.replay()
+    torch.cuda.synchronize()
+    # the graph's last step used the same weight copy as eager step (steps-1) % copies
+    for s in range(args.steps - 1, args.steps):
+        step(s)
+    torch.cuda.synchronize()
+    ref_out = [o.clone() for o in outs]
+    graph.replay()
+    torch.cuda.synchronize()
+    for o, r in zip(outs, ref_out):
+        if not torch.equal(o, r):
+            raise RuntimeError("graph replay and eager launches disagree")
+    del eager_out
+
+    # Timed region: exactly `steps` steps of the four launches (one graph replay), bracketed by
+    # a synchronize on both sides (wall clock) and by two HIP events on the stream (device time).
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record(stream)
-    for s in range(args.steps):
-        step(s)
+    graph.replay()
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -163,22 +191,30 @@ def main() -> int:
     dev_ms_step = ev0.elapsed_time(ev1) / args.steps
     value = per_layer / (ms_step * 1e-3) / 1e9
 
-    # Per-node launch duration: HIP events around `reps` back-to-back launches of one node on
-    # the launch stream (weights rotated as in the step), divided by `reps`.  This is each
-    # launch's device time including the gap to the next launch on the stream.
+    # The same steps launched one by one from Python (reported, not the value).
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(s)
+    torch.cuda.synchronize()
+    eager_ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Per-node launch duration: HIP events around a graph of `reps` back-to-back launches of one
+    # node (weights rotated as in the step), divided by `reps`: each launch's device time
+    # including the gap to the next launch on the stream.
     reps = max(20, copies * 4)
     kern_us = []
     for i in range(len(LAYER)):
-        for r in range(copies):
-            launch(i, r)
+        g1 = capture(lambda sp, i=i: [launch(i, r % copies, sp) for r in range(reps)])
+        g1.replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         a.record(stream)
-        for r in range(reps):
-            launch(i, r % copies)
+        g1.replay()
         b.record(stream)
         torch.cuda.synchronize()
         kern_us.append(1e3 * a.elapsed_time(b) / reps)
+        del g1
 
     per_kernel = []
     for i, ((name, k, n), us) in enumerate(zip(LAYER, kern_us)):
@@ -240,6 +276,7 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
         "device_ms_per_step": round(dev_ms_step, 5),
+        "eager_ms_per_step": round(eager_ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

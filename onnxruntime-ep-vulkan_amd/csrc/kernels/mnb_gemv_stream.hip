@@ -49,7 +49,7 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     // 256 chunks -> G = 64.
     double best = -1.0;
     int g = 64;
-    for (int cand : {16, 32, 64}) {
+    for (int cand : {64, 32, 16}) {                 // ties go to the wider group
         const int64_t cpl = (cpc + cand - 1) / cand;
         if (cpl > cap) continue;
         const double fill = (double)cpc / (double)(cand * cpl);

@@ -48,6 +48,7 @@ int64_t elem_bytes(int32_t dtype) { return dtype == MNB_DTYPE_F16 ? 2 : 4; }
 
 // Environment override of the planner, the counterpart of the reference's A/B controls
 // (ONNXRUNTIME_EP_VULKAN_GEMV_PACKED / _GEMV_MAX_ROWS, rust/src/ops/quant.rs:373-449).
+// Read on every plan (tests flip it at run time); getenv is a short scan of the environment.
 int forced_kernel() {
     const char* v = std::getenv("MNB_FORCE_KERNEL");
     if (!v || !*v) return 0;
