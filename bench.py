@@ -230,40 +230,45 @@ def main() -> int:
                 "kernel": f"MatMulNBits {LAYER[dom][0]} M=1 K={LAYER[dom][1]} N={LAYER[dom][2]}",
                 "per_launch_bytes": dom_bytes, "launch_us": round(kern_us[dom], 3)}
 
-    # Prefill, BASELINE configs[2] at M=2048 (not part of `value`).
-    pk, pn, pm = 3072, 8192, 2048
-    pB, pS, _ = make_weights(torch, dev, pk, pn, gen, zp=False)
-    pA = torch.randn(pm, pk, device=dev, generator=gen).to(torch.float16)
-    pY = torch.empty(pm, pn, dtype=torch.float16, device=dev)
-    pprob = mnb.problem(pm, pn, pk, BITS, BS, False)
-    pinfo = mnb.plan(pprob)
+    # Prefill: M in {256, 512, 2048}, K=3072, N=8192, implicit zero point
+    # (not part of `value`).  HIP events around a graph of `preps` launches; weights rotate over
+    # two copies so consecutive launches do not reuse an L2-resident B.
+    pk, pn = 3072, 8192
+    pw = [make_weights(torch, dev, pk, pn, gen, zp=False) for _ in range(2)]
+    prefill = []
+    for pm in (256, 512, 2048):
+        pA = torch.randn(pm, pk, device=dev, generator=gen).to(torch.float16)
+        pY = torch.empty(pm, pn, dtype=torch.float16, device=dev)
+        pprob = mnb.problem(pm, pn, pk, BITS, BS, False)
+        pinfo = mnb.plan(pprob)
 
-    def plaunch():
-        rc = lib.mnb_matmul_nbits(C.byref(pprob), pA.data_ptr(), pB.data_ptr(), pS.data_ptr(),
-                                  None, pY.data_ptr(), None, 0, sptr)
-        if rc:
-            mnb.check(rc)
+        def plaunch(r, sp, pA=pA, pY=pY, pprob=pprob):
+            pB, pS, _ = pw[r % 2]
+            rc = lib.mnb_matmul_nbits(C.byref(pprob), pA.data_ptr(), pB.data_ptr(),
+                                      pS.data_ptr(), None, pY.data_ptr(), None, 0, sp)
+            if rc:
+                mnb.check(rc)
 
-    for _ in range(3):
-        plaunch()
-    torch.cuda.synchronize()
-    reps = 10
-    pe = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(reps)]
-    for a, b in pe:
+        preps = 20
+        for r in range(3):
+            plaunch(r, sptr)
+        pg = capture(lambda sp: [plaunch(r, sp) for r in range(preps)])
+        pg.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
         a.record(stream)
-        plaunch()
+        pg.replay()
         b.record(stream)
-    torch.cuda.synchronize()
-    pus = 1e3 * sum(a.elapsed_time(b) for a, b in pe) / reps
-    pflops = 2.0 * pm * pn * pk
-    ptf = pflops / (pus * 1e-6) / 1e12
-    prefill = {"metric": "MatMulNBits prefill TFLOP/s", "M": pm, "K": pk, "N": pn,
-               "us": round(pus, 2), "TFLOP/s": round(ptf, 2),
-               "kernel": mnb.KERNEL_NAMES.get(pinfo.kernel, "?"),
-               "roofline": {"bound": "mfma", "achieved": round(ptf, 2),
-                            "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                            "frac": round(ptf / F16_MFMA_PEAK_TFLOPS, 4)}}
+        torch.cuda.synchronize()
+        pus = 1e3 * a.elapsed_time(b) / preps
+        del pg
+        ptf = 2.0 * pm * pn * pk / (pus * 1e-6) / 1e12
+        prefill.append({"M": pm, "K": pk, "N": pn, "us": round(pus, 2), "TFLOP/s": round(ptf, 2),
+                        "kernel": mnb.KERNEL_NAMES.get(pinfo.kernel, "?"),
+                        "tile": [pinfo.tile_m, pinfo.tile_n],
+                        "roofline": {"bound": "mfma", "achieved": round(ptf, 2),
+                                     "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                     "frac": round(ptf / F16_MFMA_PEAK_TFLOPS, 4)}})
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 

@@ -36,6 +36,20 @@ hipError_t launch_gemv_stream_cfg(const StreamConfig& c, const void* a, const ui
                                   const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
                                   int64_t k, int bits, int bs, hipStream_t stream);
 
+// Tile shape of the prefill GEMM (mnb_gemm.hip).
+struct GemmConfig {
+    int bm, bn;          // workgroup tile
+    int64_t tiles_m, tiles_n;
+};
+
+bool gemm_supported(int64_t m, int64_t k, int bits, int bs);
+GemmConfig gemm_config(int64_t m, int64_t n);
+hipError_t launch_gemm(const void* a, const uint8_t* b, const void* s, const uint8_t* z, void* y,
+                       int64_t m, int64_t n, int64_t k, int bits, int bs, hipStream_t stream);
+hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
+                           const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
+                           int bs, hipStream_t stream);
+
 GemvGeom gemv_geometry(int64_t m, int64_t n, int64_t k, int bits, int bs);
 bool gemv_supported(int64_t k, int bits, int block_size);
 

@@ -39,6 +39,9 @@ int hip_fail(hipError_t e, const char* what) {
     return fail(MNB_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
+// Rows above which the prefill GEMM replaces the 16-row MFMA GEMV.
+constexpr int64_t kGemmMinRows = 64;
+
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int64_t bpc_of(const mnb_problem* p) { return p->k / p->block_size; }
@@ -105,14 +108,25 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     const bool fast = p->dtype == MNB_DTYPE_F16 && mnb::gemv_supported(p->k, p->bits, p->block_size);
     const bool stream = p->dtype == MNB_DTYPE_F16 &&
                         mnb::gemv_stream_supported(p->m, p->k, p->bits, p->block_size);
+    const bool gemm = p->dtype == MNB_DTYPE_F16 &&
+                      mnb::gemm_supported(p->m, p->k, p->bits, p->block_size);
     if (fast) kern = MNB_KERNEL_GEMV_MFMA;
+    if (gemm && p->m > kGemmMinRows) kern = MNB_KERNEL_GEMM_MFMA;
     if (stream) kern = MNB_KERNEL_GEMV_STREAM;
     const int forced = forced_kernel();
     if (forced == MNB_KERNEL_GENERIC) kern = MNB_KERNEL_GENERIC;
     if (forced == MNB_KERNEL_GEMV_MFMA && fast) kern = MNB_KERNEL_GEMV_MFMA;
     if (forced == MNB_KERNEL_GEMV_STREAM && stream) kern = MNB_KERNEL_GEMV_STREAM;
+    if (forced == MNB_KERNEL_GEMM_MFMA && gemm) kern = MNB_KERNEL_GEMM_MFMA;
     out->kernel = kern;
-    if (kern == MNB_KERNEL_GEMV_STREAM) {
+    if (kern == MNB_KERNEL_GEMM_MFMA) {
+        const mnb::GemmConfig c = mnb::gemm_config(p->m, p->n);
+        out->waves_per_group = 4;
+        out->tile_n = c.bn;
+        out->tile_m = c.bm;
+        out->grid_x = c.tiles_m * c.tiles_n;
+        out->grid_y = 1;
+    } else if (kern == MNB_KERNEL_GEMV_STREAM) {
         const mnb::StreamConfig c =
             mnb::gemv_stream_config(p->m, p->n, p->k, p->bits, p->block_size);
         out->waves_per_group = c.waves_per_group;
@@ -170,7 +184,12 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
     if ((kern == MNB_KERNEL_GEMV_MFMA || kern == MNB_KERNEL_GEMV_STREAM) &&
         (!aligned(a, 16) || !aligned(b, 16)))
         kern = MNB_KERNEL_GENERIC;
-    if (kern == MNB_KERNEL_GEMV_STREAM) {
+    if (kern == MNB_KERNEL_GEMM_MFMA && (!aligned(a, 16) || !aligned(b, 16)))
+        kern = MNB_KERNEL_GENERIC;
+    if (kern == MNB_KERNEL_GEMM_MFMA) {
+        e = mnb::launch_gemm(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
+                             p->block_size, st);
+    } else if (kern == MNB_KERNEL_GEMV_STREAM) {
         e = mnb::launch_gemv_stream(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
                                     p->block_size, st);
     } else if (kern == MNB_KERNEL_GEMV_MFMA) {

@@ -80,7 +80,7 @@ def test_dequant_bit_exact(cuda, name):
     assert np.array_equal(got, d["W_bits"]), f"{np.count_nonzero(got != d['W_bits'])} mismatches"
 
 
-@pytest.mark.parametrize("kernel", ["stream", "gemv", "generic"])
+@pytest.mark.parametrize("kernel", ["stream", "gemv", "gemm", "generic"])
 @pytest.mark.parametrize("name", KATS)
 def test_integer_exact_kat(cuda, name, kernel):
     d = _load(name)
@@ -119,7 +119,7 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("kernel", ["stream", "gemv", "generic"])
+@pytest.mark.parametrize("kernel", ["stream", "gemv", "gemm", "generic"])
 @pytest.mark.parametrize("M,N,K,bits,bs,zp", SHAPES)
 def test_random_parity_f16(cuda, M, N, K, bits, bs, zp, kernel):
     inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=M * 1000 + N + K)
@@ -159,6 +159,40 @@ def test_baseline_configs_full_size(cuda, name, M, N, K, zp):
     y = _run(inp, N, K, 4, bs, cuda)
     ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
     _check_f16(y, ref, name)
+
+
+GEMM_SHAPES = [
+    # (M, N, K, bs, zp): tile edges in M and N, every block size of the GEMM path
+    (65, 64, 256, 32, False),
+    (128, 256, 512, 32, True),
+    (129, 300, 1024, 64, False),
+    (256, 8192, 3072, 32, False),      # BASELINE configs[2], M=256
+    (300, 130, 2048, 128, True),
+    (512, 512, 3072, 32, True),
+    (777, 1000, 768, 64, True),
+]
+
+
+@pytest.mark.parametrize("M,N,K,bs,zp", GEMM_SHAPES)
+def test_gemm_parity(cuda, M, N, K, bs, zp):
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=M + 7 * N + K)
+    print(f"[gpu] gemm M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
+    y = _run(inp, N, K, 4, bs, cuda, "gemm")
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
+    _check_f16(y, ref, f"gemm M={M} N={N} K={K} bs={bs}")
+
+
+@pytest.mark.parametrize("M", [512, 2048])
+def test_prefill_config_full_size(cuda, M):
+    # K=3072, N=8192, int4 bs32, implicit zero point, through the planner
+    import mnb
+    N, K = 8192, 3072
+    assert mnb.plan(mnb.problem(M, N, K, 4, 32, False)).kernel == mnb.KERNEL_GEMM_MFMA
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=32, with_zp=False, seed=20260801)
+    print(f"[gpu] prefill M={M}", flush=True)
+    y = _run(inp, N, K, 4, 32, cuda)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], None, N, K, 4, 32)
+    _check_f16(y, ref, f"prefill M={M}")
 
 
 def test_three_runs_bit_identical(cuda):
