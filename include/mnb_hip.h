@@ -54,6 +54,7 @@ extern "C" {
 #define MNB_KERNEL_GENERIC 3     /* any dtype/bits/block: per-block fp32 partial, scaled once */
 #define MNB_KERNEL_ACC4_I8 4     /* accuracy_level 4: int8 A, int8 MFMA, int32 block dots */
 #define MNB_KERNEL_GEMV_STREAM 5 /* fp16, M <= 4: coalesced 16-byte-chunk streaming GEMV */
+#define MNB_KERNEL_GROUP_MFMA 6  /* fp16, int4, block >= 32: row-tiled 16x16x32 MFMA GEMV */
 
 /* One MatMulNBits node: the attributes plus the row count of this call. */
 typedef struct mnb_problem {
@@ -101,16 +102,22 @@ int mnb_dequantize_f16(int64_t n, int64_t k, int32_t bits, int32_t block_size,
                        void* w_out_f16, void* stream);
 
 /* accuracy_level=4 activation quantiser: per (row, block) amax, scale = amax/127,
- * qa = clamp(rint(a * (127/amax)), -127, 127).  a is fp16 [m][k] (dtype MNB_DTYPE_F16) or
- * fp32; writes qa int8 [m][k], scale fp32 [m][k/bs], qsum int32 [m][k/bs]. */
+ * qa = clamp(rint(a * (127/amax)), -127, 127) (0 when amax is 0), fp32 arithmetic, round half
+ * to even.  a is fp16 [m][k] (dtype MNB_DTYPE_F16) or fp32; writes qa int8 [m][k] in natural
+ * order, scale fp32 [m][k/bs] and, when qsum is not NULL, qsum int32 [m][k/bs] = sum of qa over
+ * the block.  Stream-ordered. */
 int mnb_quantize_a_int8(int64_t m, int64_t k, int32_t block_size, int32_t dtype, const void* a,
                         int8_t* qa, float* a_scale, int32_t* qsum, void* stream);
 
-/* Expert-grouped MatMulNBits.  For expert e, rows i in [offsets[e], offsets[e+1]):
+/* Expert-grouped MatMulNBits (gpt-oss style routed experts; no counterpart in the reference,
+ * whose QMoE rows are staged without a kernel: rust/src/ops/moe.rs:92-94,118).
+ * For expert e, rows i in [offsets[e], offsets[e+1]):
  *   Y[i, :] = A[row_index[i], :] @ dequant(B_e)^T
  * B/scales/zero_points hold `num_experts` consecutive per-expert tensors of one node's layout.
- * offsets is int32 [num_experts+1] and row_index int32 [offsets[num_experts]] on the device;
- * `total_rows` must equal offsets[num_experts] and `max_rows_per_expert` bound every group. */
+ * offsets is int32 [num_experts+1] and row_index int32 [offsets[num_experts]] on the device
+ * (values in [0, a_rows)); `total_rows` must equal offsets[num_experts] and
+ * `max_rows_per_expert` bound every group (the launch covers that many rows per expert).
+ * fp16, bits = 4, block_size >= 32, K % 32 == 0.  Stream-ordered. */
 typedef struct mnb_moe_problem {
     int64_t num_experts;
     int64_t total_rows;         /* rows of Y (= assignments) */

@@ -42,12 +42,16 @@ HIP_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in architectural VGPRs, where the fp32 block epilogue reads them, instead of
+    # AGPRs that need a v_accvgpr_read per element.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     f"-I{INCLUDE}",
 ]
 
 HIP_SOURCES = [
     CSRC / "kernels" / "mnb_gemv.hip",
     CSRC / "kernels" / "mnb_gemm.hip",
+    CSRC / "kernels" / "mnb_group_gemv.hip",
     CSRC / "kernels" / "mnb_gemv_stream.hip",
     CSRC / "kernels" / "mnb_gemv_stream_b4.hip",
     CSRC / "kernels" / "mnb_gemv_stream_b8.hip",
@@ -57,7 +61,8 @@ EP_SOURCES: list[Path] = sorted((CSRC / "ep").glob("*.cpp"))
 
 
 def _headers() -> list[Path]:
-    return list(CSRC.rglob("*.hpp")) + list(INCLUDE.glob("*.h"))
+    # build.py itself is a dependency: a change of flags rebuilds every object
+    return list(CSRC.rglob("*.hpp")) + list(INCLUDE.glob("*.h")) + [Path(__file__)]
 
 
 def _stale(out: Path, deps: list[Path]) -> bool:

@@ -414,16 +414,19 @@ OrtStatus* ORT_API_CALL ci_compute(OrtNodeComputeInfo* self, void*, OrtKernelCon
 
 const char* ORT_API_CALL ep_get_name(const OrtEp*) noexcept { return kEpName; }
 
-// Whether the HIP library implements accuracy_level = 4 (int8 activations): asked of its planner,
-// so the claim never runs ahead of the kernels.
-bool int8_path_available() {
+// Whether the HIP library implements accuracy_level = 4 (int8 activations) for this node's
+// form: asked of its planner, so the claim never runs ahead of the kernels.
+bool int8_path_available(const NodeFacts& f) {
+    if (!f.has_k || !f.has_n || !f.has_bits || !f.has_block_size) return false;
     mnb_problem p{};
     p.m = 1;
-    p.n = 16;
-    p.k = 128;
-    p.bits = 4;
-    p.block_size = 32;
-    p.dtype = MNB_DTYPE_F16;
+    p.n = f.n;
+    p.k = f.k;
+    p.bits = (int32_t)f.bits;
+    p.block_size = (int32_t)f.block_size;
+    p.dtype = !f.inputs.empty() && f.inputs[0].elem_type == kElemFloat16 ? MNB_DTYPE_F16
+                                                                         : MNB_DTYPE_F32;
+    p.has_zero_points = f.inputs.size() > 3 && f.inputs[3].present;
     p.accuracy_level = 4;
     mnb_plan_info info;
     return mnb_plan(&p, &info) == MNB_OK;
@@ -448,7 +451,7 @@ void get_capability(Ep* ep, const OrtGraph* graph, OrtEpGraphSupportInfo* suppor
         const NodeFacts f = node_facts(api, node);
         if (!is_matmul_nbits(f)) continue;
         const std::string name = node_string(api, node, api->Node_GetName);
-        const ClaimDecision d = claim_matmul_nbits(f, int8_path_available());
+        const ClaimDecision d = claim_matmul_nbits(f, int8_path_available(f));
         if (!d.claim) {
             claim_log("decline %s: %s", name.c_str(), d.reason.c_str());
             continue;
@@ -491,7 +494,7 @@ std::unique_ptr<NodeKernel> compile_one(Ep* ep, const OrtGraph* graph, const Ort
     const OrtNode* node = nullptr;
     ORT_OK(api, Graph_GetNodes(graph, &node, 1));
     const NodeFacts f = node_facts(api, node);
-    const ClaimDecision d = claim_matmul_nbits(f, int8_path_available());
+    const ClaimDecision d = claim_matmul_nbits(f, int8_path_available(f));
     if (!d.claim) fail(ORT_EP_FAIL, "compiled node fails the claim predicate: %s", d.reason.c_str());
 
     auto k = std::make_unique<NodeKernel>();

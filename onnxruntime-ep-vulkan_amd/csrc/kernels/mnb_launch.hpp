@@ -50,6 +50,30 @@ hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b,
                            const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                            int bs, hipStream_t stream);
 
+// Launch shape of the row-tiled MFMA GEMV (mnb_group_gemv.hip).
+struct GroupGeom {
+    int mt;              // 16-row tiles per workgroup (1, 2 or 4)
+    int waves;           // wavefronts per workgroup (split K)
+    int64_t gx, gy, gz;  // column strips, groups, row tiles
+    size_t lds;
+};
+
+bool group_gemv_supported(int64_t k, int bits, int bs);
+GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups);
+hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const int32_t* offsets,
+                                 int64_t groups, int64_t max_rows, const uint8_t* b,
+                                 const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
+                                 int64_t k, int bits, int bs, hipStream_t stream);
+hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
+                                  int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
+                                  hipStream_t stream);
+size_t acc4_workspace_bytes(int64_t m, int64_t k, int bs);
+hipError_t launch_acc4(const void* a, bool a_f16, const int32_t* row_index,
+                       const int32_t* offsets, int64_t groups, int64_t max_rows,
+                       const uint8_t* b, const void* s, const uint8_t* z, void* y, int64_t m,
+                       int64_t n, int64_t k, int bits, int bs, void* workspace,
+                       hipStream_t stream);
+
 GemvGeom gemv_geometry(int64_t m, int64_t n, int64_t k, int bits, int bs);
 bool gemv_supported(int64_t k, int bits, int block_size);
 

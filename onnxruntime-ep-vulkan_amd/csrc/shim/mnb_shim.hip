@@ -59,6 +59,7 @@ int forced_kernel() {
     if (!std::strcmp(v, "gemm")) return MNB_KERNEL_GEMM_MFMA;
     if (!std::strcmp(v, "generic")) return MNB_KERNEL_GENERIC;
     if (!std::strcmp(v, "stream")) return MNB_KERNEL_GEMV_STREAM;
+    if (!std::strcmp(v, "group")) return MNB_KERNEL_GROUP_MFMA;
     return 0;
 }
 
@@ -102,22 +103,39 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     if (rc) return rc;
     if (!out) return fail(MNB_ERR_INVALID, "plan output is NULL");
     std::memset(out, 0, sizeof(*out));
-    if (p->accuracy_level == 4)
-        return fail(MNB_ERR_UNSUPPORTED, "accuracy_level 4 (int8 activations) is not built yet");
+    if (p->accuracy_level == 4) {
+        // int8 activations (ORT's SQNBIT_CompInt8 level): quantiser + int8 MFMA GEMV.
+        if (!mnb::group_gemv_supported(p->k, p->bits, p->block_size))
+            return fail(MNB_ERR_UNSUPPORTED,
+                        "accuracy_level 4 is implemented for bits = 4, block_size >= 32 and "
+                        "K %% 32 == 0 (got bits = %d, block_size = %d, K = %lld)",
+                        p->bits, p->block_size, (long long)p->k);
+        const mnb::GroupGeom g = mnb::group_geometry(p->m, p->n, p->k, 1);
+        out->kernel = MNB_KERNEL_ACC4_I8;
+        out->waves_per_group = g.waves;
+        out->tile_n = 16;
+        out->tile_m = 16 * g.mt;
+        out->grid_x = g.gx;
+        out->grid_y = g.gz;
+        out->workspace_bytes = (int64_t)mnb::acc4_workspace_bytes(p->m, p->k, p->block_size);
+        return MNB_OK;
+    }
+    const bool f16 = p->dtype == MNB_DTYPE_F16;
+    const bool fast = f16 && mnb::gemv_supported(p->k, p->bits, p->block_size);
+    const bool stream = f16 && mnb::gemv_stream_supported(p->m, p->k, p->bits, p->block_size);
+    const bool group = f16 && mnb::group_gemv_supported(p->k, p->bits, p->block_size);
+    const bool gemm = f16 && mnb::gemm_supported(p->m, p->k, p->bits, p->block_size);
     int kern = MNB_KERNEL_GENERIC;
-    const bool fast = p->dtype == MNB_DTYPE_F16 && mnb::gemv_supported(p->k, p->bits, p->block_size);
-    const bool stream = p->dtype == MNB_DTYPE_F16 &&
-                        mnb::gemv_stream_supported(p->m, p->k, p->bits, p->block_size);
-    const bool gemm = p->dtype == MNB_DTYPE_F16 &&
-                      mnb::gemm_supported(p->m, p->k, p->bits, p->block_size);
-    if (fast) kern = MNB_KERNEL_GEMV_MFMA;
+    if (fast) kern = MNB_KERNEL_GEMV_MFMA;               // bits 8, block 16: 16-row MFMA GEMV
+    if (group) kern = MNB_KERNEL_GROUP_MFMA;             // int4, block >= 32: any row count
     if (gemm && p->m > kGemmMinRows) kern = MNB_KERNEL_GEMM_MFMA;
-    if (stream) kern = MNB_KERNEL_GEMV_STREAM;
+    if (stream) kern = MNB_KERNEL_GEMV_STREAM;           // M <= 4
     const int forced = forced_kernel();
     if (forced == MNB_KERNEL_GENERIC) kern = MNB_KERNEL_GENERIC;
     if (forced == MNB_KERNEL_GEMV_MFMA && fast) kern = MNB_KERNEL_GEMV_MFMA;
     if (forced == MNB_KERNEL_GEMV_STREAM && stream) kern = MNB_KERNEL_GEMV_STREAM;
     if (forced == MNB_KERNEL_GEMM_MFMA && gemm) kern = MNB_KERNEL_GEMM_MFMA;
+    if (forced == MNB_KERNEL_GROUP_MFMA && group) kern = MNB_KERNEL_GROUP_MFMA;
     out->kernel = kern;
     if (kern == MNB_KERNEL_GEMM_MFMA) {
         const mnb::GemmConfig c = mnb::gemm_config(p->m, p->n);
@@ -134,6 +152,13 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
         out->tile_m = c.mr;
         out->grid_x = (c.total_waves + c.waves_per_group - 1) / c.waves_per_group;
         out->grid_y = (p->m + c.mr - 1) / c.mr;
+    } else if (kern == MNB_KERNEL_GROUP_MFMA) {
+        const mnb::GroupGeom g = mnb::group_geometry(p->m, p->n, p->k, 1);
+        out->waves_per_group = g.waves;
+        out->tile_n = 16;
+        out->tile_m = 16 * g.mt;
+        out->grid_x = g.gx;
+        out->grid_y = g.gz;
     } else if (kern == MNB_KERNEL_GEMV_MFMA) {
         const mnb::GemvGeom g = mnb::gemv_geometry(p->m, p->n, p->k, p->bits, p->block_size);
         out->waves_per_group = g.waves;
@@ -181,12 +206,22 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
     int kern = info.kernel;
     // The MFMA path loads A in 16-byte and B in 16-byte units; fall back when a caller hands
     // over a sub-aligned view.
-    if ((kern == MNB_KERNEL_GEMV_MFMA || kern == MNB_KERNEL_GEMV_STREAM) &&
+    if ((kern == MNB_KERNEL_GEMV_MFMA || kern == MNB_KERNEL_GEMV_STREAM ||
+         kern == MNB_KERNEL_GEMM_MFMA || kern == MNB_KERNEL_GROUP_MFMA) &&
         (!aligned(a, 16) || !aligned(b, 16)))
         kern = MNB_KERNEL_GENERIC;
-    if (kern == MNB_KERNEL_GEMM_MFMA && (!aligned(a, 16) || !aligned(b, 16)))
-        kern = MNB_KERNEL_GENERIC;
-    if (kern == MNB_KERNEL_GEMM_MFMA) {
+    if (kern == MNB_KERNEL_ACC4_I8) {
+        // the int8 path reads B in 16-byte units and stages its own aligned copy of A
+        if (!aligned(b, 16) || !aligned(workspace, 256))
+            return fail(MNB_ERR_INVALID, "accuracy_level 4 needs B 16-byte and the workspace "
+                                         "256-byte aligned");
+        e = mnb::launch_acc4(a, p->dtype == MNB_DTYPE_F16, nullptr, nullptr, 1, p->m, b, scales,
+                             zero_points, y, p->m, p->n, p->k, p->bits, p->block_size,
+                             workspace, st);
+    } else if (kern == MNB_KERNEL_GROUP_MFMA) {
+        e = mnb::launch_group_gemv_f16(a, nullptr, nullptr, 1, p->m, b, scales, zero_points, y,
+                                       p->m, p->n, p->k, p->bits, p->block_size, st);
+    } else if (kern == MNB_KERNEL_GEMM_MFMA) {
         e = mnb::launch_gemm(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
                              p->block_size, st);
     } else if (kern == MNB_KERNEL_GEMV_STREAM) {
@@ -227,14 +262,59 @@ int mnb_dequantize_f16(int64_t n, int64_t k, int32_t bits, int32_t block_size,
     return MNB_OK;
 }
 
-int mnb_quantize_a_int8(int64_t, int64_t, int32_t, int32_t, const void*, int8_t*, float*,
-                        int32_t*, void*) {
-    return fail(MNB_ERR_UNSUPPORTED, "accuracy_level 4 quantiser is not built yet");
+int mnb_quantize_a_int8(int64_t m, int64_t k, int32_t block_size, int32_t dtype, const void* a,
+                        int8_t* qa, float* a_scale, int32_t* qsum, void* stream) {
+    if (m < 0 || k <= 0) return fail(MNB_ERR_INVALID, "M = %lld, K = %lld", (long long)m, (long long)k);
+    if (block_size != 16 && block_size != 32 && block_size != 64 && block_size != 128)
+        return fail(MNB_ERR_UNSUPPORTED, "block_size = %d", block_size);
+    if (k % block_size) return fail(MNB_ERR_INVALID, "K is not a multiple of block_size");
+    if (dtype != MNB_DTYPE_F16 && dtype != MNB_DTYPE_F32)
+        return fail(MNB_ERR_UNSUPPORTED, "dtype %d", dtype);
+    if (m == 0) return MNB_OK;
+    if (!a || !qa || !a_scale) return fail(MNB_ERR_INVALID, "a NULL pointer was passed");
+    hipError_t e = mnb::launch_quantize_a_int8(a, dtype == MNB_DTYPE_F16, qa, a_scale, qsum,
+                                               false, m, k, block_size,
+                                               static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+    g_launches.fetch_add(1);
+    return MNB_OK;
 }
 
-int mnb_moe_grouped(const mnb_moe_problem*, const void*, const int32_t*, const int32_t*,
-                    const uint8_t*, const void*, const uint8_t*, void*, void*) {
-    return fail(MNB_ERR_UNSUPPORTED, "expert-grouped MatMulNBits is not built yet");
+int mnb_moe_grouped(const mnb_moe_problem* p, const void* a, const int32_t* row_index,
+                    const int32_t* offsets, const uint8_t* b, const void* scales,
+                    const uint8_t* zero_points, void* y, void* stream) {
+    if (!p) return fail(MNB_ERR_INVALID, "problem is NULL");
+    mnb_problem q{};
+    q.m = p->total_rows;
+    q.n = p->n;
+    q.k = p->k;
+    q.bits = p->bits;
+    q.block_size = p->block_size;
+    q.has_zero_points = p->has_zero_points;
+    q.dtype = p->dtype;
+    int rc = mnb_check_problem(&q);
+    if (rc) return rc;
+    if (p->dtype != MNB_DTYPE_F16 || !mnb::group_gemv_supported(p->k, p->bits, p->block_size))
+        return fail(MNB_ERR_UNSUPPORTED, "the grouped kernel is fp16, bits = 4, block_size >= 32, "
+                                         "K %% 32 == 0");
+    if (p->num_experts < 0 || p->num_experts > 65535 || p->max_rows_per_expert < 0 ||
+        p->a_rows < 0 || p->total_rows < 0)
+        return fail(MNB_ERR_INVALID, "negative or oversized expert/row counts");
+    if (p->total_rows == 0 || p->num_experts == 0) return MNB_OK;
+    if (!a || !row_index || !offsets || !b || !scales || !y)
+        return fail(MNB_ERR_INVALID, "a NULL pointer was passed");
+    if (p->has_zero_points && !zero_points)
+        return fail(MNB_ERR_INVALID, "has_zero_points is set but zero_points is NULL");
+    if (!aligned(a, 16) || !aligned(b, 16))
+        return fail(MNB_ERR_INVALID, "A and B must be 16-byte aligned");
+    hipError_t e = mnb::launch_group_gemv_f16(a, row_index, offsets, p->num_experts,
+                                              p->max_rows_per_expert, b, scales,
+                                              p->has_zero_points ? zero_points : nullptr, y,
+                                              p->total_rows, p->n, p->k, p->bits, p->block_size,
+                                              static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "grouped MatMulNBits launch");
+    g_launches.fetch_add(1);
+    return MNB_OK;
 }
 
 // ---- session layer ------------------------------------------------------------------------

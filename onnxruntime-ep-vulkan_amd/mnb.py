@@ -32,7 +32,9 @@ KERNEL_GEMM_MFMA = 2
 KERNEL_GENERIC = 3
 KERNEL_ACC4_I8 = 4
 KERNEL_GEMV_STREAM = 5
-KERNEL_NAMES = {1: "gemv_mfma", 2: "gemm_mfma", 3: "generic", 4: "acc4_i8", 5: "gemv_stream"}
+KERNEL_GROUP_MFMA = 6
+KERNEL_NAMES = {1: "gemv_mfma", 2: "gemm_mfma", 3: "generic", 4: "acc4_i8", 5: "gemv_stream",
+                6: "group_mfma"}
 
 
 class Problem(C.Structure):

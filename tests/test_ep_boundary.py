@@ -132,10 +132,21 @@ def test_accuracy_levels_are_claimed(host, acc):
     want = 1
     if acc == 4:
         try:
-            mnb.plan(mnb.problem(1, 16, 128, 4, 32, False, mnb.DTYPE_F16, 4))
+            mnb.plan(mnb.problem(1, 32, 64, 4, 32, True, mnb.DTYPE_F16, 4))
         except mnb.MnbError:
             want = 0
     assert host.get_capability()[0] == want
+
+
+def test_accuracy_level_4_claim_follows_the_form(host):
+    # the int8 path is int4 with block_size >= 32: level 4 at bits 8 or block 16 is declined
+    assert host.create_ep(-1) == 0
+    _graph(host, acc=4, bits=8)
+    assert host.get_capability()[0] == 0
+    _graph(host, acc=4, bs=16, K=64)
+    assert host.get_capability()[0] == 0
+    _graph(host, acc=4, bs=64, K=128)
+    assert host.get_capability()[0] == 1
 
 
 @pytest.mark.parametrize("case,over", [
