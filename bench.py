@@ -13,8 +13,12 @@ value = algorithmic bytes of the layer set (65,568,768 B) per step / step time, 
 The line also carries, measured in the same run:
   roofline      the dominant decode kernel's algorithmic bytes / its HIP-event launch time vs 8 TB/s
   prefill       MatMulNBits M=2048, K=3072, N=8192 in TFLOP/s vs 2.5 PFLOP/s fp16
+  accuracy_level_4  configs[4] (M=16, K=8192, N=3072, bs128, zp, int8 activations) in GB/s
+  moe           configs[3] (32 experts, top-4 of 64 tokens, gate_up and down) in GB/s
   cpu_baseline  the C restatement in oracle/ (kind "port"; stock ORT is not installed in this
                 image) on the host's cores, on a bounded sample of the same layer set
+`--pmc-node NODE` runs one node's launches and a 256 MiB copy only, for rocprofv3 --pmc passes
+(FETCH_SIZE, WRITE_SIZE) whose results give roofline.traffic (profiles/traffic_*.json).
 """
 
 from __future__ import annotations
@@ -53,6 +57,7 @@ def node_bytes(m: int, k: int, n: int, bs: int = BS, zp: bool = True) -> int:
 
 
 def make_weights(torch, dev, k, n, gen, bs=BS, zp=True):
+    """Packed int4 B [n, k/bs, bs/2], fp16 scales |N(0,1)|*0.02, packed zero points (seeded)."""
     bpc = k // bs
     B = torch.randint(0, 256, (n, bpc, bs // 2), dtype=torch.uint8, device=dev, generator=gen)
     S = (torch.randn(n * bpc, device=dev, generator=gen).abs() * 0.02).to(torch.float16)
@@ -108,12 +113,17 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-node", default=None,
+                    help="counter-collection mode: launch only this decode node (qkv_proj, o_proj, "
+                         "gate_up_proj, down_proj) --steps times over rotated weights, then one "
+                         "plain 256 MiB device copy for calibrating FETCH_SIZE/WRITE_SIZE; no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
               f"(MatMulNBits shards along N with no collective in the hot path)", file=sys.stderr)
         return 2
 
+    import numpy as np
     import torch
 
     import mnb
@@ -144,6 +154,20 @@ def main() -> int:
     def step(s, sp=sptr):
         for i in range(len(LAYER)):
             launch(i, s % copies, sp)
+
+    if args.pmc_node:
+        i = [x[0] for x in LAYER].index(args.pmc_node)
+        for s in range(args.steps):
+            launch(i, s % copies)
+        torch.cuda.synchronize()
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"pmc mode: {args.steps} launches of {args.pmc_node} "
+              f"({node_bytes(1, LAYER[i][1], LAYER[i][2])} algorithmic bytes each), "
+              f"then one copy of {src.numel()} bytes")
+        return 0
 
     for s in range(args.warmup):
         step(s)
@@ -270,6 +294,86 @@ def main() -> int:
                                      "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                      "frac": round(ptf / F16_MFMA_PEAK_TFLOPS, 4)}})
 
+    def graph_time_us(fn, reps):
+        """Average device time per launch of `fn(r, stream)` over a graph of `reps` launches."""
+        for r in range(2):
+            fn(r, sptr)
+        g = capture(lambda sp: [fn(r, sp) for r in range(reps)])
+        g.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return 1e3 * a.elapsed_time(b) / reps
+
+    # accuracy_level = 4, BASELINE configs[4]: M=16, K=8192, N=3072, int4 bs128 with zero points;
+    # one launch = the int8 quantiser of A + the int8 MFMA GEMV.  Weights rotated over >= 2x MALL.
+    ak, an, am, abs_ = 8192, 3072, 16, 128
+    a_bytes = node_bytes(am, ak, an, bs=abs_)
+    a_copies = max(2, -(-2 * MALL_BYTES // a_bytes))
+    a_w = [make_weights(torch, dev, ak, an, gen, bs=abs_) for _ in range(a_copies)]
+    a_A = torch.randn(am, ak, device=dev, generator=gen).to(torch.float16)
+    a_Y = torch.empty(am, an, dtype=torch.float16, device=dev)
+    a_prob = mnb.problem(am, an, ak, BITS, abs_, True, mnb.DTYPE_F16, 4)
+    a_ws_bytes = mnb.workspace_bytes(a_prob)
+    a_ws = torch.empty(a_ws_bytes, dtype=torch.uint8, device=dev)
+
+    def alaunch(r, sp):
+        B, S, Z = a_w[r % a_copies]
+        rc = lib.mnb_matmul_nbits(C.byref(a_prob), a_A.data_ptr(), B.data_ptr(), S.data_ptr(),
+                                  Z.data_ptr(), a_Y.data_ptr(), a_ws.data_ptr(), a_ws_bytes, sp)
+        if rc:
+            mnb.check(rc)
+
+    a_us = graph_time_us(alaunch, max(20, 2 * a_copies))
+    acc4 = {"config": "M=16 K=8192 N=3072 int4 bs128 zp, accuracy_level=4", "bytes": a_bytes,
+            "us": round(a_us, 3), "GB/s": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
+            "int_TOPS": round(2.0 * am * an * ak / (a_us * 1e-6) / 1e12, 2),
+            "kernel": "quantize_a_int8 + group_gemv<i8>",
+            "roofline": {"bound": "hbm", "achieved": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(a_bytes / (a_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
+    del a_w
+
+    # gpt-oss-shaped MoE, BASELINE configs[3]: 32 experts, 64 tokens, softmax top-4 routing of
+    # N(0,1) logits (seeded), per-expert int4 bs32 gate_up (2880 -> 5760) and down (2880 -> 2880).
+    E, T, TOPK, MK = 32, 64, 4, 2880
+    rng = np.random.default_rng(20260801)
+    logits = rng.standard_normal((T, E))
+    top = np.argsort(-logits, axis=1, kind="stable")[:, :TOPK]        # softmax is monotone
+    flat = top.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    m_rows = torch.from_numpy((order // TOPK).astype(np.int32)).to(dev)
+    counts = np.bincount(flat, minlength=E)
+    m_off = torch.from_numpy(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)).to(dev)
+    m_A = torch.randn(T, MK, device=dev, generator=gen).to(torch.float16)
+    moe = []
+    for name, mn in (("gate_up", 5760), ("down", 2880)):
+        bpc = MK // BS
+        wB = [torch.randint(0, 256, (E, mn, bpc, BS // 2), dtype=torch.uint8, device=dev,
+                            generator=gen) for _ in range(2)]
+        wS = [(torch.randn(E, mn * bpc, device=dev, generator=gen).abs() * 0.02).to(torch.float16)
+              for _ in range(2)]
+        mY = torch.empty(T * TOPK, mn, dtype=torch.float16, device=dev)
+        mp = mnb.MoeProblem(E, T * TOPK, int(counts.max()), T, mn, MK, BITS, BS, 0, mnb.DTYPE_F16)
+        wbytes = E * (mn * MK // 2 + 2 * mn * bpc)
+        mbytes = wbytes + 2 * T * MK + 2 * T * TOPK * mn
+
+        def mlaunch(r, sp, wB=wB, wS=wS, mY=mY, mp=mp):
+            rc = lib.mnb_moe_grouped(C.byref(mp), m_A.data_ptr(), m_rows.data_ptr(),
+                                     m_off.data_ptr(), wB[r % 2].data_ptr(), wS[r % 2].data_ptr(),
+                                     None, mY.data_ptr(), sp)
+            if rc:
+                mnb.check(rc)
+
+        m_us = graph_time_us(mlaunch, 10)
+        moe.append({"node": name, "K": MK, "N": mn, "experts": E, "bytes": mbytes,
+                    "us": round(m_us, 2), "GB/s": round(mbytes / (m_us * 1e-6) / 1e9, 1),
+                    "frac_hbm": round(mbytes / (m_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del wB, wS
+
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     line = {
@@ -295,6 +399,8 @@ def main() -> int:
         "roofline": roofline,
         "per_kernel": per_kernel,
         "prefill": prefill,
+        "accuracy_level_4": acc4,
+        "moe": moe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -62,15 +62,6 @@ __device__ __forceinline__ i32x2 qz_i8(uint32_t w, uint32_t zb) {
     return i32x2{(int32_t)lo, (int32_t)hi};
 }
 
-template <bool HAS_ZP>
-__device__ __forceinline__ int zp_nibble(const uint8_t* __restrict__ zc, int blk) {
-    if constexpr (!HAS_ZP) {
-        return 8;
-    } else {
-        return (int)((zc[blk >> 1] >> ((blk & 1) * 4)) & 0xFu);
-    }
-}
-
 }  // namespace
 
 // T: activation / scale / output type (f16, or float for the int8 path's fp32 nodes).
@@ -132,65 +123,107 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int c = wave; c < iters; c += W) {
-        const bool full = 4 * c + 3 < chunks;            // wave-uniform
-        u32x4 raw = u32x4{0u, 0u, 0u, 0u};
-        if (4 * c + g < chunks) raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bcol + 64 * c));
-        uint32_t v0 = raw.x, v1 = raw.y, v2 = raw.z, v3 = raw.w;
-        transpose_rows(v0, v1, v2, v3);
-        const uint32_t wt[4] = {v0, v1, v2, v3};
-        if constexpr (!I8) {
-            const f16* __restrict__ A = static_cast<const f16*>(Av);
+    // Each wavefront takes runs of PF consecutive 128-k iterations: all weight, scale and
+    // zero-point loads of a run are issued before any of it is computed.  Out-of-range chunks
+    // load a clamped in-bounds address and are skipped (wave-uniformly) at compute time.
+    constexpr int PF = group_pf(I8, BS, MT);
+    constexpr int CPB = BS / 32;                         // 32-k chunks per block (1, 2 or 4)
+    for (int c0 = wave * PF; c0 < iters; c0 += W * PF) {
+        u32x4 raw[PF];
+        T sr[PF][4];
+        uint8_t zr[PF][4];
+        float sa[I8 ? PF : 1][I8 ? 4 : 1][MT][4];        // int8 path: activation scales
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int c = c0 + p;
+            int ch = 4 * c + g;
+            const bool ok = ch < chunks;
+            ch = ok ? ch : chunks - 1;
+            raw[p] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(bcol - 16 * g + 16 * (int64_t)ch));
+            if (!ok) raw[p] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const int kc = 4 * c + t;
-                if (!full && kc >= chunks) break;        // wave-uniform
+                int kc = 4 * c + t;
+                kc = kc < chunks ? kc : chunks - 1;
                 const int blk = (32 * kc) / BS;
-                const float s = (float)scol[blk];
-                const f16x2 zo = zoff4(zp_nibble<HAS_ZP>(zcol, blk));
-                f16x8 bop;
-                bop.s01 = nib_pair<0>(wt[t], zo);
-                bop.s23 = nib_pair<1>(wt[t], zo);
-                bop.s45 = nib_pair<2>(wt[t], zo);
-                bop.s67 = nib_pair<3>(wt[t], zo);
+                if (!I8 || (t + 1) % CPB == 0) sr[p][t] = scol[blk];
+                if constexpr (HAS_ZP) zr[p][t] = zcol[blk >> 1];
+                else zr[p][t] = 0;
+                if constexpr (I8) {
+                    if ((t + 1) % CPB == 0) {            // block ends: one scale per output row
 #pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    const f16x8 aop = *reinterpret_cast<const f16x8*>(A + (int64_t)arow[i] * K + 32 * kc + 8 * g);
-                    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, d, 0, 0, 0);
+                        for (int i = 0; i < MT; ++i)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[i][q] = __builtin_fmaf(d[q], s, acc[i][q]);
+                            for (int q = 0; q < 4; ++q)
+                                sa[p][t][i][q] = a_scale[(int64_t)srow[i][q] * bpc + blk];
+                    }
                 }
             }
-        } else {
-            const int8_t* __restrict__ A = static_cast<const int8_t*>(Av);
-            constexpr int CPB = BS / 32;                 // chunks per block (1, 2 or 4)
-            i32x4 dot[MT];
+        }
 #pragma unroll
-            for (int i = 0; i < MT; ++i) dot[i] = i32x4{0, 0, 0, 0};
+        for (int p = 0; p < PF; ++p) {
+            const int c = c0 + p;
+            if (c >= iters) break;                       // wave-uniform
+            const bool full = 4 * c + 3 < chunks;        // wave-uniform
+            uint32_t v0 = raw[p].x, v1 = raw[p].y, v2 = raw[p].z, v3 = raw[p].w;
+            transpose_rows(v0, v1, v2, v3);
+            const uint32_t wt[4] = {v0, v1, v2, v3};
+            if constexpr (!I8) {
+                const f16* __restrict__ A = static_cast<const f16*>(Av);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int kc = 4 * c + t;
-                if (!full && kc >= chunks) break;        // wave-uniform
-                const int blk = (32 * kc) / BS;
-                const uint32_t zb = (uint32_t)(128 - zp_nibble<HAS_ZP>(zcol, blk)) * 0x01010101u;
-                const i32x2 bop = qz_i8(wt[t], zb);
-#pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    const i32x2 aop = *reinterpret_cast<const i32x2*>(A + (int64_t)arow[i] * K + 32 * kc + 8 * g);
-                    dot[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                        __builtin_bit_cast(long, aop), __builtin_bit_cast(long, bop), dot[i], 0, 0, 0);
-                }
-                if ((t + 1) % CPB == 0 || kc + 1 == chunks) {  // end of a block: scale it
-                    const float sb = (float)scol[blk];
+                for (int t = 0; t < 4; ++t) {
+                    const int kc = 4 * c + t;
+                    if (!full && kc >= chunks) break;    // wave-uniform
+                    const int blk = (32 * kc) / BS;
+                    const float s = (float)sr[p][t];
+                    int z = 8;
+                    if constexpr (HAS_ZP) z = (int)((zr[p][t] >> ((blk & 1) * 4)) & 0xFu);
+                    const f16x2 zo = zoff4(z);
+                    f16x8 bop;
+                    bop.s01 = nib_pair<0>(wt[t], zo);
+                    bop.s23 = nib_pair<1>(wt[t], zo);
+                    bop.s45 = nib_pair<2>(wt[t], zo);
+                    bop.s67 = nib_pair<3>(wt[t], zo);
 #pragma unroll
                     for (int i = 0; i < MT; ++i) {
+                        const f16x8 aop = *reinterpret_cast<const f16x8*>(A + (int64_t)arow[i] * K + 32 * kc + 8 * g);
+                        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, d, 0, 0, 0);
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const float sa = a_scale[(int64_t)srow[i][q] * bpc + blk];
-                            acc[i][q] = __builtin_fmaf((float)dot[i][q], sa * sb, acc[i][q]);
+                        for (int q = 0; q < 4; ++q) acc[i][q] = __builtin_fmaf(d[q], s, acc[i][q]);
+                    }
+                }
+            } else {
+                const int8_t* __restrict__ A = static_cast<const int8_t*>(Av);
+                i32x4 dot[MT];
+#pragma unroll
+                for (int i = 0; i < MT; ++i) dot[i] = i32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int kc = 4 * c + t;
+                    if (!full && kc >= chunks) break;    // wave-uniform
+                    const int blk = (32 * kc) / BS;
+                    int z = 8;
+                    if constexpr (HAS_ZP) z = (int)((zr[p][t] >> ((blk & 1) * 4)) & 0xFu);
+                    const uint32_t zb = (uint32_t)(128 - z) * 0x01010101u;
+                    const i32x2 bop = qz_i8(wt[t], zb);
+#pragma unroll
+                    for (int i = 0; i < MT; ++i) {
+                        const i32x2 aop = *reinterpret_cast<const i32x2*>(A + (int64_t)arow[i] * K + 32 * kc + 8 * g);
+                        dot[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                            __builtin_bit_cast(long, aop), __builtin_bit_cast(long, bop), dot[i], 0, 0, 0);
+                    }
+                    // K % BS == 0, so a block always ends on a chunk with (t + 1) % CPB == 0.
+                    if ((t + 1) % CPB == 0) {            // end of a block: scale it
+                        const float sb = (float)sr[p][t];
+#pragma unroll
+                        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q)
+                                acc[i][q] = __builtin_fmaf((float)dot[i][q], sa[p][t][i][q] * sb, acc[i][q]);
+                            dot[i] = i32x4{0, 0, 0, 0};
                         }
-                        dot[i] = i32x4{0, 0, 0, 0};
                     }
                 }
             }
@@ -280,16 +313,18 @@ bool group_gemv_supported(int64_t k, int bits, int bs) {
     return bits == 4 && bs >= 32 && k > 0 && k % 32 == 0 && k % bs == 0;
 }
 
-GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups) {
+GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups, bool i8, int bs) {
     GroupGeom g{};
     g.mt = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
     const int64_t iters = (k / 32 + 3) / 4;
+    const int pf = group_pf(i8, bs, g.mt);
+    const int64_t runs = (iters + pf - 1) / pf;          // runs of pf iterations per wavefront
     // Enough wavefronts on each 16-column strip to fill the chip: about 8 per CU in total.
     const int64_t strips = ((n + 15) / 16) * groups;
     int64_t w = (8 * 256 + strips - 1) / strips;
     if (w < 1) w = 1;
     if (w > 8) w = 8;
-    if (w > iters) w = iters;
+    if (w > runs) w = runs;
     g.waves = (int)w;
     g.gx = (n + 15) / 16;
     g.gy = groups;
@@ -347,7 +382,7 @@ hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const 
                                  int64_t k, int bits, int bs, hipStream_t st) {
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
     if (m == 0 || groups == 0) return hipSuccess;
-    const GroupGeom g = group_geometry(offsets ? max_rows : m, n, k, offsets ? groups : 1);
+    const GroupGeom g = group_geometry(offsets ? max_rows : m, n, k, offsets ? groups : 1, false, bs);
     return group_bs<f16, false>(bs, g, a, nullptr, row_index, offsets, b, s, z, y, m, n, k, st);
 }
 
@@ -401,7 +436,7 @@ hipError_t launch_acc4(const void* a, bool a_f16, const int32_t* row_index,
                                          (((size_t)m * (size_t)k + 255) & ~(size_t)255));
     hipError_t e = launch_quantize_a_int8(a, a_f16, qa, sa, nullptr, true, m, k, bs, st);
     if (e != hipSuccess) return e;
-    const GroupGeom g = group_geometry(offsets ? max_rows : m, n, k, offsets ? groups : 1);
+    const GroupGeom g = group_geometry(offsets ? max_rows : m, n, k, offsets ? groups : 1, true, bs);
     if (a_f16) return group_bs<f16, true>(bs, g, qa, sa, row_index, offsets, b, s, z, y, m, n, k, st);
     return group_bs<float, true>(bs, g, qa, sa, row_index, offsets, b, s, z, y, m, n, k, st);
 }

@@ -58,8 +58,18 @@ struct GroupGeom {
     size_t lds;
 };
 
+// 128-k iterations whose loads one wavefront issues together.  The int8 path also holds one
+// activation scale per output value and block end, so its runs shrink to keep those within
+// 32 registers per run where one iteration allows it (64 at most: block 32, 64 rows).
+constexpr int group_pf(bool i8, int bs, int mt) {
+    if (!i8) return 4;
+    const int per_iter = (128 / bs) * mt * 4;            // activation scales per iteration
+    const int pf = 32 / per_iter;
+    return pf < 1 ? 1 : (pf > 4 ? 4 : pf);
+}
+
 bool group_gemv_supported(int64_t k, int bits, int bs);
-GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups);
+GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups, bool i8, int bs);
 hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const int32_t* offsets,
                                  int64_t groups, int64_t max_rows, const uint8_t* b,
                                  const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,

@@ -110,7 +110,7 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
                         "accuracy_level 4 is implemented for bits = 4, block_size >= 32 and "
                         "K %% 32 == 0 (got bits = %d, block_size = %d, K = %lld)",
                         p->bits, p->block_size, (long long)p->k);
-        const mnb::GroupGeom g = mnb::group_geometry(p->m, p->n, p->k, 1);
+        const mnb::GroupGeom g = mnb::group_geometry(p->m, p->n, p->k, 1, true, p->block_size);
         out->kernel = MNB_KERNEL_ACC4_I8;
         out->waves_per_group = g.waves;
         out->tile_n = 16;
@@ -153,7 +153,7 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
         out->grid_x = (c.total_waves + c.waves_per_group - 1) / c.waves_per_group;
         out->grid_y = (p->m + c.mr - 1) / c.mr;
     } else if (kern == MNB_KERNEL_GROUP_MFMA) {
-        const mnb::GroupGeom g = mnb::group_geometry(p->m, p->n, p->k, 1);
+        const mnb::GroupGeom g = mnb::group_geometry(p->m, p->n, p->k, 1, false, p->block_size);
         out->waves_per_group = g.waves;
         out->tile_n = 16;
         out->tile_m = 16 * g.mt;
