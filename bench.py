@@ -66,6 +66,19 @@ def make_weights(torch, dev, k, n, gen, bs=BS, zp=True):
     return B, S, Z
 
 
+def measured_traffic(node: str, algorithmic: int):
+    """HBM bytes per launch of `node` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (profiles/traffic_<node>.json, each counter scaled by what it reads for a copy of known size),
+    or None when no such measurement exists for this node and byte count."""
+    f = ROOT / "profiles" / f"traffic_{node.removesuffix('_proj')}.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text())
+    if d.get("algorithmic_bytes_per_launch") != algorithmic:
+        return None
+    return d["traffic_bytes_per_launch"]
+
+
 def cpu_baseline(seconds: float = 10.0) -> dict:
     """The oracle's C restatement on the host cores, over the same layer set at M=1."""
     import numpy as np
@@ -250,7 +263,8 @@ def main() -> int:
     dom_bytes = node_bytes(1, LAYER[dom][1], LAYER[dom][2])
     achieved = dom_bytes / (kern_us[dom] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(LAYER[dom][0], dom_bytes),
                 "kernel": f"MatMulNBits {LAYER[dom][0]} M=1 K={LAYER[dom][1]} N={LAYER[dom][2]}",
                 "per_launch_bytes": dom_bytes, "launch_us": round(kern_us[dom], 3)}
 

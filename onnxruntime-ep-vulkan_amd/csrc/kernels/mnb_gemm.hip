@@ -1,255 +1,299 @@
 // Prefill MatMulNBits on gfx950: dequantise-into-LDS fp16 MFMA GEMM (fp16 A, int4, block >= 32).
 //
-// Work split.  A workgroup of 4 wavefronts owns a BM x BN tile of Y; the wavefronts form a 2 x 2
-// grid, each owning a (BM/2) x (BN/2) sub-tile made of 32 x 32 MFMA tiles.  K is walked in steps
-// of KS = 64 (two quant blocks of 32, or part of one block of 64/128).
+// Work split.  One workgroup of 8 wavefronts owns a 256 x 128 tile of Y; the wavefronts form a
+// 4 (M) x 2 (N) grid and each owns a 64 x 64 sub-tile of four 32 x 32 MFMA tiles.  K is walked in
+// steps of 64 (two 32-k sub-blocks).  Workgroup ids are mapped to tiles XCD by XCD: the eight
+// XCDs take consecutive workgroup ids in turn, so each XCD is given one contiguous run of tiles
+// (for the prefill shapes: one 256-row band of A, which stays in that XCD's L2, against every
+// column tile).
 //
-// Pipeline.  Global loads run two steps ahead of the MFMAs: step s+2 is requested into one of two
-// register sets while step s is multiplied out of LDS, and step s+1 (requested a full step
-// earlier) is written to the other LDS stage after it.  The B run of a column (16 bytes = 32
-// int4 weights = one quant block of 32) is turned into exact (q - zp) fp16 values with the
-// magic-number unpack (mnb_common.hpp) on its way to LDS, which stores A and B already in the
-// v_mfma_f32_32x32x16_f16 operand order: every operand fetch is one conflict-free ds_read_b128
-// of 64 consecutive 16-byte slots.
+// Data movement.  Global -> LDS uses the gfx950 LDS DMA (global_load_lds_dwordx4 / _dword):
+// no registers, no LDS write instructions.  Three A stages and four raw-B stages form a ring;
+// step s + 2's A and step s + 3's raw B are requested while step s is multiplied, so every
+// load has two steps to land.  Each step's raw int4 B (128 columns x 32 bytes) is turned once
+// per workgroup into exact (q - zp) fp16 values in an LDS buffer (magic-number unpack,
+// mnb_common.hpp) that all four row-wavefronts then read as MFMA operands; the per-column
+// fp16 scales and packed zero points ride along in the raw stage.  One barrier per step.
 //
-// Arithmetic.  Each 32 x 32 tile's partial over one quant block (32 k) is two MFMAs over the exact
-// (q - zp) operands with fp32 accumulation -- the reference kernel's per-block fp32 partial
-// (rust/shaders/glsl/templates/q_gemv.comp:571-579) -- added to the tile's accumulator scaled by
-// the block's fp32 scale.  In the 32 x 32 output layout a lane's 16 values share one column, so
-// one scale per lane per tile per block is applied.
+// LDS layouts (16-byte slots):
+//   A stage  [256 rows][8 k-chunks], chunk kc of row r at slot 8r + (kc ^ swz(r)): one DMA
+//            instruction covers 8 whole rows (8 full 128-byte lines of A), and a wavefront's
+//            MFMA operand read (32 rows x one chunk, twice) touches every bank group once.
+//   raw B    [128 cols][2 x 16 B] + scale dword per column + zero-point dword per column.
+//   (q - z)  [8 k-chunks][128 cols]: an operand read is 2 x 512 contiguous bytes.
+//
+// Arithmetic.  Each 32 x 32 tile's partial over one quant block is accumulated by MFMAs over the
+// exact (q - zp) operands in fp32 -- the reference kernel's per-block fp32 partial
+// (rust/shaders/glsl/templates/q_gemv.comp:571-579) -- and added to the tile's accumulator
+// scaled by the block's scale.  The scaled add of one sub-block is spread between the MFMAs of
+// the next, so that it runs on the VALU while the matrix core works.  For blocks of 64 or 128
+// the partial of each 64-k step is scaled on its own (the same scale twice for a 128 block).
 #include "mnb_common.hpp"
 #include "mnb_launch.hpp"
 
 namespace mnb {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 namespace {
 
-constexpr int kKS = 64;              // K per pipeline step
-constexpr int kSub = 32;             // K per scaled partial (one block of 32)
-constexpr int kSlot = 64 * 16;       // one operand slot set: 64 lanes x 16 bytes
+constexpr int kWM = 4, kWN = 2;                  // wavefront grid
+constexpr int kBM = 64 * kWM;                    // 256
+constexpr int kBN = 64 * kWN;                    // 128
+constexpr int kKS = 64;                          // K per step
+constexpr int kNA = 3;                           // A stages
+constexpr int kNR = 4;                           // raw-B stages
+constexpr int kAStage = kBM * kKS * 2;           // 32 KB
+constexpr int kRawB = kBN * kKS / 2;             // 4 KB
+constexpr int kRStage = kRawB + 256 * 4;         // + scale and zero-point dwords
+constexpr int kFStage = kBN * kKS * 2;           // 16 KB of (q - z) fp16
+constexpr int kLds = kNA * kAStage + kNR * kRStage + 2 * kFStage;   // 151552 bytes
+constexpr int kDmaPerStep = 5;                   // DMA instructions per wavefront and step
 
-template <int BM, int BN>
-constexpr size_t gemm_lds_bytes() {
-    // per stage: A + B operand slots for KS, plus fp32 scales of the step's sub-blocks
-    return 2 * ((size_t)(BM / 32) * (kKS / 16) * kSlot + (size_t)(BN / 32) * (kKS / 16) * kSlot +
-                (size_t)(kKS / kSub) * BN * 4);
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+__device__ __forceinline__ void dma16(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void_ptr)l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void_ptr)l, 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// Workgroup barrier without the release/acquire fence of __syncthreads (which would wait for
+// every outstanding DMA); the waits that matter are explicit above.
+__device__ __forceinline__ void wg_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 }  // namespace
 
-// Register staging of one step's B run for one thread (A is staged separately, one step ahead).
-struct GemmStageB {
-    u32x4 b;            // one column's 32 int4 weights (one sub-block)
-    uint32_t s;         // the sub-block's fp16 scale bits
-    uint32_t z;         // the packed zero-point byte holding the block's nibble
-};
-
-// LDS layout (per stage), operand slot sets of 64 lanes x 16 B:
-//   A: [BM/32 m-tiles][KS/16 k-slices][64]  lane l: row l%32, k 16*slice + 8*(l/32) .. +8
-//   B: [BN/32 n-tiles][KS/16 k-slices][64]  lane l: col l%32, same k
-//   S: [KS/32 sub-blocks][BN] fp32
-template <int BM, int BN, int BS, bool HAS_ZP>
-__global__ void __launch_bounds__(256, 2)
+template <int BS, bool HAS_ZP>
+__global__ void __launch_bounds__(512)
 gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ S,
               const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K,
-              int tiles_n) {
-    static_assert(BN == 128 || BN == 256, "BN");
-    static_assert(BM == 64 || BM == 128, "BM");
-    static_assert(BS >= kSub, "block size below the sub-block");
-    constexpr int MT = BM / 64;                      // 32-row tiles per wave
-    constexpr int NT = BN / 64;                      // 32-col tiles per wave
-    constexpr int SL = kKS / 16;                     // k-slices per step
-    constexpr int A_BYTES = (BM / 32) * SL * kSlot;
-    constexpr int B_BYTES = (BN / 32) * SL * kSlot;
-    constexpr int STAGE = A_BYTES + B_BYTES + (kKS / kSub) * BN * 4;
-    constexpr int A_PIECES = BM * kKS / 8;           // 16-byte pieces of A per step
-    constexpr int A_PT = A_PIECES / 256;
-    constexpr int SUBS = kKS / kSub;                 // sub-blocks per step
-    static_assert(BN * SUBS <= 256 * 2, "B staging covers at most two runs per thread");
-    static_assert(BN * SUBS == 256, "one B run per thread");
-
+              int tiles_m, int tiles_n) {
+    static_assert(BS == 32 || BS == 64 || BS == 128, "block size");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint8_t* const sA = smem;
+    uint8_t* const sR = smem + kNA * kAStage;
+    uint8_t* const sF = sR + kNR * kRStage;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 1;
     const int wn = wave & 1;
-    const int tile_m = blockIdx.x / tiles_n;
-    const int tile_n = blockIdx.x - tile_m * tiles_n;
-    const int m0 = tile_m * BM;
-    const int n0 = tile_n * BN;
+
+    const int T = tiles_m * tiles_n;
+    const int per_xcd = (T + 7) >> 3;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= T) return;                           // whole workgroup: before any barrier
+    const int tile_m = tile / tiles_n;
+    const int tile_n = tile - tile_m * tiles_n;
+    const int m0 = tile_m * kBM;
+    const int n0 = tile_n * kBN;
     const int bpc = K / BS;
-    const int zpb = (bpc * 4 + 7) / 8;
-    const int64_t col_bytes = (int64_t)K / 2;
+    const int zpb = (bpc + 1) >> 1;
     const int steps = K / kKS;
-    // B staging: thread -> (column of the tile, sub-block of the step)
-    const int b_col = tid % BN;
-    const int b_sub = tid / BN;
-    int b_gcol = n0 + b_col;
-    b_gcol = b_gcol < N ? b_gcol : N - 1;            // clamped columns are never stored
-    const uint8_t* __restrict__ b_src = B + (int64_t)b_gcol * col_bytes;
-    const uint16_t* __restrict__ s_src = reinterpret_cast<const uint16_t*>(S) + (int64_t)b_gcol * bpc;
-    const uint8_t* __restrict__ z_src = HAS_ZP ? Z + (int64_t)b_gcol * zpb : nullptr;
+    const int64_t col_bytes = K / 2;
+    auto gcol = [&](int c) { const int g = n0 + c; return g < N ? g : N - 1; };
 
-    // A piece p (16 bytes = 8 k of one row) -> (row, k chunk).  Sixteen consecutive threads take
-    // sixteen consecutive rows of one k chunk, so their LDS slots are 256 contiguous bytes (no
-    // bank conflict on the ds_write_b128) while a wavefront still reads 64-byte runs of 16 rows.
-    auto a_piece = [](int p, int& row, int& kc) {
-        row = (p & 15) + 16 * (p / (16 * (kKS / 8)));
-        kc = (p >> 4) & (kKS / 8 - 1);
-    };
-
-    auto fetch_a = [&](u32x4 (&ra)[A_PT], int step) {
-        const int k0 = step * kKS;
+    // ---- DMA sources: A (4 instructions per wavefront) ----
+    const f16* a_src[4];
 #pragma unroll
-        for (int i = 0; i < A_PT; ++i) {
-            int row, kc;
-            a_piece(tid + 256 * i, row, kc);
-            int gm = m0 + row;
-            gm = gm < M ? gm : M - 1;                // clamped rows are never stored
-            ra[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)gm * K + k0 + 8 * kc);
+    for (int j = 0; j < 4; ++j) {
+        const int row = 32 * wave + 8 * j + (lane >> 3);
+        const int kc = (lane & 7) ^ swz(row);
+        int gm = m0 + row;
+        gm = gm < M ? gm : M - 1;                    // clamped rows are never stored
+        a_src[j] = A + (int64_t)gm * K + 8 * kc;
+    }
+    // raw B (wavefronts 0-3, thread t: column t/2, 16-byte half t%2) or the per-column scale /
+    // zero-point dwords (wavefronts 4-7)
+    const uint8_t* b_src = nullptr;
+    int aux = 0;
+    if (wave < 4) b_src = B + (int64_t)gcol(tid >> 1) * col_bytes + 16 * (tid & 1);
+    else aux = tid - 256;
+
+    auto issue_a = [&](int step, int st) {
+        uint8_t* dst = sA + st * kAStage + wave * 4 * 1024;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16(a_src[j] + step * kKS, dst + j * 1024);
+    };
+    auto issue_r = [&](int step, int st) {
+        uint8_t* base = sR + st * kRStage;
+        if (wave < 4) {
+            dma16(b_src + step * (kKS / 2), base + wave * 1024);
+        } else {
+            const int blk0 = (step * kKS) / BS;
+            const int gc = gcol(aux & 127);
+            const void* src;
+            if (HAS_ZP && aux >= 128)
+                src = Z + (((int64_t)gc * zpb + (blk0 >> 1)) & ~(int64_t)3);
+            else
+                src = S + (((int64_t)gc * bpc + blk0) & ~(int64_t)1);
+            dma4(src, base + kRawB + (wave - 4) * 256);
         }
     };
 
-    auto fetch_b = [&](GemmStageB& r, int step) {
-        const int kb = step * kKS + kSub * b_sub;    // first k of this thread's B run
-        r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(b_src + kb / 2));
-        const int blk = kb / BS;
-        r.s = s_src[blk];
-        if constexpr (HAS_ZP) r.z = z_src[blk >> 1];
-        else r.z = 0u;
-    };
-
-    auto stash_a = [&](const u32x4 (&ra)[A_PT], int stage) {
-        uint8_t* st = smem + stage * STAGE;
-#pragma unroll
-        for (int i = 0; i < A_PT; ++i) {
-            int row, kc;                            // 8-wide k chunk: slice kc/2, lane half kc%2
-            a_piece(tid + 256 * i, row, kc);
-            const int slot = ((row >> 5) * SL + (kc >> 1)) * 64 + (row & 31) + 32 * (kc & 1);
-            *reinterpret_cast<u32x4*>(st + slot * 16) = ra[i];
-        }
-    };
-
-    auto stash_b = [&](const GemmStageB& r, int stage, int step) {
-        uint8_t* st = smem + stage * STAGE;
-        const int kb = step * kKS + kSub * b_sub;
-        const int blk = kb / BS;
+    // ---- raw stage -> (q - z) fp16: thread t takes column t%128, k 16*(t/128) .. +15 ----
+    const int dq_col = tid & 127;
+    const int dq_seg = tid >> 7;
+    auto dequant = [&](int step, int rst, int fst) {
+        const uint8_t* base = sR + rst * kRStage;
+        const u32x2 w = *reinterpret_cast<const u32x2*>(base + dq_col * 32 + dq_seg * 8);
         int z = 8;
-        if constexpr (HAS_ZP) z = (int)((r.z >> ((blk & 1) * 4)) & 0xFu);
-        const f16x2 zo = zoff4(z);
-        const uint32_t w[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-        uint8_t* sb = st + A_BYTES;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            // dword d = k 8d .. 8d+7 of the run: slice 2*b_sub + d/2, lane half d%2
-            f16x8 v;
-            v.s01 = nib_pair<0>(w[d], zo);
-            v.s23 = nib_pair<1>(w[d], zo);
-            v.s45 = nib_pair<2>(w[d], zo);
-            v.s67 = nib_pair<3>(w[d], zo);
-            const int slice = 2 * b_sub + (d >> 1);
-            const int slot = ((b_col >> 5) * SL + slice) * 64 + (b_col & 31) + 32 * (d & 1);
-            *reinterpret_cast<f16x8*>(sb + slot * 16) = v;
+        if constexpr (HAS_ZP) {
+            const int blk = (step * kKS + 16 * dq_seg) / BS;
+            const uint32_t zw = *reinterpret_cast<const uint32_t*>(base + kRawB + (128 + dq_col) * 4);
+            const int byte = (int)(((int64_t)gcol(dq_col) * zpb + (blk >> 1)) & 3);
+            z = (int)((zw >> (8 * byte + 4 * (blk & 1))) & 0xFu);
         }
-        float* ss = reinterpret_cast<float*>(st + A_BYTES + B_BYTES);
-        ss[b_sub * BN + b_col] = (float)__builtin_bit_cast(f16, (uint16_t)r.s);
+        const f16x2 zo = zoff4(z);
+        f16x8 v0, v1;
+        v0.s01 = nib_pair<0>(w.x, zo);
+        v0.s23 = nib_pair<1>(w.x, zo);
+        v0.s45 = nib_pair<2>(w.x, zo);
+        v0.s67 = nib_pair<3>(w.x, zo);
+        v1.s01 = nib_pair<0>(w.y, zo);
+        v1.s23 = nib_pair<1>(w.y, zo);
+        v1.s45 = nib_pair<2>(w.y, zo);
+        v1.s67 = nib_pair<3>(w.y, zo);
+        uint8_t* f = sF + fst * kFStage;
+        *reinterpret_cast<f16x8*>(f + ((2 * dq_seg) * 128 + dq_col) * 16) = v0;
+        *reinterpret_cast<f16x8*>(f + ((2 * dq_seg + 1) * 128 + dq_col) * 16) = v1;
     };
 
-    f32x16 acc[MT][NT];
+    // tile t = 2 * j + i (i: 32-row half, j: 32-column half of the wavefront's sub-tile)
+    f32x16 acc[4];
+    f32x16 pd[4];          // per tile: running partial, or a finished one awaiting its scale
+    float psc[2] = {0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int t = 0; t < 4; ++t) {
+        acc[t] = f32x16{};
+        pd[t] = f32x16{};
+    }
+    auto retire = [&](int t) {
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(pd[t][r], psc[t >> 1], acc[t][r]);
+        asm volatile("" : "+v"(acc[t]));             // keep the adds here, beside the MFMAs
+    };
 
-    auto compute = [&](int stage) {
-        const uint8_t* st = smem + stage * STAGE;
-        const float* ss = reinterpret_cast<const float*>(st + A_BYTES + B_BYTES);
+    auto compute = [&](int step, int ast, int fst, int rst, auto&& between) {
+        const uint8_t* a_base = sA + ast * kAStage;
+        const uint8_t* f_base = sF + fst * kFStage;
+        const uint8_t* auxs = sR + rst * kRStage + kRawB;
+        float sc[2][2];                              // [j][sub]
 #pragma unroll
-        for (int sub = 0; sub < SUBS; ++sub) {
-            f16x8 a[MT][2], b[NT][2];
+        for (int j = 0; j < 2; ++j) {
+            const int c = wn * 64 + 32 * j + (lane & 31);
+            const uint32_t sw = *reinterpret_cast<const uint32_t*>(auxs + c * 4);
+            if constexpr (BS == 32) {
+                sc[j][0] = (float)__builtin_bit_cast(f16, (uint16_t)(sw & 0xFFFFu));
+                sc[j][1] = (float)__builtin_bit_cast(f16, (uint16_t)(sw >> 16));
+            } else {
+                const int64_t idx = (int64_t)gcol(c) * bpc + (step * kKS) / BS;
+                const uint16_t h = (idx & 1) ? (uint16_t)(sw >> 16) : (uint16_t)(sw & 0xFFFFu);
+                sc[j][0] = sc[j][1] = (float)__builtin_bit_cast(f16, h);
+            }
+        }
+        // Operands of both sub-blocks are requested up front; LDS returns them in order.
+        f16x8 a[2][2][2], b[2][2][2];                // [sub][tile half][k half]
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int slice = 2 * sub + h;
+                const int kc = 2 * (2 * sub + h) + (lane >> 5);
 #pragma unroll
-                for (int i = 0; i < MT; ++i)
-                    a[i][h] = *reinterpret_cast<const f16x8*>(
-                        st + (((wm * MT + i) * SL + slice) * 64 + lane) * 16);
-#pragma unroll
-                for (int j = 0; j < NT; ++j)
-                    b[j][h] = *reinterpret_cast<const f16x8*>(
-                        st + A_BYTES + (((wn * NT + j) * SL + slice) * 64 + lane) * 16);
-            }
-#pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                const float sc = ss[sub * BN + (wn * NT + j) * 32 + (lane & 31)];
-#pragma unroll
-                for (int i = 0; i < MT; ++i) {
-                    f32x16 d = {};
-                    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][0], b[j][0], d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][1], b[j][1], d, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(d[r], sc, acc[i][j][r]);
+                for (int i = 0; i < 2; ++i) {
+                    const int row = wm * 64 + 32 * i + (lane & 31);
+                    a[sub][i][h] = *reinterpret_cast<const f16x8*>(
+                        a_base + (row * 8 + (kc ^ swz(row))) * 16);
                 }
-                if constexpr (MT * NT > 2) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = wn * 64 + 32 * j + (lane & 31);
+                    b[sub][j][h] = *reinterpret_cast<const f16x8*>(f_base + (kc * 128 + col) * 16);
+                }
             }
-            // Keep the scheduler from hoisting the next sub-block's MFMAs above this one's
-            // epilogue: that would hold twice the partial tiles live and spill.
-            __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            if (sub == 1) between();
+            // A block of 32 starts at every sub-block; blocks of 64 and 128 are scaled per step.
+            const bool fresh = BS == 32 || sub == 0;
+            if (fresh) {
+                // each tile's finished partial is scaled into acc right before its registers
+                // take the next partial's first MFMA
+                retire(0);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int i = t & 1, j = t >> 1;
+                    f32x16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][i][0], b[sub][j][0], f32x16{}, 0, 0, 0);
+                    pd[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][i][1], b[sub][j][1], c, 0, 0, 0);
+                    if (t < 3) retire(t + 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int i = t & 1, j = t >> 1;
+                    f32x16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][i][0], b[sub][j][0], pd[t], 0, 0, 0);
+                    pd[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][i][1], b[sub][j][1], c, 0, 0, 0);
+                }
+            }
+            if (BS == 32 || sub == 1) {              // the partial is complete: keep its scales
+                psc[0] = sc[0][sub];
+                psc[1] = sc[1][sub];
+                asm volatile("" : "+v"(psc[0]), "+v"(psc[1]));
+            }
         }
     };
 
-    // A is requested one step ahead (it is read by many workgroups and mostly hits in L2); B,
-    // streamed from HBM, two steps ahead in two register sets.
-    u32x4 ra[A_PT];
-    GemmStageB r0, r1;
-    fetch_a(ra, 0);
-    fetch_b(r0, 0);
-    if (steps > 1) fetch_b(r1, 1);
-    stash_a(ra, 0);
-    stash_b(r0, 0, 0);
-    __syncthreads();
+    // ---- prologue: raw(0) | A(0) raw(1) | A(1) raw(2) ----
+    issue_r(0, 0);
+    issue_a(0, 0);
+    if (steps > 1) { issue_r(1, 1); issue_a(1, 1); }
+    if (steps > 2) issue_r(2, 2);
+    if (steps > 2) wait_vm_lgkm0<2 * kDmaPerStep>(); else wait_vm_lgkm0<0>();
+    wg_barrier();
+    dequant(0, 0, 0);
 
-    // Two steps per trip so that the register sets are named at compile time.
-    for (int s = 0; s < steps; s += 2) {
-        // step s: stage 0 holds it, r1 holds B of step s+1, r0 is free
-        if (s + 1 < steps) fetch_a(ra, s + 1);
-        if (s + 2 < steps) fetch_b(r0, s + 2);
-        compute(0);
-        if (s + 1 < steps) {
-            stash_a(ra, 1);
-            stash_b(r1, 1, s + 1);
-        }
-        __syncthreads();
-        if (s + 1 >= steps) break;
-        // step s+1: stage 1 holds it, r0 holds B of step s+2, r1 is free
-        if (s + 2 < steps) fetch_a(ra, s + 2);
-        if (s + 3 < steps) fetch_b(r1, s + 3);
-        compute(1);
-        if (s + 2 < steps) {
-            stash_a(ra, 0);
-            stash_b(r0, 0, s + 2);
-        }
-        __syncthreads();
+    for (int s = 0; s < steps; ++s) {
+        // A(s) and raw(s+1) were requested two steps ago; the previous step's five may still
+        // be in flight (all requests are counted in issue order).
+        if (s + 2 < steps) wait_vm_lgkm0<kDmaPerStep>(); else wait_vm_lgkm0<0>();
+        wg_barrier();
+        if (s + 2 < steps) issue_a(s + 2, (s + 2) % kNA);
+        if (s + 3 < steps) issue_r(s + 3, (s + 3) % kNR);
+        compute(s, s % kNA, s & 1, s % kNR, [&]() {
+            if (s + 1 < steps) dequant(s + 1, (s + 1) % kNR, (s + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+        });
     }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) retire(t);
 
     // ---- store: lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + r%4 of each tile ----
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
+    for (int t = 0; t < 4; ++t) {
+        const int i = t & 1, j = t >> 1;
+        const int col = n0 + wn * 64 + 32 * j + (lane & 31);
+        if (col >= N) continue;
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const int col = n0 + (wn * NT + j) * 32 + (lane & 31);
-            if (col >= N) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + (wm * MT + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < M) Y[(int64_t)row * N + col] = (f16)acc[i][j][r];
-            }
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (row < M) Y[(int64_t)row * N + col] = (f16)acc[t][r];
         }
     }
 }
@@ -258,65 +302,57 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
 // Host side
 // ------------------------------------------------------------------------------------------
 
-bool gemm_supported(int64_t m, int64_t k, int bits, int bs) {
-    return m > 0 && bits == 4 && bs >= kSub && k > 0 && k % kKS == 0 && k % bs == 0;
+bool gemm_supported(int64_t m, int64_t n, int64_t k, int bits, int bs, bool has_zp) {
+    if (m <= 0 || n <= 0 || bits != 4 || k <= 0 || k % kKS) return false;
+    if (bs != 32 && bs != 64 && bs != 128) return false;
+    if (k % bs) return false;
+    const int64_t bpc = k / bs;
+    // The scale and zero-point dwords of the last column must not reach past the arrays.
+    if (bs > 32 && (n * bpc) % 2) return false;
+    if (has_zp && (n * ((bpc + 1) / 2)) % 4) return false;
+    return true;
 }
 
 GemmConfig gemm_config(int64_t m, int64_t n) {
     GemmConfig c{};
-    // 128 x 128 while that still yields two workgroups per CU; otherwise 64-row tiles.
-    const int64_t mid = ((m + 127) / 128) * ((n + 127) / 128);
-    if (mid >= 512) {
-        c.bm = 128;
-        c.bn = 128;
-    } else {
-        c.bm = 64;
-        c.bn = 128;
-    }
-    c.tiles_m = (m + c.bm - 1) / c.bm;
-    c.tiles_n = (n + c.bn - 1) / c.bn;
+    c.bm = kBM;
+    c.bn = kBN;
+    c.tiles_m = (m + kBM - 1) / kBM;
+    c.tiles_n = (n + kBN - 1) / kBN;
     return c;
 }
 
-template <int BM, int BN, int BS, bool HAS_ZP>
+template <int BS, bool HAS_ZP>
 static hipError_t gemm_go(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                           const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
                           hipStream_t st) {
-    constexpr size_t lds = gemm_lds_bytes<BM, BN>();
-    auto kern = gemm_f16_mfma<BM, BN, BS, HAS_ZP>;
+    auto kern = gemm_f16_mfma<BS, HAS_ZP>;
     // More than 64 KB of dynamic LDS must be allowed explicitly (for the current device).
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     if (e != hipSuccess) return e;
-    const dim3 grid((unsigned)(c.tiles_m * c.tiles_n), 1, 1);
-    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, static_cast<const f16*>(a), b,
+    const int64_t tiles = c.tiles_m * c.tiles_n;
+    const dim3 grid((unsigned)(8 * ((tiles + 7) / 8)), 1, 1);
+    hipLaunchKernelGGL(kern, grid, dim3(512), kLds, st, static_cast<const f16*>(a), b,
                        static_cast<const f16*>(s), z, static_cast<f16*>(y), (int)m, (int)n,
-                       (int)k, (int)c.tiles_n);
+                       (int)k, (int)c.tiles_m, (int)c.tiles_n);
     return hipGetLastError();
-}
-
-template <int BS, bool HAS_ZP>
-static hipError_t gemm_tile(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
-                            const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
-                            hipStream_t st) {
-    if (c.bm == 128 && c.bn == 128) return gemm_go<128, 128, BS, HAS_ZP>(c, a, b, s, z, y, m, n, k, st);
-    if (c.bm == 64 && c.bn == 128) return gemm_go<64, 128, BS, HAS_ZP>(c, a, b, s, z, y, m, n, k, st);
-    return hipErrorInvalidValue;
 }
 
 template <int BS>
 static hipError_t gemm_zp(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                           const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
                           hipStream_t st) {
-    if (z) return gemm_tile<BS, true>(c, a, b, s, z, y, m, n, k, st);
-    return gemm_tile<BS, false>(c, a, b, s, z, y, m, n, k, st);
+    if (z) return gemm_go<BS, true>(c, a, b, s, z, y, m, n, k, st);
+    return gemm_go<BS, false>(c, a, b, s, z, y, m, n, k, st);
 }
 
 hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                            const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                            int bs, hipStream_t st) {
     if (m == 0) return hipSuccess;
-    if (!gemm_supported(m, k, bits, bs)) return hipErrorInvalidValue;
+    if (!gemm_supported(m, n, k, bits, bs, z != nullptr)) return hipErrorInvalidValue;
+    if (c.bm != kBM || c.bn != kBN) return hipErrorInvalidValue;
     switch (bs) {
         case 32: return gemm_zp<32>(c, a, b, s, z, y, m, n, k, st);
         case 64: return gemm_zp<64>(c, a, b, s, z, y, m, n, k, st);

@@ -42,7 +42,7 @@ struct GemmConfig {
     int64_t tiles_m, tiles_n;
 };
 
-bool gemm_supported(int64_t m, int64_t k, int bits, int bs);
+bool gemm_supported(int64_t m, int64_t n, int64_t k, int bits, int bs, bool has_zp);
 GemmConfig gemm_config(int64_t m, int64_t n);
 hipError_t launch_gemm(const void* a, const uint8_t* b, const void* s, const uint8_t* z, void* y,
                        int64_t m, int64_t n, int64_t k, int bits, int bs, hipStream_t stream);

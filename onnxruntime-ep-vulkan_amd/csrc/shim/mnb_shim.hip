@@ -124,7 +124,8 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     const bool fast = f16 && mnb::gemv_supported(p->k, p->bits, p->block_size);
     const bool stream = f16 && mnb::gemv_stream_supported(p->m, p->k, p->bits, p->block_size);
     const bool group = f16 && mnb::group_gemv_supported(p->k, p->bits, p->block_size);
-    const bool gemm = f16 && mnb::gemm_supported(p->m, p->k, p->bits, p->block_size);
+    const bool gemm = f16 && mnb::gemm_supported(p->m, p->n, p->k, p->bits, p->block_size,
+                                                  p->has_zero_points != 0);
     int kern = MNB_KERNEL_GENERIC;
     if (fast) kern = MNB_KERNEL_GEMV_MFMA;               // bits 8, block 16: 16-row MFMA GEMV
     if (group) kern = MNB_KERNEL_GROUP_MFMA;             // int4, block >= 32: any row count
@@ -210,6 +211,12 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
          kern == MNB_KERNEL_GEMM_MFMA || kern == MNB_KERNEL_GROUP_MFMA) &&
         (!aligned(a, 16) || !aligned(b, 16)))
         kern = MNB_KERNEL_GENERIC;
+    // The GEMM's LDS DMA also fetches scales and zero points as aligned dwords; the row-tiled
+    // GEMV takes any other case of the same form.
+    if (kern == MNB_KERNEL_GEMM_MFMA &&
+        (!aligned(scales, 4) || !aligned(zero_points, 4) ||
+         !mnb::gemm_supported(p->m, p->n, p->k, p->bits, p->block_size, zero_points != nullptr)))
+        kern = MNB_KERNEL_GROUP_MFMA;
     if (kern == MNB_KERNEL_ACC4_I8) {
         // the int8 path reads B in 16-byte units and stages its own aligned copy of A
         if (!aligned(b, 16) || !aligned(workspace, 256))
