@@ -23,6 +23,7 @@
 // e-th of `experts` consecutive per-expert B / scales / zero_points tensors.  The dense form is
 // one group with rows 0 .. M-1.  The W wavefronts of a workgroup split the K iterations and are
 // summed in a fixed order through LDS, so results are run-to-run deterministic.
+#include <algorithm>
 #include <type_traits>
 
 #include "mnb_common.hpp"
@@ -72,14 +73,18 @@ __global__ void __launch_bounds__(512)
 group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
            const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
            const uint8_t* __restrict__ B, const T* __restrict__ S, const uint8_t* __restrict__ Z,
-           T* __restrict__ Y, int M, int N, int K) {
+           T* __restrict__ Y, int M, int N, int K, int ksplit, int runs_per_split,
+           f32x4* __restrict__ part, int* __restrict__ cnt) {
     extern __shared__ f32x4 red[];                       // [W][MT][64]
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int W = blockDim.x >> 6;
     const int nl = lane & 15;
     const int g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    // blockIdx.x = strip * ksplit + split: the split's workgroups share the strip's K range.
+    const int strip = blockIdx.x / ksplit;
+    const int split = blockIdx.x - strip * ksplit;
+    const int n0 = strip * 16;
     const int col = min(n0 + nl, N - 1);
     const int bpc = K / BS;
     const int zpb = (bpc * 4 + 7) / 8;
@@ -100,42 +105,101 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     const int r0 = row_lo + blockIdx.z * 16 * MT;
     if (r0 >= row_hi) return;                            // whole workgroup leaves: no barrier yet
     const uint8_t* __restrict__ bcol = B + wofs_b + (int64_t)col * (K / 2) + 16 * g;
-    const T* __restrict__ scol = S + wofs_s + (int64_t)col * bpc;
-    const uint8_t* __restrict__ zcol = HAS_ZP ? Z + wofs_z + (int64_t)col * zpb : nullptr;
 
     // A row of each 16-row tile this lane feeds (MFMA A operand: row l%16).
     int arow[MT];
-    int srow[MT][4];                                     // rows of the lane's output values
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
         int r = r0 + 16 * i + nl;
         r = r < row_hi ? r : row_hi - 1;
         arow[i] = row_index ? row_index[r] : r;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            int rr = r0 + 16 * i + 4 * g + q;
-            rr = rr < row_hi ? rr : row_hi - 1;
-            srow[i][q] = row_index ? row_index[rr] : rr;
-        }
     }
 
     f32x4 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Each wavefront takes runs of PF consecutive 128-k iterations: all weight, scale and
-    // zero-point loads of a run are issued before any of it is computed.  Out-of-range chunks
-    // load a clamped in-bounds address and are skipped (wave-uniformly) at compute time.
     constexpr int PF = group_pf(I8, BS, MT);
     constexpr int CPB = BS / 32;                         // 32-k chunks per block (1, 2 or 4)
-    for (int c0 = wave * PF; c0 < iters; c0 += W * PF) {
+    const int c_lo = split * runs_per_split * PF;
+    const int c_hi = min(iters, c_lo + runs_per_split * PF);
+
+    // The strip's scales and zero points over this workgroup's K range are staged in LDS with
+    // coalesced loads once: per 32-k chunk each lane then reads them from LDS instead of
+    // issuing scattered 1- and 2-byte global loads (which would dominate the kernel).
+    const int b_lo = (128 * c_lo) / BS;
+    const int b_hi = (32 * min(4 * c_hi, chunks)) / BS;  // K % BS == 0: exact
+    const int nblk = b_hi - b_lo;
+    const int spitch = (nblk + 3) & ~3;
+    const int z_lo = b_lo >> 1;
+    const int nz = ((b_hi - 1) >> 1) - z_lo + 1;
+    const int zpitch = (nz + 3) & ~3;
+    T* const sS = reinterpret_cast<T*>(red + W * MT * 64);
+    uint8_t* const sZ = reinterpret_cast<uint8_t*>(sS + 16 * spitch);
+    for (int idx = threadIdx.x; idx < 16 * nblk; idx += blockDim.x) {
+        const int n = idx / nblk;
+        const int j = idx - n * nblk;
+        const int cc = min(n0 + n, N - 1);
+        sS[n * spitch + j] = S[wofs_s + (int64_t)cc * bpc + b_lo + j];
+    }
+    if constexpr (HAS_ZP) {
+        for (int idx = threadIdx.x; idx < 16 * nz; idx += blockDim.x) {
+            const int n = idx / nz;
+            const int j = idx - n * nz;
+            const int cc = min(n0 + n, N - 1);
+            sZ[n * zpitch + j] = Z[wofs_z + (int64_t)cc * zpb + z_lo + j];
+        }
+    }
+    // int8 path: the tile rows' activation scales over the same blocks, [block][16 * MT rows],
+    // so a lane's four output rows are one 16-byte LDS read.
+    float* const sA = reinterpret_cast<float*>(sZ + (HAS_ZP ? 16 * zpitch : 0));
+    if constexpr (I8) {
+        for (int idx = threadIdx.x; idx < 16 * MT * nblk; idx += blockDim.x) {
+            const int b = idx / (16 * MT);
+            const int rr = idx - b * (16 * MT);
+            int r = r0 + rr;
+            r = r < row_hi ? r : row_hi - 1;
+            const int ar = row_index ? row_index[r] : r;
+            sA[idx] = a_scale[(int64_t)ar * bpc + b_lo + b];
+        }
+    }
+    __syncthreads();
+    const T* __restrict__ lS = sS + nl * spitch;
+    const uint8_t* __restrict__ lZ = sZ + nl * zpitch;
+
+    // Each wavefront takes runs of PF consecutive 128-k iterations: all weight loads of a run
+    // are issued before any of it is computed.  Out-of-range chunks load a clamped in-bounds
+    // address and are dropped by a zero scale at compute time.
+    for (int c0 = c_lo + wave * PF; c0 < c_hi; c0 += W * PF) {
         u32x4 raw[PF];
         T sr[PF][4];
         uint8_t zr[PF][4];
         float sa[I8 ? PF : 1][I8 ? 4 : 1][MT][4];        // int8 path: activation scales
+        // Activation operands of the run, when they fit in 64 registers (else loaded per chunk).
+        constexpr int A_REGS = I8 ? 2 : 4;
+        constexpr bool PRE_A = PF * 4 * MT * A_REGS <= 64;
+        u32x4 apre[PRE_A ? PF : 1][PRE_A ? 4 : 1][PRE_A ? MT : 1];
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             const int c = c0 + p;
+            if constexpr (PRE_A) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    int kc = 4 * c + t;
+                    kc = kc < chunks ? kc : chunks - 1;
+#pragma unroll
+                    for (int i = 0; i < MT; ++i) {
+                        if constexpr (I8) {
+                            const u32x2 v = *reinterpret_cast<const u32x2*>(
+                                static_cast<const int8_t*>(Av) + (int64_t)arow[i] * K + 32 * kc + 8 * g);
+                            apre[p][t][i] = u32x4{v.x, v.y, 0u, 0u};
+                        } else {
+                            apre[p][t][i] = *reinterpret_cast<const u32x4*>(
+                                static_cast<const f16*>(Av) + (int64_t)arow[i] * K + 32 * kc + 8 * g);
+                        }
+                    }
+                }
+            }
             int ch = 4 * c + g;
             const bool ok = ch < chunks;
             ch = ok ? ch : chunks - 1;
@@ -146,26 +210,31 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
             for (int t = 0; t < 4; ++t) {
                 int kc = 4 * c + t;
                 kc = kc < chunks ? kc : chunks - 1;
-                const int blk = (32 * kc) / BS;
-                if (!I8 || (t + 1) % CPB == 0) sr[p][t] = scol[blk];
-                if constexpr (HAS_ZP) zr[p][t] = zcol[blk >> 1];
+                int blk = (32 * kc) / BS;
+                blk = blk < b_hi ? blk : b_hi - 1;       // past the range: any staged value
+                if (!I8 || (t + 1) % CPB == 0) sr[p][t] = lS[blk - b_lo];
+                if constexpr (HAS_ZP) zr[p][t] = lZ[(blk >> 1) - z_lo];
                 else zr[p][t] = 0;
                 if constexpr (I8) {
                     if ((t + 1) % CPB == 0) {            // block ends: one scale per output row
 #pragma unroll
-                        for (int i = 0; i < MT; ++i)
+                        for (int i = 0; i < MT; ++i) {
+                            const f32x4 v = *reinterpret_cast<const f32x4*>(
+                                sA + (blk - b_lo) * (16 * MT) + 16 * i + 4 * g);
 #pragma unroll
-                            for (int q = 0; q < 4; ++q)
-                                sa[p][t][i][q] = a_scale[(int64_t)srow[i][q] * bpc + blk];
+                            for (int q = 0; q < 4; ++q) sa[p][t][i][q] = v[q];
+                        }
                     }
                 }
             }
         }
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
+            // Branch-free: an iteration past the split's range or a chunk past K is computed on
+            // clamped in-bounds data and dropped by a zero scale (a branch here would let the
+            // compiler sink the prefetched loads into it).
             const int c = c0 + p;
-            if (c >= iters) break;                       // wave-uniform
-            const bool full = 4 * c + 3 < chunks;        // wave-uniform
+            const bool in_run = c < c_hi;                // wave-uniform
             uint32_t v0 = raw[p].x, v1 = raw[p].y, v2 = raw[p].z, v3 = raw[p].w;
             transpose_rows(v0, v1, v2, v3);
             const uint32_t wt[4] = {v0, v1, v2, v3};
@@ -174,9 +243,8 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const int kc = 4 * c + t;
-                    if (!full && kc >= chunks) break;    // wave-uniform
                     const int blk = (32 * kc) / BS;
-                    const float s = (float)sr[p][t];
+                    const float s = (in_run && kc < chunks) ? (float)sr[p][t] : 0.f;
                     int z = 8;
                     if constexpr (HAS_ZP) z = (int)((zr[p][t] >> ((blk & 1) * 4)) & 0xFu);
                     const f16x2 zo = zoff4(z);
@@ -187,7 +255,9 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
                     bop.s67 = nib_pair<3>(wt[t], zo);
 #pragma unroll
                     for (int i = 0; i < MT; ++i) {
-                        const f16x8 aop = *reinterpret_cast<const f16x8*>(A + (int64_t)arow[i] * K + 32 * kc + 8 * g);
+                        f16x8 aop;
+                        if constexpr (PRE_A) aop = __builtin_bit_cast(f16x8, apre[p][t][i]);
+                        else aop = *reinterpret_cast<const f16x8*>(A + (int64_t)arow[i] * K + 32 * min(kc, chunks - 1) + 8 * g);
                         f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
                         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, d, 0, 0, 0);
 #pragma unroll
@@ -202,7 +272,6 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const int kc = 4 * c + t;
-                    if (!full && kc >= chunks) break;    // wave-uniform
                     const int blk = (32 * kc) / BS;
                     int z = 8;
                     if constexpr (HAS_ZP) z = (int)((zr[p][t] >> ((blk & 1) * 4)) & 0xFu);
@@ -210,13 +279,16 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
                     const i32x2 bop = qz_i8(wt[t], zb);
 #pragma unroll
                     for (int i = 0; i < MT; ++i) {
-                        const i32x2 aop = *reinterpret_cast<const i32x2*>(A + (int64_t)arow[i] * K + 32 * kc + 8 * g);
+                        i32x2 aop;
+                        if constexpr (PRE_A) aop = i32x2{(int32_t)apre[p][t][i].x, (int32_t)apre[p][t][i].y};
+                        else aop = *reinterpret_cast<const i32x2*>(A + (int64_t)arow[i] * K + 32 * min(kc, chunks - 1) + 8 * g);
                         dot[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
                             __builtin_bit_cast(long, aop), __builtin_bit_cast(long, bop), dot[i], 0, 0, 0);
                     }
-                    // K % BS == 0, so a block always ends on a chunk with (t + 1) % CPB == 0.
+                    // K % BS == 0, so a block always ends on a chunk with (t + 1) % CPB == 0,
+                    // and a block is either wholly inside K or wholly past it.
                     if ((t + 1) % CPB == 0) {            // end of a block: scale it
-                        const float sb = (float)sr[p][t];
+                        const float sb = (in_run && kc < chunks) ? (float)sr[p][t] : 0.f;
 #pragma unroll
                         for (int i = 0; i < MT; ++i) {
 #pragma unroll
@@ -234,6 +306,55 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
 #pragma unroll
     for (int i = 0; i < MT; ++i) red[(wave * MT + i) * 64 + lane] = acc[i];
     __syncthreads();
+    if (ksplit > 1) {
+        // K split over workgroups: each writes its partial tile; the last to arrive (device-
+        // scope counter) adds the partials in split order and stores Y, then re-arms the
+        // counter.  Partials move through device-coherent (agent-scope) atomic stores and
+        // loads, so no workgroup has to write back or invalidate its XCD's L2.
+        const int sid = (blockIdx.z * gridDim.y + blockIdx.y) * (gridDim.x / ksplit) + strip;
+        float* mine = reinterpret_cast<float*>(part + ((int64_t)sid * ksplit + split) * (MT * 64));
+        for (int idx = threadIdx.x; idx < 64 * MT; idx += blockDim.x) {
+            f32x4 sum = red[idx];
+            for (int w = 1; w < W; ++w) sum += red[w * MT * 64 + idx];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                __hip_atomic_store(mine + 4 * idx + q, sum[q], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);                   // the partial has reached memory
+        __syncthreads();
+        __shared__ int last;
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(cnt + sid, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == ksplit - 1;
+        __syncthreads();
+        if (!last) return;
+        const float* all = reinterpret_cast<const float*>(part + (int64_t)sid * ksplit * (MT * 64));
+        for (int idx = threadIdx.x; idx < 64 * MT; idx += blockDim.x) {
+            f32x4 sum;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                sum[q] = __hip_atomic_load(all + 4 * idx + q, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            for (int p = 1; p < ksplit; ++p)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    sum[q] += __hip_atomic_load(all + p * (MT * 64 * 4) + 4 * idx + q,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int i = idx >> 6;
+            const int ll = idx & 63;
+            const int cc = n0 + (ll & 15);
+            if (cc >= N) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = r0 + 16 * i + 4 * (ll >> 4) + q;
+                if (r < row_hi) Y[(int64_t)r * N + cc] = (T)sum[q];
+            }
+        }
+        if (threadIdx.x == 0)
+            __hip_atomic_store(cnt + sid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     for (int idx = threadIdx.x; idx < 64 * MT; idx += blockDim.x) {
         f32x4 sum = red[idx];
         for (int w = 1; w < W; ++w) sum += red[w * MT * 64 + idx];
@@ -254,20 +375,36 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
 // qa = clamp(rint(a * (127 / amax)), -127, 127) (0 when amax == 0), all in fp32 with
 // round-half-even.  PERMUTED writes each group of eight as [0,2,4,6,1,3,5,7] (the order
 // qz_i8 produces weights in); otherwise natural order plus the block sums of qa.
-template <typename T, int BS, bool PERMUTED>
+template <typename T, int BS, bool PERMUTED, bool VEC>
 __global__ void __launch_bounds__(256)
 quantize_a_int8(const T* __restrict__ A, int8_t* __restrict__ qa, float* __restrict__ scale,
-                int32_t* __restrict__ qsum, int M, int K) {
+                int32_t* __restrict__ qsum, int M, int K, int* __restrict__ cnt, int ncnt) {
     constexpr int G = BS / 8;                            // threads per block: 2..16
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // the split-K counters of the int8 GEMV that follows start at zero
+    for (int64_t i = t; i < ncnt; i += (int64_t)gridDim.x * blockDim.x) cnt[i] = 0;
     const int64_t groups = (int64_t)M * (K / 8);
     const bool live = t < groups;
     const int64_t tt = live ? t : groups - 1;
     const int row = (int)(tt / (K / 8));
     const int k0 = (int)(tt % (K / 8)) * 8;
     float a[8];
+    if constexpr (VEC) {                                 // 16-byte aligned rows: wide loads
+        const T* src = A + (int64_t)row * K + k0;
+        if constexpr (sizeof(T) == 2) {
+            const f16x8 v = *reinterpret_cast<const f16x8*>(src);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) a[e] = (float)A[(int64_t)row * K + k0 + e];
+            for (int e = 0; e < 8; ++e) a[e] = (float)v[e];
+        } else {
+            const f32x4 v0 = *reinterpret_cast<const f32x4*>(src);
+            const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { a[e] = v0[e]; a[e + 4] = v1[e]; }
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = (float)A[(int64_t)row * K + k0 + e];
+    }
     float amax = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(a[e]));
@@ -288,13 +425,20 @@ quantize_a_int8(const T* __restrict__ A, int8_t* __restrict__ qa, float* __restr
     const int blk = k0 / BS;
     const int bpc = K / BS;
     int8_t* out = qa + (int64_t)row * K + k0;
-    if constexpr (PERMUTED) {
-        const int order[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    constexpr int order_p[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    int8_t o[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = (int8_t)q[order[e]];
+    for (int e = 0; e < 8; ++e) o[e] = (int8_t)q[PERMUTED ? order_p[e] : e];
+    if constexpr (VEC) {
+        u32x2 w;
+        w.x = (uint32_t)(uint8_t)o[0] | ((uint32_t)(uint8_t)o[1] << 8) |
+              ((uint32_t)(uint8_t)o[2] << 16) | ((uint32_t)(uint8_t)o[3] << 24);
+        w.y = (uint32_t)(uint8_t)o[4] | ((uint32_t)(uint8_t)o[5] << 8) |
+              ((uint32_t)(uint8_t)o[6] << 16) | ((uint32_t)(uint8_t)o[7] << 24);
+        *reinterpret_cast<u32x2*>(out) = w;
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) out[e] = (int8_t)q[e];
+        for (int e = 0; e < 8; ++e) out[e] = o[e];
     }
     if (k0 % BS == 0) scale[(int64_t)row * bpc + blk] = amax / 127.0f;
     if (qsum) {
@@ -313,23 +457,35 @@ bool group_gemv_supported(int64_t k, int bits, int bs) {
     return bits == 4 && bs >= 32 && k > 0 && k % 32 == 0 && k % bs == 0;
 }
 
-GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups, bool i8, int bs) {
+GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups, bool i8, int bs,
+                         bool allow_split) {
     GroupGeom g{};
     g.mt = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
     const int64_t iters = (k / 32 + 3) / 4;
     const int pf = group_pf(i8, bs, g.mt);
     const int64_t runs = (iters + pf - 1) / pf;          // runs of pf iterations per wavefront
-    // Enough wavefronts on each 16-column strip to fill the chip: about 8 per CU in total.
-    const int64_t strips = ((n + 15) / 16) * groups;
-    int64_t w = (8 * 256 + strips - 1) / strips;
-    if (w < 1) w = 1;
-    if (w > 8) w = 8;
-    if (w > runs) w = runs;
-    g.waves = (int)w;
     g.gx = (n + 15) / 16;
     g.gy = groups;
     g.gz = (rows + 16 * g.mt - 1) / (16 * g.mt);
-    g.lds = (size_t)g.waves * g.mt * 64 * sizeof(f32x4);
+    // Enough wavefronts on each 16-column strip to fill the chip: about 8 per CU in total.
+    const int64_t strips = g.gx * groups * (allow_split ? g.gz : 1);
+    int64_t w = (8 * 256 + strips - 1) / strips;
+    if (w < 1) w = 1;
+    if (w > runs) w = runs;
+    // More than 8 wavefronts per strip: split K over workgroups as well.
+    int64_t ks = (allow_split && w > 8) ? (w + 7) / 8 : 1;
+    int64_t rps = (runs + ks - 1) / ks;
+    ks = (runs + rps - 1) / rps;                         // no empty split
+    w = ks > 1 ? rps : w;
+    if (w > 8) w = 8;
+    g.waves = (int)w;
+    g.ksplit = (int)ks;
+    g.runs_per_split = (int)rps;
+    // LDS: the wavefronts' partial tiles, then the strip's staged scales (fp32 at most) and
+    // zero points over one split's K range.
+    const int64_t nblk = std::min<int64_t>(k / bs, rps * pf * 128 / bs + 1);
+    g.lds = (size_t)g.waves * g.mt * 64 * sizeof(f32x4) + 16 * ((nblk + 3) & ~3) * sizeof(float) +
+            16 * ((nblk / 2 + 2 + 3) & ~3) + (i8 ? (size_t)16 * g.mt * nblk * sizeof(float) : 0);
     return g;
 }
 
@@ -337,14 +493,22 @@ template <typename T, bool I8, int BS, bool HAS_ZP>
 static hipError_t group_mt(const GroupGeom& g, const void* a, const float* a_scale,
                            const int32_t* row_index, const int32_t* offsets, const uint8_t* b,
                            const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
-                           int64_t k, hipStream_t st) {
-    const dim3 grid((unsigned)g.gx, (unsigned)g.gy, (unsigned)g.gz);
+                           int64_t k, f32x4* part, int* cnt, hipStream_t st) {
+    const dim3 grid((unsigned)(g.gx * g.ksplit), (unsigned)g.gy, (unsigned)g.gz);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     const T* S = static_cast<const T*>(s);
     T* Y = static_cast<T*>(y);
 #define MNB_GROUP_GO(MT_)                                                                          \
-    hipLaunchKernelGGL((group_gemv<T, I8, BS, HAS_ZP, MT_>), grid, block, g.lds, st, a, a_scale, \
-                       row_index, offsets, b, S, z, Y, (int)m, (int)n, (int)k)
+    do {                                                                                          \
+        auto kern = group_gemv<T, I8, BS, HAS_ZP, MT_>;                                           \
+        if (g.lds > 64 * 1024) {                                                                  \
+            const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),      \
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)g.lds);                          \
+            if (ea != hipSuccess) return ea;                                                      \
+        }                                                                                         \
+        hipLaunchKernelGGL(kern, grid, block, g.lds, st, a, a_scale, row_index, offsets, b, S, z, \
+                           Y, (int)m, (int)n, (int)k, g.ksplit, g.runs_per_split, part, cnt);     \
+    } while (0)
     switch (g.mt) {
         case 1: MNB_GROUP_GO(1); break;
         case 2: MNB_GROUP_GO(2); break;
@@ -358,20 +522,20 @@ template <typename T, bool I8, int BS>
 static hipError_t group_zp(const GroupGeom& g, const void* a, const float* a_scale,
                            const int32_t* row_index, const int32_t* offsets, const uint8_t* b,
                            const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
-                           int64_t k, hipStream_t st) {
-    if (z) return group_mt<T, I8, BS, true>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, st);
-    return group_mt<T, I8, BS, false>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, st);
+                           int64_t k, f32x4* part, int* cnt, hipStream_t st) {
+    if (z) return group_mt<T, I8, BS, true>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, part, cnt, st);
+    return group_mt<T, I8, BS, false>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, part, cnt, st);
 }
 
 template <typename T, bool I8>
 static hipError_t group_bs(int bs, const GroupGeom& g, const void* a, const float* a_scale,
                            const int32_t* row_index, const int32_t* offsets, const uint8_t* b,
                            const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
-                           int64_t k, hipStream_t st) {
+                           int64_t k, f32x4* part, int* cnt, hipStream_t st) {
     switch (bs) {
-        case 32: return group_zp<T, I8, 32>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, st);
-        case 64: return group_zp<T, I8, 64>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, st);
-        case 128: return group_zp<T, I8, 128>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, st);
+        case 32: return group_zp<T, I8, 32>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, part, cnt, st);
+        case 64: return group_zp<T, I8, 64>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, part, cnt, st);
+        case 128: return group_zp<T, I8, 128>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, part, cnt, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -382,25 +546,39 @@ hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const 
                                  int64_t k, int bits, int bs, hipStream_t st) {
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
     if (m == 0 || groups == 0) return hipSuccess;
-    const GroupGeom g = group_geometry(offsets ? max_rows : m, n, k, offsets ? groups : 1, false, bs);
-    return group_bs<f16, false>(bs, g, a, nullptr, row_index, offsets, b, s, z, y, m, n, k, st);
+    const GroupGeom g =
+        group_geometry(offsets ? max_rows : m, n, k, offsets ? groups : 1, false, bs, false);
+    return group_bs<f16, false>(bs, g, a, nullptr, row_index, offsets, b, s, z, y, m, n, k,
+                                nullptr, nullptr, st);
 }
 
 hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
-                                  hipStream_t st) {
+                                  hipStream_t st, int* cnt, int64_t ncnt) {
     if (m == 0) return hipSuccess;
     if (k % bs || (bs != 16 && bs != 32 && bs != 64 && bs != 128)) return hipErrorInvalidValue;
     const int64_t groups = m * (k / 8);
     const dim3 grid((unsigned)((groups + 255) / 256));
+    const bool vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(qa) % 8 == 0);
 #define MNB_Q(T_, BS_)                                                                            \
     do {                                                                                          \
-        if (permuted)                                                                             \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, true>), grid, dim3(256), 0, st,          \
-                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k);      \
+        if (permuted && vec)                                                                      \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, true, true>), grid, dim3(256), 0, st,    \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
+                               (int)ncnt);                                                        \
+        else if (vec)                                                                             \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, false, true>), grid, dim3(256), 0, st,   \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
+                               (int)ncnt);                                                        \
+        else if (permuted)                                                                        \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, true, false>), grid, dim3(256), 0, st,   \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
+                               (int)ncnt);                                                        \
         else                                                                                      \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, false>), grid, dim3(256), 0, st,         \
-                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k);      \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, false, false>), grid, dim3(256), 0, st,  \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
+                               (int)ncnt);                                                        \
     } while (0)
 #define MNB_QBS(T_)                                                                               \
     switch (bs) {                                                                                 \
@@ -419,26 +597,51 @@ hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* 
     return hipGetLastError();
 }
 
-size_t acc4_workspace_bytes(int64_t m, int64_t k, int bs) {
-    const size_t qa = ((size_t)m * (size_t)k + 255) & ~(size_t)255;
-    return qa + (size_t)m * (size_t)(k / bs) * sizeof(float);
+// accuracy_level = 4 workspace: qa [m][k] int8 | a_scale [m][k/bs] fp32 | split-K partial
+// tiles | split-K counters, each part 256-byte aligned.
+namespace {
+struct Acc4Layout {
+    size_t qa, sa, part, cnt, total;
+    int64_t nsid;
+};
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+Acc4Layout acc4_layout(const GroupGeom& g, int64_t m, int64_t k, int bs) {
+    Acc4Layout l{};
+    l.qa = 0;
+    l.sa = align256((size_t)m * (size_t)k);
+    l.part = l.sa + align256((size_t)m * (size_t)(k / bs) * sizeof(float));
+    l.nsid = g.gx * g.gy * g.gz;
+    const size_t part_bytes = g.ksplit > 1
+        ? (size_t)l.nsid * g.ksplit * g.mt * 64 * sizeof(f32x4) : 0;
+    l.cnt = l.part + align256(part_bytes);
+    l.total = l.cnt + align256((size_t)(g.ksplit > 1 ? l.nsid : 0) * sizeof(int));
+    return l;
+}
+}  // namespace
+
+size_t acc4_workspace_bytes(int64_t m, int64_t n, int64_t k, int bs) {
+    const GroupGeom g = group_geometry(m, n, k, 1, true, bs, true);
+    return acc4_layout(g, m, k, bs).total;
 }
 
-hipError_t launch_acc4(const void* a, bool a_f16, const int32_t* row_index,
-                       const int32_t* offsets, int64_t groups, int64_t max_rows,
-                       const uint8_t* b, const void* s, const uint8_t* z, void* y, int64_t m,
-                       int64_t n, int64_t k, int bits, int bs, void* workspace,
-                       hipStream_t st) {
+hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
+                       const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
+                       int bs, void* workspace, hipStream_t st) {
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
-    if (m == 0 || groups == 0) return hipSuccess;
-    int8_t* qa = static_cast<int8_t*>(workspace);
-    float* sa = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
-                                         (((size_t)m * (size_t)k + 255) & ~(size_t)255));
-    hipError_t e = launch_quantize_a_int8(a, a_f16, qa, sa, nullptr, true, m, k, bs, st);
+    if (m == 0) return hipSuccess;
+    const GroupGeom g = group_geometry(m, n, k, 1, true, bs, true);
+    const Acc4Layout l = acc4_layout(g, m, k, bs);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    int8_t* qa = reinterpret_cast<int8_t*>(ws + l.qa);
+    float* sa = reinterpret_cast<float*>(ws + l.sa);
+    f32x4* part = g.ksplit > 1 ? reinterpret_cast<f32x4*>(ws + l.part) : nullptr;
+    int* cnt = g.ksplit > 1 ? reinterpret_cast<int*>(ws + l.cnt) : nullptr;
+    hipError_t e = launch_quantize_a_int8(a, a_f16, qa, sa, nullptr, true, m, k, bs, st, cnt,
+                                          g.ksplit > 1 ? l.nsid : 0);
     if (e != hipSuccess) return e;
-    const GroupGeom g = group_geometry(offsets ? max_rows : m, n, k, offsets ? groups : 1, true, bs);
-    if (a_f16) return group_bs<f16, true>(bs, g, qa, sa, row_index, offsets, b, s, z, y, m, n, k, st);
-    return group_bs<float, true>(bs, g, qa, sa, row_index, offsets, b, s, z, y, m, n, k, st);
+    if (a_f16)
+        return group_bs<f16, true>(bs, g, qa, sa, nullptr, nullptr, b, s, z, y, m, n, k, part, cnt, st);
+    return group_bs<float, true>(bs, g, qa, sa, nullptr, nullptr, b, s, z, y, m, n, k, part, cnt, st);
 }
 
 }  // namespace mnb

@@ -53,7 +53,9 @@ hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b,
 // Launch shape of the row-tiled MFMA GEMV (mnb_group_gemv.hip).
 struct GroupGeom {
     int mt;              // 16-row tiles per workgroup (1, 2 or 4)
-    int waves;           // wavefronts per workgroup (split K)
+    int waves;           // wavefronts per workgroup (split K within the workgroup)
+    int ksplit;          // workgroups per strip (split K across workgroups; int8 path only)
+    int runs_per_split;  // prefetched runs of iterations per split
     int64_t gx, gy, gz;  // column strips, groups, row tiles
     size_t lds;
 };
@@ -69,20 +71,20 @@ constexpr int group_pf(bool i8, int bs, int mt) {
 }
 
 bool group_gemv_supported(int64_t k, int bits, int bs);
-GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups, bool i8, int bs);
+GroupGeom group_geometry(int64_t rows, int64_t n, int64_t k, int64_t groups, bool i8, int bs,
+                         bool allow_split);
 hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const int32_t* offsets,
                                  int64_t groups, int64_t max_rows, const uint8_t* b,
                                  const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
                                  int64_t k, int bits, int bs, hipStream_t stream);
+// cnt / ncnt: split-K counters of a following int8 GEMV, cleared by the quantiser (may be null).
 hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
-                                  hipStream_t stream);
-size_t acc4_workspace_bytes(int64_t m, int64_t k, int bs);
-hipError_t launch_acc4(const void* a, bool a_f16, const int32_t* row_index,
-                       const int32_t* offsets, int64_t groups, int64_t max_rows,
-                       const uint8_t* b, const void* s, const uint8_t* z, void* y, int64_t m,
-                       int64_t n, int64_t k, int bits, int bs, void* workspace,
-                       hipStream_t stream);
+                                  hipStream_t stream, int* cnt = nullptr, int64_t ncnt = 0);
+size_t acc4_workspace_bytes(int64_t m, int64_t n, int64_t k, int bs);
+hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
+                       const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
+                       int bs, void* workspace, hipStream_t stream);
 
 GemvGeom gemv_geometry(int64_t m, int64_t n, int64_t k, int bits, int bs);
 bool gemv_supported(int64_t k, int bits, int block_size);

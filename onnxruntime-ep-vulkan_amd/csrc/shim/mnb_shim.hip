@@ -110,14 +110,16 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
                         "accuracy_level 4 is implemented for bits = 4, block_size >= 32 and "
                         "K %% 32 == 0 (got bits = %d, block_size = %d, K = %lld)",
                         p->bits, p->block_size, (long long)p->k);
-        const mnb::GroupGeom g = mnb::group_geometry(p->m, p->n, p->k, 1, true, p->block_size);
+        const mnb::GroupGeom g =
+            mnb::group_geometry(p->m, p->n, p->k, 1, true, p->block_size, true);
         out->kernel = MNB_KERNEL_ACC4_I8;
         out->waves_per_group = g.waves;
         out->tile_n = 16;
         out->tile_m = 16 * g.mt;
-        out->grid_x = g.gx;
+        out->grid_x = g.gx * g.ksplit;
         out->grid_y = g.gz;
-        out->workspace_bytes = (int64_t)mnb::acc4_workspace_bytes(p->m, p->k, p->block_size);
+        out->workspace_bytes =
+            (int64_t)mnb::acc4_workspace_bytes(p->m, p->n, p->k, p->block_size);
         return MNB_OK;
     }
     const bool f16 = p->dtype == MNB_DTYPE_F16;
@@ -140,7 +142,7 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     out->kernel = kern;
     if (kern == MNB_KERNEL_GEMM_MFMA) {
         const mnb::GemmConfig c = mnb::gemm_config(p->m, p->n);
-        out->waves_per_group = 4;
+        out->waves_per_group = 8;
         out->tile_n = c.bn;
         out->tile_m = c.bm;
         out->grid_x = c.tiles_m * c.tiles_n;
@@ -154,7 +156,8 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
         out->grid_x = (c.total_waves + c.waves_per_group - 1) / c.waves_per_group;
         out->grid_y = (p->m + c.mr - 1) / c.mr;
     } else if (kern == MNB_KERNEL_GROUP_MFMA) {
-        const mnb::GroupGeom g = mnb::group_geometry(p->m, p->n, p->k, 1, false, p->block_size);
+        const mnb::GroupGeom g =
+            mnb::group_geometry(p->m, p->n, p->k, 1, false, p->block_size, false);
         out->waves_per_group = g.waves;
         out->tile_n = 16;
         out->tile_m = 16 * g.mt;
@@ -222,9 +225,8 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
         if (!aligned(b, 16) || !aligned(workspace, 256))
             return fail(MNB_ERR_INVALID, "accuracy_level 4 needs B 16-byte and the workspace "
                                          "256-byte aligned");
-        e = mnb::launch_acc4(a, p->dtype == MNB_DTYPE_F16, nullptr, nullptr, 1, p->m, b, scales,
-                             zero_points, y, p->m, p->n, p->k, p->bits, p->block_size,
-                             workspace, st);
+        e = mnb::launch_acc4(a, p->dtype == MNB_DTYPE_F16, b, scales, zero_points, y, p->m,
+                             p->n, p->k, p->bits, p->block_size, workspace, st);
     } else if (kern == MNB_KERNEL_GROUP_MFMA) {
         e = mnb::launch_group_gemv_f16(a, nullptr, nullptr, 1, p->m, b, scales, zero_points, y,
                                        p->m, p->n, p->k, p->bits, p->block_size, st);

@@ -72,9 +72,13 @@ def test_group_gemv_parity(cuda, M, N, K, bs, zp):
     _check(y.cpu().numpy(), ref, f"group M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("M,K,bs,dtype", [(1, 256, 128, np.float16), (16, 8192, 128, np.float16),
-                                          (3, 512, 32, np.float32), (7, 1024, 64, np.float16)])
-def test_quantizer_bit_exact(cuda, M, K, bs, dtype):
+@pytest.mark.parametrize("M,K,bs,dtype,offset", [(1, 256, 128, np.float16, 0),
+                                                 (16, 8192, 128, np.float16, 0),
+                                                 (3, 512, 32, np.float32, 0),
+                                                 (7, 1024, 64, np.float16, 0),
+                                                 (5, 512, 32, np.float16, 1),   # sub-aligned A
+                                                 (2, 256, 16, np.float32, 1)])
+def test_quantizer_bit_exact(cuda, M, K, bs, dtype, offset):
     import mnb
     import torch
     rng = np.random.default_rng(M * K)
@@ -85,7 +89,9 @@ def test_quantizer_bit_exact(cuda, M, K, bs, dtype):
     qa = torch.empty(M, K, dtype=torch.int8, device=cuda)
     sa = torch.empty(M, K // bs, dtype=torch.float32, device=cuda)
     qs = torch.empty(M, K // bs, dtype=torch.int32, device=cuda)
-    tA = _dev(A, cuda)
+    # offset 1: A starts one element into its buffer, so the element-wise load path runs
+    buf = _dev(np.concatenate([np.zeros(offset, dtype), A.ravel()]), cuda)
+    tA = buf[offset:]
     dt = mnb.DTYPE_F16 if dtype == np.float16 else mnb.DTYPE_F32
     s = int(torch.cuda.current_stream().cuda_stream)
     mnb.check(mnb.load().mnb_quantize_a_int8(M, K, bs, dt, tA.data_ptr(), qa.data_ptr(),
@@ -104,6 +110,8 @@ ACC4 = [
     (5, 100, 2880, 32, False),
     (40, 48, 512, 64, True),
     (200, 96, 1024, 128, False),       # many row tiles
+    (1, 256, 8192, 32, True),          # K split over 4 workgroups per strip
+    (2, 200, 16384, 64, True),         # K split, ragged last strip
 ]
 
 
@@ -128,6 +136,29 @@ def test_accuracy_level_4(cuda, M, N, K, bs, zp):
     err = y.astype(np.float64) - ref
     assert float(np.sqrt(np.mean(err ** 2))) <= 1.2e-2 * rms
     assert orc.max_err_rms_normalised(y, ref) <= 6e-2
+
+
+def test_accuracy_level_4_split_k_reuses_workspace(cuda):
+    # The K-split int8 GEMV hands partial tiles between workgroups through the workspace and a
+    # counter per strip that the quantiser clears: three calls on one workspace (inputs x, y, x)
+    # must each match the level-4 definition, and the first and third must be bit-identical.
+    import mnb
+    import torch
+    M, N, K, bs = 1, 256, 8192, 32
+    assert mnb.plan(mnb.problem(M, N, K, 4, bs, True, mnb.DTYPE_F16, 4)).grid_x > (N + 15) // 16
+    ins = [orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=True, seed=s) for s in (5, 6)]
+    ws = torch.zeros(mnb.workspace_bytes(mnb.problem(M, N, K, 4, bs, True, mnb.DTYPE_F16, 4)),
+                     dtype=torch.uint8, device=cuda)
+    outs = []
+    for inp in (ins[0], ins[1], ins[0]):
+        t = [_dev(inp[k], cuda) for k in ("A", "B", "scales", "zp")]
+        y = mnb.matmul_nbits(*t, N, K, 4, bs, accuracy_level=4, workspace=ws)
+        torch.cuda.synchronize()
+        y = y.cpu().numpy()
+        _check(y, orc.matmul_nbits_acc4(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs),
+               "acc4 split-K")
+        outs.append(y)
+    assert np.array_equal(outs[0].view(np.uint16), outs[2].view(np.uint16))
 
 
 def test_accuracy_level_4_fp32_node(cuda):
