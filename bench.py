@@ -130,6 +130,9 @@ def main() -> int:
                     help="counter-collection mode: launch only this decode node (qkv_proj, o_proj, "
                          "gate_up_proj, down_proj) --steps times over rotated weights, then one "
                          "plain 256 MiB device copy for calibrating FETCH_SIZE/WRITE_SIZE; no JSON")
+    ap.add_argument("--pmc-prefill", type=int, default=None, metavar="M",
+                    help="counter-collection mode: launch only the prefill GEMM (K=3072, N=8192) "
+                         "at M rows --steps times; no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -167,6 +170,21 @@ def main() -> int:
     def step(s, sp=sptr):
         for i in range(len(LAYER)):
             launch(i, s % copies, sp)
+
+    if args.pmc_prefill:
+        pm, pk, pn = args.pmc_prefill, 3072, 8192
+        pw = [make_weights(torch, dev, pk, pn, gen, zp=False) for _ in range(2)]
+        pA = torch.randn(pm, pk, device=dev, generator=gen).to(torch.float16)
+        pY = torch.empty(pm, pn, dtype=torch.float16, device=dev)
+        pprob = mnb.problem(pm, pn, pk, BITS, BS, False)
+        for r in range(args.steps):
+            pB, pS, _ = pw[r % 2]
+            mnb.check(lib.mnb_matmul_nbits(C.byref(pprob), pA.data_ptr(), pB.data_ptr(),
+                                           pS.data_ptr(), None, pY.data_ptr(), None, 0, sptr))
+        torch.cuda.synchronize()
+        print(f"pmc mode: {args.steps} launches of the prefill GEMM M={pm} K={pk} N={pn} "
+              f"({mnb.KERNEL_NAMES.get(mnb.plan(pprob).kernel)})")
+        return 0
 
     if args.pmc_node:
         i = [x[0] for x in LAYER].index(args.pmc_node)
@@ -306,7 +324,11 @@ def main() -> int:
                         "tile": [pinfo.tile_m, pinfo.tile_n],
                         "roofline": {"bound": "mfma", "achieved": round(ptf, 2),
                                      "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                     "frac": round(ptf / F16_MFMA_PEAK_TFLOPS, 4)}})
+                                     "frac": round(ptf / F16_MFMA_PEAK_TFLOPS, 4),
+                                     "traffic": measured_traffic(
+                                         f"prefill_m{pm}",
+                                         pm * pk * 2 + pn * pk // 2 + pn * (pk // BS) * 2
+                                         + pm * pn * 2)}})
 
     def graph_time_us(fn, reps):
         """Average device time per launch of `fn(r, stream)` over a graph of `reps` launches."""
