@@ -410,6 +410,41 @@ def main() -> int:
                     "frac_hbm": round(mbytes / (m_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         del wB, wS
 
+    # The EP's Compute call (mnb_session_run, synchronous) for qkv at M=1: host I/O (A and Y in
+    # pageable host memory, staged through HBM, as ORT hands them over by default) against
+    # device-resident A and Y (MI355X_EP_DEVICE_MEMORY=1).  Wall clock per call, median.
+    sess = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(sess)))
+    qk, qn = LAYER[0][1], LAYER[0][2]
+    qB, qS, qZ = (t.cpu().numpy() for t in layers[0][0])
+    qw = C.c_void_p()
+    mnb.check(lib.mnb_weights_upload(sess, C.byref(probs[0]), qB.ctypes.data, qB.nbytes,
+                                     qS.ctypes.data, qS.nbytes, qZ.ctypes.data, qZ.nbytes,
+                                     C.byref(qw)))
+    hA = np.ascontiguousarray(acts[0].cpu().numpy())
+    hY = np.empty((1, qn), dtype=np.float16)
+    dA, dY = acts[0], torch.empty(1, qn, dtype=torch.float16, device=dev)
+
+    def io_call_us(a_ptr, a_dev, y_ptr, y_dev, reps=300):
+        for _ in range(20):
+            mnb.check(lib.mnb_session_run(sess, qw, 1, a_ptr, a_dev, y_ptr, y_dev))
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            mnb.check(lib.mnb_session_run(sess, qw, 1, a_ptr, a_dev, y_ptr, y_dev))
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e6
+
+    host_us = io_call_us(hA.ctypes.data, 0, hY.ctypes.data, 0)
+    dev_us = io_call_us(dA.data_ptr(), 1, dY.data_ptr(), 1)
+    torch.cuda.synchronize()
+    same = bool(np.array_equal(hY.view(np.uint16), dY.cpu().numpy().view(np.uint16)))
+    lib.mnb_weights_release(qw)
+    lib.mnb_session_destroy(sess)
+    session_io = {"node": f"{LAYER[0][0]} M=1 K={qk} N={qn}", "host_io_us": round(host_us, 2),
+                  "device_io_us": round(dev_us, 2), "outputs_identical": same,
+                  "note": "median wall clock of one synchronous EP Compute call (mnb_session_run)"}
+
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 
     line = {
@@ -437,6 +472,7 @@ def main() -> int:
         "prefill": prefill,
         "accuracy_level_4": acc4,
         "moe": moe,
+        "session_io": session_io,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -156,9 +156,25 @@ int mnb_weights_upload(mnb_session* s, const mnb_problem* node, const void* b_ho
                        const void* zp_host, size_t zp_bytes, mnb_weights** out);
 int mnb_weights_release(mnb_weights* w);
 
+/* Device memory behind the EP's ORT allocator and data transfer (replace the reference's
+ * Vulkan allocator and transfer: rust/src/allocator.rs, rust/src/transfer.rs, wired in
+ * rust/src/factory.rs:1043-1285).  Allocations are plain hipMalloc memory of the given device;
+ * copies are synchronous. */
+#define MNB_COPY_HOST_TO_DEVICE 1
+#define MNB_COPY_DEVICE_TO_HOST 2
+#define MNB_COPY_DEVICE_TO_DEVICE 3
+int mnb_device_malloc(int device_index, size_t bytes, void** out);
+int mnb_device_free(int device_index, void* p);
+int mnb_memcpy(int device_index, void* dst, const void* src, size_t bytes, int kind);
+
 /* Compute with device-resident A and Y (stream-ordered on the session stream, no sync). */
 int mnb_session_run_device(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_dev,
                            void* y_dev);
+/* Compute with A and Y each in host memory or in the session device's memory (flags): host
+ * tensors are staged through HBM; returns after the stream has finished (ORT's synchronous
+ * Compute of a non-stream-aware EP, rust/src/ep.rs:2538-2716). */
+int mnb_session_run(mnb_session* s, const mnb_weights* w, int64_t m, const void* a,
+                    int a_on_device, void* y, int y_on_device);
 /* Compute with host A and Y: stage A in, launch, copy Y out, synchronise (ORT host I/O). */
 int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,
                          void* y_host);

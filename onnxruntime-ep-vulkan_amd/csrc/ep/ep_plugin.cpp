@@ -12,6 +12,12 @@
 //             first Compute, keyed by host pointer, rust/src/vk/session.rs:1633-1700), and
 //             Compute stages A in, launches one HIP kernel and copies Y out
 //             (rust/src/ep.rs:2538-2716, rust/src/vk/session.rs:1036).
+// With MI355X_EP_DEVICE_MEMORY=1 (off by default, as the reference's
+// ONNXRUNTIME_EP_VULKAN_DEVICE_MEMORY, rust/src/factory.rs:487-504) the EP also advertises its
+// HBM to ORT: an OrtAllocator over hipMalloc per device, an OrtDataTransferImpl for host <-> HBM
+// copies, and the default memory device, so ORT keeps A and Y in HBM and Compute launches on
+// device pointers with no staging (reference: rust/src/factory.rs:1043-1285, allocator.rs,
+// transfer.rs).
 // Every vtable entry is wrapped so that a C++ exception becomes an OrtStatus and never unwinds
 // into ORT (the reference's guard_ffi_*, rust/src/lib.rs:99-206).  A Compute failure is always
 // reported as a status; nothing is recomputed on the CPU.
@@ -19,7 +25,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cctype>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <new>
@@ -113,6 +121,17 @@ OrtStatus* guarded(const OrtApi* api, const char* where, F&& f) {
 bool env_flag(const char* name) {
     const char* v = std::getenv(name);
     return v && *v && std::strcmp(v, "0") != 0;
+}
+
+// The one reader of MI355X_EP_DEVICE_MEMORY.  The mode ships off, so only an explicit "on"
+// spelling enables it; anything else (including typos of "off") leaves the host-I/O path.
+bool device_memory_requested() {
+    const char* v = std::getenv("MI355X_EP_DEVICE_MEMORY");
+    if (!v) return false;
+    std::string s;
+    for (const char* p = v; *p; ++p)
+        if (!std::isspace((unsigned char)*p)) s += (char)std::tolower((unsigned char)*p);
+    return s == "1" || s == "true" || s == "yes" || s == "on";
 }
 
 void claim_log(const char* fmt, ...) {
@@ -289,6 +308,9 @@ struct Ep {
     mnb_session* session = nullptr;
     bool keep_constant_initializers = false;
     bool claim_enabled = true;
+    // Device-memory mode: the HBM memory device ORT places this EP's tensors on (owned by the
+    // factory's memory info), else null.
+    const OrtMemoryDevice* memory_device = nullptr;
     std::mutex mu;
 };
 
@@ -298,7 +320,42 @@ struct Factory {
     const OrtEpApi* ep_api = nullptr;
     uint32_t version = 0;
     std::string registered_name;
+    bool device_memory = false;     // MI355X_EP_DEVICE_MEMORY, read once at CreateEpFactories
+    std::mutex mi_mu;
+    std::map<int, OrtMemoryInfo*> memory_infos;   // per HIP device; released with the factory
 };
+
+// The OrtMemoryInfo describing HIP device `device`'s HBM, created once and owned by the factory
+// (ORT keeps pointers to what EpDevice_AddAllocatorInfo registers).
+const OrtMemoryInfo* factory_memory_info(Factory* f, int device) {
+    std::lock_guard<std::mutex> lk(f->mi_mu);
+    auto it = f->memory_infos.find(device);
+    if (it != f->memory_infos.end()) return it->second;
+    const std::string name = "MI355X_HBM_" + std::to_string(device);
+    OrtMemoryInfo* mi = nullptr;
+    ort_check(f->api,
+              f->api->CreateMemoryInfo_V2(name.c_str(), OrtMemoryInfoDeviceType_GPU, kAmdVendorId,
+                                          device, OrtDeviceMemoryType_DEFAULT, 256,
+                                          OrtDeviceAllocator, &mi),
+              "CreateMemoryInfo_V2");
+    f->memory_infos[device] = mi;
+    return mi;
+}
+
+// Whether an ORT memory device is this EP's HBM (an AMD GPU's default memory), and which HIP
+// ordinal it names.
+bool is_our_hbm(const OrtEpApi* ep_api, const OrtMemoryDevice* md, int* device) {
+    if (!md) return false;
+    if (ep_api->MemoryDevice_GetDeviceType(md) != OrtMemoryInfoDeviceType_GPU) return false;
+    if (ep_api->MemoryDevice_GetVendorId(md) != kAmdVendorId) return false;
+    if (ep_api->MemoryDevice_GetMemoryType(md) != OrtDeviceMemoryType_DEFAULT) return false;
+    if (device) *device = (int)ep_api->MemoryDevice_GetDeviceId(md);
+    return true;
+}
+
+bool is_host_memory(const OrtEpApi* ep_api, const OrtMemoryDevice* md) {
+    return !md || ep_api->MemoryDevice_GetDeviceType(md) == OrtMemoryInfoDeviceType_CPU;
+}
 
 Factory* as_factory(const OrtEpFactory* p) {
     return reinterpret_cast<Factory*>(const_cast<OrtEpFactory*>(p));
@@ -375,11 +432,23 @@ void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     ORT_OK(api, GetTensorMutableData(y, &ydata));
     const void* adata = tensor_data(api, a);
 
+    // Where A and Y live: host memory, or (device-memory mode) this EP's HBM.
+    bool a_dev = false, y_dev = false;
+    if (ep->memory_device) {
+        int da = -1, dy = -1;
+        a_dev = is_our_hbm(ep->ep_api, ep->ep_api->Value_GetMemoryDevice(a), &da);
+        y_dev = is_our_hbm(ep->ep_api, ep->ep_api->Value_GetMemoryDevice(y), &dy);
+        if ((a_dev && da != ep->device) || (y_dev && dy != ep->device))
+            fail(ORT_INVALID_ARGUMENT, "a tensor lives on HIP device %d, this EP runs on %d",
+                 a_dev && da != ep->device ? da : dy, ep->device);
+    }
+
     std::lock_guard<std::mutex> lk(k.mu);
     if (!k.resident) {
         // Weights that are not constant initializers arrive with every call: upload them.
         const void* host[3] = {nullptr, nullptr, nullptr};
         size_t bytes[3] = {0, 0, 0};
+        std::vector<uint8_t> staged[3];
         for (int r = 0; r < 3; ++r) {
             if (k.fused_w[r] == SIZE_MAX) continue;
             if (k.fused_w[r] >= nin) fail(ORT_EP_FAIL, "weight input %d is missing", r + 1);
@@ -388,6 +457,14 @@ void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
             if (!v) continue;
             host[r] = tensor_data(api, v);
             bytes[r] = tensor_bytes(api, v);
+            int dw = -1;
+            if (ep->memory_device && is_our_hbm(ep->ep_api, ep->ep_api->Value_GetMemoryDevice(v), &dw)) {
+                // a weight that ORT placed in HBM: bring it to the host for the upload
+                staged[r].resize(bytes[r]);
+                mnb_ok(mnb_memcpy(dw, staged[r].data(), host[r], bytes[r], MNB_COPY_DEVICE_TO_HOST),
+                       "reading a device-resident weight");
+                host[r] = staged[r].data();
+            }
         }
         if (k.weights) {
             mnb_weights_release(k.weights);
@@ -397,7 +474,8 @@ void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
                                   host[2], bytes[2], &k.weights),
                "uploading MatMulNBits weights");
     }
-    mnb_ok(mnb_session_run_host(ep->session, k.weights, m, adata, ydata), "MatMulNBits kernel");
+    mnb_ok(mnb_session_run(ep->session, k.weights, m, adata, a_dev ? 1 : 0, ydata, y_dev ? 1 : 0),
+           "MatMulNBits kernel");
     g_compute_count.fetch_add(1);
 }
 
@@ -413,6 +491,14 @@ OrtStatus* ORT_API_CALL ci_compute(OrtNodeComputeInfo* self, void*, OrtKernelCon
 // ---- OrtEp ----------------------------------------------------------------------------------
 
 const char* ORT_API_CALL ep_get_name(const OrtEp*) noexcept { return kEpName; }
+
+// Device-memory mode: the HBM of the EP's device (reference: rust/src/ep.rs:423-434, which
+// returns null there because its tensors stay in host memory).
+OrtStatus* ORT_API_CALL ep_get_default_memory_device(const OrtEp* self,
+                                                     const OrtMemoryDevice** device) noexcept {
+    if (device) *device = self ? as_ep(self)->memory_device : nullptr;
+    return nullptr;
+}
 
 // Whether the HIP library implements accuracy_level = 4 (int8 activations) for this node's
 // form: asked of its planner, so the claim never runs ahead of the kernels.
@@ -655,6 +741,12 @@ void get_supported_devices(Factory* f, const OrtHardwareDevice* const* devices, 
         OrtStatus* st = f->ep_api->CreateEpDevice(&f->base, pool[i], meta, nullptr, &epd);
         if (meta) api->ReleaseKeyValuePairs(meta);
         ort_check(api, st, "CreateEpDevice");
+        if (f->device_memory) {
+            // Advertise the device's HBM so ORT asks CreateAllocator for it.  A failure leaves
+            // a working host-I/O EP (reference: rust/src/factory.rs:406-417, :605-660).
+            OrtStatus* as = f->ep_api->EpDevice_AddAllocatorInfo(epd, factory_memory_info(f, hip[i]));
+            if (as) claim_log("EpDevice_AddAllocatorInfo failed: %s", status_text(api, as).c_str());
+        }
         ep_devices[written++] = epd;
     }
     *num_out = written;
@@ -701,6 +793,10 @@ OrtStatus* ORT_API_CALL f_create_ep(OrtEpFactory* self, const OrtHardwareDevice*
         ep->api = api;
         ep->ep_api = f->ep_api;
         ep->device = device;
+        if (f->device_memory) {
+            ep->memory_device = f->ep_api->MemoryInfo_GetMemoryDevice(factory_memory_info(f, device));
+            if (f->version >= 27) ep->base.GetDefaultMemoryDevice = ep_get_default_memory_device;
+        }
         if (session_option(api, so, "ep.keep_constant_initializers", &opt))
             ep->keep_constant_initializers = opt == "1" || opt == "true";
         // ep.max_claim_ops: comma-separated allowlist (reference: rust/src/ep.rs:39-160);
@@ -720,17 +816,117 @@ void ORT_API_CALL f_release_ep(OrtEpFactory*, OrtEp* p) noexcept {
     delete ep;
 }
 
-OrtStatus* ORT_API_CALL f_create_allocator(OrtEpFactory*, const OrtMemoryInfo*,
-                                           const OrtKeyValuePairs*, OrtAllocator** out) noexcept {
-    if (out) *out = nullptr;   // host I/O: ORT's CPU allocator serves every tensor
-    return nullptr;
+// ---- device memory: allocator and data transfer --------------------------------------------
+
+// An OrtAllocator over hipMalloc on one HIP device (reference counterpart: the Vulkan handle
+// allocator, rust/src/allocator.rs).  The memory info it reports is the factory's.
+struct DeviceAllocator {
+    OrtAllocator base;              // first member
+    int device = 0;
+    const OrtMemoryInfo* info = nullptr;
+};
+
+void* ORT_API_CALL da_alloc(OrtAllocator* self, size_t size) noexcept {
+    auto* a = reinterpret_cast<DeviceAllocator*>(self);
+    void* p = nullptr;
+    if (!a || mnb_device_malloc(a->device, size, &p) != MNB_OK) return nullptr;
+    return p;
 }
 
-void ORT_API_CALL f_release_allocator(OrtEpFactory*, OrtAllocator*) noexcept {}
+void ORT_API_CALL da_free(OrtAllocator* self, void* p) noexcept {
+    auto* a = reinterpret_cast<DeviceAllocator*>(self);
+    if (a && p) (void)mnb_device_free(a->device, p);
+}
 
-OrtStatus* ORT_API_CALL f_create_data_transfer(OrtEpFactory*, OrtDataTransferImpl** out) noexcept {
+const OrtMemoryInfo* ORT_API_CALL da_info(const OrtAllocator* self) noexcept {
+    return self ? reinterpret_cast<const DeviceAllocator*>(self)->info : nullptr;
+}
+
+OrtStatus* ORT_API_CALL f_create_allocator(OrtEpFactory* self, const OrtMemoryInfo* memory_info,
+                                           const OrtKeyValuePairs*, OrtAllocator** out) noexcept {
+    if (out) *out = nullptr;        // defined before anything can fail
+    Factory* f = as_factory(self);
+    return guarded(f ? f->api : nullptr, "CreateAllocator", [&] {
+        if (!f || !out || !memory_info || !f->device_memory) return;   // host I/O: no allocator
+        int device = -1;
+        if (!is_our_hbm(f->ep_api, f->ep_api->MemoryInfo_GetMemoryDevice(memory_info), &device))
+            return;                 // a memory info this EP did not advertise: decline
+        auto a = std::make_unique<DeviceAllocator>();
+        std::memset(&a->base, 0, sizeof(a->base));
+        a->base.version = f->version;
+        a->base.Alloc = da_alloc;
+        a->base.Free = da_free;
+        a->base.Info = da_info;
+        a->base.Reserve = da_alloc;
+        a->device = device;
+        a->info = factory_memory_info(f, device);
+        *out = &a.release()->base;
+    });
+}
+
+void ORT_API_CALL f_release_allocator(OrtEpFactory*, OrtAllocator* a) noexcept {
+    delete reinterpret_cast<DeviceAllocator*>(a);
+}
+
+// Host <-> HBM and HBM <-> HBM copies of whole tensors (reference: rust/src/transfer.rs).
+struct DataTransfer {
+    OrtDataTransferImpl base;       // first member
+    Factory* factory = nullptr;
+};
+
+void ORT_API_CALL dt_release(OrtDataTransferImpl* self) noexcept {
+    delete reinterpret_cast<DataTransfer*>(self);
+}
+
+bool ORT_API_CALL dt_can_copy(const OrtDataTransferImpl* self, const OrtMemoryDevice* src,
+                              const OrtMemoryDevice* dst) noexcept {
+    const auto* t = reinterpret_cast<const DataTransfer*>(self);
+    if (!t || !src || !dst) return false;
+    const OrtEpApi* e = t->factory->ep_api;
+    const bool s_hbm = is_our_hbm(e, src, nullptr), d_hbm = is_our_hbm(e, dst, nullptr);
+    const bool s_host = e->MemoryDevice_GetDeviceType(src) == OrtMemoryInfoDeviceType_CPU;
+    const bool d_host = e->MemoryDevice_GetDeviceType(dst) == OrtMemoryInfoDeviceType_CPU;
+    return (s_hbm && (d_hbm || d_host)) || (s_host && d_hbm);
+}
+
+OrtStatus* ORT_API_CALL dt_copy(OrtDataTransferImpl* self, const OrtValue** src, OrtValue** dst,
+                                OrtSyncStream**, size_t n) noexcept {
+    auto* t = reinterpret_cast<DataTransfer*>(self);
+    const OrtApi* api = t ? t->factory->api : nullptr;
+    return guarded(api, "CopyTensors", [&] {
+        if (!t || (n && (!src || !dst))) fail(ORT_INVALID_ARGUMENT, "null CopyTensors argument");
+        const OrtEpApi* e = t->factory->ep_api;
+        for (size_t i = 0; i < n; ++i) {
+            const size_t sb = tensor_bytes(api, src[i]), db = tensor_bytes(api, dst[i]);
+            if (sb != db) fail(ORT_INVALID_ARGUMENT, "copy of %zu bytes into a %zu-byte tensor", sb, db);
+            int sd = -1, dd = -1;
+            const bool s_hbm = is_our_hbm(e, e->Value_GetMemoryDevice(src[i]), &sd);
+            const bool d_hbm = is_our_hbm(e, e->Value_GetMemoryDevice(dst[i]), &dd);
+            if (!s_hbm && !d_hbm) fail(ORT_INVALID_ARGUMENT, "neither tensor is in this EP's HBM");
+            void* dp = nullptr;
+            ORT_OK(api, GetTensorMutableData(dst[i], &dp));
+            const void* sp = tensor_data(api, src[i]);
+            const int kind = s_hbm && d_hbm ? MNB_COPY_DEVICE_TO_DEVICE
+                                            : (s_hbm ? MNB_COPY_DEVICE_TO_HOST : MNB_COPY_HOST_TO_DEVICE);
+            mnb_ok(mnb_memcpy(d_hbm ? dd : sd, dp, sp, sb, kind), "tensor copy");
+        }
+    });
+}
+
+OrtStatus* ORT_API_CALL f_create_data_transfer(OrtEpFactory* self, OrtDataTransferImpl** out) noexcept {
     if (out) *out = nullptr;
-    return nullptr;
+    Factory* f = as_factory(self);
+    return guarded(f ? f->api : nullptr, "CreateDataTransfer", [&] {
+        if (!f || !out || !f->device_memory) return;     // host I/O needs no copies
+        auto t = std::make_unique<DataTransfer>();
+        std::memset(&t->base, 0, sizeof(t->base));
+        t->base.ort_version_supported = f->version;
+        t->base.Release = dt_release;
+        t->base.CanCopy = dt_can_copy;
+        t->base.CopyTensors = dt_copy;
+        t->factory = f;
+        *out = &t.release()->base;
+    });
 }
 
 OrtStatus* ORT_API_CALL f_create_sync_stream(OrtEpFactory*, const OrtMemoryDevice*,
@@ -808,6 +1004,7 @@ MI355X_EXPORT OrtStatus* CreateEpFactories(const char* registered_name,
         f->ep_api = n.ep_api;
         f->version = n.version;
         f->registered_name = registered_name ? registered_name : kEpName;
+        f->device_memory = device_memory_requested();
         OrtEpFactory& b = f->base;
         b.ort_version_supported = n.version;
         b.GetName = f_get_name;
@@ -828,7 +1025,12 @@ MI355X_EXPORT OrtStatus* CreateEpFactories(const char* registered_name,
 }
 
 MI355X_EXPORT OrtStatus* ReleaseEpFactory(OrtEpFactory* factory) {
-    delete as_factory(factory);
+    Factory* f = as_factory(factory);
+    if (f) {
+        for (auto& kv : f->memory_infos)
+            if (kv.second) f->api->ReleaseMemoryInfo(kv.second);
+    }
+    delete f;
     return nullptr;
 }
 

@@ -370,6 +370,45 @@ int mnb_device_arch(int device_index, char* buf, size_t len) {
     return MNB_OK;
 }
 
+int mnb_device_malloc(int device_index, size_t bytes, void** out) {
+    if (!out) return fail(MNB_ERR_INVALID, "out is NULL");
+    *out = nullptr;
+    if (bytes == 0) return MNB_OK;
+    hipError_t e = hipSetDevice(device_index);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    e = hipMalloc(out, bytes);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return fail(MNB_ERR_NOMEM, "hipMalloc(%zu) on device %d: %s", bytes, device_index,
+                    hipGetErrorString(e));
+    }
+    return MNB_OK;
+}
+
+int mnb_device_free(int device_index, void* p) {
+    if (!p) return MNB_OK;
+    hipError_t e = hipSetDevice(device_index);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    e = hipFree(p);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipFree");
+}
+
+int mnb_memcpy(int device_index, void* dst, const void* src, size_t bytes, int kind) {
+    if (bytes == 0) return MNB_OK;
+    if (!dst || !src) return fail(MNB_ERR_INVALID, "a NULL copy pointer was passed");
+    hipMemcpyKind k;
+    switch (kind) {
+        case MNB_COPY_HOST_TO_DEVICE: k = hipMemcpyHostToDevice; break;
+        case MNB_COPY_DEVICE_TO_HOST: k = hipMemcpyDeviceToHost; break;
+        case MNB_COPY_DEVICE_TO_DEVICE: k = hipMemcpyDeviceToDevice; break;
+        default: return fail(MNB_ERR_INVALID, "copy kind %d", kind);
+    }
+    hipError_t e = hipSetDevice(device_index);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    e = hipMemcpy(dst, src, bytes, k);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipMemcpy");
+}
+
 int mnb_session_create(int device_index, mnb_session** out) {
     if (!out) return fail(MNB_ERR_INVALID, "out is NULL");
     *out = nullptr;
@@ -507,30 +546,46 @@ int mnb_session_run_device(mnb_session* s, const mnb_weights* w, int64_t m, cons
     return run_locked(s, w, m, a_dev, y_dev);
 }
 
-int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,
-                         void* y_host) {
+int mnb_session_run(mnb_session* s, const mnb_weights* w, int64_t m, const void* a,
+                    int a_on_device, void* y, int y_on_device) {
     if (!s || !w) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
     if (m < 0) return fail(MNB_ERR_INVALID, "M = %lld is negative", (long long)m);
     if (m == 0) return MNB_OK;
-    if (!a_host || !y_host) return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    if (!a || !y) return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
     std::lock_guard<std::mutex> lk(s->mu);
     (void)hipSetDevice(s->device);
     const size_t eb = (size_t)elem_bytes(w->node.dtype);
     const size_t a_bytes = (size_t)m * (size_t)w->node.k * eb;
     const size_t y_bytes = (size_t)m * (size_t)w->node.n * eb;
-    int rc = grow(&s->a_dev, &s->a_cap, a_bytes);
+    const void* a_dev = a;
+    void* y_dev = y;
+    int rc;
+    if (!a_on_device) {                                  // stage A into HBM
+        rc = grow(&s->a_dev, &s->a_cap, a_bytes);
+        if (rc) return rc;
+        hipError_t e = hipMemcpyAsync(s->a_dev, a, a_bytes, hipMemcpyHostToDevice, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "A upload");
+        a_dev = s->a_dev;
+    }
+    if (!y_on_device) {
+        rc = grow(&s->y_dev, &s->y_cap, y_bytes);
+        if (rc) return rc;
+        y_dev = s->y_dev;
+    }
+    rc = run_locked(s, w, m, a_dev, y_dev);
     if (rc) return rc;
-    rc = grow(&s->y_dev, &s->y_cap, y_bytes);
-    if (rc) return rc;
-    hipError_t e = hipMemcpyAsync(s->a_dev, a_host, a_bytes, hipMemcpyHostToDevice, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "A upload");
-    rc = run_locked(s, w, m, s->a_dev, s->y_dev);
-    if (rc) return rc;
-    e = hipMemcpyAsync(y_host, s->y_dev, y_bytes, hipMemcpyDeviceToHost, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "Y download");
-    e = hipStreamSynchronize(s->stream);
+    if (!y_on_device) {
+        hipError_t e = hipMemcpyAsync(y, s->y_dev, y_bytes, hipMemcpyDeviceToHost, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "Y download");
+    }
+    hipError_t e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     return MNB_OK;
+}
+
+int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,
+                         void* y_host) {
+    return mnb_session_run(s, w, m, a_host, 0, y_host, 0);
 }
 
 }  // extern "C"

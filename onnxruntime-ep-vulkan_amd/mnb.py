@@ -102,6 +102,10 @@ def load() -> C.CDLL:
         "mnb_weights_release": (C.c_int, [vp]),
         "mnb_session_run_device": (C.c_int, [vp, vp, i64, vp, vp]),
         "mnb_session_run_host": (C.c_int, [vp, vp, i64, vp, vp]),
+        "mnb_session_run": (C.c_int, [vp, vp, i64, vp, C.c_int, vp, C.c_int]),
+        "mnb_device_malloc": (C.c_int, [C.c_int, sz, C.POINTER(vp)]),
+        "mnb_device_free": (C.c_int, [C.c_int, vp]),
+        "mnb_memcpy": (C.c_int, [C.c_int, vp, vp, sz, C.c_int]),
         "mnb_launch_count": (C.c_uint64, []),
     }
     for name, (res, args) in sig.items():

@@ -20,6 +20,8 @@ FLOAT, UINT8, INT32, FLOAT16 = 1, 2, 6, 10
 NP_ELEM = {np.dtype(np.float32): FLOAT, np.dtype(np.uint8): UINT8, np.dtype(np.int32): INT32,
            np.dtype(np.float16): FLOAT16}
 ORT_INVALID_ARGUMENT = 2
+MEM_CPU, MEM_GPU = 0, 1          # OrtMemoryInfoDeviceType
+AMD, NVIDIA = 0x1002, 0x10DE
 ORT_EP_FAIL = 11   # onnxruntime_error_code.h: OK=0, FAIL, INVALID_ARGUMENT, ..., INVALID_GRAPH=10, EP_FAIL=11
 
 _lib = None
@@ -55,6 +57,16 @@ def lib() -> C.CDLL:
             "mock_compute": (C.c_int, [C.c_int]),
             "mock_fetch": (C.c_int, [C.c_char_p, C.c_void_p, C.c_size_t, i64p, C.c_int]),
             "mock_shutdown": (C.c_int, []),
+            "mock_live_memory_infos": (C.c_long, []),
+            "mock_allocator_infos": (C.c_int, [C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_uint),
+                                               C.POINTER(C.c_int)]),
+            "mock_create_allocator_for": (C.c_int, [C.c_int, C.c_uint, C.c_int, C.c_int]),
+            "mock_can_copy": (C.c_int, [C.c_int, C.c_uint, C.c_int, C.c_uint]),
+            "mock_default_memory_device": (C.c_int, [C.POINTER(C.c_int), C.POINTER(C.c_uint),
+                                                     C.POINTER(C.c_int)]),
+            "mock_device_io_setup": (C.c_int, [C.c_int]),
+            "mock_feed_device": (C.c_int, [C.c_char_p, C.c_int, C.c_int, i64p, C.c_void_p,
+                                           C.c_size_t]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -151,6 +163,33 @@ class Host:
         self._keep.append(arr)
         assert self.L.mock_feed(name.encode(), NP_ELEM[arr.dtype], arr.ndim, _dims(arr.shape),
                                 arr.ctypes.data, arr.nbytes) == 0
+
+    def feed_device(self, name, arr: np.ndarray):
+        """A graph input placed in device memory through the EP's allocator and data transfer."""
+        arr = np.ascontiguousarray(arr)
+        rc = self.L.mock_feed_device(name.encode(), NP_ELEM[arr.dtype], arr.ndim, _dims(arr.shape),
+                                     arr.ctypes.data, arr.nbytes)
+        assert rc == 0, err()
+
+    # ---- device memory ----
+    def allocator_infos(self, i):
+        t, v, d = C.c_int(), C.c_uint(), C.c_int()
+        n = self.L.mock_allocator_infos(i, C.byref(t), C.byref(v), C.byref(d))
+        return n, (t.value, v.value, d.value)
+
+    def create_allocator_for(self, type_, vendor, device_id, mem=0) -> int:
+        return self.L.mock_create_allocator_for(type_, vendor, device_id, mem)
+
+    def can_copy(self, src, dst) -> int:
+        return self.L.mock_can_copy(src[0], src[1], dst[0], dst[1])
+
+    def default_memory_device(self):
+        t, v, d = C.c_int(), C.c_uint(), C.c_int()
+        r = self.L.mock_default_memory_device(C.byref(t), C.byref(v), C.byref(d))
+        return r, (t.value, v.value, d.value)
+
+    def device_io_setup(self, i=0) -> int:
+        return self.L.mock_device_io_setup(i)
 
     def compute(self, group=0) -> int:
         return self.L.mock_compute(group)

@@ -47,12 +47,26 @@ struct OrtValueInfo {
     bool constant = false;
     std::vector<uint8_t> init;       // initializer bytes when constant
 };
+struct OrtMemoryDevice {
+    OrtMemoryInfoDeviceType type;
+    OrtDeviceMemoryType mem;
+    uint32_t vendor;
+    int32_t id;
+};
+struct OrtMemoryInfo {
+    std::string name;
+    OrtMemoryDevice dev;
+    size_t alignment;
+    OrtAllocatorType alloc_type;
+};
+static const OrtMemoryDevice kHostDevice{OrtMemoryInfoDeviceType_CPU, OrtDeviceMemoryType_DEFAULT, 0, 0};
 struct OrtValue {
     int32_t elem = 0;
     std::vector<int64_t> dims;
     const void* data = nullptr;      // borrowed (inputs, initializers) or owned (outputs)
     std::vector<uint8_t> owned;
     size_t bytes = 0;
+    const OrtMemoryDevice* md = &kHostDevice;   // where `data` lives
 };
 struct OrtOpAttr {
     std::string name;
@@ -80,6 +94,7 @@ struct OrtEpDevice {
     OrtEpFactory* factory;
     const OrtHardwareDevice* hw;
     OrtKeyValuePairs meta;
+    std::vector<const OrtMemoryInfo*> alloc_infos;   // EpDevice_AddAllocatorInfo (borrowed, as ORT)
 };
 struct OrtEpGraphSupportInfo {
     const OrtGraph* graph;
@@ -292,6 +307,12 @@ OrtStatus* ORT_API_CALL m_KernelContext_GetInput(const OrtKernelContext* c, size
     *out = c->inputs[i];
     return nullptr;
 }
+// Device-memory mode of the host: outputs are allocated with the EP's device allocator (as ORT
+// does for an EP whose default memory device is its GPU); every such buffer is freed at reset.
+OrtAllocator* g_out_alloc = nullptr;
+const OrtMemoryDevice* g_out_md = nullptr;
+std::vector<void*> g_dev_buffers;
+
 OrtStatus* ORT_API_CALL m_KernelContext_GetOutput(OrtKernelContext* c, size_t i, const int64_t* dims,
                                                   size_t rank, OrtValue** out) NX {
     if (i >= c->out_elem.size()) return mk_status(ORT_INVALID_ARGUMENT, "output index out of range");
@@ -301,8 +322,16 @@ OrtStatus* ORT_API_CALL m_KernelContext_GetOutput(OrtKernelContext* c, size_t i,
     size_t n = 1;
     for (int64_t d : v->dims) n *= (size_t)d;
     v->bytes = n * elem_size(v->elem);
-    v->owned.assign(v->bytes + 16, 0xCD);   // poison: unwritten output is detectable
-    v->data = v->owned.data();
+    if (g_out_alloc) {
+        void* p = g_out_alloc->Alloc(g_out_alloc, v->bytes ? v->bytes : 1);
+        if (!p) return mk_status(ORT_FAIL, "device allocator returned NULL");
+        g_dev_buffers.push_back(p);
+        v->data = p;
+        v->md = g_out_md;
+    } else {
+        v->owned.assign(v->bytes + 16, 0xCD);   // poison: unwritten output is detectable
+        v->data = v->owned.data();
+    }
     *out = v.get();
     if (c->outputs.size() <= i) c->outputs.resize(i + 1);
     c->outputs[i] = std::move(v);
@@ -343,7 +372,46 @@ OrtStatus* ORT_API_CALL m_GetSessionConfigEntry(const OrtSessionOptions* so, con
     return nullptr;
 }
 
+long g_live_mem_infos = 0;
+OrtStatus* ORT_API_CALL m_CreateMemoryInfo_V2(const char* name, OrtMemoryInfoDeviceType type,
+                                              uint32_t vendor, int32_t id, OrtDeviceMemoryType mem,
+                                              size_t alignment, OrtAllocatorType at,
+                                              OrtMemoryInfo** out) NX {
+    *out = new OrtMemoryInfo{name ? name : "", OrtMemoryDevice{type, mem, vendor, id}, alignment, at};
+    ++g_live_mem_infos;
+    return nullptr;
+}
+void ORT_API_CALL m_ReleaseMemoryInfo(OrtMemoryInfo* mi) NX {
+    if (!mi) return;
+    --g_live_mem_infos;
+    delete mi;
+}
+
 // ---- OrtEpApi implementation ------------------------------------------------------------------
+
+OrtStatus* ORT_API_CALL m_EpDevice_AddAllocatorInfo(OrtEpDevice* d, const OrtMemoryInfo* mi) NX {
+    if (!d || !mi) return mk_status(ORT_INVALID_ARGUMENT, "null AddAllocatorInfo argument");
+    for (const OrtMemoryInfo*& e : d->alloc_infos)
+        if (e->alloc_type == mi->alloc_type && e->dev.mem == mi->dev.mem) {
+            e = mi;                 // "multiple calls for the same entry type replace"
+            return nullptr;
+        }
+    d->alloc_infos.push_back(mi);
+    return nullptr;
+}
+const OrtMemoryDevice* ORT_API_CALL m_MemoryInfo_GetMemoryDevice(const OrtMemoryInfo* mi) NX {
+    return mi ? &mi->dev : nullptr;
+}
+const OrtMemoryDevice* ORT_API_CALL m_Value_GetMemoryDevice(const OrtValue* v) NX {
+    return v ? v->md : nullptr;
+}
+bool ORT_API_CALL m_MemoryDevice_AreEqual(const OrtMemoryDevice* a, const OrtMemoryDevice* b) NX {
+    return a && b && a->type == b->type && a->mem == b->mem && a->vendor == b->vendor && a->id == b->id;
+}
+OrtMemoryInfoDeviceType ORT_API_CALL m_MemoryDevice_GetDeviceType(const OrtMemoryDevice* d) NX { return d->type; }
+OrtDeviceMemoryType ORT_API_CALL m_MemoryDevice_GetMemoryType(const OrtMemoryDevice* d) NX { return d->mem; }
+uint32_t ORT_API_CALL m_MemoryDevice_GetVendorId(const OrtMemoryDevice* d) NX { return d->vendor; }
+uint32_t ORT_API_CALL m_MemoryDevice_GetDeviceId(const OrtMemoryDevice* d) NX { return (uint32_t)d->id; }
 
 std::vector<std::unique_ptr<OrtEpDevice>> g_ep_devices;
 
@@ -430,8 +498,18 @@ void init_api() {
     g_api.HasSessionConfigEntry = m_HasSessionConfigEntry;
     g_api.GetSessionConfigEntry = m_GetSessionConfigEntry;
     g_api.GetEpApi = m_GetEpApi;
+    g_api.CreateMemoryInfo_V2 = m_CreateMemoryInfo_V2;
+    g_api.ReleaseMemoryInfo = m_ReleaseMemoryInfo;
     g_ep_api.CreateEpDevice = m_CreateEpDevice;
     g_ep_api.EpGraphSupportInfo_AddNodesToFuse = m_AddNodesToFuse;
+    g_ep_api.EpDevice_AddAllocatorInfo = m_EpDevice_AddAllocatorInfo;
+    g_ep_api.MemoryInfo_GetMemoryDevice = m_MemoryInfo_GetMemoryDevice;
+    g_ep_api.Value_GetMemoryDevice = m_Value_GetMemoryDevice;
+    g_ep_api.MemoryDevice_AreEqual = m_MemoryDevice_AreEqual;
+    g_ep_api.MemoryDevice_GetDeviceType = m_MemoryDevice_GetDeviceType;
+    g_ep_api.MemoryDevice_GetMemoryType = m_MemoryDevice_GetMemoryType;
+    g_ep_api.MemoryDevice_GetVendorId = m_MemoryDevice_GetVendorId;
+    g_ep_api.MemoryDevice_GetDeviceId = m_MemoryDevice_GetDeviceId;
 }
 
 // ---- host state ---------------------------------------------------------------------------------
@@ -464,6 +542,10 @@ struct Host {
     // host tensors for compute
     std::map<std::string, OrtValue> feeds;
     std::map<std::string, OrtValue> fetches;
+    // device-memory mode
+    OrtAllocator* dev_alloc = nullptr;
+    OrtDataTransferImpl* dt = nullptr;
+    const OrtMemoryDevice* dev_md = nullptr;
 };
 Host* g = nullptr;
 
@@ -604,8 +686,15 @@ int mock_create_ep_n(int num_devices) {
 
 const char* mock_ep_name(void) { return g && g->ep ? g->ep->GetName(g->ep) : nullptr; }
 
+static void free_device_buffers() {
+    if (g_out_alloc)
+        for (void* p : g_dev_buffers) g_out_alloc->Free(g_out_alloc, p);
+    g_dev_buffers.clear();
+}
+
 void mock_graph_reset(void) {
     if (!g) return;
+    free_device_buffers();
     g->values.clear();
     g->nodes.clear();
     g->graph = OrtGraph();
@@ -789,7 +878,8 @@ int mock_compute(int i) {
         dst.dims = ctx.outputs[o]->dims;
         dst.owned = ctx.outputs[o]->owned;
         dst.bytes = ctx.outputs[o]->bytes;
-        dst.data = dst.owned.data();
+        dst.md = ctx.outputs[o]->md;
+        dst.data = dst.md == &kHostDevice ? (const void*)dst.owned.data() : ctx.outputs[o]->data;
     }
     return 0;
 }
@@ -806,14 +896,161 @@ int mock_fetch(const char* name, void* dst, size_t bytes, int64_t* dims, int max
         set_err("destination holds %zu bytes, output has %zu", bytes, v.bytes);
         return -1;
     }
-    std::memcpy(dst, v.data, v.bytes);
+    if (v.md != &kHostDevice) {
+        if (!g->dt) {
+            set_err("a device output and no data transfer");
+            return -1;
+        }
+        OrtValue h;
+        h.elem = v.elem;
+        h.dims = v.dims;
+        h.data = dst;
+        h.bytes = v.bytes;
+        const OrtValue* src[1] = {&v};
+        OrtValue* dsts[1] = {&h};
+        int rc = status_rc(g->dt->CopyTensors(g->dt, src, dsts, nullptr, 1));
+        if (rc) return -1;
+    } else {
+        std::memcpy(dst, v.data, v.bytes);
+    }
     for (int d = 0; d < (int)v.dims.size() && d < max_rank; ++d) dims[d] = v.dims[d];
     return (int)v.dims.size();
+}
+
+// ---- device memory (MI355X_EP_DEVICE_MEMORY) --------------------------------------------------
+
+long mock_live_memory_infos(void) { return g_live_mem_infos; }
+
+// Allocator infos EP device `i` registered with EpDevice_AddAllocatorInfo; `type`, `vendor`,
+// `id` receive the first one's memory device.
+int mock_allocator_infos(int i, int* type, unsigned* vendor, int* id) {
+    if (!g || i < 0 || i >= (int)g->ep_devices.size()) return -1;
+    const auto& v = g->ep_devices[i]->alloc_infos;
+    if (!v.empty()) {
+        *type = (int)v[0]->dev.type;
+        *vendor = v[0]->dev.vendor;
+        *id = v[0]->dev.id;
+    }
+    return (int)v.size();
+}
+
+// CreateAllocator for a memory info of the given description: 1 = an allocator came back (it
+// is released again), 0 = declined, < 0 = an error status.
+int mock_create_allocator_for(int type, unsigned vendor, int id, int mem) {
+    if (!g || !g->factory) return -1;
+    OrtMemoryInfo mi{"probe", OrtMemoryDevice{(OrtMemoryInfoDeviceType)type, (OrtDeviceMemoryType)mem,
+                                              vendor, id}, 256, OrtDeviceAllocator};
+    OrtAllocator* a = reinterpret_cast<OrtAllocator*>(0x1);
+    int rc = status_rc(g->factory->CreateAllocator(g->factory, &mi, nullptr, &a));
+    if (a == reinterpret_cast<OrtAllocator*>(0x1)) {
+        set_err("CreateAllocator left its out-parameter unwritten");
+        return -2;
+    }
+    if (rc) return -rc;
+    if (!a) return 0;
+    g->factory->ReleaseAllocator(g->factory, a);
+    return 1;
+}
+
+// CanCopy between two memory devices: 1 / 0, or -1 when the factory offers no data transfer.
+int mock_can_copy(int stype, unsigned svendor, int dtype, unsigned dvendor) {
+    if (!g || !g->factory) return -1;
+    OrtDataTransferImpl* dt = nullptr;
+    if (status_rc(g->factory->CreateDataTransfer(g->factory, &dt))) return -2;
+    if (!dt) return -1;
+    OrtMemoryDevice s{(OrtMemoryInfoDeviceType)stype, OrtDeviceMemoryType_DEFAULT, svendor, 0};
+    OrtMemoryDevice d{(OrtMemoryInfoDeviceType)dtype, OrtDeviceMemoryType_DEFAULT, dvendor, 0};
+    const bool ok = dt->CanCopy(dt, &s, &d);
+    dt->Release(dt);
+    return ok ? 1 : 0;
+}
+
+// The EP's GetDefaultMemoryDevice: 1 = a device (written out), 0 = NULL, -2 = slot not set.
+int mock_default_memory_device(int* type, unsigned* vendor, int* id) {
+    if (!g || !g->ep) return -1;
+    if (!g->ep->GetDefaultMemoryDevice) return -2;
+    const OrtMemoryDevice* md = nullptr;
+    int rc = status_rc(g->ep->GetDefaultMemoryDevice(g->ep, &md));
+    if (rc) return -rc;
+    if (!md) return 0;
+    *type = (int)md->type;
+    *vendor = md->vendor;
+    *id = md->id;
+    return 1;
+}
+
+// Device-memory session set-up the way ORT does it for an EP whose default memory device is its
+// GPU: the factory's allocator for EP device `i`'s registered memory info, its data transfer,
+// and outputs allocated in device memory.
+int mock_device_io_setup(int i) {
+    if (!g || !g->factory || i < 0 || i >= (int)g->ep_devices.size()) return -1;
+    if (g->ep_devices[i]->alloc_infos.empty()) {
+        set_err("EP device %d registered no allocator info", i);
+        return -1;
+    }
+    const OrtMemoryInfo* mi = g->ep_devices[i]->alloc_infos[0];
+    OrtAllocator* a = nullptr;
+    int rc = status_rc(g->factory->CreateAllocator(g->factory, mi, nullptr, &a));
+    if (rc) return rc;
+    if (!a) {
+        set_err("CreateAllocator declined the EP's own memory info");
+        return -1;
+    }
+    OrtDataTransferImpl* dt = nullptr;
+    rc = status_rc(g->factory->CreateDataTransfer(g->factory, &dt));
+    if (rc || !dt) {
+        g->factory->ReleaseAllocator(g->factory, a);
+        if (!rc) set_err("no data transfer");
+        return rc ? rc : -1;
+    }
+    g->dev_alloc = a;
+    g->dt = dt;
+    g->dev_md = &mi->dev;
+    g_out_alloc = a;
+    g_out_md = &mi->dev;
+    return 0;
+}
+
+// A graph input placed in device memory: allocated with the EP's allocator and filled from
+// `data` through the EP's data transfer (as ORT's MemcpyFromHost would).
+int mock_feed_device(const char* name, int elem, int rank, const int64_t* dims, const void* data,
+                     size_t bytes) {
+    if (!g || !g->dev_alloc || !g->dt) {
+        set_err("device I/O is not set up");
+        return -1;
+    }
+    void* p = g->dev_alloc->Alloc(g->dev_alloc, bytes ? bytes : 1);
+    if (!p) {
+        set_err("device allocation failed");
+        return -1;
+    }
+    g_dev_buffers.push_back(p);
+    OrtValue h;
+    h.elem = elem;
+    h.dims.assign(dims, dims + rank);
+    h.data = data;
+    h.bytes = bytes;
+    OrtValue d = h;
+    d.data = p;
+    d.md = g->dev_md;
+    const OrtValue* src[1] = {&h};
+    OrtValue* dst[1] = {&d};
+    int rc = status_rc(g->dt->CopyTensors(g->dt, src, dst, nullptr, 1));
+    if (rc) return rc;
+    g->feeds[name] = d;
+    return 0;
 }
 
 // Releases compute infos, the EP and the factory (in ORT's order) and unloads the library.
 int mock_shutdown(void) {
     if (!g) return 0;
+    free_device_buffers();
+    if (g->dev_alloc && g->factory) g->factory->ReleaseAllocator(g->factory, g->dev_alloc);
+    g->dev_alloc = nullptr;
+    g_out_alloc = nullptr;
+    g_out_md = nullptr;
+    if (g->dt) g->dt->Release(g->dt);
+    g->dt = nullptr;
     if (g->ep) {
         std::vector<OrtNodeComputeInfo*> infos;
         for (auto& gr : g->groups)

@@ -220,3 +220,60 @@ def test_compile_without_a_device_fails_cleanly(host):
     rc = host.compile()
     assert rc == mh.ORT_EP_FAIL, (rc, mh.err())
     assert "HIP" in mh.err() or "device" in mh.err()
+
+
+# ---- device-memory mode (MI355X_EP_DEVICE_MEMORY; reference: rust/src/factory.rs:487-504) ----
+
+@pytest.fixture
+def dm_host(monkeypatch):
+    # The factory reads the switch once, at CreateEpFactories.
+    monkeypatch.setenv("MI355X_EP_DEVICE_MEMORY", "1")
+    h = mh.Host(28)
+    assert h.init_rc == 0, mh.err()
+    yield h
+    assert h.close() == 0
+    assert mh.lib().mock_live_statuses() == 0
+    assert mh.lib().mock_live_memory_infos() == 0, "the factory leaked an OrtMemoryInfo"
+
+
+def test_device_memory_is_off_by_default(host):
+    # no allocator, no data transfer, no default memory device: ORT keeps every tensor on the host
+    assert host.create_allocator_for(mh.MEM_GPU, mh.AMD, 0) == 0
+    assert host.can_copy((mh.MEM_CPU, 0), (mh.MEM_GPU, mh.AMD)) == -1
+    assert host.create_ep(-1) == 0, mh.err()
+    assert host.default_memory_device()[0] == -2
+
+
+@pytest.mark.parametrize("spelling", ["0", "off", "false", "no", "of", ""])
+def test_device_memory_switch_fails_towards_host_io(monkeypatch, spelling):
+    monkeypatch.setenv("MI355X_EP_DEVICE_MEMORY", spelling)
+    h = mh.Host(28)
+    try:
+        assert h.create_allocator_for(mh.MEM_GPU, mh.AMD, 0) == 0
+    finally:
+        assert h.close() == 0
+
+
+def test_device_allocator_serves_only_its_own_memory(dm_host):
+    assert dm_host.create_allocator_for(mh.MEM_GPU, mh.AMD, 0) == 1
+    assert dm_host.create_allocator_for(mh.MEM_GPU, mh.AMD, 3) == 1
+    assert dm_host.create_allocator_for(mh.MEM_CPU, 0, 0) == 0
+    assert dm_host.create_allocator_for(mh.MEM_GPU, mh.NVIDIA, 0) == 0
+    assert dm_host.create_allocator_for(mh.MEM_GPU, mh.AMD, 0, mem=5) == 0   # HOST_ACCESSIBLE
+
+
+def test_data_transfer_copies_host_and_hbm_only(dm_host):
+    host_, amd, nv = (mh.MEM_CPU, 0), (mh.MEM_GPU, mh.AMD), (mh.MEM_GPU, mh.NVIDIA)
+    assert dm_host.can_copy(host_, amd) == 1
+    assert dm_host.can_copy(amd, host_) == 1
+    assert dm_host.can_copy(amd, amd) == 1
+    assert dm_host.can_copy(host_, host_) == 0
+    assert dm_host.can_copy(nv, host_) == 0
+    assert dm_host.can_copy(host_, nv) == 0
+
+
+def test_default_memory_device_is_the_eps_hbm(dm_host, monkeypatch):
+    dm_host.option("ep.device_index", 2)
+    assert dm_host.create_ep(-1) == 0, mh.err()
+    r, (t, vendor, dev) = dm_host.default_memory_device()
+    assert r == 1 and t == mh.MEM_GPU and vendor == mh.AMD and dev == 2

@@ -149,3 +149,58 @@ def test_wrong_activation_width_is_rejected(host):
     assert host.compile() == 0, mh.err()
     host.feed(a_name, np.zeros((1, 128), np.float16))
     assert host.compute(0) == mh.ORT_INVALID_ARGUMENT
+
+
+@pytest.fixture
+def dm_host(cuda, monkeypatch):
+    # MI355X_EP_DEVICE_MEMORY=1: ORT-style device I/O through the EP's allocator and data transfer
+    monkeypatch.setenv("MI355X_EP_DEVICE_MEMORY", "1")
+    h = mh.Host(28)
+    assert h.init_rc == 0, mh.err()
+    assert h.supported_devices(n_amd=1) == 1
+    n, (t, vendor, dev) = h.allocator_infos(0)
+    assert n == 1 and t == mh.MEM_GPU and vendor == mh.AMD, "HBM was not advertised"
+    assert h.create_ep(0) == 0, mh.err()
+    assert h.default_memory_device()[0] == 1
+    yield h
+    assert h.close() == 0
+    assert mh.lib().mock_live_statuses() == 0
+    assert mh.lib().mock_live_memory_infos() == 0
+
+
+@pytest.mark.parametrize("M,N,K,bs,zp", [(1, 9216, 3072, 32, True), (16, 3072, 8192, 128, True),
+                                          (300, 512, 1024, 32, False)])
+def test_device_resident_io_matches_oracle(dm_host, M, N, K, bs, zp):
+    print(f"[gpu] ep device I/O M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=M + 3 * N)
+    dm_host.reset()
+    a_name, y_name = mh.add_matmul_nbits(dm_host, "mm", inp, N, K, 4, bs, (M, K))
+    assert dm_host.get_capability() == (1, ["mm:drop"])
+    assert dm_host.compile() == 0, mh.err()
+    assert dm_host.device_io_setup(0) == 0, mh.err()
+    before = mh.EP_COUNT()
+    dm_host.feed_device(a_name, inp["A"])            # A in HBM, Y allocated in HBM
+    assert dm_host.compute(0) == 0, mh.err()
+    assert mh.EP_COUNT() == before + 1
+    y = dm_host.fetch(y_name, np.float16, M * N)     # read back through the data transfer
+    _check(y, orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs),
+           "device I/O")
+
+
+def test_device_resident_weights_as_graph_inputs(dm_host):
+    N, K = 64, 256
+    inp = orc.make_inputs(3, N, K, with_zp=True, seed=12)
+    dm_host.reset()
+    a_name, y_name = mh.add_matmul_nbits(dm_host, "mm", inp, N, K, 4, 32, (3, K),
+                                         const_weights=False)
+    assert dm_host.get_capability()[1] == ["mm:keep"]
+    assert dm_host.compile() == 0, mh.err()
+    assert dm_host.device_io_setup(0) == 0, mh.err()
+    dm_host.feed_device(a_name, inp["A"])
+    dm_host.feed_device("mm_B", inp["B"])
+    dm_host.feed_device("mm_scales", inp["scales"])
+    dm_host.feed_device("mm_zp", inp["zp"])
+    assert dm_host.compute(0) == 0, mh.err()
+    y = dm_host.fetch(y_name, np.float16, 3 * N)
+    _check(y, orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, 32),
+           "device-resident weights")
