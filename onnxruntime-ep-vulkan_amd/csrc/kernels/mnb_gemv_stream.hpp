@@ -228,18 +228,25 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
 #pragma unroll
                     for (int r = 0; r < MR; ++r) {
                         float t = 0.f;
+                        float t16 = 0.f;
 #pragma unroll
                         for (int d = s * DW_PER_SEG; d < (s + 1) * DW_PER_SEG; ++d) {
                             if constexpr (BITS == 4) {
-                                t = __builtin_amdgcn_fdot2(sub_pair<4, 0>(w[d]), ap[r][j][4 * d + 0], t, false);
-                                t = __builtin_amdgcn_fdot2(sub_pair<4, 1>(w[d]), ap[r][j][4 * d + 1], t, false);
-                                t = __builtin_amdgcn_fdot2(sub_pair<4, 2>(w[d]), ap[r][j][4 * d + 2], t, false);
-                                t = __builtin_amdgcn_fdot2(sub_pair<4, 3>(w[d]), ap[r][j][4 * d + 3], t, false);
+                                // Nibble pairs 0 and 2 sit in bits 0-3 of each half (q * 2^-24);
+                                // pairs 1 and 3 are masked in place at bits 4-7 (16q * 2^-24,
+                                // still subnormal) and summed apart, scaled by 1/16 below:
+                                // one shift per dword instead of three.
+                                const uint32_t wh = w[d] >> 8;
+                                t = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x000F000Fu), ap[r][j][4 * d + 0], t, false);
+                                t = __builtin_amdgcn_fdot2(as_h2(wh & 0x000F000Fu), ap[r][j][4 * d + 2], t, false);
+                                t16 = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x00F000F0u), ap[r][j][4 * d + 1], t16, false);
+                                t16 = __builtin_amdgcn_fdot2(as_h2(wh & 0x00F000F0u), ap[r][j][4 * d + 3], t16, false);
                             } else {
                                 t = __builtin_amdgcn_fdot2(sub_pair<8, 0>(w[d]), ap[r][j][2 * d + 0], t, false);
                                 t = __builtin_amdgcn_fdot2(sub_pair<8, 1>(w[d]), ap[r][j][2 * d + 1], t, false);
                             }
                         }
+                        t = __builtin_fmaf(t16, 0.0625f, t);
                         acc[r][u] = __builtin_fmaf(s24, t, acc[r][u]);
                         acc[r][u] = __builtin_fmaf(sz, asum[r][j][s], acc[r][u]);
                     }
