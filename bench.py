@@ -291,6 +291,41 @@ def main() -> int:
     # two copies so consecutive launches do not reuse an L2-resident B.
     pk, pn = 3072, 8192
     pw = [make_weights(torch, dev, pk, pn, gen, zp=False) for _ in range(2)]
+
+    # The fp16 MFMA rate the chip sustains on its own (mnb_calibrate_mfma: 16 independent
+    # accumulators per wavefront, no memory traffic), once on random N(0,1) operands and once on
+    # constant ones.  Under a full-chip MFMA load the clock follows the power the matrix cores
+    # draw, so random data (the prefill GEMM's kind) runs well below the nominal peak.
+    def mfma_ceiling(random_operands: bool, wgs: int = 512, iters: int = 1000) -> float:
+        ops = (torch.randn(wgs * 256 * 64, device=dev, generator=gen).to(torch.float16)
+               if random_operands else None)
+        out = torch.empty(wgs * 256, dtype=torch.float32, device=dev)
+
+        def call():
+            mnb.check(lib.mnb_calibrate_mfma(wgs, iters, None if ops is None else ops.data_ptr(),
+                                             out.data_ptr(), sptr))
+        call()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(3):
+            call()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = 1e3 * a.elapsed_time(b) / 3
+        return wgs * 4 * iters * 16 * 32768 / (us * 1e-6) / 1e12
+
+    ceil_rand = mfma_ceiling(True)
+    ceil_const = mfma_ceiling(False)
+    # the same loop on 32 workgroups (32 of the 256 CUs), scaled to the whole chip: the per-CU
+    # rate when the chip is far from its power limit
+    ceil_rand32 = mfma_ceiling(True, wgs=32) * 256 / 32
+    mfma_cal = {"random_operands_tflops": round(ceil_rand, 1),
+                "constant_operands_tflops": round(ceil_const, 1),
+                "random_operands_32_cus_scaled_tflops": round(ceil_rand32, 1),
+                "nominal_peak_tflops": F16_MFMA_PEAK_TFLOPS,
+                "kernel": "mnb_calibrate_mfma: 512 workgroups x 4 wavefronts x 1000 x 16 "
+                          "v_mfma_f32_32x32x16_f16, operands in registers"}
     prefill = []
     for pm in (256, 512, 2048):
         pA = torch.randn(pm, pk, device=dev, generator=gen).to(torch.float16)
@@ -328,7 +363,9 @@ def main() -> int:
                                      "traffic": measured_traffic(
                                          f"prefill_m{pm}",
                                          pm * pk * 2 + pn * pk // 2 + pn * (pk // BS) * 2
-                                         + pm * pn * 2)}})
+                                         + pm * pn * 2),
+                                     "ceiling_random_operands": round(ceil_rand, 1),
+                                     "frac_of_ceiling": round(ptf / ceil_rand, 4)}})
 
     def graph_time_us(fn, reps):
         """Average device time per launch of `fn(r, stream)` over a graph of `reps` launches."""
@@ -470,6 +507,7 @@ def main() -> int:
         "roofline": roofline,
         "per_kernel": per_kernel,
         "prefill": prefill,
+        "mfma_calibration": mfma_cal,
         "accuracy_level_4": acc4,
         "moe": moe,
         "session_io": session_io,

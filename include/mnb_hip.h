@@ -182,6 +182,14 @@ int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const 
 /* Number of MatMulNBits-family kernel launches made by this process (proves the GPU ran). */
 uint64_t mnb_launch_count(void);
 
+/* Roofline calibration; no counterpart in the reference (a measurement utility for bench.py).
+ * Runs `workgroups` x 4 wavefronts x `iters` x 16 v_mfma_f32_32x32x16_f16 (32768 flops each) on
+ * operands read once from `operands_f16` (workgroups * 256 * 8 fp16x8 values, 16-byte aligned;
+ * NULL = constant operands) and writes one float per thread to `out` (workgroups * 256).  The
+ * rate it sustains on random operands is the chip's power-limited fp16 MFMA ceiling. */
+int mnb_calibrate_mfma(int32_t workgroups, int32_t iters, const void* operands_f16, float* out,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,11 +42,12 @@ HIP_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA results in architectural VGPRs, where the fp32 block epilogue reads them, instead of
-    # AGPRs that need a v_accvgpr_read per element.
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     f"-I{INCLUDE}",
 ]
+# MFMA results in architectural VGPRs, where the fp32 block epilogues read them, instead of AGPRs
+# that need a v_accvgpr_read per element -- for every kernel but the calibration loop, whose
+# sixteen accumulators are only ever read by MFMAs.
+VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 HIP_SOURCES = [
     CSRC / "kernels" / "mnb_gemv.hip",
@@ -55,6 +56,7 @@ HIP_SOURCES = [
     CSRC / "kernels" / "mnb_gemv_stream.hip",
     CSRC / "kernels" / "mnb_gemv_stream_b4.hip",
     CSRC / "kernels" / "mnb_gemv_stream_b8.hip",
+    CSRC / "kernels" / "mnb_calibrate.hip",
     CSRC / "shim" / "mnb_shim.hip",
 ]
 EP_SOURCES: list[Path] = sorted((CSRC / "ep").glob("*.cpp"))
@@ -82,7 +84,8 @@ def _run(cmd: list[str]) -> None:
 def _compile_hip(src: Path, force: bool) -> Path:
     obj = OBJ / (src.stem + ".o")
     if force or _stale(obj, [src] + _headers()):
-        _run([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)])
+        extra = [] if src.stem == "mnb_calibrate" else VGPR_MFMA
+        _run([HIPCC, *HIP_FLAGS, *extra, "-c", str(src), "-o", str(obj)])
     return obj
 
 

@@ -100,4 +100,8 @@ hipError_t launch_generic(const void* a, const uint8_t* b, const void* s, const 
 hipError_t launch_dequant_f16(const uint8_t* b, const void* s, const uint8_t* z, void* w,
                               int64_t n, int64_t k, int bits, int bs, hipStream_t stream);
 
+// Roofline calibration (mnb_calibrate.hip): workgroups x 4 wavefronts x iters x 16 MFMAs.
+hipError_t launch_mfma_calibrate(const void* operands, float* out, int workgroups, int iters,
+                                 hipStream_t stream);
+
 }  // namespace mnb

@@ -73,6 +73,19 @@ int mnb_version(void) { return 1; }
 
 uint64_t mnb_launch_count(void) { return g_launches.load(); }
 
+int mnb_calibrate_mfma(int32_t workgroups, int32_t iters, const void* operands_f16, float* out,
+                       void* stream) {
+    if (workgroups < 1 || workgroups > 65536 || iters < 1 || iters > 1000000)
+        return fail(MNB_ERR_INVALID, "workgroups = %d, iters = %d", workgroups, iters);
+    if (!out) return fail(MNB_ERR_INVALID, "out is NULL");
+    if (operands_f16 && !aligned(operands_f16, 16))
+        return fail(MNB_ERR_INVALID, "operands must be 16-byte aligned");
+    hipError_t e = mnb::launch_mfma_calibrate(operands_f16, out, workgroups, iters,
+                                              static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "calibration launch");
+    return MNB_OK;
+}
+
 int mnb_check_problem(const mnb_problem* p) {
     if (!p) return fail(MNB_ERR_INVALID, "problem is NULL");
     if (p->bits != 4 && p->bits != 8)

@@ -107,6 +107,7 @@ def load() -> C.CDLL:
         "mnb_device_free": (C.c_int, [C.c_int, vp]),
         "mnb_memcpy": (C.c_int, [C.c_int, vp, vp, sz, C.c_int]),
         "mnb_launch_count": (C.c_uint64, []),
+        "mnb_calibrate_mfma": (C.c_int, [i32, i32, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
