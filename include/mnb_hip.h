@@ -135,6 +135,48 @@ int mnb_moe_grouped(const mnb_moe_problem* p, const void* a, const int32_t* row_
                     const int32_t* offsets, const uint8_t* b, const void* scales,
                     const uint8_t* zero_points, void* y, void* stream);
 
+/* Fused QMoE: com.microsoft::QMoE with int4 experts and SwiGLU (gpt-oss style).  No kernel
+ * counterpart in the reference, which registers the op staged and declines top-k > 2
+ * (rust/src/ops/moe.rs:40-118; gpt-oss attribute values docs/OP_COVERAGE.md:831-835); the
+ * arithmetic is the build's declared reading of ONNX Runtime's QMoE (third-party):
+ *   softmax over the E router logits of each token, the k largest (ties to the lower expert
+ *   id), renormalised to sum to one when normalize_routing is set;
+ *   h = x W1_e^T + b1_e (W1_e: 2I x H int4, symmetric, implied zero point 8);
+ *   act = gate * sigmoid(alpha * gate) * (linear + beta), gate = min(gate, limit) and
+ *   linear = clamp(linear, -limit, limit) when has_swiglu_limit, gate/linear = columns
+ *   (2i, 2i+1) when swiglu_fusion = 1 or (i, I+i) when 2;
+ *   y[t] = sum over the token's experts of w * (act W2_e^T + b2_e) (W2_e: H x I).
+ * Weights: fc1 [E][2I][H/2] and fc2 [E][H][I/2] uint8, low nibble first (per expert the
+ * MatMulNBits B layout); scales fp16 [E][N][K/block_size]; biases fp16 [E][2I] and [E][H] or
+ * NULL.  x and y fp16 [rows][H]; router logits fp16 or fp32 [rows][E].  Limits: E <= 1024,
+ * k <= min(8, E), rows * k <= 16384, H and I multiples of 32 and of block_size.  Intermediates
+ * (h before the bias, act, act W2^T before the bias) are stored as fp16; accumulation is fp32.
+ * Stream-ordered; the workspace (mnb_qmoe_workspace_bytes, 256-byte aligned) holds the routing
+ * tables and the intermediates. */
+typedef struct mnb_qmoe_problem {
+    int64_t rows;               /* tokens (leading dims of x folded) */
+    int64_t hidden;             /* H: K of fc1, N of fc2 */
+    int64_t inter;              /* I: fc1 has 2I output channels (gate and linear) */
+    int64_t num_experts;        /* E */
+    int32_t k;                  /* experts per token */
+    int32_t block_size;         /* quantisation block along K of fc1 and fc2: 32, 64 or 128 */
+    int32_t swiglu_fusion;      /* 1 interleaved, 2 concatenated */
+    int32_t normalize_routing;
+    float activation_alpha;
+    float activation_beta;
+    float swiglu_limit;
+    int32_t has_swiglu_limit;
+    int32_t router_dtype;       /* MNB_DTYPE_F16 or MNB_DTYPE_F32 */
+    int32_t dtype;              /* MNB_DTYPE_F16 */
+} mnb_qmoe_problem;
+
+int mnb_qmoe_check(const mnb_qmoe_problem* p);
+int mnb_qmoe_workspace_bytes(const mnb_qmoe_problem* p, size_t* bytes);
+int mnb_qmoe(const mnb_qmoe_problem* p, const void* x, const void* router_logits,
+             const uint8_t* fc1_weights, const void* fc1_scales, const void* fc1_bias,
+             const uint8_t* fc2_weights, const void* fc2_scales, const void* fc2_bias, void* y,
+             void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- session layer: one device, one stream, weights uploaded once ---------------------- */
 
 typedef struct mnb_session mnb_session;
@@ -178,6 +220,26 @@ int mnb_session_run(mnb_session* s, const mnb_weights* w, int64_t m, const void*
 /* Compute with host A and Y: stage A in, launch, copy Y out, synchronise (ORT host I/O). */
 int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,
                          void* y_host);
+
+/* QMoE weights of one node uploaded once (the constant-initializer upload of
+ * rust/src/vk/session.rs:1633-1700, applied to the expert tensors).  Byte sizes are checked
+ * against the problem.  scales_per_channel: fc1 scales [E][2I] and fc2 scales [E][H] (one
+ * scale per output channel, QMoE without a block_size attribute), expanded here to blocks of
+ * node->block_size; otherwise [E][N][K/block_size].  Biases may be NULL. */
+typedef struct mnb_qmoe_weights mnb_qmoe_weights;
+int mnb_qmoe_weights_upload(mnb_session* s, const mnb_qmoe_problem* node,
+                            int32_t scales_per_channel, const void* fc1_weights,
+                            size_t fc1_weights_bytes, const void* fc1_scales,
+                            size_t fc1_scales_bytes, const void* fc1_bias, size_t fc1_bias_bytes,
+                            const void* fc2_weights, size_t fc2_weights_bytes,
+                            const void* fc2_scales, size_t fc2_scales_bytes, const void* fc2_bias,
+                            size_t fc2_bias_bytes, mnb_qmoe_weights** out);
+int mnb_qmoe_weights_release(mnb_qmoe_weights* w);
+/* One QMoE Compute with x, the router logits and y each in host memory or in the session
+ * device's memory; host tensors are staged through HBM; returns after the stream finished. */
+int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows, const void* x,
+                         int x_on_device, const void* router_logits, int logits_on_device,
+                         void* y, int y_on_device);
 
 /* Number of MatMulNBits-family kernel launches made by this process (proves the GPU ran). */
 uint64_t mnb_launch_count(void);

@@ -552,6 +552,22 @@ hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const 
                                 nullptr, nullptr, st);
 }
 
+hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index,
+                                         const int32_t* offsets, int64_t groups,
+                                         int64_t rows_bound, int64_t rows_hint, const uint8_t* b,
+                                         const void* s, const uint8_t* z, void* y, int64_t m,
+                                         int64_t n, int64_t k, int bits, int bs, hipStream_t st) {
+    if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
+    if (m == 0 || groups == 0) return hipSuccess;
+    // Tile height from the expected rows per group; enough row tiles for the bound (tiles past
+    // a group's last row leave at once).
+    GroupGeom g = group_geometry(std::max<int64_t>(1, std::min(rows_hint, rows_bound)), n, k,
+                                 groups, false, bs, false);
+    g.gz = (rows_bound + 16 * g.mt - 1) / (16 * g.mt);
+    return group_bs<f16, false>(bs, g, a, nullptr, row_index, offsets, b, s, z, y, m, n, k,
+                                nullptr, nullptr, st);
+}
+
 hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
                                   hipStream_t st, int* cnt, int64_t ncnt) {

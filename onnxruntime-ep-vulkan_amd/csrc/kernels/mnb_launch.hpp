@@ -77,6 +77,14 @@ hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const 
                                  int64_t groups, int64_t max_rows, const uint8_t* b,
                                  const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
                                  int64_t k, int bits, int bs, hipStream_t stream);
+// The same with rows per group known only on the device: `rows_bound` bounds every group (the
+// grid covers it), `rows_hint` (the expected rows per group) sets the tile height.
+hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index,
+                                         const int32_t* offsets, int64_t groups,
+                                         int64_t rows_bound, int64_t rows_hint, const uint8_t* b,
+                                         const void* s, const uint8_t* z, void* y, int64_t m,
+                                         int64_t n, int64_t k, int bits, int bs,
+                                         hipStream_t stream);
 // cnt / ncnt: split-K counters of a following int8 GEMV, cleared by the quantiser (may be null).
 hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
@@ -99,6 +107,17 @@ hipError_t launch_generic(const void* a, const uint8_t* b, const void* s, const 
 
 hipError_t launch_dequant_f16(const uint8_t* b, const void* s, const uint8_t* z, void* w,
                               int64_t n, int64_t k, int bits, int bs, hipStream_t stream);
+
+// Fused QMoE (mnb_qmoe.hip).
+struct QmoeArgs {
+    int64_t rows, hidden, inter, experts;
+    int k, block_size, fusion, normalize, has_limit, router_f32;
+    float alpha, beta, limit;
+};
+size_t qmoe_workspace_bytes(const QmoeArgs& q);
+hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, const uint8_t* fc1,
+                       const void* fc1_s, const void* fc1_b, const uint8_t* fc2, const void* fc2_s,
+                       const void* fc2_b, void* y, void* workspace, hipStream_t stream);
 
 // Roofline calibration (mnb_calibrate.hip): workgroups x 4 wavefronts x iters x 16 MFMAs.
 hipError_t launch_mfma_calibrate(const void* operands, float* out, int workgroups, int iters,

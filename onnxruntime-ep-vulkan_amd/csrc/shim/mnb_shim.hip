@@ -15,7 +15,9 @@
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <cmath>
 #include <string>
+#include <vector>
 
 #include "../../../include/mnb_hip.h"
 #include "../kernels/mnb_launch.hpp"
@@ -339,6 +341,94 @@ int mnb_moe_grouped(const mnb_moe_problem* p, const void* a, const int32_t* row_
     return MNB_OK;
 }
 
+// ---- fused QMoE ---------------------------------------------------------------------------
+
+static mnb::QmoeArgs qmoe_args(const mnb_qmoe_problem* p) {
+    mnb::QmoeArgs q{};
+    q.rows = p->rows;
+    q.hidden = p->hidden;
+    q.inter = p->inter;
+    q.experts = p->num_experts;
+    q.k = p->k;
+    q.block_size = p->block_size;
+    q.fusion = p->swiglu_fusion;
+    q.normalize = p->normalize_routing ? 1 : 0;
+    q.has_limit = p->has_swiglu_limit ? 1 : 0;
+    q.router_f32 = p->router_dtype == MNB_DTYPE_F32 ? 1 : 0;
+    q.alpha = p->activation_alpha;
+    q.beta = p->activation_beta;
+    q.limit = p->swiglu_limit;
+    return q;
+}
+
+int mnb_qmoe_check(const mnb_qmoe_problem* p) {
+    if (!p) return fail(MNB_ERR_INVALID, "problem is NULL");
+    if (p->rows < 0) return fail(MNB_ERR_INVALID, "rows = %lld is negative", (long long)p->rows);
+    if (p->num_experts < 1 || p->num_experts > 1024)
+        return fail(MNB_ERR_UNSUPPORTED, "num_experts = %lld; this library routes 1..1024",
+                    (long long)p->num_experts);
+    if (p->k < 1 || p->k > 8 || p->k > p->num_experts)
+        return fail(MNB_ERR_UNSUPPORTED, "k = %d; this library routes 1..min(8, E)", p->k);
+    if (p->rows * p->k > 16384)
+        return fail(MNB_ERR_UNSUPPORTED, "rows * k = %lld exceeds 16384",
+                    (long long)(p->rows * p->k));
+    if (p->block_size != 32 && p->block_size != 64 && p->block_size != 128)
+        return fail(MNB_ERR_UNSUPPORTED, "block_size = %d; the expert kernels take 32/64/128",
+                    p->block_size);
+    if (p->hidden <= 0 || p->inter <= 0 || p->hidden % 32 || p->inter % 32 ||
+        p->hidden % p->block_size || p->inter % p->block_size)
+        return fail(MNB_ERR_UNSUPPORTED, "hidden = %lld and inter = %lld must be positive "
+                    "multiples of 32 and of block_size", (long long)p->hidden, (long long)p->inter);
+    if (p->hidden >= (1ll << 31) || 2 * p->inter >= (1ll << 31))
+        return fail(MNB_ERR_UNSUPPORTED, "extents do not fit 32 bits");
+    if (p->swiglu_fusion != 1 && p->swiglu_fusion != 2)
+        return fail(MNB_ERR_UNSUPPORTED, "swiglu_fusion = %d; this library implements 1 "
+                    "(interleaved) and 2 (concatenated)", p->swiglu_fusion);
+    if (p->dtype != MNB_DTYPE_F16) return fail(MNB_ERR_UNSUPPORTED, "QMoE runs fp16 tensors");
+    if (p->router_dtype != MNB_DTYPE_F16 && p->router_dtype != MNB_DTYPE_F32)
+        return fail(MNB_ERR_INVALID, "router dtype %d", p->router_dtype);
+    if (!std::isfinite(p->activation_alpha) || !std::isfinite(p->activation_beta) ||
+        (p->has_swiglu_limit && !std::isfinite(p->swiglu_limit)))
+        return fail(MNB_ERR_INVALID, "activation_alpha, activation_beta and swiglu_limit must be "
+                                     "finite");
+    return MNB_OK;
+}
+
+int mnb_qmoe_workspace_bytes(const mnb_qmoe_problem* p, size_t* bytes) {
+    if (!bytes) return fail(MNB_ERR_INVALID, "bytes is NULL");
+    *bytes = 0;
+    const int rc = mnb_qmoe_check(p);
+    if (rc) return rc;
+    *bytes = mnb::qmoe_workspace_bytes(qmoe_args(p));
+    return MNB_OK;
+}
+
+int mnb_qmoe(const mnb_qmoe_problem* p, const void* x, const void* router_logits,
+             const uint8_t* fc1_weights, const void* fc1_scales, const void* fc1_bias,
+             const uint8_t* fc2_weights, const void* fc2_scales, const void* fc2_bias, void* y,
+             void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = mnb_qmoe_check(p);
+    if (rc) return rc;
+    if (p->rows == 0) return MNB_OK;
+    if (!x || !router_logits || !fc1_weights || !fc1_scales || !fc2_weights || !fc2_scales || !y)
+        return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    const mnb::QmoeArgs q = qmoe_args(p);
+    const size_t need = mnb::qmoe_workspace_bytes(q);
+    if (!workspace || workspace_bytes < need)
+        return fail(MNB_ERR_INVALID, "workspace holds %zu bytes, QMoE needs %zu", workspace_bytes,
+                    need);
+    if (!aligned(workspace, 256)) return fail(MNB_ERR_INVALID, "workspace must be 256-byte aligned");
+    if (!aligned(x, 16) || !aligned(fc1_weights, 16) || !aligned(fc2_weights, 16) ||
+        !aligned(y, 16) || (fc2_bias && !aligned(fc2_bias, 16)))
+        return fail(MNB_ERR_INVALID, "x, y, the weights and fc2_bias must be 16-byte aligned");
+    hipError_t e = mnb::launch_qmoe(q, x, router_logits, fc1_weights, fc1_scales, fc1_bias,
+                                    fc2_weights, fc2_scales, fc2_bias, y, workspace,
+                                    static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "QMoE launch");
+    g_launches.fetch_add(1);
+    return MNB_OK;
+}
+
 // ---- session layer ------------------------------------------------------------------------
 
 struct mnb_session {
@@ -594,6 +684,153 @@ int mnb_session_run(mnb_session* s, const mnb_weights* w, int64_t m, const void*
     hipError_t e = hipStreamSynchronize(s->stream);
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     return MNB_OK;
+}
+
+struct mnb_qmoe_weights {
+    mnb_session* s = nullptr;
+    mnb_qmoe_problem node{};
+    void* buf[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};  // w1 s1 b1 w2 s2 b2
+};
+
+int mnb_qmoe_weights_release(mnb_qmoe_weights* w) {
+    if (!w) return MNB_OK;
+    (void)hipSetDevice(w->s->device);
+    (void)hipStreamSynchronize(w->s->stream);
+    for (void* b : w->buf)
+        if (b) (void)hipFree(b);
+    delete w;
+    return MNB_OK;
+}
+
+int mnb_qmoe_weights_upload(mnb_session* s, const mnb_qmoe_problem* node,
+                            int32_t scales_per_channel, const void* fc1_weights,
+                            size_t fc1_weights_bytes, const void* fc1_scales,
+                            size_t fc1_scales_bytes, const void* fc1_bias, size_t fc1_bias_bytes,
+                            const void* fc2_weights, size_t fc2_weights_bytes,
+                            const void* fc2_scales, size_t fc2_scales_bytes, const void* fc2_bias,
+                            size_t fc2_bias_bytes, mnb_qmoe_weights** out) {
+    if (!s || !node || !out) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    *out = nullptr;
+    mnb_qmoe_problem p = *node;
+    p.rows = 0;
+    int rc = mnb_qmoe_check(&p);
+    if (rc) return rc;
+    const size_t E = (size_t)p.num_experts, H = (size_t)p.hidden, I = (size_t)p.inter;
+    const size_t bs = (size_t)p.block_size;
+    const size_t n[2] = {2 * I, H}, kk[2] = {H, I};
+    const void* src_w[2] = {fc1_weights, fc2_weights};
+    const size_t got_w[2] = {fc1_weights_bytes, fc2_weights_bytes};
+    const void* src_s[2] = {fc1_scales, fc2_scales};
+    const size_t got_s[2] = {fc1_scales_bytes, fc2_scales_bytes};
+    const void* src_b[2] = {fc1_bias, fc2_bias};
+    const size_t got_b[2] = {fc1_bias_bytes, fc2_bias_bytes};
+    std::vector<uint16_t> expanded[2];
+    const void* host[6];
+    size_t size[6];
+    for (int f = 0; f < 2; ++f) {
+        const size_t want_w = E * n[f] * kk[f] / 2;
+        const size_t blocks = kk[f] / bs;
+        const size_t want_s = E * n[f] * (scales_per_channel ? 1 : blocks) * 2;
+        const size_t want_b = E * n[f] * 2;
+        if (!src_w[f] || got_w[f] != want_w)
+            return fail(MNB_ERR_INVALID, "fc%d weights hold %zu bytes, the layout needs %zu", f + 1,
+                        got_w[f], want_w);
+        if (!src_s[f] || got_s[f] != want_s)
+            return fail(MNB_ERR_INVALID, "fc%d scales hold %zu bytes, the layout needs %zu", f + 1,
+                        got_s[f], want_s);
+        if (src_b[f] && got_b[f] != want_b)
+            return fail(MNB_ERR_INVALID, "fc%d bias holds %zu bytes, the layout needs %zu", f + 1,
+                        got_b[f], want_b);
+        host[3 * f] = src_w[f];
+        size[3 * f] = want_w;
+        if (scales_per_channel) {
+            // one scale per output channel: the same scale for every block of the channel
+            const uint16_t* sc = static_cast<const uint16_t*>(src_s[f]);
+            expanded[f].resize(E * n[f] * blocks);
+            for (size_t c = 0; c < E * n[f]; ++c)
+                for (size_t b = 0; b < blocks; ++b) expanded[f][c * blocks + b] = sc[c];
+            host[3 * f + 1] = expanded[f].data();
+            size[3 * f + 1] = expanded[f].size() * 2;
+        } else {
+            host[3 * f + 1] = src_s[f];
+            size[3 * f + 1] = want_s;
+        }
+        host[3 * f + 2] = src_b[f];
+        size[3 * f + 2] = src_b[f] ? want_b : 0;
+    }
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    mnb_qmoe_weights* w = new (std::nothrow) mnb_qmoe_weights();
+    if (!w) return fail(MNB_ERR_NOMEM, "weights allocation failed");
+    w->s = s;
+    w->node = p;
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 6 && e == hipSuccess; ++i) {
+        if (!host[i]) continue;
+        e = hipMalloc(&w->buf[i], size[i]);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(w->buf[i], host[i], size[i], hipMemcpyHostToDevice, s->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) {
+        for (void* b : w->buf)
+            if (b) (void)hipFree(b);
+        delete w;
+        return hip_fail(e, "QMoE weight upload");
+    }
+    *out = w;
+    return MNB_OK;
+}
+
+int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows, const void* x,
+                         int x_on_device, const void* router_logits, int logits_on_device,
+                         void* y, int y_on_device) {
+    if (!s || !w) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    mnb_qmoe_problem p = w->node;
+    p.rows = rows;
+    int rc = mnb_qmoe_check(&p);
+    if (rc) return rc;
+    if (rows == 0) return MNB_OK;
+    if (!x || !router_logits || !y) return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    const size_t x_bytes = (size_t)rows * (size_t)p.hidden * 2;
+    const size_t l_bytes = (size_t)rows * (size_t)p.num_experts *
+                           (p.router_dtype == MNB_DTYPE_F32 ? 4 : 2);
+    const size_t ws = mnb::qmoe_workspace_bytes(qmoe_args(&p));
+    // one staging buffer for x and the logits, one for y; the workspace after them
+    const size_t x_off = 0, l_off = (x_bytes + 255) & ~(size_t)255;
+    const size_t stage = l_off + l_bytes;
+    rc = grow(&s->a_dev, &s->a_cap, stage);
+    if (rc) return rc;
+    rc = grow(&s->y_dev, &s->y_cap, x_bytes);
+    if (rc) return rc;
+    rc = grow(&s->ws, &s->ws_cap, ws);
+    if (rc) return rc;
+    uint8_t* st = static_cast<uint8_t*>(s->a_dev);
+    const void* xd = x;
+    const void* ld = router_logits;
+    void* yd = y_on_device ? y : s->y_dev;
+    hipError_t e = hipSuccess;
+    if (!x_on_device) {
+        e = hipMemcpyAsync(st + x_off, x, x_bytes, hipMemcpyHostToDevice, s->stream);
+        xd = st + x_off;
+    }
+    if (e == hipSuccess && !logits_on_device) {
+        e = hipMemcpyAsync(st + l_off, router_logits, l_bytes, hipMemcpyHostToDevice, s->stream);
+        ld = st + l_off;
+    }
+    if (e != hipSuccess) return hip_fail(e, "QMoE input upload");
+    rc = mnb_qmoe(&p, xd, ld, static_cast<const uint8_t*>(w->buf[0]), w->buf[1], w->buf[2],
+                  static_cast<const uint8_t*>(w->buf[3]), w->buf[4], w->buf[5], yd, s->ws,
+                  s->ws_cap, s->stream);
+    if (rc) return rc;
+    if (!y_on_device) {
+        e = hipMemcpyAsync(y, s->y_dev, x_bytes, hipMemcpyDeviceToHost, s->stream);
+        if (e != hipSuccess) return hip_fail(e, "QMoE output download");
+    }
+    e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
 int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,

@@ -62,6 +62,17 @@ class MoeProblem(C.Structure):
     ]
 
 
+class QmoeProblem(C.Structure):
+    _fields_ = [
+        ("rows", C.c_int64), ("hidden", C.c_int64), ("inter", C.c_int64),
+        ("num_experts", C.c_int64), ("k", C.c_int32), ("block_size", C.c_int32),
+        ("swiglu_fusion", C.c_int32), ("normalize_routing", C.c_int32),
+        ("activation_alpha", C.c_float), ("activation_beta", C.c_float),
+        ("swiglu_limit", C.c_float), ("has_swiglu_limit", C.c_int32),
+        ("router_dtype", C.c_int32), ("dtype", C.c_int32),
+    ]
+
+
 class MnbError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"mnb error {code}: {msg}")
@@ -108,6 +119,14 @@ def load() -> C.CDLL:
         "mnb_memcpy": (C.c_int, [C.c_int, vp, vp, sz, C.c_int]),
         "mnb_launch_count": (C.c_uint64, []),
         "mnb_calibrate_mfma": (C.c_int, [i32, i32, vp, vp, vp]),
+        "mnb_qmoe_check": (C.c_int, [C.POINTER(QmoeProblem)]),
+        "mnb_qmoe_workspace_bytes": (C.c_int, [C.POINTER(QmoeProblem), C.POINTER(sz)]),
+        "mnb_qmoe": (C.c_int, [C.POINTER(QmoeProblem), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                               sz, vp]),
+        "mnb_qmoe_weights_upload": (C.c_int, [vp, C.POINTER(QmoeProblem), i32, vp, sz, vp, sz,
+                                              vp, sz, vp, sz, vp, sz, vp, sz, C.POINTER(vp)]),
+        "mnb_qmoe_weights_release": (C.c_int, [vp]),
+        "mnb_session_run_qmoe": (C.c_int, [vp, vp, i64, vp, C.c_int, vp, C.c_int, vp, C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -180,6 +199,35 @@ def dequantize_f16(B, scales, zp, N: int, K: int, bits: int = 4, block_size: int
         out = torch.empty(N, K, dtype=torch.float16, device=B.device)
     check(load().mnb_dequantize_f16(N, K, bits, block_size, _ptr(B), _ptr(scales), _ptr(zp),
                                     _ptr(out), _stream(stream)))
+    return out
+
+
+def qmoe_problem(rows, hidden, inter, experts, k, block_size=32, fusion=1, normalize=True,
+                 alpha=1.702, beta=1.0, limit=7.0, router_f32=False) -> QmoeProblem:
+    return QmoeProblem(int(rows), int(hidden), int(inter), int(experts), int(k), int(block_size),
+                       int(fusion), int(bool(normalize)), float(alpha), float(beta),
+                       float(limit if limit is not None else 0.0), int(limit is not None),
+                       DTYPE_F32 if router_f32 else DTYPE_F16, DTYPE_F16)
+
+
+def qmoe(x, logits, fc1, fc1_scales, fc2, fc2_scales, *, k: int, inter: int, block_size: int = 32,
+         fc1_bias=None, fc2_bias=None, fusion: int = 1, normalize: bool = True,
+         alpha: float = 1.702, beta: float = 1.0, limit: float | None = 7.0, out=None,
+         workspace=None, stream=None):
+    """Fused QMoE on CUDA tensors through the C ABI (block scales ``[E, N, K/bs]``)."""
+    import torch
+    rows, hidden = int(x.shape[0]), int(x.shape[1])
+    p = qmoe_problem(rows, hidden, inter, int(logits.shape[1]), k, block_size, fusion, normalize,
+                     alpha, beta, limit, logits.dtype == torch.float32)
+    if out is None:
+        out = torch.empty(rows, hidden, dtype=torch.float16, device=x.device)
+    ws = C.c_size_t(0)
+    check(load().mnb_qmoe_workspace_bytes(C.byref(p), C.byref(ws)))
+    if workspace is None:
+        workspace = torch.empty(max(int(ws.value), 1), dtype=torch.uint8, device=x.device)
+    check(load().mnb_qmoe(C.byref(p), _ptr(x), _ptr(logits), _ptr(fc1), _ptr(fc1_scales),
+                          _ptr(fc1_bias), _ptr(fc2), _ptr(fc2_scales), _ptr(fc2_bias), _ptr(out),
+                          _ptr(workspace), int(workspace.numel()), _stream(stream)))
     return out
 
 
