@@ -111,4 +111,151 @@ inline ClaimDecision claim_matmul_nbits(const NodeFacts& f, bool int8_path) {
     return ClaimDecision{true, {}};
 }
 
+// ---- com.microsoft::QMoE ---------------------------------------------------------------------
+//
+// The reference registers QMoE with a fingerprint and no kernel (rust/src/ops/moe.rs:40-118:
+// 8..21 inputs, one output, `k` required, top-1/2 only, activations silu/swiglu/relu/gelu,
+// use_sparse_mixer 0, int weights).  This EP has the kernel (the HIP library's fused QMoE) and
+// claims what it implements, which is the gpt-oss form the reference records
+// (docs/OP_COVERAGE.md:831-835) widened in top-k and narrowed in activation:
+//   * k in 1..8 (the reference: 1..2), k <= E;
+//   * activation_type "swiglu" only, with swiglu_fusion 1 (interleaved) or 2 (concatenated);
+//     fusion 0 means separate fc3 weights, which this EP does not implement (ORT's own CPU
+//     kernel refuses it as well, docs/OP_COVERAGE.md:2199-2204);
+//   * use_sparse_mixer 0; expert_weight_bits 4; quant_type absent or "int"; block_size absent
+//     or 0 (one scale per output channel) or 32/64/128;
+//   * x float16 [.., H]; router logits float16 or float [rows, E];
+//   * fc1 [E, 2I, H/2] and fc2 [E, H, I/2] uint8, scales float16 [E, N] or [E, N, K/bs],
+//     optional float16 biases [E, 2I] and [E, H], all constant initializers with static shapes;
+//     inputs 8 and above (fc3, zero points, FP4/FP8 scales) absent;
+//   * H and I multiples of 32 and of block_size, E <= 1024.
+
+struct QmoeFacts {
+    std::string op_type;
+    std::string domain;
+    std::vector<InputFacts> inputs;
+    size_t num_outputs = 0;
+    bool has_k = false;
+    int64_t k = 0;
+    std::string activation_type = "relu";        // ORT's default
+    int64_t normalize_routing_weights = 0;
+    int64_t use_sparse_mixer = 0;
+    int64_t swiglu_fusion = 0;
+    int64_t expert_weight_bits = 4;
+    int64_t block_size = 0;
+    int64_t weights_prepacked = 0;
+    bool has_quant_type = false;
+    std::string quant_type;
+    float activation_alpha = 1.0f;
+    float activation_beta = 0.0f;
+    bool has_swiglu_limit = false;
+    float swiglu_limit = 0.0f;
+};
+
+// Extents read off the weight shapes when the claim succeeds.
+struct QmoeShape {
+    int64_t experts = 0, hidden = 0, inter = 0;
+    bool per_channel = false;
+};
+
+inline bool is_qmoe(const std::string& op_type, const std::string& domain) {
+    return op_type == "QMoE" && domain == "com.microsoft";
+}
+
+inline bool static_dims(const InputFacts& f, size_t rank) {
+    if (!f.has_shape || f.dims.size() != rank) return false;
+    for (int64_t d : f.dims)
+        if (d <= 0) return false;
+    return true;
+}
+
+inline ClaimDecision claim_qmoe(const QmoeFacts& f, QmoeShape* shape = nullptr) {
+    if (!is_qmoe(f.op_type, f.domain)) return decline("not com.microsoft::QMoE");
+    if (f.inputs.size() < 8 || f.inputs.size() > 21)
+        return decline("QMoE arity outside 8..21 inputs");
+    if (f.num_outputs != 1) return decline("QMoE must have exactly one output");
+    if (!f.has_k) return decline("the required attribute k is missing");
+    if (f.activation_type != "swiglu")
+        return decline("activation_type = " + f.activation_type + "; this EP implements swiglu");
+    if (f.swiglu_fusion != 1 && f.swiglu_fusion != 2)
+        return decline("swiglu_fusion = " + std::to_string(f.swiglu_fusion) +
+                       "; this EP implements 1 (interleaved) and 2 (concatenated)");
+    if (f.use_sparse_mixer != 0) return decline("use_sparse_mixer changes the routing");
+    if (f.expert_weight_bits != 4)
+        return decline("expert_weight_bits = " + std::to_string(f.expert_weight_bits) +
+                       "; this EP implements 4");
+    if (f.has_quant_type && f.quant_type != "int")
+        return decline("quant_type = " + f.quant_type + "; this EP implements int");
+    if (f.weights_prepacked != 0) return decline("weights_prepacked is set");
+    if (f.block_size != 0 && f.block_size != 32 && f.block_size != 64 && f.block_size != 128)
+        return decline("block_size = " + std::to_string(f.block_size) +
+                       "; this EP implements per-channel (0) and 32/64/128");
+    for (size_t i = 8; i < f.inputs.size(); ++i)
+        if (f.inputs[i].present)
+            return decline("input " + std::to_string(i) +
+                           " (fc3 / zero points / FP4-FP8 scales) is not implemented");
+    const InputFacts& x = f.inputs[0];
+    const InputFacts& r = f.inputs[1];
+    if (!x.present || x.elem_type != kElemFloat16) return decline("input is not float16");
+    if (!r.present || (r.elem_type != kElemFloat16 && r.elem_type != kElemFloat))
+        return decline("router_probs is neither float16 nor float");
+    for (int i : {2, 3, 5, 6})
+        if (!f.inputs[(size_t)i].present)
+            return decline("expert weight input " + std::to_string(i) + " is absent");
+    for (size_t i = 2; i < 8; ++i)
+        if (f.inputs[i].present && !f.inputs[i].constant)
+            return decline("expert tensors must be constant initializers");
+    const InputFacts& w1 = f.inputs[2];
+    const InputFacts& s1 = f.inputs[3];
+    const InputFacts& b1 = f.inputs[4];
+    const InputFacts& w2 = f.inputs[5];
+    const InputFacts& s2 = f.inputs[6];
+    const InputFacts& b2 = f.inputs[7];
+    if (w1.elem_type != kElemUint8 || w2.elem_type != kElemUint8)
+        return decline("expert weights must be packed uint8");
+    if (s1.elem_type != kElemFloat16 || s2.elem_type != kElemFloat16)
+        return decline("expert scales must be float16");
+    if ((b1.present && b1.elem_type != kElemFloat16) || (b2.present && b2.elem_type != kElemFloat16))
+        return decline("expert biases must be float16");
+    if (!static_dims(w1, 3) || !static_dims(w2, 3))
+        return decline("expert weights need static [E, N, K/2] shapes");
+    const int64_t E = w1.dims[0], N1 = w1.dims[1], H = 2 * w1.dims[2];
+    if (N1 % 2) return decline("fc1 has an odd number of output channels");
+    const int64_t I = N1 / 2;
+    if (w2.dims[0] != E || w2.dims[1] != H || 2 * w2.dims[2] != I)
+        return decline("fc2's shape does not match fc1's (expected [E, H, I/2])");
+    if (E > 1024) return decline("more than 1024 experts");
+    if (f.k < 1 || f.k > 8 || f.k > E)
+        return decline("k = " + std::to_string(f.k) + "; this EP routes 1..min(8, E)");
+    const int64_t bs = f.block_size == 0 ? 32 : f.block_size;
+    if (H % 32 || I % 32 || H % bs || I % bs)
+        return decline("hidden and inter sizes must be multiples of 32 and of block_size");
+    const bool per_channel = f.block_size == 0;
+    auto scales_ok = [&](const InputFacts& s, int64_t n, int64_t kk) {
+        if (per_channel) return static_dims(s, 2) && s.dims[0] == E && s.dims[1] == n;
+        return static_dims(s, 3) && s.dims[0] == E && s.dims[1] == n && s.dims[2] == kk / bs;
+    };
+    if (!scales_ok(s1, N1, H) || !scales_ok(s2, H, I))
+        return decline(per_channel ? "scales must be [E, N] (per channel)"
+                                   : "scales must be [E, N, K/block_size]");
+    if ((b1.present && !(static_dims(b1, 2) && b1.dims[0] == E && b1.dims[1] == N1)) ||
+        (b2.present && !(static_dims(b2, 2) && b2.dims[0] == E && b2.dims[1] == H)))
+        return decline("biases must be [E, 2I] and [E, H]");
+    if (x.has_shape) {
+        if (x.dims.empty()) return decline("input is a scalar");
+        if (x.dims.back() >= 0 && x.dims.back() != H) return decline("input's last dim is not H");
+    }
+    if (r.has_shape) {
+        if (r.dims.size() != 2) return decline("router_probs must be 2-D");
+        if (r.dims[1] >= 0 && r.dims[1] != E) return decline("router_probs' last dim is not E");
+    }
+    if (shape) {
+        shape->experts = E;
+        shape->hidden = H;
+        shape->inter = I;
+        shape->per_channel = per_channel;
+    }
+    return ClaimDecision{true, {}};
+}
+
 }  // namespace mi355x_ep

@@ -244,6 +244,72 @@ NodeFacts node_facts(const OrtApi* api, const OrtNode* node) {
     return f;
 }
 
+bool float_attr(const OrtApi* api, const OrtNode* node, const char* name, float* out) {
+    const OrtOpAttr* attr = nullptr;
+    OrtStatus* st = api->Node_GetAttributeByName(node, name, &attr);
+    if (st) {
+        api->ReleaseStatus(st);
+        return false;
+    }
+    if (!attr) return false;
+    float v = 0.f;
+    size_t got = 0;
+    st = api->ReadOpAttr(attr, ORT_OP_ATTR_FLOAT, &v, sizeof(v), &got);
+    if (st) {
+        api->ReleaseStatus(st);
+        return false;
+    }
+    *out = v;
+    return true;
+}
+
+// ReadOpAttr reports the byte count a string needs when the buffer is too small; the string is
+// read with a buffer of that size (no terminator is written).
+bool string_attr(const OrtApi* api, const OrtNode* node, const char* name, std::string* out) {
+    const OrtOpAttr* attr = nullptr;
+    OrtStatus* st = api->Node_GetAttributeByName(node, name, &attr);
+    if (st) {
+        api->ReleaseStatus(st);
+        return false;
+    }
+    if (!attr) return false;
+    size_t need = 0;
+    st = api->ReadOpAttr(attr, ORT_OP_ATTR_STRING, nullptr, 0, &need);
+    if (st) api->ReleaseStatus(st);
+    std::string buf(need, '\0');
+    size_t got = 0;
+    st = api->ReadOpAttr(attr, ORT_OP_ATTR_STRING, need ? &buf[0] : nullptr, need, &got);
+    if (st) {
+        api->ReleaseStatus(st);
+        return false;
+    }
+    buf.resize(std::min(got, need));
+    *out = buf;
+    return true;
+}
+
+QmoeFacts qmoe_facts(const OrtApi* api, const OrtNode* node) {
+    QmoeFacts f;
+    f.op_type = node_string(api, node, api->Node_GetOperatorType);
+    f.domain = node_string(api, node, api->Node_GetDomain);
+    if (!is_qmoe(f.op_type, f.domain)) return f;
+    for (const OrtValueInfo* vi : node_inputs(api, node)) f.inputs.push_back(input_facts(api, vi));
+    f.num_outputs = node_outputs(api, node).size();
+    f.has_k = int_attr(api, node, "k", &f.k);
+    string_attr(api, node, "activation_type", &f.activation_type);
+    int_attr(api, node, "normalize_routing_weights", &f.normalize_routing_weights);
+    int_attr(api, node, "use_sparse_mixer", &f.use_sparse_mixer);
+    int_attr(api, node, "swiglu_fusion", &f.swiglu_fusion);
+    int_attr(api, node, "expert_weight_bits", &f.expert_weight_bits);
+    int_attr(api, node, "block_size", &f.block_size);
+    int_attr(api, node, "weights_prepacked", &f.weights_prepacked);
+    f.has_quant_type = string_attr(api, node, "quant_type", &f.quant_type);
+    float_attr(api, node, "activation_alpha", &f.activation_alpha);
+    float_attr(api, node, "activation_beta", &f.activation_beta);
+    f.has_swiglu_limit = float_attr(api, node, "swiglu_limit", &f.swiglu_limit);
+    return f;
+}
+
 // Session option `key` (ORT prefixes EP options with "ep.<name>."; both spellings are read).
 bool session_option(const OrtApi* api, const OrtSessionOptions* so, const std::string& key,
                     std::string* value) {
@@ -291,6 +357,17 @@ struct NodeKernel {
     mnb_weights* weights = nullptr; // resident weights, or the last per-call upload
     std::mutex mu;
     std::string name;
+    // QMoE node (qmoe set): x and router logits by fused-input index, expert tensors resident.
+    bool qmoe = false;
+    mnb_qmoe_problem qprob{};
+    size_t fused_router = SIZE_MAX;
+    int32_t router_elem = 0;
+    mnb_qmoe_weights* qweights = nullptr;
+
+    ~NodeKernel() {
+        if (weights) mnb_weights_release(weights);
+        if (qweights) mnb_qmoe_weights_release(qweights);
+    }
 };
 
 struct ComputeInfo {
@@ -353,10 +430,6 @@ bool is_our_hbm(const OrtEpApi* ep_api, const OrtMemoryDevice* md, int* device) 
     return true;
 }
 
-bool is_host_memory(const OrtEpApi* ep_api, const OrtMemoryDevice* md) {
-    return !md || ep_api->MemoryDevice_GetDeviceType(md) == OrtMemoryInfoDeviceType_CPU;
-}
-
 Factory* as_factory(const OrtEpFactory* p) {
     return reinterpret_cast<Factory*>(const_cast<OrtEpFactory*>(p));
 }
@@ -401,10 +474,65 @@ int32_t tensor_elem_type(const OrtApi* api, const OrtValue* v, std::vector<int64
     return (int32_t)et;
 }
 
+// Whether a tensor lives in this EP's HBM (device-memory mode), checking the device ordinal.
+bool on_our_device(Ep* ep, const OrtValue* v) {
+    if (!ep->memory_device || !v) return false;
+    int d = -1;
+    if (!is_our_hbm(ep->ep_api, ep->ep_api->Value_GetMemoryDevice(v), &d)) return false;
+    if (d != ep->device)
+        fail(ORT_INVALID_ARGUMENT, "a tensor lives on HIP device %d, this EP runs on %d", d, ep->device);
+    return true;
+}
+
+void compute_qmoe(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
+    const OrtApi* api = ep->api;
+    size_t nin = 0;
+    ORT_OK(api, KernelContext_GetInputCount(ctx, &nin));
+    if (k.fused_a >= nin || k.fused_router >= nin)
+        fail(ORT_EP_FAIL, "fused QMoE node has %zu inputs", nin);
+    const OrtValue* x = nullptr;
+    const OrtValue* r = nullptr;
+    ORT_OK(api, KernelContext_GetInput(ctx, k.fused_a, &x));
+    ORT_OK(api, KernelContext_GetInput(ctx, k.fused_router, &r));
+    if (!x || !r) fail(ORT_INVALID_ARGUMENT, "input or router_probs is missing");
+    std::vector<int64_t> xd, rd;
+    if (tensor_elem_type(api, x, &xd) != kElemFloat16)
+        fail(ORT_INVALID_ARGUMENT, "QMoE input is not float16");
+    if (tensor_elem_type(api, r, &rd) != k.router_elem)
+        fail(ORT_INVALID_ARGUMENT, "router_probs has another element type than at Compile");
+    if (xd.empty() || xd.back() != k.qprob.hidden)
+        fail(ORT_INVALID_ARGUMENT, "input's last dimension is not the hidden size %lld",
+             (long long)k.qprob.hidden);
+    int64_t rows = 1;
+    for (size_t i = 0; i + 1 < xd.size(); ++i) {
+        if (xd[i] < 0) fail(ORT_INVALID_ARGUMENT, "input has a negative extent");
+        rows *= xd[i];
+    }
+    if (rd.size() != 2 || rd[0] != rows || rd[1] != k.qprob.num_experts)
+        fail(ORT_INVALID_ARGUMENT, "router_probs must be [%lld, %lld]", (long long)rows,
+             (long long)k.qprob.num_experts);
+    OrtValue* y = nullptr;
+    ORT_OK(api, KernelContext_GetOutput(ctx, 0, xd.data(), xd.size(), &y));
+    if (!y) fail(ORT_EP_FAIL, "ORT returned no output tensor");
+    if (rows == 0) return;
+    void* ydata = nullptr;
+    ORT_OK(api, GetTensorMutableData(y, &ydata));
+    const bool x_dev = on_our_device(ep, x), r_dev = on_our_device(ep, r), y_dev = on_our_device(ep, y);
+    std::lock_guard<std::mutex> lk(k.mu);
+    mnb_ok(mnb_session_run_qmoe(ep->session, k.qweights, rows, tensor_data(api, x), x_dev ? 1 : 0,
+                                tensor_data(api, r), r_dev ? 1 : 0, ydata, y_dev ? 1 : 0),
+           "QMoE kernels");
+    g_compute_count.fetch_add(1);
+}
+
 void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     const OrtApi* api = ep->api;
     if (env_flag("MI355X_EP_FORCE_COMPUTE_FAILURE"))
         fail(ORT_EP_FAIL, "forced Compute failure (MI355X_EP_FORCE_COMPUTE_FAILURE is set)");
+    if (k.qmoe) {
+        compute_qmoe(ep, k, ctx);
+        return;
+    }
     size_t nin = 0;
     ORT_OK(api, KernelContext_GetInputCount(ctx, &nin));
     if (k.fused_a >= nin) fail(ORT_EP_FAIL, "fused node has %zu inputs; A expected at %zu", nin, k.fused_a);
@@ -534,6 +662,23 @@ void get_capability(Ep* ep, const OrtGraph* graph, OrtEpGraphSupportInfo* suppor
     if (!ep->claim_enabled) return;
     for (const OrtNode* node : nodes) {
         if (!node) continue;
+        const std::string op = node_string(api, node, api->Node_GetOperatorType);
+        const std::string dom = node_string(api, node, api->Node_GetDomain);
+        if (is_qmoe(op, dom)) {
+            const std::string name = node_string(api, node, api->Node_GetName);
+            const ClaimDecision d = claim_qmoe(qmoe_facts(api, node));
+            if (!d.claim) {
+                claim_log("decline %s: %s", name.c_str(), d.reason.c_str());
+                continue;
+            }
+            OrtNodeFusionOptions opts{};
+            opts.ort_version_supported = ep->factory->version;
+            opts.drop_constant_initializers = !ep->keep_constant_initializers;
+            ort_check(api, ep->ep_api->EpGraphSupportInfo_AddNodesToFuse(support, &node, 1, &opts),
+                      "EpGraphSupportInfo_AddNodesToFuse");
+            claim_log("claim %s (QMoE)", name.c_str());
+            continue;
+        }
         const NodeFacts f = node_facts(api, node);
         if (!is_matmul_nbits(f)) continue;
         const std::string name = node_string(api, node, api->Node_GetName);
@@ -572,13 +717,86 @@ mnb_session* ep_session(Ep* ep) {
     return ep->session;
 }
 
+// Fused-node input index of each body-node input, matched by value name (SIZE_MAX if absent).
+std::vector<size_t> fused_input_map(const OrtApi* api, const OrtNode* node, const OrtNode* fused) {
+    const std::vector<const OrtValueInfo*> body_in = node_inputs(api, node);
+    const std::vector<const OrtValueInfo*> fused_in = node_inputs(api, fused);
+    std::vector<std::string> fused_names;
+    for (const OrtValueInfo* vi : fused_in) fused_names.push_back(value_name(api, vi));
+    std::vector<size_t> out(body_in.size(), SIZE_MAX);
+    for (size_t i = 0; i < body_in.size(); ++i) {
+        if (!body_in[i]) continue;
+        const std::string nm = value_name(api, body_in[i]);
+        for (size_t j = 0; j < fused_names.size(); ++j)
+            if (fused_names[j] == nm) {
+                out[i] = j;
+                break;
+            }
+    }
+    return out;
+}
+
+std::unique_ptr<NodeKernel> compile_qmoe(Ep* ep, const OrtNode* node, const OrtNode* fused) {
+    const OrtApi* api = ep->api;
+    const QmoeFacts f = qmoe_facts(api, node);
+    QmoeShape shape;
+    const ClaimDecision d = claim_qmoe(f, &shape);
+    if (!d.claim) fail(ORT_EP_FAIL, "compiled node fails the QMoE claim predicate: %s", d.reason.c_str());
+    auto k = std::make_unique<NodeKernel>();
+    k->qmoe = true;
+    k->name = node_string(api, node, api->Node_GetName);
+    mnb_qmoe_problem& p = k->qprob;
+    p.hidden = shape.hidden;
+    p.inter = shape.inter;
+    p.num_experts = shape.experts;
+    p.k = (int32_t)f.k;
+    p.block_size = f.block_size == 0 ? 32 : (int32_t)f.block_size;
+    p.swiglu_fusion = (int32_t)f.swiglu_fusion;
+    p.normalize_routing = f.normalize_routing_weights != 0;
+    p.activation_alpha = f.activation_alpha;
+    p.activation_beta = f.activation_beta;
+    p.swiglu_limit = f.swiglu_limit;
+    p.has_swiglu_limit = f.has_swiglu_limit ? 1 : 0;
+    p.router_dtype = f.inputs[1].elem_type == kElemFloat16 ? MNB_DTYPE_F16 : MNB_DTYPE_F32;
+    p.dtype = MNB_DTYPE_F16;
+    k->router_elem = f.inputs[1].elem_type;
+    mnb_ok(mnb_qmoe_check(&p), "QMoE attributes");
+    const std::vector<size_t> map = fused_input_map(api, node, fused);
+    k->fused_a = map[0];
+    k->fused_router = map[1];
+    if (k->fused_a == SIZE_MAX || k->fused_router == SIZE_MAX)
+        fail(ORT_EP_FAIL, "input or router_probs is not an input of the fused node");
+    // Expert tensors: constant initializers (the claim requires it), read now, uploaded once.
+    const std::vector<const OrtValueInfo*> body_in = node_inputs(api, node);
+    const void* host[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    size_t bytes[6] = {0, 0, 0, 0, 0, 0};
+    for (int r = 0; r < 6; ++r) {
+        const size_t bi = (size_t)r + 2;
+        if (!f.inputs[bi].present) continue;
+        const OrtValue* v = nullptr;
+        ORT_OK(api, ValueInfo_GetInitializerValue(body_in[bi], &v));
+        if (!v) fail(ORT_EP_FAIL, "QMoE input %zu has no initializer value", bi);
+        host[r] = tensor_data(api, v);
+        bytes[r] = tensor_bytes(api, v);
+    }
+    mnb_ok(mnb_qmoe_weights_upload(ep_session(ep), &p, shape.per_channel ? 1 : 0, host[0],
+                                   bytes[0], host[1], bytes[1], host[2], bytes[2], host[3],
+                                   bytes[3], host[4], bytes[4], host[5], bytes[5], &k->qweights),
+           "uploading QMoE expert weights at Compile");
+    k->resident = true;
+    return k;
+}
+
 std::unique_ptr<NodeKernel> compile_one(Ep* ep, const OrtGraph* graph, const OrtNode* fused) {
     const OrtApi* api = ep->api;
     size_t n = 0;
     ORT_OK(api, Graph_GetNumNodes(graph, &n));
-    if (n != 1) fail(ORT_EP_FAIL, "a fused MatMulNBits island holds %zu nodes, expected 1", n);
+    if (n != 1) fail(ORT_EP_FAIL, "a fused island holds %zu nodes, expected 1", n);
     const OrtNode* node = nullptr;
     ORT_OK(api, Graph_GetNodes(graph, &node, 1));
+    if (is_qmoe(node_string(api, node, api->Node_GetOperatorType),
+                node_string(api, node, api->Node_GetDomain)))
+        return compile_qmoe(ep, node, fused);
     const NodeFacts f = node_facts(api, node);
     const ClaimDecision d = claim_matmul_nbits(f, int8_path_available(f));
     if (!d.claim) fail(ORT_EP_FAIL, "compiled node fails the claim predicate: %s", d.reason.c_str());
@@ -665,10 +883,7 @@ OrtStatus* ORT_API_CALL ep_compile(OrtEp* self, const OrtGraph** graphs, const O
         }
     });
     if (st) {
-        for (ComputeInfo* ci : made) {
-            if (ci->kernel && ci->kernel->weights) mnb_weights_release(ci->kernel->weights);
-            delete ci;
-        }
+        for (ComputeInfo* ci : made) delete ci;      // the kernel releases its weights
         return st;
     }
     for (size_t i = 0; i < count; ++i) infos[i] = &made[i]->base;
@@ -677,10 +892,7 @@ OrtStatus* ORT_API_CALL ep_compile(OrtEp* self, const OrtGraph** graphs, const O
 
 void ORT_API_CALL ep_release_infos(OrtEp*, OrtNodeComputeInfo** infos, size_t n) noexcept {
     for (size_t i = 0; infos && i < n; ++i) {
-        ComputeInfo* ci = as_info(infos[i]);
-        if (!ci) continue;
-        if (ci->kernel && ci->kernel->weights) mnb_weights_release(ci->kernel->weights);
-        delete ci;
+        delete as_info(infos[i]);                       // the kernel releases its weights
     }
 }
 

@@ -144,7 +144,13 @@ class Host:
         assert self.L.mock_add_value(name.encode(), elem, len(shape), _dims(shape), ptr, nbytes) == 0
 
     def node(self, op, domain, name, inputs, outputs, attrs: dict):
-        a = ",".join(f"{k}={int(v)}" for k, v in attrs.items())
+        def fmt(k, v):
+            if isinstance(v, str):
+                return f"{k}:s={v}"
+            if isinstance(v, float):
+                return f"{k}:f={v!r}"
+            return f"{k}={int(v)}"
+        a = ",".join(fmt(k, v) for k, v in attrs.items())
         rc = self.L.mock_add_node(op.encode(), domain.encode(), name.encode(),
                                   ",".join(inputs).encode(), ",".join(outputs).encode(), a.encode())
         assert rc == 0, err()
@@ -228,3 +234,37 @@ def add_matmul_nbits(h: Host, name: str, inp: dict, N: int, K: int, bits: int, b
         attrs["accuracy_level"] = acc_level
     h.node("MatMulNBits", "com.microsoft", name, ins, [y_name], attrs)
     return a_name, y_name
+
+
+def add_qmoe(h: Host, name: str, inp: dict, *, k: int, x_shape, router_elem=FLOAT16,
+             attrs_over: dict | None = None, const_weights=True, extra_inputs=(),
+             y_name=None):
+    """Adds one com.microsoft::QMoE node (gpt-oss attribute set) from an oracle
+    make_qmoe_inputs() dict: input, router_probs, fc1 weights/scales/bias, fc2
+    weights/scales/bias.  Per-channel scales ([E, N]) leave block_size out."""
+    x_name, r_name, y_name = f"{name}_x", f"{name}_router", y_name or f"{name}_y"
+    E = inp["fc1"].shape[0]
+    rows = int(np.prod(x_shape[:-1])) if all(d >= 0 for d in x_shape[:-1]) else -1
+    h.value(x_name, FLOAT16, x_shape)
+    h.value(r_name, router_elem, (rows, E))
+    h.value(y_name, FLOAT16, x_shape)
+    ins = [x_name, r_name]
+    for role in ("fc1", "fc1_scales", "fc1_bias", "fc2", "fc2_scales", "fc2_bias"):
+        arr = inp.get(role)
+        if arr is None:
+            ins.append("")
+            continue
+        vn = f"{name}_{role}"
+        elem = UINT8 if role in ("fc1", "fc2") else FLOAT16
+        h.value(vn, elem, arr.shape, arr if const_weights else None)
+        ins.append(vn)
+    ins.extend(extra_inputs)
+    attrs = {"k": k, "activation_type": "swiglu", "activation_alpha": 1.702,
+             "activation_beta": 1.0, "swiglu_limit": 7.0, "swiglu_fusion": 1,
+             "normalize_routing_weights": 1, "use_sparse_mixer": 0, "expert_weight_bits": 4}
+    if inp["fc1_scales"].ndim == 3:
+        attrs["block_size"] = inp["fc1"].shape[2] * 2 // inp["fc1_scales"].shape[2]
+    attrs.update(attrs_over or {})
+    attrs = {a: v for a, v in attrs.items() if v is not None}
+    h.node("QMoE", "com.microsoft", name, ins, [y_name], attrs)
+    return x_name, r_name, y_name

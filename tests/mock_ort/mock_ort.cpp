@@ -70,7 +70,10 @@ struct OrtValue {
 };
 struct OrtOpAttr {
     std::string name;
+    OrtOpAttrType type = ORT_OP_ATTR_INT;
     int64_t value = 0;
+    float fvalue = 0.f;
+    std::string svalue;
 };
 struct OrtNode {
     std::string op_type, domain, name;
@@ -215,10 +218,20 @@ OrtStatus* ORT_API_CALL m_Node_GetAttributeByName(const OrtNode* n, const char* 
 }
 OrtStatus* ORT_API_CALL m_ReadOpAttr(const OrtOpAttr* a, OrtOpAttrType type, void* data, size_t len,
                                      size_t* out) NX {
-    if (type != ORT_OP_ATTR_INT) return mk_status(ORT_INVALID_ARGUMENT, "mock holds INT attributes only");
-    *out = sizeof(int64_t);
-    if (len < sizeof(int64_t)) return mk_status(ORT_INVALID_ARGUMENT, "buffer too small");
-    std::memcpy(data, &a->value, sizeof(int64_t));
+    // as ORT: the requested type must be the attribute's; `out` is the byte count needed (on
+    // failure) or written (on success); strings are written without a terminator
+    if (type != a->type) return mk_status(ORT_INVALID_ARGUMENT, "attribute type mismatch");
+    const void* src = nullptr;
+    size_t need = 0;
+    switch (type) {
+        case ORT_OP_ATTR_INT: src = &a->value; need = sizeof(int64_t); break;
+        case ORT_OP_ATTR_FLOAT: src = &a->fvalue; need = sizeof(float); break;
+        case ORT_OP_ATTR_STRING: src = a->svalue.data(); need = a->svalue.size(); break;
+        default: return mk_status(ORT_INVALID_ARGUMENT, "mock holds INT, FLOAT and STRING attributes");
+    }
+    *out = need;
+    if (len < need || (need && !data)) return mk_status(ORT_INVALID_ARGUMENT, "buffer too small");
+    if (need) std::memcpy(data, src, need);
     return nullptr;
 }
 OrtStatus* ORT_API_CALL m_GetValueInfoName(const OrtValueInfo* v, const char** out) NX {
@@ -720,7 +733,7 @@ int mock_add_value(const char* name, int elem, int rank, const int64_t* dims, co
 }
 
 // A node: inputs/outputs are comma-separated value names ("" = absent optional input);
-// int_attrs is "K=64,N=32,bits=4".
+// attrs is "K=64,N=32,bits=4"; "name:f=1.5" is a float and "name:s=swiglu" a string attribute.
 int mock_add_node(const char* op, const char* domain, const char* name, const char* inputs,
                   const char* outputs, const char* int_attrs) {
     auto n = std::make_unique<OrtNode>();
@@ -750,7 +763,22 @@ int mock_add_node(const char* op, const char* domain, const char* name, const ch
     for (const std::string& kv : split(int_attrs, ',')) {
         if (kv.empty()) continue;
         const size_t eq = kv.find('=');
-        n->attrs.push_back(OrtOpAttr{kv.substr(0, eq), std::atoll(kv.c_str() + eq + 1)});
+        std::string key = kv.substr(0, eq);
+        const std::string val = kv.substr(eq + 1);
+        OrtOpAttr a;
+        const size_t colon = key.find(':');
+        const char kind = colon == std::string::npos ? 'i' : key[colon + 1];
+        a.name = key.substr(0, colon);
+        if (kind == 'f') {
+            a.type = ORT_OP_ATTR_FLOAT;
+            a.fvalue = std::strtof(val.c_str(), nullptr);
+        } else if (kind == 's') {
+            a.type = ORT_OP_ATTR_STRING;
+            a.svalue = val;
+        } else {
+            a.value = std::atoll(val.c_str());
+        }
+        n->attrs.push_back(a);
     }
     g->graph.nodes.push_back(n.get());
     g->nodes.push_back(std::move(n));
