@@ -15,6 +15,8 @@ The line also carries, measured in the same run:
   prefill       MatMulNBits M=2048, K=3072, N=8192 in TFLOP/s vs 2.5 PFLOP/s fp16
   accuracy_level_4  configs[4] (M=16, K=8192, N=3072, bs128, zp, int8 activations) in GB/s
   moe           configs[3] (32 experts, top-4 of 64 tokens, gate_up and down) in GB/s
+  qmoe          configs[3] as one fused QMoE op (routing, both expert GEMVs, SwiGLU, combine)
+  mfma_calibration  the fp16 MFMA rate the chip sustains on random and on constant operands
   cpu_baseline  the C restatement in oracle/ (kind "port"; stock ORT is not installed in this
                 image) on the host's cores, on a bounded sample of the same layer set
 `--pmc-node NODE` runs one node's launches and a 256 MiB copy only, for rocprofv3 --pmc passes
@@ -447,6 +449,52 @@ def main() -> int:
                     "frac_hbm": round(mbytes / (m_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         del wB, wS
 
+    # The whole gpt-oss QMoE layer of configs[3] as one fused op (mnb_qmoe): device routing of
+    # the same 64 x 32 N(0,1) logits, fc1 (gate_up, with bias) + SwiGLU (alpha 1.702, beta 1,
+    # limit 7, interleaved) + fc2 (down, with bias) + weighted combine.  Expert tensors rotated
+    # over two copies (896 MB > 2x MALL).  Algorithmic bytes: all 32 experts' weights, scales
+    # and biases (every expert is routed to with near certainty), x, the logits and y.
+    q_I = 2880
+    q_prob = mnb.qmoe_problem(T, MK, q_I, E, TOPK, BS, 1, True, 1.702, 1.0, 7.0)
+    q_ws_n = C.c_size_t(0)
+    mnb.check(lib.mnb_qmoe_workspace_bytes(C.byref(q_prob), C.byref(q_ws_n)))
+    q_ws = torch.empty(int(q_ws_n.value), dtype=torch.uint8, device=dev)
+    q_x = torch.randn(T, MK, device=dev, generator=gen).to(torch.float16)
+    q_lg = torch.from_numpy(logits.astype(np.float16)).to(dev)
+    q_y = torch.empty(T, MK, dtype=torch.float16, device=dev)
+
+    def qtensors():
+        w1 = torch.randint(0, 256, (E, 2 * q_I, MK // 2), dtype=torch.uint8, device=dev, generator=gen)
+        s1 = (torch.randn(E, 2 * q_I, MK // BS, device=dev, generator=gen).abs() * 0.02).to(torch.float16)
+        b1 = (torch.randn(E, 2 * q_I, device=dev, generator=gen) * 0.1).to(torch.float16)
+        w2 = torch.randint(0, 256, (E, MK, q_I // 2), dtype=torch.uint8, device=dev, generator=gen)
+        s2 = (torch.randn(E, MK, q_I // BS, device=dev, generator=gen).abs() * 0.02).to(torch.float16)
+        b2 = (torch.randn(E, MK, device=dev, generator=gen) * 0.1).to(torch.float16)
+        return w1, s1, b1, w2, s2, b2
+
+    q_w = [qtensors() for _ in range(2)]
+    q_bytes = sum(t.numel() * t.element_size() for t in q_w[0]) + 2 * T * MK * 2 + 2 * T * E
+
+    def qlaunch(r, sp):
+        w1, s1, b1, w2, s2, b2 = q_w[r % 2]
+        rc = lib.mnb_qmoe(C.byref(q_prob), q_x.data_ptr(), q_lg.data_ptr(), w1.data_ptr(),
+                          s1.data_ptr(), b1.data_ptr(), w2.data_ptr(), s2.data_ptr(),
+                          b2.data_ptr(), q_y.data_ptr(), q_ws.data_ptr(), q_ws.numel(), sp)
+        if rc:
+            mnb.check(rc)
+
+    q_us = graph_time_us(qlaunch, 10)
+    qmoe = {"config": "gpt-oss-20b QMoE layer: 64 tokens, 32 experts, top-4, H = I = 2880, "
+                      "int4 bs32, biases, SwiGLU alpha 1.702 beta 1 limit 7",
+            "bytes": q_bytes, "us": round(q_us, 2),
+            "GB/s": round(q_bytes / (q_us * 1e-6) / 1e9, 1),
+            "kernels": "qmoe_route + group_gemv (fc1) + qmoe_swiglu + group_gemv (fc2) + "
+                       "qmoe_combine",
+            "roofline": {"bound": "hbm", "achieved": round(q_bytes / (q_us * 1e-6) / 1e9, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(q_bytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
+    del q_w
+
     # The EP's Compute call (mnb_session_run, synchronous) for qkv at M=1: host I/O (A and Y in
     # pageable host memory, staged through HBM, as ORT hands them over by default) against
     # device-resident A and Y (MI355X_EP_DEVICE_MEMORY=1).  Wall clock per call, median.
@@ -510,6 +558,7 @@ def main() -> int:
         "mfma_calibration": mfma_cal,
         "accuracy_level_4": acc4,
         "moe": moe,
+        "qmoe": qmoe,
         "session_io": session_io,
         "cpu_baseline": cpu,
     }

@@ -136,32 +136,63 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     const int zpitch = (nz + 3) & ~3;
     T* const sS = reinterpret_cast<T*>(red + W * MT * 64);
     uint8_t* const sZ = reinterpret_cast<uint8_t*>(sS + 16 * spitch);
-    for (int idx = threadIdx.x; idx < 16 * nblk; idx += blockDim.x) {
-        const int n = idx / nblk;
-        const int j = idx - n * nblk;
-        const int cc = min(n0 + n, N - 1);
-        sS[n * spitch + j] = S[wofs_s + (int64_t)cc * bpc + b_lo + j];
-    }
-    if constexpr (HAS_ZP) {
-        for (int idx = threadIdx.x; idx < 16 * nz; idx += blockDim.x) {
-            const int n = idx / nz;
-            const int j = idx - n * nz;
-            const int cc = min(n0 + n, N - 1);
-            sZ[n * zpitch + j] = Z[wofs_z + (int64_t)cc * zpb + z_lo + j];
+    // Staging loads are issued eight at a time before any of them is stored, so a wavefront
+    // waits for one memory round trip per batch rather than one per element (with one
+    // wavefront per workgroup a strip stages ~20 elements per lane).
+    auto stage = [&](int total, auto&& load, auto&& store) {
+        constexpr int kB = 8;
+        for (int base = (int)threadIdx.x; base < total; base += kB * (int)blockDim.x) {
+            decltype(load(0)) v[kB];
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                const int idx = base + b * (int)blockDim.x;
+                v[b] = load(idx < total ? idx : total - 1);
+            }
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                const int idx = base + b * (int)blockDim.x;
+                if (idx < total) store(idx, v[b]);
+            }
         }
+    };
+    stage(16 * nblk,
+          [&](int idx) {
+              const int n = idx / nblk;
+              const int j = idx - n * nblk;
+              const int cc = min(n0 + n, N - 1);
+              return S[wofs_s + (int64_t)cc * bpc + b_lo + j];
+          },
+          [&](int idx, T v) {
+              const int n = idx / nblk;
+              sS[n * spitch + (idx - n * nblk)] = v;
+          });
+    if constexpr (HAS_ZP) {
+        stage(16 * nz,
+              [&](int idx) {
+                  const int n = idx / nz;
+                  const int j = idx - n * nz;
+                  const int cc = min(n0 + n, N - 1);
+                  return Z[wofs_z + (int64_t)cc * zpb + z_lo + j];
+              },
+              [&](int idx, uint8_t v) {
+                  const int n = idx / nz;
+                  sZ[n * zpitch + (idx - n * nz)] = v;
+              });
     }
     // int8 path: the tile rows' activation scales over the same blocks, [block][16 * MT rows],
     // so a lane's four output rows are one 16-byte LDS read.
     float* const sA = reinterpret_cast<float*>(sZ + (HAS_ZP ? 16 * zpitch : 0));
     if constexpr (I8) {
-        for (int idx = threadIdx.x; idx < 16 * MT * nblk; idx += blockDim.x) {
-            const int b = idx / (16 * MT);
-            const int rr = idx - b * (16 * MT);
-            int r = r0 + rr;
-            r = r < row_hi ? r : row_hi - 1;
-            const int ar = row_index ? row_index[r] : r;
-            sA[idx] = a_scale[(int64_t)ar * bpc + b_lo + b];
-        }
+        stage(16 * MT * nblk,
+              [&](int idx) {
+                  const int b = idx / (16 * MT);
+                  const int rr = idx - b * (16 * MT);
+                  int r = r0 + rr;
+                  r = r < row_hi ? r : row_hi - 1;
+                  const int ar = row_index ? row_index[r] : r;
+                  return a_scale[(int64_t)ar * bpc + b_lo + b];
+              },
+              [&](int idx, float v) { sA[idx] = v; });
     }
     __syncthreads();
     const T* __restrict__ lS = sS + nl * spitch;

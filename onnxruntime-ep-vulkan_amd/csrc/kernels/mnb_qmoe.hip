@@ -6,10 +6,11 @@
 // The op's arithmetic is ONNX Runtime's (third-party, not under the reference); this file
 // implements the build's declared reading of it:
 //
-//   1. qmoe_route      one workgroup: per token softmax over the E router logits, the k largest
-//                      (ties to the lower expert id), optionally renormalised; then a stable
-//                      counting sort of the T*k (token, slot) assignments by expert: offsets[E+1],
-//                      the token of every grouped row, the grouped row of every assignment.
+//   1. qmoe_topk       one wavefront per token: softmax over the E router logits, the k largest
+//                      (ties to the lower expert id), optionally renormalised;
+//      qmoe_group      one workgroup: counting sort of the T*k (token, slot) assignments by
+//                      expert: offsets[E+1], the token of every grouped row, the grouped row of
+//                      every assignment.
 //   2. group_gemv      h = x W1_e^T for every grouped row (the MatMulNBits expert-grouped GEMV,
 //                      rows gathered through the sort), fp16 out.
 //   3. qmoe_swiglu     act = SwiGLU(h + b1_e): gate/linear interleaved or concatenated,
@@ -39,104 +40,169 @@ __device__ __forceinline__ float ld(const L* p, int64_t i) {
 
 }  // namespace
 
+// Routing, part 1: one wavefront per token (four per workgroup), the logits of experts
+// e = lane + 64 j in registers: wave-wide max and sum for the softmax, then k rounds of a
+// wave-wide arg-max (the lower id wins a tie) over the experts not yet chosen.
 template <typename L>
-__global__ void __launch_bounds__(kRouteThreads)
-qmoe_route(const L* __restrict__ logits, int T, int E, int k, int normalize,
-           int32_t* __restrict__ expert_of, float* __restrict__ weight_of,
-           int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
-           int32_t* __restrict__ pos_of, int32_t* __restrict__ expert_of_row) {
-    extern __shared__ int16_t sx[];                      // [T * k] expert of each assignment
-    __shared__ int32_t cnt[kRouteThreads];
-    const int tid = threadIdx.x;
-    for (int t = tid; t < T; t += kRouteThreads) {
-        const L* lg = logits + (int64_t)t * E;
-        float mx = -INFINITY;
-        for (int e = 0; e < E; ++e) mx = fmaxf(mx, ld(lg, e));
-        float sum = 0.f;
-        for (int e = 0; e < E; ++e) sum += expf(ld(lg, e) - mx);
-        int sel[8];
-        float p[8];
-        float psum = 0.f;
-        for (int s = 0; s < k; ++s) {
-            // the largest logit not yet chosen; strict '>' keeps the lower id on ties
-            int best = -1;
-            float bv = -INFINITY;
-            for (int e = 0; e < E; ++e) {
-                bool taken = false;
-                for (int j = 0; j < s; ++j) taken |= sel[j] == e;
-                const float v = ld(lg, e);
-                if (!taken && (best < 0 || v > bv)) {
-                    best = e;
-                    bv = v;
-                }
+__global__ void __launch_bounds__(256)
+qmoe_topk(const L* __restrict__ logits, int T, int E, int k, int normalize,
+          int32_t* __restrict__ expert_of, float* __restrict__ weight_of) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;                                  // whole wavefront
+    const int nj = (E + 63) / 64;                        // <= 16
+    const L* lg = logits + (int64_t)t * E;
+    float v[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = (j < nj && e < E) ? ld(lg, e) : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int e = lane + 64 * j;
+        if (j < nj && e < E) sum += expf(v[j] - mx);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    uint32_t taken = 0;                                  // bit j: expert lane + 64 j chosen
+    int my_e = 0;                                        // lane s keeps slot s
+    float my_p = 0.f, psum = 0.f;
+    for (int s = 0; s < k; ++s) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int e = lane + 64 * j;
+            if (j < nj && e < E && !((taken >> j) & 1u) && (bi == 0x7fffffff || v[j] > bv)) {
+                bv = v[j];
+                bi = e;
             }
-            sel[s] = best;
-            p[s] = expf(bv - mx) / sum;
-            psum += p[s];
         }
-        for (int s = 0; s < k; ++s) {
-            const int a = t * k + s;
-            expert_of[a] = sel[s];
-            weight_of[a] = normalize ? p[s] / psum : p[s];
-            sx[a] = (int16_t)sel[s];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        const float p = expf(bv - mx) / sum;
+        psum += p;
+        if (lane == s) {
+            my_e = bi;
+            my_p = p;
         }
     }
-    __syncthreads();
-    const int R = T * k;
-    for (int e = tid; e < E; e += kRouteThreads) {
-        int c = 0;
-        for (int a = 0; a < R; ++a) c += sx[a] == e;
-        cnt[e] = c;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int run = 0;
-        for (int e = 0; e < E; ++e) {
-            const int c = cnt[e];
-            offsets[e] = run;
-            cnt[e] = run;
-            run += c;
-        }
-        offsets[E] = run;
-    }
-    __syncthreads();
-    // assignments of expert e in ascending (token, slot) order
-    for (int e = tid; e < E; e += kRouteThreads) {
-        int pos = cnt[e];
-        for (int a = 0; a < R; ++a) {
-            if (sx[a] != e) continue;
-            row_token[pos] = a / k;
-            pos_of[a] = pos;
-            expert_of_row[pos] = e;
-            ++pos;
-        }
+    if (lane < k) {
+        expert_of[t * k + lane] = my_e;
+        weight_of[t * k + lane] = normalize ? my_p / psum : my_p;
     }
 }
 
+// Routing, part 2 (one workgroup): counting sort of the T*k assignments by expert.  An LDS
+// atomic gives each assignment its slot within its expert (every grouped row is computed on its
+// own, so results do not depend on that order); a scan of the counts gives the offsets.
+__global__ void __launch_bounds__(kRouteThreads)
+qmoe_group(const int32_t* __restrict__ expert_of, int R, int E, int k,
+           int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
+           int32_t* __restrict__ pos_of, int32_t* __restrict__ expert_of_row) {
+    __shared__ int32_t cnt[kRouteThreads];
+    __shared__ int32_t tmp[kRouteThreads];
+    const int tid = threadIdx.x;
+    constexpr int kPer = 16;                             // R <= 16 * 1024
+    for (int e = tid; e < E; e += kRouteThreads) cnt[e] = 0;
+    __syncthreads();
+    int ex[kPer], sl[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int a = tid + kRouteThreads * j;
+        ex[j] = a < R ? expert_of[a] : -1;
+        sl[j] = ex[j] >= 0 ? atomicAdd(&cnt[ex[j]], 1) : 0;
+    }
+    __syncthreads();
+    // inclusive scan of cnt[0..E) (Hillis-Steele), kept beside the counts
+    const int c = tid < E ? cnt[tid] : 0;
+    int run = c;
+    for (int d = 1; d < E; d <<= 1) {
+        if (tid < E) tmp[tid] = run;
+        __syncthreads();
+        if (tid < E && tid >= d) run += tmp[tid - d];
+        __syncthreads();
+    }
+    if (tid < E) {
+        cnt[tid] = run - c;                              // exclusive: first row of expert tid
+        offsets[tid] = run - c;
+        if (tid == E - 1) offsets[E] = run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int a = tid + kRouteThreads * j;
+        if (a >= R) break;
+        const int pos = cnt[ex[j]] + sl[j];
+        row_token[pos] = a / k;
+        pos_of[a] = pos;
+        expert_of_row[pos] = ex[j];
+    }
+}
+
+// Thread: four consecutive outputs of one grouped row (inter % 4 == 0).
 __global__ void __launch_bounds__(256)
 qmoe_swiglu(const f16* __restrict__ h, const f16* __restrict__ b1,
             const int32_t* __restrict__ expert_of_row, f16* __restrict__ act, int64_t rows,
             int64_t inter, int fusion, float alpha, float beta, float limit, int has_limit) {
-    const int64_t total = rows * inter;
+    typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+    const int64_t quads = inter / 4;
+    const int64_t total = rows * quads;
     for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * 256) {
-        const int64_t r = idx / inter;
-        const int64_t i = idx - r * inter;
-        const int64_t gi = fusion == 1 ? 2 * i : i;
-        const int64_t li = fusion == 1 ? 2 * i + 1 : inter + i;
+        const int64_t r = idx / quads;
+        const int64_t i = (idx - r * quads) * 4;
         const f16* hr = h + r * 2 * inter;
-        float g = (float)hr[gi];
-        float l = (float)hr[li];
-        if (b1) {
-            const f16* br = b1 + (int64_t)expert_of_row[r] * 2 * inter;
-            g += (float)br[gi];
-            l += (float)br[li];
+        const f16* br = b1 ? b1 + (int64_t)expert_of_row[r] * 2 * inter : nullptr;
+        float g[4], l[4];
+        if (fusion == 1) {                               // (gate, linear) pairs at 2i, 2i + 1
+            const f16x8 v = *reinterpret_cast<const f16x8*>(hr + 2 * i);
+            f16x8 b = {};
+            if (br) b = *reinterpret_cast<const f16x8*>(br + 2 * i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                g[j] = (float)v[2 * j] + (float)b[2 * j];
+                l[j] = (float)v[2 * j + 1] + (float)b[2 * j + 1];
+            }
+        } else {                                         // gates at i, linears at inter + i
+            const f16x4_t vg = *reinterpret_cast<const f16x4_t*>(hr + i);
+            const f16x4_t vl = *reinterpret_cast<const f16x4_t*>(hr + inter + i);
+            f16x4_t bg = {}, bl = {};
+            if (br) {
+                bg = *reinterpret_cast<const f16x4_t*>(br + i);
+                bl = *reinterpret_cast<const f16x4_t*>(br + inter + i);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                g[j] = (float)vg[j] + (float)bg[j];
+                l[j] = (float)vl[j] + (float)bl[j];
+            }
         }
-        if (has_limit) {
-            g = fminf(g, limit);
-            l = fminf(fmaxf(l, -limit), limit);
+        f16x4_t out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float gj = g[j], lj = l[j];
+            if (has_limit) {
+                gj = fminf(gj, limit);
+                lj = fminf(fmaxf(lj, -limit), limit);
+            }
+            out[j] = (f16)(gj / (1.f + expf(-alpha * gj)) * (lj + beta));
         }
-        act[idx] = (f16)(g / (1.f + expf(-alpha * g)) * (l + beta));
+        *reinterpret_cast<f16x4_t*>(act + r * inter + i) = out;
     }
 }
 
@@ -229,17 +295,17 @@ hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, con
     f16* act = reinterpret_cast<f16*>(ws + l.act);
     f16* o = reinterpret_cast<f16*>(ws + l.o);
     const int64_t R = q.rows * q.k;
-    const size_t route_lds = (size_t)R * sizeof(int16_t);
+    const unsigned tk_grid = (unsigned)((q.rows + 3) / 4);
     if (q.router_f32)
-        hipLaunchKernelGGL(qmoe_route<float>, dim3(1), dim3(kRouteThreads), route_lds, st,
+        hipLaunchKernelGGL(qmoe_topk<float>, dim3(tk_grid), dim3(256), 0, st,
                            static_cast<const float*>(logits), (int)q.rows, (int)q.experts, q.k,
-                           q.normalize, expert_of, weight_of, offsets, row_token, pos_of,
-                           expert_of_row);
+                           q.normalize, expert_of, weight_of);
     else
-        hipLaunchKernelGGL(qmoe_route<f16>, dim3(1), dim3(kRouteThreads), route_lds, st,
+        hipLaunchKernelGGL(qmoe_topk<f16>, dim3(tk_grid), dim3(256), 0, st,
                            static_cast<const f16*>(logits), (int)q.rows, (int)q.experts, q.k,
-                           q.normalize, expert_of, weight_of, offsets, row_token, pos_of,
-                           expert_of_row);
+                           q.normalize, expert_of, weight_of);
+    hipLaunchKernelGGL(qmoe_group, dim3(1), dim3(kRouteThreads), 0, st, expert_of, (int)R,
+                       (int)q.experts, q.k, offsets, row_token, pos_of, expert_of_row);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // expected rows per expert (twice the mean, at least one) sets the GEMV tile height
@@ -247,7 +313,7 @@ hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, con
     e = launch_group_gemv_f16_bounded(x, row_token, offsets, q.experts, q.rows, hint, fc1, fc1_s,
                                       nullptr, h, R, 2 * q.inter, q.hidden, 4, q.block_size, st);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(qmoe_swiglu, dim3(grid_for(R * q.inter)), dim3(256), 0, st, h,
+    hipLaunchKernelGGL(qmoe_swiglu, dim3(grid_for(R * q.inter / 4)), dim3(256), 0, st, h,
                        static_cast<const f16*>(fc1_b), expert_of_row, act, R, q.inter, q.fusion,
                        q.alpha, q.beta, q.limit, q.has_limit);
     e = hipGetLastError();

@@ -419,8 +419,9 @@ int mnb_qmoe(const mnb_qmoe_problem* p, const void* x, const void* router_logits
                     need);
     if (!aligned(workspace, 256)) return fail(MNB_ERR_INVALID, "workspace must be 256-byte aligned");
     if (!aligned(x, 16) || !aligned(fc1_weights, 16) || !aligned(fc2_weights, 16) ||
-        !aligned(y, 16) || (fc2_bias && !aligned(fc2_bias, 16)))
-        return fail(MNB_ERR_INVALID, "x, y, the weights and fc2_bias must be 16-byte aligned");
+        !aligned(y, 16) || (fc1_bias && !aligned(fc1_bias, 16)) ||
+        (fc2_bias && !aligned(fc2_bias, 16)))
+        return fail(MNB_ERR_INVALID, "x, y, the weights and the biases must be 16-byte aligned");
     hipError_t e = mnb::launch_qmoe(q, x, router_logits, fc1_weights, fc1_scales, fc1_bias,
                                     fc2_weights, fc2_scales, fc2_bias, y, workspace,
                                     static_cast<hipStream_t>(stream));
