@@ -177,6 +177,30 @@ int mnb_qmoe(const mnb_qmoe_problem* p, const void* x, const void* router_logits
              const uint8_t* fc2_weights, const void* fc2_scales, const void* fc2_bias, void* y,
              void* workspace, size_t workspace_bytes, void* stream);
 
+/* RMSNorm over the last axis, with the residual add fused:
+ * com.microsoft::SkipSimplifiedLayerNormalization (has_skip) and SimplifiedLayerNormalization.
+ * Replaces the reference's skip_simplified_layer_norm / simplified_layer_norm kernels
+ * (rust/src/ops/norm.rs:68-140, bound in rust/src/ops/common/templates.rs:426-660):
+ *   r = x + skip + bias (fp32 from the stored values; skip and bias optional);
+ *   y = r / sqrt(mean(r^2) + epsilon) * gamma, stored in the tensor type;
+ *   sum_out (optional, the node's output slot 3) = r stored in the tensor type.
+ * x, skip, y, sum_out [rows][hidden]; gamma, bias [hidden]; fp16 or fp32, 16-byte aligned;
+ * hidden a multiple of 8 (fp16) or 4 (fp32), at most 8192 (fp16) or 4096 (fp32).
+ * Stream-ordered. */
+typedef struct mnb_rmsnorm_problem {
+    int64_t rows;
+    int64_t hidden;
+    float epsilon;
+    int32_t has_skip;
+    int32_t has_bias;
+    int32_t want_sum;
+    int32_t dtype;              /* MNB_DTYPE_F16 or MNB_DTYPE_F32 */
+} mnb_rmsnorm_problem;
+
+int mnb_rmsnorm_check(const mnb_rmsnorm_problem* p);
+int mnb_skip_rmsnorm(const mnb_rmsnorm_problem* p, const void* x, const void* skip,
+                     const void* gamma, const void* bias, void* y, void* sum_out, void* stream);
+
 /* ---- session layer: one device, one stream, weights uploaded once ---------------------- */
 
 typedef struct mnb_session mnb_session;
@@ -240,6 +264,19 @@ int mnb_qmoe_weights_release(mnb_qmoe_weights* w);
 int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows, const void* x,
                          int x_on_device, const void* router_logits, int logits_on_device,
                          void* y, int y_on_device);
+
+/* RMSNorm node constants (gamma, optional bias) uploaded once, and one Compute with x, skip,
+ * y and the residual sum each in host memory or the session device's memory (the last two
+ * may be NULL when the problem has no skip / no sum output).  Returns after the stream. */
+typedef struct mnb_rmsnorm_weights mnb_rmsnorm_weights;
+int mnb_rmsnorm_weights_upload(mnb_session* s, const mnb_rmsnorm_problem* node,
+                               const void* gamma, size_t gamma_bytes, const void* bias,
+                               size_t bias_bytes, mnb_rmsnorm_weights** out);
+int mnb_rmsnorm_weights_release(mnb_rmsnorm_weights* w);
+int mnb_session_run_rmsnorm(mnb_session* s, const mnb_rmsnorm_weights* w, int64_t rows,
+                            const void* x, int x_on_device, const void* skip,
+                            int skip_on_device, void* y, int y_on_device, void* sum_out,
+                            int sum_on_device);
 
 /* Number of MatMulNBits-family kernel launches made by this process (proves the GPU ran). */
 uint64_t mnb_launch_count(void);

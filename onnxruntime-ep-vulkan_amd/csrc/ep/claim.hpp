@@ -258,4 +258,95 @@ inline ClaimDecision claim_qmoe(const QmoeFacts& f, QmoeShape* shape = nullptr) 
     return ClaimDecision{true, {}};
 }
 
+// ---- RMSNorm: SkipSimplifiedLayerNormalization / SimplifiedLayerNormalization ----------------
+//
+// Mirrors the reference rows (rust/src/ops/norm.rs:53-140): the skip form (com.microsoft, 3..5
+// inputs, up to 4 outputs) and the plain form (com.microsoft and the default domain, in which
+// the ORT GenAI builder emits it, norm.rs:118-133; 2 inputs, 1 output, the last axis).  Like the
+// reference, output slots that the kernel does not write are declined: the plain form's
+// inv_std_var (norm.rs:97-108) and the skip form's mean and inv_std_var (slots 1 and 2); the
+// skip form's residual sum (slot 3) is written.  Narrower than the reference where this EP
+// needs constants: gamma and the optional bias must be constant initializers of static length
+// H, uploaded at Compile.  Widened: the skip form's optional bias (input 3) is applied.
+
+struct NormFacts {
+    std::string op_type;
+    std::string domain;
+    std::vector<InputFacts> inputs;
+    std::vector<bool> outputs;                   // per declared slot: present
+    bool has_axis = false;
+    int64_t axis = -1;
+    bool has_stash_type = false;
+    int64_t stash_type = 1;
+    float epsilon = 1e-5f;                       // the reference's default (templates.rs:399)
+};
+
+inline bool is_skip_norm(const std::string& op, const std::string& domain) {
+    return op == "SkipSimplifiedLayerNormalization" && domain == "com.microsoft";
+}
+inline bool is_plain_norm(const std::string& op, const std::string& domain) {
+    return op == "SimplifiedLayerNormalization" &&
+           (domain == "com.microsoft" || domain.empty() || domain == "ai.onnx");
+}
+
+// The element budget of the HIP kernel: H a multiple of 8 (fp16) or 4 (fp32) elements, at
+// most 8192 (fp16) or 4096 (fp32).
+inline bool norm_hidden_ok(int64_t h, bool f16) {
+    const int64_t cn = f16 ? 8 : 4;
+    return h > 0 && h % cn == 0 && h / cn <= 1024;
+}
+
+inline ClaimDecision claim_norm(const NormFacts& f, int64_t* hidden = nullptr) {
+    const bool skip = is_skip_norm(f.op_type, f.domain);
+    if (!skip && !is_plain_norm(f.op_type, f.domain))
+        return decline("not a (Skip)SimplifiedLayerNormalization");
+    const size_t nin = f.inputs.size();
+    if (skip ? (nin < 3 || nin > 5) : nin != 2)
+        return decline(skip ? "arity outside 3..5 inputs" : "arity is not 2 inputs");
+    if (f.outputs.empty() || !f.outputs[0]) return decline("output 0 is absent");
+    if (skip) {
+        if (f.outputs.size() > 4) return decline("more than 4 outputs");
+        if ((f.outputs.size() > 1 && f.outputs[1]) || (f.outputs.size() > 2 && f.outputs[2]))
+            return decline("asks for mean or inv_std_var (outputs 1 and 2), which are not written");
+    } else if (f.outputs.size() > 1 && f.outputs[1]) {
+        return decline("asks for inv_std_var (output 1), which is not written");
+    }
+    if (nin > 4 && f.inputs[4].present) return decline("input 4 is not implemented");
+    const InputFacts& x = f.inputs[0];
+    if (!x.present || (x.elem_type != kElemFloat16 && x.elem_type != kElemFloat))
+        return decline("input is neither float16 nor float");
+    if (!x.has_shape || x.dims.empty() || x.dims.back() <= 0)
+        return decline("the normalised extent (last dim) must be static");
+    const int64_t H = x.dims.back();
+    if (f.has_axis) {
+        const int64_t rank = (int64_t)x.dims.size();
+        if (f.axis != -1 && f.axis != rank - 1) return decline("normalises over another axis than the last");
+    }
+    if (f.has_stash_type && f.stash_type != 1) return decline("stash_type other than float");
+    const bool f16 = x.elem_type == kElemFloat16;
+    if (!norm_hidden_ok(H, f16))
+        return decline("hidden size " + std::to_string(H) + " is outside the kernel's range");
+    const size_t gi = skip ? 2 : 1;
+    auto const_vec = [&](size_t i) {
+        const InputFacts& v = f.inputs[i];
+        return v.present && v.constant && v.elem_type == x.elem_type && v.has_shape &&
+               v.dims.size() == 1 && v.dims[0] == H;
+    };
+    if (!const_vec(gi)) return decline("gamma must be a constant [H] of the input's type");
+    if (skip) {
+        const InputFacts& k = f.inputs[1];
+        if (!k.present || k.elem_type != x.elem_type) return decline("skip must share the input's type");
+        if (k.has_shape) {
+            if (k.dims.size() != x.dims.size()) return decline("skip's rank differs from the input's");
+            for (size_t i = 0; i < k.dims.size(); ++i)
+                if (k.dims[i] >= 0 && x.dims[i] >= 0 && k.dims[i] != x.dims[i])
+                    return decline("skip's shape differs from the input's (broadcast skip)");
+        }
+        if (nin > 3 && f.inputs[3].present && !const_vec(3))
+            return decline("bias must be a constant [H] of the input's type");
+    }
+    if (hidden) *hidden = H;
+    return ClaimDecision{true, {}};
+}
+
 }  // namespace mi355x_ep

@@ -310,6 +310,19 @@ QmoeFacts qmoe_facts(const OrtApi* api, const OrtNode* node) {
     return f;
 }
 
+NormFacts norm_facts(const OrtApi* api, const OrtNode* node) {
+    NormFacts f;
+    f.op_type = node_string(api, node, api->Node_GetOperatorType);
+    f.domain = node_string(api, node, api->Node_GetDomain);
+    if (!is_skip_norm(f.op_type, f.domain) && !is_plain_norm(f.op_type, f.domain)) return f;
+    for (const OrtValueInfo* vi : node_inputs(api, node)) f.inputs.push_back(input_facts(api, vi));
+    for (const OrtValueInfo* vi : node_outputs(api, node)) f.outputs.push_back(vi != nullptr);
+    f.has_axis = int_attr(api, node, "axis", &f.axis);
+    f.has_stash_type = int_attr(api, node, "stash_type", &f.stash_type);
+    float_attr(api, node, "epsilon", &f.epsilon);
+    return f;
+}
+
 // Session option `key` (ORT prefixes EP options with "ep.<name>."; both spellings are read).
 bool session_option(const OrtApi* api, const OrtSessionOptions* so, const std::string& key,
                     std::string* value) {
@@ -363,10 +376,18 @@ struct NodeKernel {
     size_t fused_router = SIZE_MAX;
     int32_t router_elem = 0;
     mnb_qmoe_weights* qweights = nullptr;
+    // RMSNorm node (norm set): skip by fused-input index; y and the residual sum by fused-output
+    // index (SIZE_MAX when the node has no such output).
+    bool norm = false;
+    mnb_rmsnorm_problem nprob{};
+    size_t fused_skip = SIZE_MAX;
+    size_t fused_y = SIZE_MAX, fused_sum = SIZE_MAX;
+    mnb_rmsnorm_weights* nweights = nullptr;
 
     ~NodeKernel() {
         if (weights) mnb_weights_release(weights);
         if (qweights) mnb_qmoe_weights_release(qweights);
+        if (nweights) mnb_rmsnorm_weights_release(nweights);
     }
 };
 
@@ -525,12 +546,59 @@ void compute_qmoe(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     g_compute_count.fetch_add(1);
 }
 
+void compute_norm(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
+    const OrtApi* api = ep->api;
+    size_t nin = 0;
+    ORT_OK(api, KernelContext_GetInputCount(ctx, &nin));
+    if (k.fused_a >= nin || (k.nprob.has_skip && k.fused_skip >= nin))
+        fail(ORT_EP_FAIL, "fused norm node has %zu inputs", nin);
+    const OrtValue* x = nullptr;
+    const OrtValue* sk = nullptr;
+    ORT_OK(api, KernelContext_GetInput(ctx, k.fused_a, &x));
+    if (k.nprob.has_skip) ORT_OK(api, KernelContext_GetInput(ctx, k.fused_skip, &sk));
+    if (!x || (k.nprob.has_skip && !sk)) fail(ORT_INVALID_ARGUMENT, "the input or skip is missing");
+    const int32_t want = k.nprob.dtype == MNB_DTYPE_F16 ? kElemFloat16 : kElemFloat;
+    std::vector<int64_t> xd, kd;
+    if (tensor_elem_type(api, x, &xd) != want) fail(ORT_INVALID_ARGUMENT, "input element type changed");
+    if (xd.empty() || xd.back() != k.nprob.hidden)
+        fail(ORT_INVALID_ARGUMENT, "input's last dimension is not %lld", (long long)k.nprob.hidden);
+    int64_t rows = 1;
+    for (size_t i = 0; i + 1 < xd.size(); ++i) {
+        if (xd[i] < 0) fail(ORT_INVALID_ARGUMENT, "input has a negative extent");
+        rows *= xd[i];
+    }
+    if (sk && (tensor_elem_type(api, sk, &kd) != want || kd != xd))
+        fail(ORT_INVALID_ARGUMENT, "skip's type or shape differs from the input's");
+    OrtValue* y = nullptr;
+    OrtValue* sum = nullptr;
+    ORT_OK(api, KernelContext_GetOutput(ctx, k.fused_y, xd.data(), xd.size(), &y));
+    if (k.fused_sum != SIZE_MAX)
+        ORT_OK(api, KernelContext_GetOutput(ctx, k.fused_sum, xd.data(), xd.size(), &sum));
+    if (!y || (k.fused_sum != SIZE_MAX && !sum)) fail(ORT_EP_FAIL, "ORT returned no output tensor");
+    if (rows == 0) return;
+    void* yd = nullptr;
+    void* sd = nullptr;
+    ORT_OK(api, GetTensorMutableData(y, &yd));
+    if (sum) ORT_OK(api, GetTensorMutableData(sum, &sd));
+    std::lock_guard<std::mutex> lk(k.mu);
+    mnb_ok(mnb_session_run_rmsnorm(ep->session, k.nweights, rows, tensor_data(api, x),
+                                   on_our_device(ep, x) ? 1 : 0, sk ? tensor_data(api, sk) : nullptr,
+                                   on_our_device(ep, sk) ? 1 : 0, yd, on_our_device(ep, y) ? 1 : 0,
+                                   sd, on_our_device(ep, sum) ? 1 : 0),
+           "RMSNorm kernel");
+    g_compute_count.fetch_add(1);
+}
+
 void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     const OrtApi* api = ep->api;
     if (env_flag("MI355X_EP_FORCE_COMPUTE_FAILURE"))
         fail(ORT_EP_FAIL, "forced Compute failure (MI355X_EP_FORCE_COMPUTE_FAILURE is set)");
     if (k.qmoe) {
         compute_qmoe(ep, k, ctx);
+        return;
+    }
+    if (k.norm) {
+        compute_norm(ep, k, ctx);
         return;
     }
     size_t nin = 0;
@@ -664,6 +732,21 @@ void get_capability(Ep* ep, const OrtGraph* graph, OrtEpGraphSupportInfo* suppor
         if (!node) continue;
         const std::string op = node_string(api, node, api->Node_GetOperatorType);
         const std::string dom = node_string(api, node, api->Node_GetDomain);
+        if (is_skip_norm(op, dom) || is_plain_norm(op, dom)) {
+            const std::string name = node_string(api, node, api->Node_GetName);
+            const ClaimDecision d = claim_norm(norm_facts(api, node));
+            if (!d.claim) {
+                claim_log("decline %s: %s", name.c_str(), d.reason.c_str());
+                continue;
+            }
+            OrtNodeFusionOptions opts{};
+            opts.ort_version_supported = ep->factory->version;
+            opts.drop_constant_initializers = !ep->keep_constant_initializers;
+            ort_check(api, ep->ep_api->EpGraphSupportInfo_AddNodesToFuse(support, &node, 1, &opts),
+                      "EpGraphSupportInfo_AddNodesToFuse");
+            claim_log("claim %s (%s)", name.c_str(), op.c_str());
+            continue;
+        }
         if (is_qmoe(op, dom)) {
             const std::string name = node_string(api, node, api->Node_GetName);
             const ClaimDecision d = claim_qmoe(qmoe_facts(api, node));
@@ -787,6 +870,64 @@ std::unique_ptr<NodeKernel> compile_qmoe(Ep* ep, const OrtNode* node, const OrtN
     return k;
 }
 
+// Fused-node output index of each body-node output, matched by value name (SIZE_MAX if absent).
+std::vector<size_t> fused_output_map(const OrtApi* api, const OrtNode* node, const OrtNode* fused) {
+    const std::vector<const OrtValueInfo*> body = node_outputs(api, node);
+    const std::vector<const OrtValueInfo*> fo = node_outputs(api, fused);
+    std::vector<size_t> out(body.size(), SIZE_MAX);
+    for (size_t i = 0; i < body.size(); ++i) {
+        if (!body[i]) continue;
+        const std::string nm = value_name(api, body[i]);
+        for (size_t j = 0; j < fo.size(); ++j)
+            if (fo[j] && value_name(api, fo[j]) == nm) {
+                out[i] = j;
+                break;
+            }
+    }
+    return out;
+}
+
+std::unique_ptr<NodeKernel> compile_norm(Ep* ep, const OrtNode* node, const OrtNode* fused) {
+    const OrtApi* api = ep->api;
+    const NormFacts f = norm_facts(api, node);
+    int64_t hidden = 0;
+    const ClaimDecision d = claim_norm(f, &hidden);
+    if (!d.claim) fail(ORT_EP_FAIL, "compiled node fails the norm claim predicate: %s", d.reason.c_str());
+    const bool skip = is_skip_norm(f.op_type, f.domain);
+    auto k = std::make_unique<NodeKernel>();
+    k->norm = true;
+    k->name = node_string(api, node, api->Node_GetName);
+    mnb_rmsnorm_problem& p = k->nprob;
+    p.hidden = hidden;
+    p.epsilon = f.epsilon;
+    p.has_skip = skip ? 1 : 0;
+    p.has_bias = skip && f.inputs.size() > 3 && f.inputs[3].present ? 1 : 0;
+    p.dtype = f.inputs[0].elem_type == kElemFloat16 ? MNB_DTYPE_F16 : MNB_DTYPE_F32;
+    mnb_ok(mnb_rmsnorm_check(&p), "norm attributes");
+    const std::vector<size_t> in_map = fused_input_map(api, node, fused);
+    const std::vector<size_t> out_map = fused_output_map(api, node, fused);
+    k->fused_a = in_map[0];
+    if (skip) k->fused_skip = in_map[1];
+    if (k->fused_a == SIZE_MAX || (skip && k->fused_skip == SIZE_MAX))
+        fail(ORT_EP_FAIL, "the input or skip tensor is not an input of the fused node");
+    k->fused_y = out_map[0];
+    if (k->fused_y == SIZE_MAX) fail(ORT_EP_FAIL, "output 0 is not an output of the fused node");
+    if (skip && out_map.size() > 3) k->fused_sum = out_map[3];
+    const std::vector<const OrtValueInfo*> body_in = node_inputs(api, node);
+    const size_t gi = skip ? 2 : 1;
+    const OrtValue* gv = nullptr;
+    const OrtValue* bv = nullptr;
+    ORT_OK(api, ValueInfo_GetInitializerValue(body_in[gi], &gv));
+    if (p.has_bias) ORT_OK(api, ValueInfo_GetInitializerValue(body_in[3], &bv));
+    if (!gv || (p.has_bias && !bv)) fail(ORT_EP_FAIL, "gamma or bias has no initializer value");
+    mnb_ok(mnb_rmsnorm_weights_upload(ep_session(ep), &p, tensor_data(api, gv),
+                                      tensor_bytes(api, gv), bv ? tensor_data(api, bv) : nullptr,
+                                      bv ? tensor_bytes(api, bv) : 0, &k->nweights),
+           "uploading norm constants at Compile");
+    k->resident = true;
+    return k;
+}
+
 std::unique_ptr<NodeKernel> compile_one(Ep* ep, const OrtGraph* graph, const OrtNode* fused) {
     const OrtApi* api = ep->api;
     size_t n = 0;
@@ -794,9 +935,10 @@ std::unique_ptr<NodeKernel> compile_one(Ep* ep, const OrtGraph* graph, const Ort
     if (n != 1) fail(ORT_EP_FAIL, "a fused island holds %zu nodes, expected 1", n);
     const OrtNode* node = nullptr;
     ORT_OK(api, Graph_GetNodes(graph, &node, 1));
-    if (is_qmoe(node_string(api, node, api->Node_GetOperatorType),
-                node_string(api, node, api->Node_GetDomain)))
-        return compile_qmoe(ep, node, fused);
+    const std::string op = node_string(api, node, api->Node_GetOperatorType);
+    const std::string dom = node_string(api, node, api->Node_GetDomain);
+    if (is_qmoe(op, dom)) return compile_qmoe(ep, node, fused);
+    if (is_skip_norm(op, dom) || is_plain_norm(op, dom)) return compile_norm(ep, node, fused);
     const NodeFacts f = node_facts(api, node);
     const ClaimDecision d = claim_matmul_nbits(f, int8_path_available(f));
     if (!d.claim) fail(ORT_EP_FAIL, "compiled node fails the claim predicate: %s", d.reason.c_str());

@@ -119,6 +119,12 @@ hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, con
                        const void* fc1_s, const void* fc1_b, const uint8_t* fc2, const void* fc2_s,
                        const void* fc2_b, void* y, void* workspace, hipStream_t stream);
 
+// RMSNorm with optional fused residual add (mnb_rmsnorm.hip).
+bool rmsnorm_supported(int64_t hidden, bool f16);
+hipError_t launch_skip_rmsnorm(const void* x, const void* skip, const void* gamma,
+                               const void* bias, void* y, void* sum_out, int64_t rows,
+                               int64_t hidden, float eps, bool f16, hipStream_t stream);
+
 // Roofline calibration (mnb_calibrate.hip): workgroups x 4 wavefronts x iters x 16 MFMAs.
 hipError_t launch_mfma_calibrate(const void* operands, float* out, int workgroups, int iters,
                                  hipStream_t stream);

@@ -430,6 +430,45 @@ int mnb_qmoe(const mnb_qmoe_problem* p, const void* x, const void* router_logits
     return MNB_OK;
 }
 
+// ---- RMSNorm --------------------------------------------------------------------------------
+
+int mnb_rmsnorm_check(const mnb_rmsnorm_problem* p) {
+    if (!p) return fail(MNB_ERR_INVALID, "problem is NULL");
+    if (p->rows < 0) return fail(MNB_ERR_INVALID, "rows = %lld is negative", (long long)p->rows);
+    if (p->dtype != MNB_DTYPE_F16 && p->dtype != MNB_DTYPE_F32)
+        return fail(MNB_ERR_INVALID, "dtype %d", p->dtype);
+    if (!mnb::rmsnorm_supported(p->hidden, p->dtype == MNB_DTYPE_F16))
+        return fail(MNB_ERR_UNSUPPORTED, "hidden = %lld: a positive multiple of %d up to %d",
+                    (long long)p->hidden, p->dtype == MNB_DTYPE_F16 ? 8 : 4,
+                    p->dtype == MNB_DTYPE_F16 ? 8192 : 4096);
+    if (!std::isfinite(p->epsilon) || p->epsilon < 0.f)
+        return fail(MNB_ERR_INVALID, "epsilon must be finite and non-negative");
+    if (p->has_bias && !p->has_skip)
+        return fail(MNB_ERR_INVALID, "a bias comes with the skip input");
+    return MNB_OK;
+}
+
+int mnb_skip_rmsnorm(const mnb_rmsnorm_problem* p, const void* x, const void* skip,
+                     const void* gamma, const void* bias, void* y, void* sum_out, void* stream) {
+    int rc = mnb_rmsnorm_check(p);
+    if (rc) return rc;
+    if (p->rows == 0) return MNB_OK;
+    if (!x || !gamma || !y || (p->has_skip && !skip) || (p->has_bias && !bias) ||
+        (p->want_sum && !sum_out))
+        return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    for (const void* q : {x, skip, gamma, bias, static_cast<const void*>(y),
+                          static_cast<const void*>(sum_out)})
+        if (q && !aligned(q, 16)) return fail(MNB_ERR_INVALID, "tensors must be 16-byte aligned");
+    hipError_t e = mnb::launch_skip_rmsnorm(x, p->has_skip ? skip : nullptr, gamma,
+                                            p->has_bias ? bias : nullptr, y,
+                                            p->want_sum ? sum_out : nullptr, p->rows, p->hidden,
+                                            p->epsilon, p->dtype == MNB_DTYPE_F16,
+                                            static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "RMSNorm launch");
+    g_launches.fetch_add(1);
+    return MNB_OK;
+}
+
 // ---- session layer ------------------------------------------------------------------------
 
 struct mnb_session {
@@ -830,6 +869,108 @@ int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows
         e = hipMemcpyAsync(y, s->y_dev, x_bytes, hipMemcpyDeviceToHost, s->stream);
         if (e != hipSuccess) return hip_fail(e, "QMoE output download");
     }
+    e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+struct mnb_rmsnorm_weights {
+    mnb_session* s = nullptr;
+    mnb_rmsnorm_problem node{};
+    void* gamma = nullptr;
+    void* bias = nullptr;
+};
+
+int mnb_rmsnorm_weights_release(mnb_rmsnorm_weights* w) {
+    if (!w) return MNB_OK;
+    (void)hipSetDevice(w->s->device);
+    (void)hipStreamSynchronize(w->s->stream);
+    if (w->gamma) (void)hipFree(w->gamma);
+    if (w->bias) (void)hipFree(w->bias);
+    delete w;
+    return MNB_OK;
+}
+
+int mnb_rmsnorm_weights_upload(mnb_session* s, const mnb_rmsnorm_problem* node,
+                               const void* gamma, size_t gamma_bytes, const void* bias,
+                               size_t bias_bytes, mnb_rmsnorm_weights** out) {
+    if (!s || !node || !out) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    *out = nullptr;
+    mnb_rmsnorm_problem p = *node;
+    p.rows = 0;
+    int rc = mnb_rmsnorm_check(&p);
+    if (rc) return rc;
+    const size_t want = (size_t)p.hidden * (size_t)elem_bytes(p.dtype);
+    if (!gamma || gamma_bytes != want)
+        return fail(MNB_ERR_INVALID, "gamma holds %zu bytes, the node needs %zu", gamma_bytes, want);
+    if (p.has_bias && (!bias || bias_bytes != want))
+        return fail(MNB_ERR_INVALID, "bias holds %zu bytes, the node needs %zu", bias_bytes, want);
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    mnb_rmsnorm_weights* w = new (std::nothrow) mnb_rmsnorm_weights();
+    if (!w) return fail(MNB_ERR_NOMEM, "weights allocation failed");
+    w->s = s;
+    w->node = p;
+    hipError_t e = hipMalloc(&w->gamma, want);
+    if (e == hipSuccess) e = hipMemcpyAsync(w->gamma, gamma, want, hipMemcpyHostToDevice, s->stream);
+    if (e == hipSuccess && p.has_bias) {
+        e = hipMalloc(&w->bias, want);
+        if (e == hipSuccess) e = hipMemcpyAsync(w->bias, bias, want, hipMemcpyHostToDevice, s->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) {
+        if (w->gamma) (void)hipFree(w->gamma);
+        if (w->bias) (void)hipFree(w->bias);
+        delete w;
+        return hip_fail(e, "RMSNorm constant upload");
+    }
+    *out = w;
+    return MNB_OK;
+}
+
+int mnb_session_run_rmsnorm(mnb_session* s, const mnb_rmsnorm_weights* w, int64_t rows,
+                            const void* x, int x_on_device, const void* skip,
+                            int skip_on_device, void* y, int y_on_device, void* sum_out,
+                            int sum_on_device) {
+    if (!s || !w) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    mnb_rmsnorm_problem p = w->node;
+    p.rows = rows;
+    p.want_sum = sum_out != nullptr;
+    int rc = mnb_rmsnorm_check(&p);
+    if (rc) return rc;
+    if (rows == 0) return MNB_OK;
+    if (!x || !y || (p.has_skip && !skip))
+        return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    const size_t bytes = (size_t)rows * (size_t)p.hidden * (size_t)elem_bytes(p.dtype);
+    const size_t slot = (bytes + 255) & ~(size_t)255;
+    // inputs staged one after the other in the A buffer, outputs in the Y buffer
+    rc = grow(&s->a_dev, &s->a_cap, 2 * slot);
+    if (rc) return rc;
+    rc = grow(&s->y_dev, &s->y_cap, 2 * slot);
+    if (rc) return rc;
+    uint8_t* in = static_cast<uint8_t*>(s->a_dev);
+    uint8_t* outb = static_cast<uint8_t*>(s->y_dev);
+    const void* xd = x;
+    const void* kd = p.has_skip ? skip : nullptr;
+    void* yd = y_on_device ? y : outb;
+    void* qd = sum_out ? (sum_on_device ? sum_out : outb + slot) : nullptr;
+    hipError_t e = hipSuccess;
+    if (!x_on_device) {
+        e = hipMemcpyAsync(in, x, bytes, hipMemcpyHostToDevice, s->stream);
+        xd = in;
+    }
+    if (e == hipSuccess && p.has_skip && !skip_on_device) {
+        e = hipMemcpyAsync(in + slot, skip, bytes, hipMemcpyHostToDevice, s->stream);
+        kd = in + slot;
+    }
+    if (e != hipSuccess) return hip_fail(e, "RMSNorm input upload");
+    rc = mnb_skip_rmsnorm(&p, xd, kd, w->gamma, w->bias, yd, qd, s->stream);
+    if (rc) return rc;
+    if (!y_on_device) e = hipMemcpyAsync(y, yd, bytes, hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess && sum_out && !sum_on_device)
+        e = hipMemcpyAsync(sum_out, qd, bytes, hipMemcpyDeviceToHost, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "RMSNorm output download");
     e = hipStreamSynchronize(s->stream);
     return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
 }

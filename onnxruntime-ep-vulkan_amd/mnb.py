@@ -73,6 +73,14 @@ class QmoeProblem(C.Structure):
     ]
 
 
+class RmsNormProblem(C.Structure):
+    _fields_ = [
+        ("rows", C.c_int64), ("hidden", C.c_int64), ("epsilon", C.c_float),
+        ("has_skip", C.c_int32), ("has_bias", C.c_int32), ("want_sum", C.c_int32),
+        ("dtype", C.c_int32),
+    ]
+
+
 class MnbError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"mnb error {code}: {msg}")
@@ -127,6 +135,13 @@ def load() -> C.CDLL:
                                               vp, sz, vp, sz, vp, sz, vp, sz, C.POINTER(vp)]),
         "mnb_qmoe_weights_release": (C.c_int, [vp]),
         "mnb_session_run_qmoe": (C.c_int, [vp, vp, i64, vp, C.c_int, vp, C.c_int, vp, C.c_int]),
+        "mnb_rmsnorm_check": (C.c_int, [C.POINTER(RmsNormProblem)]),
+        "mnb_skip_rmsnorm": (C.c_int, [C.POINTER(RmsNormProblem), vp, vp, vp, vp, vp, vp, vp]),
+        "mnb_rmsnorm_weights_upload": (C.c_int, [vp, C.POINTER(RmsNormProblem), vp, sz, vp, sz,
+                                                 C.POINTER(vp)]),
+        "mnb_rmsnorm_weights_release": (C.c_int, [vp]),
+        "mnb_session_run_rmsnorm": (C.c_int, [vp, vp, i64, vp, C.c_int, vp, C.c_int, vp, C.c_int,
+                                              vp, C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -229,6 +244,24 @@ def qmoe(x, logits, fc1, fc1_scales, fc2, fc2_scales, *, k: int, inter: int, blo
                           _ptr(fc1_bias), _ptr(fc2), _ptr(fc2_scales), _ptr(fc2_bias), _ptr(out),
                           _ptr(workspace), int(workspace.numel()), _stream(stream)))
     return out
+
+
+def skip_rmsnorm(x, gamma, *, skip=None, bias=None, epsilon: float = 1e-5, want_sum=False,
+                 out=None, sum_out=None, stream=None):
+    """(Skip)SimplifiedLayerNormalization on CUDA tensors over the last axis; returns
+    ``(y, residual_sum or None)``."""
+    import torch
+    hidden = int(x.shape[-1])
+    rows = x.numel() // hidden if hidden else 0
+    p = RmsNormProblem(rows, hidden, float(epsilon), int(skip is not None), int(bias is not None),
+                       int(bool(want_sum)), DTYPE_F16 if x.dtype == torch.float16 else DTYPE_F32)
+    if out is None:
+        out = torch.empty_like(x)
+    if want_sum and sum_out is None:
+        sum_out = torch.empty_like(x)
+    check(load().mnb_skip_rmsnorm(C.byref(p), _ptr(x), _ptr(skip), _ptr(gamma), _ptr(bias),
+                                  _ptr(out), _ptr(sum_out) if want_sum else None, _stream(stream)))
+    return out, (sum_out if want_sum else None)
 
 
 def launch_count() -> int:

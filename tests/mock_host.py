@@ -268,3 +268,34 @@ def add_qmoe(h: Host, name: str, inp: dict, *, k: int, x_shape, router_elem=FLOA
     attrs = {a: v for a, v in attrs.items() if v is not None}
     h.node("QMoE", "com.microsoft", name, ins, [y_name], attrs)
     return x_name, r_name, y_name
+
+
+def add_norm(h: Host, name: str, inp: dict, x_shape, *, skip=True, bias=False, with_sum=True,
+             epsilon=1e-5, domain="com.microsoft", elem=FLOAT16, attrs_over: dict | None = None,
+             outputs=None, const_gamma=True):
+    """Adds a SkipSimplifiedLayerNormalization (skip=True) or SimplifiedLayerNormalization node
+    from an oracle/rmsnorm make_inputs() dict; `outputs` overrides the output slot names."""
+    H = x_shape[-1]
+    x_name, k_name, y_name, s_name = (f"{name}_x", f"{name}_skip", f"{name}_y", f"{name}_sum")
+    h.value(x_name, elem, x_shape)
+    h.value(y_name, elem, x_shape)
+    h.value(f"{name}_gamma", elem, (H,), inp["gamma"] if const_gamma else None)
+    ins = [x_name]
+    if skip:
+        h.value(k_name, elem, x_shape)
+        ins.append(k_name)
+    ins.append(f"{name}_gamma")
+    if skip and bias:
+        h.value(f"{name}_bias", elem, (H,), inp["bias"])
+        ins.append(f"{name}_bias")
+    if outputs is None:
+        if skip:
+            h.value(s_name, elem, x_shape)
+            outputs = [y_name, "", "", s_name] if with_sum else [y_name]
+        else:
+            outputs = [y_name]
+    attrs = {"epsilon": float(epsilon)}
+    attrs.update(attrs_over or {})
+    op = "SkipSimplifiedLayerNormalization" if skip else "SimplifiedLayerNormalization"
+    h.node(op, domain, name, ins, outputs, attrs)
+    return x_name, k_name, y_name, s_name

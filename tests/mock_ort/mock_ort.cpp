@@ -753,6 +753,10 @@ int mock_add_node(const char* op, const char* domain, const char* name, const ch
         n->inputs.push_back(it->second.get());
     }
     for (const std::string& s : split(outputs, ',')) {
+        if (s.empty()) {                                  // an absent optional output
+            n->outputs.push_back(nullptr);
+            continue;
+        }
         auto it = g->values.find(s);
         if (it == g->values.end()) {
             set_err("unknown value %s", s.c_str());
@@ -816,7 +820,8 @@ int mock_get_capability(int nested, char* out, size_t len) {
                 seen.insert(v->name);
                 gr.fused->inputs.push_back(v);
             }
-            for (OrtValueInfo* v : n->outputs) gr.fused->outputs.push_back(v);
+            for (OrtValueInfo* v : n->outputs)
+                if (v) gr.fused->outputs.push_back(v);       // ORT's fused node: real outputs only
         }
         g->groups.push_back(std::move(gr));
     }

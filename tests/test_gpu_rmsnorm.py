@@ -1,0 +1,95 @@
+"""GPU parity of the RMSNorm kernels (mnb_skip_rmsnorm, mnb_session_run_rmsnorm) against
+oracle/rmsnorm.py.
+
+Bars: the residual sum (output slot 3) is bit-exact against IEEE fp32 arithmetic in the stated
+order, ((x + skip) + bias) each add rounded to fp32, then stored in the tensor type; the
+normalised output is within max relative error 2e-3 over significant elements (|y_ref| >= 0.1
+RMS) and RMS-normalised for fp16 (output rounding alone is up to 4.9e-4), 1e-5 for fp32,
+against the float64 oracle.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import matmul_nbits as orc
+from oracle import rmsnorm as rn
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    import torch
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _check(y, sm, inp, skip, bias, eps, dtype):
+    ref, r = rn.skip_rmsnorm(inp["x"], inp["gamma"], inp["skip"] if skip else None,
+                             inp["bias"] if bias else None, eps)
+    tol = 2e-3 if dtype == np.float16 else 1e-5
+    assert orc.max_rel_err_significant(y, ref) <= tol
+    assert orc.max_err_rms_normalised(y, ref) <= tol
+    if sm is not None:
+        want = residual_fp32(inp, skip, bias).astype(dtype)
+        u = np.uint16 if dtype == np.float16 else np.uint32
+        assert np.array_equal(sm.astype(dtype).view(u), want.view(u))
+
+
+def residual_fp32(inp, skip=True, bias=False):
+    """((x + skip) + bias), every add rounded to fp32 (IEEE, numpy float32)."""
+    r = inp["x"].astype(np.float32)
+    if skip:
+        r = r + inp["skip"].astype(np.float32)
+    if bias:
+        r = r + inp["bias"].astype(np.float32)
+    return r
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 3072), (7, 2880), (64, 4096), (5, 8192), (3, 128),
+                                         (33, 3072)])
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+@pytest.mark.parametrize("skip,bias,want_sum", [(True, False, True), (True, True, True),
+                                                (False, False, False), (True, False, False)])
+def test_rmsnorm_matches_oracle(cuda, rows, hidden, dtype, skip, bias, want_sum):
+    import mnb
+    import torch
+
+    if dtype == np.float32 and hidden > 4096:
+        pytest.skip("fp32 rows are limited to 4096 elements")
+    inp = rn.make_inputs(rows, hidden, dtype=dtype, seed=rows + hidden)
+    d = {k: _t(v, cuda) for k, v in inp.items()}
+    y, sm = mnb.skip_rmsnorm(d["x"], d["gamma"], skip=d["skip"] if skip else None,
+                             bias=d["bias"] if bias else None, epsilon=1e-5, want_sum=want_sum)
+    torch.cuda.synchronize()
+    _check(y.cpu().numpy().astype(np.float64), None if sm is None else sm.cpu().numpy(), inp,
+           skip, bias, 1e-5, dtype)
+
+
+def test_rmsnorm_session_host_io(cuda):
+    import mnb
+
+    rows, hidden = 9, 3072
+    inp = rn.make_inputs(rows, hidden, seed=11)
+    lib = mnb.load()
+    sess = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(sess)))
+    w = C.c_void_p()
+    p = mnb.RmsNormProblem(0, hidden, 1e-5, 1, 1, 1, mnb.DTYPE_F16)
+    try:
+        g, b = inp["gamma"], inp["bias"]
+        mnb.check(lib.mnb_rmsnorm_weights_upload(sess, C.byref(p), g.ctypes.data, g.nbytes,
+                                                 b.ctypes.data, b.nbytes, C.byref(w)))
+        y = np.empty((rows, hidden), np.float16)
+        sm = np.empty((rows, hidden), np.float16)
+        for _ in range(2):
+            mnb.check(lib.mnb_session_run_rmsnorm(sess, w, rows, inp["x"].ctypes.data, 0,
+                                                  inp["skip"].ctypes.data, 0, y.ctypes.data, 0,
+                                                  sm.ctypes.data, 0))
+            _check(y.astype(np.float64), sm, inp, True, True, 1e-5, np.float16)
+    finally:
+        if w.value:
+            lib.mnb_rmsnorm_weights_release(w)
+        lib.mnb_session_destroy(sess)
