@@ -201,6 +201,42 @@ int mnb_rmsnorm_check(const mnb_rmsnorm_problem* p);
 int mnb_skip_rmsnorm(const mnb_rmsnorm_problem* p, const void* x, const void* skip,
                      const void* gamma, const void* bias, void* y, void* sum_out, void* stream);
 
+/* com.microsoft::GroupQueryAttention, the form the reference claims
+ * (rust/src/ops/attention.rs:172-269) and computes (translate_gqa, attention.rs:388-735, kernel
+ * rust/shaders/glsl/gqa_f16.comp): packed QKV, do_rotary=1 with half-rotation (neox) RoPE,
+ * causal softmax, KV cache with seqlens_k.  fp16 tensors:
+ *   packed_qkv [B, S, (Nq + 2 Nkv) D]; past_key/past_value [B, Nkv, past_len_max, D];
+ *   seqlens_k [B] int32 (device memory); cos_cache/sin_cache [max_seq, rotary_dim / 2];
+ *   attn_out [B, S, Nq D]; present_key/present_value [B, Nkv, present_len, D].
+ * Per batch past_len = clamp(seqlens_k[b] + 1 - S, 0, past_len_max); query s sits at
+ * tok_pos = past_len + s (cos/sin row min(tok_pos, max_seq - 1)) and attends to keys
+ * [0, tok_pos].  The new rotated K and V are written to present at tok_pos when
+ * tok_pos < present_len.  present_len is past_len_max + S or more (growing cache: the past
+ * tokens [0, past_len) are copied into present) or equal to past_len_max (shared buffer:
+ * present_key may be past_key itself, updated in place; if it is another buffer the past tokens
+ * are copied too).  Present positions past past_len + S are left as they were.  Tensors 16-byte
+ * aligned; head_dim a multiple of 16 up to 256.  Stream-ordered. */
+typedef struct mnb_gqa_problem {
+    int64_t batch;              /* B */
+    int64_t seq_len;            /* S, new tokens per batch row */
+    int64_t past_len_max;       /* past_key.shape[2] */
+    int64_t present_len;        /* present_key.shape[2] */
+    int64_t max_seq;            /* cos_cache.shape[0] */
+    int32_t num_heads;          /* Nq, a positive multiple of kv_num_heads */
+    int32_t kv_num_heads;       /* Nkv */
+    int32_t head_dim;           /* D */
+    int32_t rotary_dim;         /* even, 2 .. D */
+    float scale;                /* applied to q . k before the softmax */
+    int32_t dtype;              /* MNB_DTYPE_F16 */
+} mnb_gqa_problem;
+
+int mnb_gqa_check(const mnb_gqa_problem* p);
+int mnb_gqa_workspace_bytes(const mnb_gqa_problem* p, size_t* bytes);
+int mnb_gqa(const mnb_gqa_problem* p, const void* packed_qkv, const void* past_key,
+            const void* past_value, const int32_t* seqlens_k, const void* cos_cache,
+            const void* sin_cache, void* attn_out, void* present_key, void* present_value,
+            void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- session layer: one device, one stream, weights uploaded once ---------------------- */
 
 typedef struct mnb_session mnb_session;
@@ -277,6 +313,27 @@ int mnb_session_run_rmsnorm(mnb_session* s, const mnb_rmsnorm_weights* w, int64_
                             const void* x, int x_on_device, const void* skip,
                             int skip_on_device, void* y, int y_on_device, void* sum_out,
                             int sum_on_device);
+
+/* GroupQueryAttention node constants (the cos/sin caches, constant initializers in the graphs
+ * the reference targets) uploaded once, and one Compute whose shapes come from `shape` (its
+ * head counts, head_dim, rotary_dim, max_seq, scale and dtype must match the node's).  Each
+ * tensor is in host memory or the session device's memory per bit of `on_device`
+ * (MNB_GQA_ON_DEVICE_*); host tensors are staged through HBM, and a present tensor passed as
+ * the same host pointer as its past tensor is updated in place.  Returns after the stream. */
+#define MNB_GQA_ON_DEVICE_QKV 1u
+#define MNB_GQA_ON_DEVICE_PAST 2u          /* past_key and past_value */
+#define MNB_GQA_ON_DEVICE_SEQLENS 4u
+#define MNB_GQA_ON_DEVICE_OUT 8u
+#define MNB_GQA_ON_DEVICE_PRESENT 16u      /* present_key and present_value */
+typedef struct mnb_gqa_caches mnb_gqa_caches;
+int mnb_gqa_caches_upload(mnb_session* s, const mnb_gqa_problem* node, const void* cos_cache,
+                          size_t cos_bytes, const void* sin_cache, size_t sin_bytes,
+                          mnb_gqa_caches** out);
+int mnb_gqa_caches_release(mnb_gqa_caches* c);
+int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_problem* shape,
+                        const void* packed_qkv, const void* past_key, const void* past_value,
+                        const int32_t* seqlens_k, void* attn_out, void* present_key,
+                        void* present_value, uint32_t on_device);
 
 /* Number of MatMulNBits-family kernel launches made by this process (proves the GPU ran). */
 uint64_t mnb_launch_count(void);

@@ -59,6 +59,7 @@ HIP_SOURCES = [
     CSRC / "kernels" / "mnb_calibrate.hip",
     CSRC / "kernels" / "mnb_qmoe.hip",
     CSRC / "kernels" / "mnb_rmsnorm.hip",
+    CSRC / "kernels" / "mnb_gqa.hip",
     CSRC / "shim" / "mnb_shim.hip",
 ]
 EP_SOURCES: list[Path] = sorted((CSRC / "ep").glob("*.cpp"))

@@ -125,6 +125,26 @@ hipError_t launch_skip_rmsnorm(const void* x, const void* skip, const void* gamm
                                const void* bias, void* y, void* sum_out, int64_t rows,
                                int64_t hidden, float eps, bool f16, hipStream_t stream);
 
+// GroupQueryAttention with packed QKV and fused RoPE (mnb_gqa.hip).
+struct GqaArgs {
+    int64_t batch, seq, past_stride, present_len, max_seq;
+    int nq, nkv, d, rot;
+    float scale;
+    bool copy_past;      // present is its own buffer: the past tokens are copied into it
+};
+struct GqaPlan {
+    int waves;           // wavefronts per workgroup (16 query rows each)
+    int splits;          // workgroups along the keys of one row block
+    int64_t row_blocks;  // row blocks per (batch, KV head)
+    int64_t chunk;       // keys per split (a multiple of 64)
+};
+bool gqa_supported(int head_dim);
+GqaPlan gqa_plan(const GqaArgs& a);
+size_t gqa_workspace_bytes(const GqaArgs& a);
+hipError_t launch_gqa(const GqaArgs& a, const void* qkv, const void* past_k, const void* past_v,
+                      const int32_t* seqlens, const void* cos_cache, const void* sin_cache,
+                      void* out, void* pres_k, void* pres_v, void* workspace, hipStream_t stream);
+
 // Roofline calibration (mnb_calibrate.hip): workgroups x 4 wavefronts x iters x 16 MFMAs.
 hipError_t launch_mfma_calibrate(const void* operands, float* out, int workgroups, int iters,
                                  hipStream_t stream);

@@ -469,6 +469,102 @@ int mnb_skip_rmsnorm(const mnb_rmsnorm_problem* p, const void* x, const void* sk
     return MNB_OK;
 }
 
+// ---- GroupQueryAttention ----------------------------------------------------------------------
+
+static mnb::GqaArgs gqa_args(const mnb_gqa_problem* p, bool copy_past) {
+    mnb::GqaArgs a{};
+    a.batch = p->batch;
+    a.seq = p->seq_len;
+    a.past_stride = p->past_len_max;
+    a.present_len = p->present_len;
+    a.max_seq = p->max_seq;
+    a.nq = p->num_heads;
+    a.nkv = p->kv_num_heads;
+    a.d = p->head_dim;
+    a.rot = p->rotary_dim;
+    a.scale = p->scale;
+    a.copy_past = copy_past;
+    return a;
+}
+
+int mnb_gqa_check(const mnb_gqa_problem* p) {
+    if (!p) return fail(MNB_ERR_INVALID, "problem is NULL");
+    if (p->batch < 0 || p->seq_len < 0 || p->past_len_max < 0 || p->present_len < 0)
+        return fail(MNB_ERR_INVALID, "batch, seq_len, past_len_max and present_len must be >= 0");
+    if (p->dtype != MNB_DTYPE_F16)
+        return fail(MNB_ERR_UNSUPPORTED, "GroupQueryAttention runs fp16 tensors");
+    if (p->num_heads < 1 || p->kv_num_heads < 1 || p->num_heads % p->kv_num_heads)
+        return fail(MNB_ERR_UNSUPPORTED, "num_heads = %d and kv_num_heads = %d; num_heads must "
+                    "be a positive multiple of kv_num_heads", p->num_heads, p->kv_num_heads);
+    if (!mnb::gqa_supported(p->head_dim))
+        return fail(MNB_ERR_UNSUPPORTED, "head_dim = %d; this library takes multiples of 16 up "
+                    "to 256", p->head_dim);
+    if (p->rotary_dim < 2 || p->rotary_dim % 2 || p->rotary_dim > p->head_dim)
+        return fail(MNB_ERR_INVALID, "rotary_dim = %d is not an even value in 2..head_dim = %d",
+                    p->rotary_dim, p->head_dim);
+    if (p->max_seq < 1) return fail(MNB_ERR_INVALID, "max_seq = %lld", (long long)p->max_seq);
+    if (p->present_len < p->past_len_max + p->seq_len && p->present_len != p->past_len_max)
+        return fail(MNB_ERR_INVALID, "present length %lld is neither the shared-buffer extent "
+                    "(%lld) nor the growing-cache extent (%lld + %lld or more)",
+                    (long long)p->present_len, (long long)p->past_len_max,
+                    (long long)p->past_len_max, (long long)p->seq_len);
+    if (!std::isfinite(p->scale)) return fail(MNB_ERR_INVALID, "scale is not finite");
+    const double heads = (double)p->num_heads + 2.0 * p->kv_num_heads;
+    if ((double)p->batch * p->seq_len * heads * p->head_dim >= (double)(1ll << 40) ||
+        (double)p->batch * p->kv_num_heads * (p->present_len + p->past_len_max) * p->head_dim >=
+            (double)(1ll << 40) ||
+        (double)p->batch * p->num_heads * p->seq_len >= (double)(1ll << 31))
+        return fail(MNB_ERR_UNSUPPORTED, "extents too large");
+    return MNB_OK;
+}
+
+int mnb_gqa_workspace_bytes(const mnb_gqa_problem* p, size_t* bytes) {
+    if (!bytes) return fail(MNB_ERR_INVALID, "bytes is NULL");
+    *bytes = 0;
+    const int rc = mnb_gqa_check(p);
+    if (rc) return rc;
+    if (p->batch && p->seq_len) *bytes = mnb::gqa_workspace_bytes(gqa_args(p, false));
+    return MNB_OK;
+}
+
+int mnb_gqa(const mnb_gqa_problem* p, const void* packed_qkv, const void* past_key,
+            const void* past_value, const int32_t* seqlens_k, const void* cos_cache,
+            const void* sin_cache, void* attn_out, void* present_key, void* present_value,
+            void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = mnb_gqa_check(p);
+    if (rc) return rc;
+    if (p->batch == 0 || p->seq_len == 0) return MNB_OK;
+    if (!packed_qkv || !seqlens_k || !cos_cache || !sin_cache || !attn_out ||
+        (p->past_len_max && (!past_key || !past_value)) ||
+        (p->present_len && (!present_key || !present_value)))
+        return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    const bool alias_k = p->past_len_max && present_key == past_key;
+    const bool alias_v = p->past_len_max && present_value == past_value;
+    if (alias_k != alias_v)
+        return fail(MNB_ERR_INVALID, "present_key and present_value must both alias their past "
+                                     "tensors or neither");
+    if (alias_k && p->present_len != p->past_len_max)
+        return fail(MNB_ERR_INVALID, "present aliases past but present length %lld differs from "
+                    "the past buffer's %lld", (long long)p->present_len,
+                    (long long)p->past_len_max);
+    for (const void* q : {packed_qkv, past_key, past_value, static_cast<const void*>(attn_out),
+                          static_cast<const void*>(present_key),
+                          static_cast<const void*>(present_value)})
+        if (q && !aligned(q, 16)) return fail(MNB_ERR_INVALID, "tensors must be 16-byte aligned");
+    const mnb::GqaArgs a = gqa_args(p, !alias_k);
+    const size_t need = mnb::gqa_workspace_bytes(a);
+    if (!workspace || workspace_bytes < need)
+        return fail(MNB_ERR_INVALID, "workspace holds %zu bytes, GroupQueryAttention needs %zu",
+                    workspace_bytes, need);
+    if (!aligned(workspace, 256)) return fail(MNB_ERR_INVALID, "workspace must be 256-byte aligned");
+    hipError_t e = mnb::launch_gqa(a, packed_qkv, past_key, past_value, seqlens_k, cos_cache,
+                                   sin_cache, attn_out, present_key, present_value, workspace,
+                                   static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "GroupQueryAttention launch");
+    g_launches.fetch_add(1);
+    return MNB_OK;
+}
+
 // ---- session layer ------------------------------------------------------------------------
 
 struct mnb_session {
@@ -971,6 +1067,151 @@ int mnb_session_run_rmsnorm(mnb_session* s, const mnb_rmsnorm_weights* w, int64_
     if (e == hipSuccess && sum_out && !sum_on_device)
         e = hipMemcpyAsync(sum_out, qd, bytes, hipMemcpyDeviceToHost, s->stream);
     if (e != hipSuccess) return hip_fail(e, "RMSNorm output download");
+    e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+struct mnb_gqa_caches {
+    mnb_session* s = nullptr;
+    mnb_gqa_problem node{};
+    void* cos = nullptr;
+    void* sin = nullptr;
+};
+
+int mnb_gqa_caches_release(mnb_gqa_caches* c) {
+    if (!c) return MNB_OK;
+    (void)hipSetDevice(c->s->device);
+    (void)hipStreamSynchronize(c->s->stream);
+    if (c->cos) (void)hipFree(c->cos);
+    if (c->sin) (void)hipFree(c->sin);
+    delete c;
+    return MNB_OK;
+}
+
+int mnb_gqa_caches_upload(mnb_session* s, const mnb_gqa_problem* node, const void* cos_cache,
+                          size_t cos_bytes, const void* sin_cache, size_t sin_bytes,
+                          mnb_gqa_caches** out) {
+    if (!s || !node || !out) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    *out = nullptr;
+    mnb_gqa_problem p = *node;
+    p.batch = 0;
+    p.seq_len = 0;
+    p.past_len_max = 0;
+    p.present_len = 0;
+    int rc = mnb_gqa_check(&p);
+    if (rc) return rc;
+    const size_t want = (size_t)p.max_seq * (size_t)(p.rotary_dim / 2) * 2;
+    if (!cos_cache || cos_bytes != want || !sin_cache || sin_bytes != want)
+        return fail(MNB_ERR_INVALID, "cos/sin caches hold %zu and %zu bytes, the node needs %zu "
+                    "each", cos_bytes, sin_bytes, want);
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    mnb_gqa_caches* c = new (std::nothrow) mnb_gqa_caches();
+    if (!c) return fail(MNB_ERR_NOMEM, "cache allocation failed");
+    c->s = s;
+    c->node = p;
+    hipError_t e = hipMalloc(&c->cos, want);
+    if (e == hipSuccess) e = hipMalloc(&c->sin, want);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->cos, cos_cache, want, hipMemcpyHostToDevice, s->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->sin, sin_cache, want, hipMemcpyHostToDevice, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e != hipSuccess) {
+        if (c->cos) (void)hipFree(c->cos);
+        if (c->sin) (void)hipFree(c->sin);
+        delete c;
+        return hip_fail(e, "GroupQueryAttention cache upload");
+    }
+    *out = c;
+    return MNB_OK;
+}
+
+int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_problem* shape,
+                        const void* packed_qkv, const void* past_key, const void* past_value,
+                        const int32_t* seqlens_k, void* attn_out, void* present_key,
+                        void* present_value, uint32_t on_device) {
+    if (!s || !c || !shape) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    const mnb_gqa_problem& n = c->node;
+    if (shape->num_heads != n.num_heads || shape->kv_num_heads != n.kv_num_heads ||
+        shape->head_dim != n.head_dim || shape->rotary_dim != n.rotary_dim ||
+        shape->max_seq != n.max_seq || shape->scale != n.scale || shape->dtype != n.dtype)
+        return fail(MNB_ERR_INVALID, "the call's head counts, head_dim, rotary_dim, max_seq, scale "
+                                     "or dtype differ from the node's");
+    const mnb_gqa_problem p = *shape;
+    int rc = mnb_gqa_check(&p);
+    if (rc) return rc;
+    if (p.batch == 0 || p.seq_len == 0) return MNB_OK;
+    if (!packed_qkv || !seqlens_k || !attn_out ||
+        (p.past_len_max && (!past_key || !past_value)) ||
+        (p.present_len && (!present_key || !present_value)))
+        return fail(MNB_ERR_INVALID, "a NULL tensor pointer was passed");
+    const bool qkv_dev = on_device & MNB_GQA_ON_DEVICE_QKV;
+    const bool past_dev = on_device & MNB_GQA_ON_DEVICE_PAST;
+    const bool seq_dev = on_device & MNB_GQA_ON_DEVICE_SEQLENS;
+    const bool out_dev = on_device & MNB_GQA_ON_DEVICE_OUT;
+    const bool pres_dev = on_device & MNB_GQA_ON_DEVICE_PRESENT;
+    // a present tensor given as its past tensor (same memory) is updated in place
+    const bool in_place = p.past_len_max && present_key == past_key && past_dev == pres_dev;
+    if (in_place != (p.past_len_max && present_value == past_value && past_dev == pres_dev))
+        return fail(MNB_ERR_INVALID, "present_key and present_value must both alias their past "
+                                     "tensors or neither");
+    std::lock_guard<std::mutex> lk(s->mu);
+    (void)hipSetDevice(s->device);
+    const size_t heads = (size_t)p.num_heads + 2 * (size_t)p.kv_num_heads;
+    const size_t qkv_b = (size_t)p.batch * p.seq_len * heads * p.head_dim * 2;
+    const size_t past_b = (size_t)p.batch * p.kv_num_heads * p.past_len_max * p.head_dim * 2;
+    const size_t seq_b = (size_t)p.batch * 4;
+    const size_t out_b = (size_t)p.batch * p.seq_len * p.num_heads * p.head_dim * 2;
+    const size_t pres_b = (size_t)p.batch * p.kv_num_heads * p.present_len * p.head_dim * 2;
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    // inputs staged in the A buffer, outputs in the Y buffer
+    const size_t o_qkv = 0, o_pk = al(qkv_b), o_pv = o_pk + al(past_b), o_seq = o_pv + al(past_b);
+    const size_t in_total = o_seq + al(seq_b);
+    const size_t o_out = 0, o_rk = al(out_b), o_rv = o_rk + al(pres_b);
+    const size_t out_total = o_rv + al(pres_b);
+    rc = grow(&s->a_dev, &s->a_cap, in_total);
+    if (!rc) rc = grow(&s->y_dev, &s->y_cap, out_total);
+    size_t ws = 0;
+    if (!rc) rc = mnb_gqa_workspace_bytes(&p, &ws);
+    if (!rc) rc = grow(&s->ws, &s->ws_cap, ws);
+    if (rc) return rc;
+    uint8_t* in = static_cast<uint8_t*>(s->a_dev);
+    uint8_t* ob = static_cast<uint8_t*>(s->y_dev);
+    const void* qd = packed_qkv;
+    const void* pkd = past_key;
+    const void* pvd = past_value;
+    const int32_t* sd = seqlens_k;
+    void* od = out_dev ? attn_out : ob + o_out;
+    void* rkd = present_key;
+    void* rvd = present_value;
+    hipError_t e = hipSuccess;
+    auto up = [&](const void* src, size_t off, size_t bytes) -> const void* {
+        if (e == hipSuccess && bytes)
+            e = hipMemcpyAsync(in + off, src, bytes, hipMemcpyHostToDevice, s->stream);
+        return in + off;
+    };
+    if (!qkv_dev) qd = up(packed_qkv, o_qkv, qkv_b);
+    if (!past_dev && p.past_len_max) {
+        pkd = up(past_key, o_pk, past_b);
+        pvd = up(past_value, o_pv, past_b);
+    }
+    if (!seq_dev) sd = static_cast<const int32_t*>(up(seqlens_k, o_seq, seq_b));
+    if (e != hipSuccess) return hip_fail(e, "GroupQueryAttention input upload");
+    if (in_place) {
+        rkd = const_cast<void*>(pkd);
+        rvd = const_cast<void*>(pvd);
+    } else if (!pres_dev && p.present_len) {
+        rkd = ob + o_rk;
+        rvd = ob + o_rv;
+    }
+    rc = mnb_gqa(&p, qd, pkd, pvd, sd, c->cos, c->sin, od, rkd, rvd, s->ws, s->ws_cap, s->stream);
+    if (rc) return rc;
+    if (!out_dev) e = hipMemcpyAsync(attn_out, od, out_b, hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess && !pres_dev && p.present_len) {
+        e = hipMemcpyAsync(present_key, rkd, pres_b, hipMemcpyDeviceToHost, s->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(present_value, rvd, pres_b, hipMemcpyDeviceToHost, s->stream);
+    }
+    if (e != hipSuccess) return hip_fail(e, "GroupQueryAttention output download");
     e = hipStreamSynchronize(s->stream);
     return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
 }

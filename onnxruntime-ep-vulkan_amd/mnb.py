@@ -81,6 +81,19 @@ class RmsNormProblem(C.Structure):
     ]
 
 
+class GqaProblem(C.Structure):
+    _fields_ = [
+        ("batch", C.c_int64), ("seq_len", C.c_int64), ("past_len_max", C.c_int64),
+        ("present_len", C.c_int64), ("max_seq", C.c_int64), ("num_heads", C.c_int32),
+        ("kv_num_heads", C.c_int32), ("head_dim", C.c_int32), ("rotary_dim", C.c_int32),
+        ("scale", C.c_float), ("dtype", C.c_int32),
+    ]
+
+
+GQA_ON_DEVICE_QKV, GQA_ON_DEVICE_PAST, GQA_ON_DEVICE_SEQLENS = 1, 2, 4
+GQA_ON_DEVICE_OUT, GQA_ON_DEVICE_PRESENT = 8, 16
+
+
 class MnbError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"mnb error {code}: {msg}")
@@ -142,6 +155,15 @@ def load() -> C.CDLL:
         "mnb_rmsnorm_weights_release": (C.c_int, [vp]),
         "mnb_session_run_rmsnorm": (C.c_int, [vp, vp, i64, vp, C.c_int, vp, C.c_int, vp, C.c_int,
                                               vp, C.c_int]),
+        "mnb_gqa_check": (C.c_int, [C.POINTER(GqaProblem)]),
+        "mnb_gqa_workspace_bytes": (C.c_int, [C.POINTER(GqaProblem), C.POINTER(sz)]),
+        "mnb_gqa": (C.c_int, [C.POINTER(GqaProblem), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz,
+                              vp]),
+        "mnb_gqa_caches_upload": (C.c_int, [vp, C.POINTER(GqaProblem), vp, sz, vp, sz,
+                                            C.POINTER(vp)]),
+        "mnb_gqa_caches_release": (C.c_int, [vp]),
+        "mnb_session_run_gqa": (C.c_int, [vp, vp, C.POINTER(GqaProblem), vp, vp, vp, vp, vp, vp,
+                                          vp, C.c_uint32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -262,6 +284,46 @@ def skip_rmsnorm(x, gamma, *, skip=None, bias=None, epsilon: float = 1e-5, want_
     check(load().mnb_skip_rmsnorm(C.byref(p), _ptr(x), _ptr(skip), _ptr(gamma), _ptr(bias),
                                   _ptr(out), _ptr(sum_out) if want_sum else None, _stream(stream)))
     return out, (sum_out if want_sum else None)
+
+
+def gqa_problem(batch: int, seq_len: int, past_len_max: int, present_len: int, max_seq: int,
+                num_heads: int, kv_num_heads: int, head_dim: int, rotary_dim: int,
+                scale: float | None = None) -> GqaProblem:
+    if scale is None:
+        scale = head_dim ** -0.5
+    return GqaProblem(batch, seq_len, past_len_max, present_len, max_seq, num_heads, kv_num_heads,
+                      head_dim, rotary_dim, float(scale), DTYPE_F16)
+
+
+def gqa(qkv, past_k, past_v, seqlens_k, cos, sin, *, num_heads: int, kv_num_heads: int,
+        scale: float | None = None, rotary_dim: int | None = None, present_len: int | None = None,
+        present_k=None, present_v=None, stream=None):
+    """GroupQueryAttention (packed QKV, fused RoPE) on CUDA tensors; returns
+    ``(attn_out, present_key, present_value)``.  ``present_k``/``present_v`` may be the past
+    tensors themselves (shared-buffer convention, updated in place)."""
+    import torch
+    B, S, P = (int(x) for x in qkv.shape)
+    D = P // (num_heads + 2 * kv_num_heads)
+    past = int(past_k.shape[2]) if past_k is not None else 0
+    if present_len is None:
+        present_len = int(present_k.shape[2]) if present_k is not None else past + S
+    rd = rotary_dim if rotary_dim is not None else 2 * int(cos.shape[1])
+    p = gqa_problem(B, S, past, present_len, int(cos.shape[0]), num_heads, kv_num_heads, D, rd,
+                    scale)
+    dev = qkv.device
+    out = torch.empty((B, S, num_heads * D), dtype=torch.float16, device=dev)
+    if present_k is None:
+        present_k = torch.zeros((B, kv_num_heads, present_len, D), dtype=torch.float16, device=dev)
+    if present_v is None:
+        present_v = torch.zeros((B, kv_num_heads, present_len, D), dtype=torch.float16, device=dev)
+    lib = load()
+    ws_bytes = C.c_size_t()
+    check(lib.mnb_gqa_workspace_bytes(C.byref(p), C.byref(ws_bytes)))
+    ws = torch.empty(max(int(ws_bytes.value), 1), dtype=torch.uint8, device=dev)
+    check(lib.mnb_gqa(C.byref(p), _ptr(qkv), _ptr(past_k), _ptr(past_v), _ptr(seqlens_k),
+                      _ptr(cos), _ptr(sin), _ptr(out), _ptr(present_k), _ptr(present_v),
+                      _ptr(ws), int(ws_bytes.value), _stream(stream)))
+    return out, present_k, present_v
 
 
 def launch_count() -> int:
