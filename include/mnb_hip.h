@@ -314,17 +314,20 @@ int mnb_session_run_rmsnorm(mnb_session* s, const mnb_rmsnorm_weights* w, int64_
                             int skip_on_device, void* y, int y_on_device, void* sum_out,
                             int sum_on_device);
 
-/* GroupQueryAttention node constants (the cos/sin caches, constant initializers in the graphs
- * the reference targets) uploaded once, and one Compute whose shapes come from `shape` (its
- * head counts, head_dim, rotary_dim, max_seq, scale and dtype must match the node's).  Each
- * tensor is in host memory or the session device's memory per bit of `on_device`
- * (MNB_GQA_ON_DEVICE_*); host tensors are staged through HBM, and a present tensor passed as
- * the same host pointer as its past tensor is updated in place.  Returns after the stream. */
+/* GroupQueryAttention node record: the cos/sin caches uploaded once when they are constant
+ * initializers (as in the graphs the reference targets), or NULL when every call passes them.
+ * One Compute takes its shapes from `shape` (head counts, head_dim, rotary_dim, scale and dtype
+ * must match the node's; max_seq too when the caches are resident).  cos_cache/sin_cache NULL
+ * use the resident caches.  Each tensor is in host memory or the session device's memory per
+ * bit of `on_device` (MNB_GQA_ON_DEVICE_*); host tensors are staged through HBM, and a present
+ * tensor passed as the same memory as its past tensor is updated in place.  Returns after the
+ * stream has finished. */
 #define MNB_GQA_ON_DEVICE_QKV 1u
 #define MNB_GQA_ON_DEVICE_PAST 2u          /* past_key and past_value */
 #define MNB_GQA_ON_DEVICE_SEQLENS 4u
 #define MNB_GQA_ON_DEVICE_OUT 8u
 #define MNB_GQA_ON_DEVICE_PRESENT 16u      /* present_key and present_value */
+#define MNB_GQA_ON_DEVICE_CACHES 32u       /* per-call cos_cache and sin_cache */
 typedef struct mnb_gqa_caches mnb_gqa_caches;
 int mnb_gqa_caches_upload(mnb_session* s, const mnb_gqa_problem* node, const void* cos_cache,
                           size_t cos_bytes, const void* sin_cache, size_t sin_bytes,
@@ -332,8 +335,9 @@ int mnb_gqa_caches_upload(mnb_session* s, const mnb_gqa_problem* node, const voi
 int mnb_gqa_caches_release(mnb_gqa_caches* c);
 int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_problem* shape,
                         const void* packed_qkv, const void* past_key, const void* past_value,
-                        const int32_t* seqlens_k, void* attn_out, void* present_key,
-                        void* present_value, uint32_t on_device);
+                        const int32_t* seqlens_k, const void* cos_cache, const void* sin_cache,
+                        void* attn_out, void* present_key, void* present_value,
+                        uint32_t on_device);
 
 /* Number of MatMulNBits-family kernel launches made by this process (proves the GPU ran). */
 uint64_t mnb_launch_count(void);

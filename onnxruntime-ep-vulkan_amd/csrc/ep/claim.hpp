@@ -13,6 +13,7 @@
 // exercise it directly.
 #pragma once
 
+#include <cmath>
 #include <cstdint>
 #include <string>
 #include <vector>
@@ -26,6 +27,7 @@ enum ElemType : int32_t {
     kElemFloat = 1,
     kElemUint8 = 2,
     kElemFloat16 = 10,
+    kElemInt32 = 6,
 };
 
 struct InputFacts {
@@ -346,6 +348,117 @@ inline ClaimDecision claim_norm(const NormFacts& f, int64_t* hidden = nullptr) {
             return decline("bias must be a constant [H] of the input's type");
     }
     if (hidden) *hidden = H;
+    return ClaimDecision{true, {}};
+}
+
+// ---- com.microsoft::GroupQueryAttention ------------------------------------------------------
+//
+// The claimed form is the reference's (rust/src/ops/attention.rs:172-269 claim, :388-560
+// translate): packed QKV in input 0 with inputs 1 and 2 absent, past_key/past_value and
+// seqlens_k present, do_rotary = 1 with half-rotation RoPE (rotary_interleaved = 0) from the
+// cos/sin caches in inputs 7 and 8, fp16, and every numerics-changing option off
+// (local_window_size -1, softcap 0, smooth_softmax <= 0, qk_output 0, no KV quantisation, inputs
+// 10..15 absent).  The reference reads only input 0's shape, so it would compute a separate-QKV
+// node with a wrong head_dim; that form is declined here.
+
+struct GqaFacts {
+    std::string op_type;
+    std::string domain;
+    std::vector<InputFacts> inputs;
+    std::vector<InputFacts> outputs;             // declared outputs (present false when absent)
+    bool has_num_heads = false, has_kv_num_heads = false, has_scale = false;
+    int64_t num_heads = 0, kv_num_heads = 0;
+    int64_t local_window_size = -1, do_rotary = 0, rotary_interleaved = 0;
+    int64_t smooth_softmax = 0, qk_output = 0, kv_cache_bit_width = 0;
+    int64_t rotary_embedding_dim = 0;
+    float softcap = 0.f, scale = 0.f;
+    std::string k_quant_type = "NONE", v_quant_type = "NONE";
+};
+
+struct GqaShape {
+    int64_t head_dim = 0, rotary_dim = 0, packed = 0;
+    int64_t declared_present_len = -1;           // present_key.shape[2] when static, else -1
+    float scale = 0.f;                           // the effective softmax scale
+};
+
+inline bool is_gqa(const std::string& op, const std::string& domain) {
+    return op == "GroupQueryAttention" && domain == "com.microsoft";
+}
+
+// The kernel's head_dim range: a multiple of 16 up to 256.
+inline bool gqa_head_dim_ok(int64_t d) { return d >= 16 && d <= 256 && d % 16 == 0; }
+
+inline ClaimDecision claim_gqa(const GqaFacts& f, GqaShape* shape = nullptr) {
+    if (!is_gqa(f.op_type, f.domain)) return decline("not a com.microsoft GroupQueryAttention");
+    const size_t nin = f.inputs.size();
+    auto has = [&](size_t i) { return i < nin && f.inputs[i].present; };
+    auto typed = [&](size_t i, int32_t t) { return has(i) && f.inputs[i].elem_type == t; };
+    if (!typed(0, kElemFloat16)) return decline("packed_qkv (input 0) must be float16");
+    if (has(1) || has(2))
+        return decline("separate key/value inputs: only the packed-QKV form is implemented");
+    if (!typed(3, kElemFloat16) || !typed(4, kElemFloat16))
+        return decline("past_key and past_value (inputs 3 and 4) must be present float16 tensors");
+    if (!has(5)) return decline("seqlens_k (input 5) is required for the per-batch past length");
+    if (f.inputs[5].elem_type != kElemInt32) return decline("seqlens_k must be int32");
+    if (!f.has_num_heads || !f.has_kv_num_heads) return decline("num_heads and kv_num_heads are required");
+    if (f.num_heads <= 0 || f.kv_num_heads <= 0 || f.num_heads % f.kv_num_heads)
+        return decline("num_heads must be a positive multiple of kv_num_heads");
+    if (f.local_window_size != -1) return decline("local_window_size other than -1 (sliding window)");
+    if (f.softcap != 0.f) return decline("softcap other than 0");
+    if (f.smooth_softmax > 0) return decline("smooth_softmax (attention sink) is not implemented");
+    if (f.qk_output != 0) return decline("qk_output other than 0");
+    if (f.kv_cache_bit_width != 0 || f.k_quant_type != "NONE" || f.v_quant_type != "NONE")
+        return decline("a quantised KV cache is not implemented");
+    if (f.do_rotary != 1) return decline("do_rotary other than 1: RoPE is fused, the kernel needs it");
+    if (f.rotary_interleaved != 0) return decline("rotary_interleaved = 1 (alternating pairs)");
+    if (!typed(7, kElemFloat16) || !typed(8, kElemFloat16))
+        return decline("cos_cache and sin_cache (inputs 7 and 8) must be present float16 tensors");
+    static const char* const kOptional[] = {"attention_bias", "head_sink", "k_scale", "v_scale",
+                                            "q_norm_weight", "k_norm_weight"};
+    for (size_t i = 10; i < nin && i < 16; ++i)
+        if (f.inputs[i].present) return decline(std::string(kOptional[i - 10]) + " is not implemented");
+    if (nin > 16) return decline("more than 16 inputs");
+    const InputFacts& x = f.inputs[0];
+    if (!x.has_shape || x.dims.size() != 3 || x.dims[2] <= 0)
+        return decline("packed_qkv must be rank 3 with a static last dimension");
+    const int64_t heads = f.num_heads + 2 * f.kv_num_heads;
+    if (x.dims[2] % heads) return decline("packed width is not (num_heads + 2 kv_num_heads) x head_dim");
+    const int64_t D = x.dims[2] / heads;
+    if (!gqa_head_dim_ok(D)) return decline("head_dim " + std::to_string(D) + " is outside the kernel's range");
+    for (size_t i : {size_t(3), size_t(4)}) {
+        const InputFacts& p = f.inputs[i];
+        if (!p.has_shape) continue;
+        if (p.dims.size() != 4) return decline("past_key/past_value must be rank 4");
+        if ((p.dims[1] >= 0 && p.dims[1] != f.kv_num_heads) || (p.dims[3] >= 0 && p.dims[3] != D))
+            return decline("past_key/past_value are not [B, kv_num_heads, S, head_dim]");
+    }
+    int64_t rd = f.rotary_embedding_dim;
+    const InputFacts& c = f.inputs[7];
+    if (rd <= 0) {
+        if (!c.has_shape || c.dims.size() != 2 || c.dims[1] <= 0)
+            return decline("no rotary_embedding_dim and cos_cache has no static second dimension: "
+                           "the rotary width is not recoverable");
+        rd = 2 * c.dims[1];
+    }
+    if (rd > D || rd % 2) return decline("rotary_dim is not an even value at most head_dim");
+    for (size_t i : {size_t(7), size_t(8)}) {
+        const InputFacts& t = f.inputs[i];
+        if (t.has_shape && (t.dims.size() != 2 || (t.dims[1] >= 0 && t.dims[1] != rd / 2)))
+            return decline("cos/sin caches are not [max_seq, rotary_dim / 2]");
+    }
+    if (f.outputs.size() < 3 || !f.outputs[0].present || !f.outputs[1].present || !f.outputs[2].present)
+        return decline("output, present_key and present_value are required outputs");
+    if (f.outputs.size() > 3 && f.outputs[3].present) return decline("output_qk is not written");
+    if (shape) {
+        shape->head_dim = D;
+        shape->rotary_dim = rd;
+        shape->packed = x.dims[2];
+        const InputFacts& pk = f.outputs[1];
+        shape->declared_present_len =
+            pk.has_shape && pk.dims.size() == 4 && pk.dims[2] > 0 ? pk.dims[2] : -1;
+        // ORT's schema: a scale of 0 (the attribute's default) means 1 / sqrt(head_dim)
+        shape->scale = f.has_scale && f.scale != 0.f ? f.scale : 1.f / std::sqrt((float)D);
+    }
     return ClaimDecision{true, {}};
 }
 

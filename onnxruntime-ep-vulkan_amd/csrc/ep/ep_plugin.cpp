@@ -323,6 +323,29 @@ NormFacts norm_facts(const OrtApi* api, const OrtNode* node) {
     return f;
 }
 
+GqaFacts gqa_facts(const OrtApi* api, const OrtNode* node) {
+    GqaFacts f;
+    f.op_type = node_string(api, node, api->Node_GetOperatorType);
+    f.domain = node_string(api, node, api->Node_GetDomain);
+    if (!is_gqa(f.op_type, f.domain)) return f;
+    for (const OrtValueInfo* vi : node_inputs(api, node)) f.inputs.push_back(input_facts(api, vi));
+    for (const OrtValueInfo* vi : node_outputs(api, node)) f.outputs.push_back(input_facts(api, vi));
+    f.has_num_heads = int_attr(api, node, "num_heads", &f.num_heads);
+    f.has_kv_num_heads = int_attr(api, node, "kv_num_heads", &f.kv_num_heads);
+    int_attr(api, node, "local_window_size", &f.local_window_size);
+    int_attr(api, node, "do_rotary", &f.do_rotary);
+    int_attr(api, node, "rotary_interleaved", &f.rotary_interleaved);
+    int_attr(api, node, "smooth_softmax", &f.smooth_softmax);
+    int_attr(api, node, "qk_output", &f.qk_output);
+    int_attr(api, node, "kv_cache_bit_width", &f.kv_cache_bit_width);
+    int_attr(api, node, "rotary_embedding_dim", &f.rotary_embedding_dim);
+    float_attr(api, node, "softcap", &f.softcap);
+    f.has_scale = float_attr(api, node, "scale", &f.scale);
+    string_attr(api, node, "k_quant_type", &f.k_quant_type);
+    string_attr(api, node, "v_quant_type", &f.v_quant_type);
+    return f;
+}
+
 // Session option `key` (ORT prefixes EP options with "ep.<name>."; both spellings are read).
 bool session_option(const OrtApi* api, const OrtSessionOptions* so, const std::string& key,
                     std::string* value) {
@@ -383,11 +406,22 @@ struct NodeKernel {
     size_t fused_skip = SIZE_MAX;
     size_t fused_y = SIZE_MAX, fused_sum = SIZE_MAX;
     mnb_rmsnorm_weights* nweights = nullptr;
+    // GroupQueryAttention node (gqa set): fused-input index of qkv (fused_a), past_key,
+    // past_value, seqlens_k, cos_cache, sin_cache (the caches SIZE_MAX when resident) and
+    // fused-output index of the output, present_key and present_value.
+    bool gqa = false;
+    mnb_gqa_problem gprob{};        // node constants; shapes filled per call
+    int64_t gqa_packed = 0;
+    int64_t gqa_present_len = -1;   // declared present length, or -1 (growing: past + S)
+    size_t gqa_in[6] = {SIZE_MAX, SIZE_MAX, SIZE_MAX, SIZE_MAX, SIZE_MAX, SIZE_MAX};
+    size_t gqa_out[3] = {SIZE_MAX, SIZE_MAX, SIZE_MAX};
+    mnb_gqa_caches* gcaches = nullptr;
 
     ~NodeKernel() {
         if (weights) mnb_weights_release(weights);
         if (qweights) mnb_qmoe_weights_release(qweights);
         if (nweights) mnb_rmsnorm_weights_release(nweights);
+        if (gcaches) mnb_gqa_caches_release(gcaches);
     }
 };
 
@@ -589,6 +623,86 @@ void compute_norm(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     g_compute_count.fetch_add(1);
 }
 
+// One GroupQueryAttention Compute.  present's length is the declared one when the graph states
+// it (shared buffer or growing), else past + S (growing), as translate_gqa decides
+// (rust/src/ops/attention.rs:585-600).
+void compute_gqa(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
+    const OrtApi* api = ep->api;
+    size_t nin = 0;
+    ORT_OK(api, KernelContext_GetInputCount(ctx, &nin));
+    const OrtValue* in[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+    for (int i = 0; i < 6; ++i) {
+        if (k.gqa_in[i] == SIZE_MAX) continue;
+        if (k.gqa_in[i] >= nin) fail(ORT_EP_FAIL, "fused GroupQueryAttention node has %zu inputs", nin);
+        ORT_OK(api, KernelContext_GetInput(ctx, k.gqa_in[i], &in[i]));
+        if (!in[i]) fail(ORT_INVALID_ARGUMENT, "GroupQueryAttention input %d is missing", i);
+    }
+    const mnb_gqa_problem& n = k.gprob;
+    std::vector<int64_t> qd, pkd, pvd, sd, cd, snd;
+    if (tensor_elem_type(api, in[0], &qd) != kElemFloat16 || qd.size() != 3 || qd[2] != k.gqa_packed)
+        fail(ORT_INVALID_ARGUMENT, "packed_qkv must be float16 [B, S, %lld]", (long long)k.gqa_packed);
+    const int64_t B = qd[0], S = qd[1];
+    if (B < 0 || S < 0) fail(ORT_INVALID_ARGUMENT, "packed_qkv has a negative extent");
+    if (tensor_elem_type(api, in[1], &pkd) != kElemFloat16 ||
+        tensor_elem_type(api, in[2], &pvd) != kElemFloat16 || pkd.size() != 4 || pkd != pvd ||
+        pkd[0] != B || pkd[1] != n.kv_num_heads || pkd[3] != n.head_dim || pkd[2] < 0)
+        fail(ORT_INVALID_ARGUMENT, "past_key/past_value must be float16 [%lld, %d, L, %d]",
+             (long long)B, n.kv_num_heads, n.head_dim);
+    if (tensor_elem_type(api, in[3], &sd) != kElemInt32 || sd.size() != 1 || sd[0] != B)
+        fail(ORT_INVALID_ARGUMENT, "seqlens_k must be int32 [%lld]", (long long)B);
+    int64_t max_seq = n.max_seq;
+    if (in[4]) {
+        if (tensor_elem_type(api, in[4], &cd) != kElemFloat16 ||
+            tensor_elem_type(api, in[5], &snd) != kElemFloat16 || cd.size() != 2 || cd != snd ||
+            cd[1] != n.rotary_dim / 2 || cd[0] < 1)
+            fail(ORT_INVALID_ARGUMENT, "cos_cache/sin_cache must be float16 [max_seq, %d]",
+                 n.rotary_dim / 2);
+        max_seq = cd[0];
+    }
+    mnb_gqa_problem p = n;
+    p.batch = B;
+    p.seq_len = S;
+    p.past_len_max = pkd[2];
+    p.present_len = k.gqa_present_len > 0 ? k.gqa_present_len : pkd[2] + S;
+    p.max_seq = max_seq;
+    mnb_ok(mnb_gqa_check(&p), "GroupQueryAttention shapes");
+    const int64_t od[3] = {B, S, (int64_t)n.num_heads * n.head_dim};
+    const int64_t kd[4] = {B, n.kv_num_heads, p.present_len, n.head_dim};
+    OrtValue* out[3] = {nullptr, nullptr, nullptr};
+    ORT_OK(api, KernelContext_GetOutput(ctx, k.gqa_out[0], od, 3, &out[0]));
+    ORT_OK(api, KernelContext_GetOutput(ctx, k.gqa_out[1], kd, 4, &out[1]));
+    ORT_OK(api, KernelContext_GetOutput(ctx, k.gqa_out[2], kd, 4, &out[2]));
+    if (!out[0] || !out[1] || !out[2]) fail(ORT_EP_FAIL, "ORT returned no output tensor");
+    if (B == 0 || S == 0) return;
+    void* o[3] = {nullptr, nullptr, nullptr};
+    for (int i = 0; i < 3; ++i) ORT_OK(api, GetTensorMutableData(out[i], &o[i]));
+    const bool past_dev = on_our_device(ep, in[1]);
+    if (past_dev != on_our_device(ep, in[2]))
+        fail(ORT_INVALID_ARGUMENT, "past_key and past_value live in different memories");
+    const bool pres_dev = on_our_device(ep, out[1]);
+    if (pres_dev != on_our_device(ep, out[2]))
+        fail(ORT_INVALID_ARGUMENT, "present_key and present_value live in different memories");
+    uint32_t flags = 0;
+    if (on_our_device(ep, in[0])) flags |= MNB_GQA_ON_DEVICE_QKV;
+    if (past_dev) flags |= MNB_GQA_ON_DEVICE_PAST;
+    if (on_our_device(ep, in[3])) flags |= MNB_GQA_ON_DEVICE_SEQLENS;
+    if (on_our_device(ep, out[0])) flags |= MNB_GQA_ON_DEVICE_OUT;
+    if (pres_dev) flags |= MNB_GQA_ON_DEVICE_PRESENT;
+    if (in[4]) {
+        if (on_our_device(ep, in[4]) != on_our_device(ep, in[5]))
+            fail(ORT_INVALID_ARGUMENT, "cos_cache and sin_cache live in different memories");
+        if (on_our_device(ep, in[4])) flags |= MNB_GQA_ON_DEVICE_CACHES;
+    }
+    std::lock_guard<std::mutex> lk(k.mu);
+    mnb_ok(mnb_session_run_gqa(ep->session, k.gcaches, &p, tensor_data(api, in[0]),
+                               tensor_data(api, in[1]), tensor_data(api, in[2]),
+                               static_cast<const int32_t*>(tensor_data(api, in[3])),
+                               in[4] ? tensor_data(api, in[4]) : nullptr,
+                               in[5] ? tensor_data(api, in[5]) : nullptr, o[0], o[1], o[2], flags),
+           "GroupQueryAttention kernels");
+    g_compute_count.fetch_add(1);
+}
+
 void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     const OrtApi* api = ep->api;
     if (env_flag("MI355X_EP_FORCE_COMPUTE_FAILURE"))
@@ -599,6 +713,10 @@ void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     }
     if (k.norm) {
         compute_norm(ep, k, ctx);
+        return;
+    }
+    if (k.gqa) {
+        compute_gqa(ep, k, ctx);
         return;
     }
     size_t nin = 0;
@@ -745,6 +863,21 @@ void get_capability(Ep* ep, const OrtGraph* graph, OrtEpGraphSupportInfo* suppor
             ort_check(api, ep->ep_api->EpGraphSupportInfo_AddNodesToFuse(support, &node, 1, &opts),
                       "EpGraphSupportInfo_AddNodesToFuse");
             claim_log("claim %s (%s)", name.c_str(), op.c_str());
+            continue;
+        }
+        if (is_gqa(op, dom)) {
+            const std::string name = node_string(api, node, api->Node_GetName);
+            const ClaimDecision d = claim_gqa(gqa_facts(api, node));
+            if (!d.claim) {
+                claim_log("decline %s: %s", name.c_str(), d.reason.c_str());
+                continue;
+            }
+            OrtNodeFusionOptions opts{};
+            opts.ort_version_supported = ep->factory->version;
+            opts.drop_constant_initializers = !ep->keep_constant_initializers;
+            ort_check(api, ep->ep_api->EpGraphSupportInfo_AddNodesToFuse(support, &node, 1, &opts),
+                      "EpGraphSupportInfo_AddNodesToFuse");
+            claim_log("claim %s (GroupQueryAttention)", name.c_str());
             continue;
         }
         if (is_qmoe(op, dom)) {
@@ -928,6 +1061,72 @@ std::unique_ptr<NodeKernel> compile_norm(Ep* ep, const OrtNode* node, const OrtN
     return k;
 }
 
+std::unique_ptr<NodeKernel> compile_gqa(Ep* ep, const OrtNode* node, const OrtNode* fused) {
+    const OrtApi* api = ep->api;
+    const GqaFacts f = gqa_facts(api, node);
+    GqaShape shape;
+    const ClaimDecision d = claim_gqa(f, &shape);
+    if (!d.claim)
+        fail(ORT_EP_FAIL, "compiled node fails the GroupQueryAttention claim predicate: %s",
+             d.reason.c_str());
+    auto k = std::make_unique<NodeKernel>();
+    k->gqa = true;
+    k->name = node_string(api, node, api->Node_GetName);
+    mnb_gqa_problem& p = k->gprob;
+    p.num_heads = (int32_t)f.num_heads;
+    p.kv_num_heads = (int32_t)f.kv_num_heads;
+    p.head_dim = (int32_t)shape.head_dim;
+    p.rotary_dim = (int32_t)shape.rotary_dim;
+    p.scale = shape.scale;
+    p.dtype = MNB_DTYPE_F16;
+    k->gqa_packed = shape.packed;
+    k->gqa_present_len = shape.declared_present_len;
+    const std::vector<size_t> in_map = fused_input_map(api, node, fused);
+    const std::vector<size_t> out_map = fused_output_map(api, node, fused);
+    const size_t body[6] = {0, 3, 4, 5, 7, 8};
+    // cos/sin: constant initializers are read now and uploaded once; otherwise fused inputs
+    const bool resident = f.inputs[7].constant && f.inputs[8].constant;
+    for (int i = 0; i < 6; ++i) {
+        if (i >= 4 && resident) continue;
+        k->gqa_in[i] = in_map[body[i]];
+        if (k->gqa_in[i] == SIZE_MAX)
+            fail(ORT_EP_FAIL, "GroupQueryAttention input %zu is not an input of the fused node", body[i]);
+    }
+    for (int i = 0; i < 3; ++i) {
+        k->gqa_out[i] = out_map[i];
+        if (k->gqa_out[i] == SIZE_MAX)
+            fail(ORT_EP_FAIL, "GroupQueryAttention output %d is not an output of the fused node", i);
+    }
+    const void* cos_host = nullptr;
+    const void* sin_host = nullptr;
+    size_t cos_bytes = 0, sin_bytes = 0;
+    p.max_seq = 1;
+    if (resident) {
+        const std::vector<const OrtValueInfo*> body_in = node_inputs(api, node);
+        const OrtValue* cv = nullptr;
+        const OrtValue* sv = nullptr;
+        ORT_OK(api, ValueInfo_GetInitializerValue(body_in[7], &cv));
+        ORT_OK(api, ValueInfo_GetInitializerValue(body_in[8], &sv));
+        if (!cv || !sv) fail(ORT_EP_FAIL, "cos_cache or sin_cache has no initializer value");
+        std::vector<int64_t> cd, sd;
+        if (tensor_elem_type(api, cv, &cd) != kElemFloat16 ||
+            tensor_elem_type(api, sv, &sd) != kElemFloat16 || cd.size() != 2 || cd != sd ||
+            cd[1] != p.rotary_dim / 2 || cd[0] < 1)
+            fail(ORT_EP_FAIL, "cos/sin caches are not float16 [max_seq, %d]", p.rotary_dim / 2);
+        p.max_seq = cd[0];
+        cos_host = tensor_data(api, cv);
+        sin_host = tensor_data(api, sv);
+        cos_bytes = tensor_bytes(api, cv);
+        sin_bytes = tensor_bytes(api, sv);
+    }
+    mnb_ok(mnb_gqa_check(&p), "GroupQueryAttention attributes");
+    mnb_ok(mnb_gqa_caches_upload(ep_session(ep), &p, cos_host, cos_bytes, sin_host, sin_bytes,
+                                 &k->gcaches),
+           "uploading the cos/sin caches at Compile");
+    k->resident = resident;
+    return k;
+}
+
 std::unique_ptr<NodeKernel> compile_one(Ep* ep, const OrtGraph* graph, const OrtNode* fused) {
     const OrtApi* api = ep->api;
     size_t n = 0;
@@ -939,6 +1138,7 @@ std::unique_ptr<NodeKernel> compile_one(Ep* ep, const OrtGraph* graph, const Ort
     const std::string dom = node_string(api, node, api->Node_GetDomain);
     if (is_qmoe(op, dom)) return compile_qmoe(ep, node, fused);
     if (is_skip_norm(op, dom) || is_plain_norm(op, dom)) return compile_norm(ep, node, fused);
+    if (is_gqa(op, dom)) return compile_gqa(ep, node, fused);
     const NodeFacts f = node_facts(api, node);
     const ClaimDecision d = claim_matmul_nbits(f, int8_path_available(f));
     if (!d.claim) fail(ORT_EP_FAIL, "compiled node fails the claim predicate: %s", d.reason.c_str());

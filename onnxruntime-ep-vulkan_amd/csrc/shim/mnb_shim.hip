@@ -1101,7 +1101,8 @@ int mnb_gqa_caches_upload(mnb_session* s, const mnb_gqa_problem* node, const voi
     int rc = mnb_gqa_check(&p);
     if (rc) return rc;
     const size_t want = (size_t)p.max_seq * (size_t)(p.rotary_dim / 2) * 2;
-    if (!cos_cache || cos_bytes != want || !sin_cache || sin_bytes != want)
+    const bool resident = cos_cache || sin_cache;
+    if (resident && (!cos_cache || cos_bytes != want || !sin_cache || sin_bytes != want))
         return fail(MNB_ERR_INVALID, "cos/sin caches hold %zu and %zu bytes, the node needs %zu "
                     "each", cos_bytes, sin_bytes, want);
     std::lock_guard<std::mutex> lk(s->mu);
@@ -1110,6 +1111,10 @@ int mnb_gqa_caches_upload(mnb_session* s, const mnb_gqa_problem* node, const voi
     if (!c) return fail(MNB_ERR_NOMEM, "cache allocation failed");
     c->s = s;
     c->node = p;
+    if (!resident) {
+        *out = c;
+        return MNB_OK;
+    }
     hipError_t e = hipMalloc(&c->cos, want);
     if (e == hipSuccess) e = hipMalloc(&c->sin, want);
     if (e == hipSuccess) e = hipMemcpyAsync(c->cos, cos_cache, want, hipMemcpyHostToDevice, s->stream);
@@ -1127,13 +1132,20 @@ int mnb_gqa_caches_upload(mnb_session* s, const mnb_gqa_problem* node, const voi
 
 int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_problem* shape,
                         const void* packed_qkv, const void* past_key, const void* past_value,
-                        const int32_t* seqlens_k, void* attn_out, void* present_key,
+                        const int32_t* seqlens_k, const void* cos_cache,
+                        const void* sin_cache, void* attn_out, void* present_key,
                         void* present_value, uint32_t on_device) {
     if (!s || !c || !shape) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
     const mnb_gqa_problem& n = c->node;
+    const bool own_caches = cos_cache || sin_cache;
+    if (own_caches && (!cos_cache || !sin_cache))
+        return fail(MNB_ERR_INVALID, "pass both cos_cache and sin_cache or neither");
+    if (!own_caches && !c->cos)
+        return fail(MNB_ERR_INVALID, "the node has no resident cos/sin caches; pass them");
     if (shape->num_heads != n.num_heads || shape->kv_num_heads != n.kv_num_heads ||
         shape->head_dim != n.head_dim || shape->rotary_dim != n.rotary_dim ||
-        shape->max_seq != n.max_seq || shape->scale != n.scale || shape->dtype != n.dtype)
+        (!own_caches && shape->max_seq != n.max_seq) || shape->scale != n.scale ||
+        shape->dtype != n.dtype)
         return fail(MNB_ERR_INVALID, "the call's head counts, head_dim, rotary_dim, max_seq, scale "
                                      "or dtype differ from the node's");
     const mnb_gqa_problem p = *shape;
@@ -1149,6 +1161,7 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
     const bool seq_dev = on_device & MNB_GQA_ON_DEVICE_SEQLENS;
     const bool out_dev = on_device & MNB_GQA_ON_DEVICE_OUT;
     const bool pres_dev = on_device & MNB_GQA_ON_DEVICE_PRESENT;
+    const bool cache_dev = on_device & MNB_GQA_ON_DEVICE_CACHES;
     // a present tensor given as its past tensor (same memory) is updated in place
     const bool in_place = p.past_len_max && present_key == past_key && past_dev == pres_dev;
     if (in_place != (p.past_len_max && present_value == past_value && past_dev == pres_dev))
@@ -1164,8 +1177,11 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
     const size_t pres_b = (size_t)p.batch * p.kv_num_heads * p.present_len * p.head_dim * 2;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     // inputs staged in the A buffer, outputs in the Y buffer
+    const size_t cache_b = own_caches && !cache_dev
+                               ? (size_t)p.max_seq * (size_t)(p.rotary_dim / 2) * 2 : 0;
     const size_t o_qkv = 0, o_pk = al(qkv_b), o_pv = o_pk + al(past_b), o_seq = o_pv + al(past_b);
-    const size_t in_total = o_seq + al(seq_b);
+    const size_t o_cos = o_seq + al(seq_b), o_sin = o_cos + al(cache_b);
+    const size_t in_total = o_sin + al(cache_b);
     const size_t o_out = 0, o_rk = al(out_b), o_rv = o_rk + al(pres_b);
     const size_t out_total = o_rv + al(pres_b);
     rc = grow(&s->a_dev, &s->a_cap, in_total);
@@ -1195,6 +1211,12 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
         pvd = up(past_value, o_pv, past_b);
     }
     if (!seq_dev) sd = static_cast<const int32_t*>(up(seqlens_k, o_seq, seq_b));
+    const void* cd = own_caches ? cos_cache : c->cos;
+    const void* snd = own_caches ? sin_cache : c->sin;
+    if (own_caches && !cache_dev) {
+        cd = up(cos_cache, o_cos, cache_b);
+        snd = up(sin_cache, o_sin, cache_b);
+    }
     if (e != hipSuccess) return hip_fail(e, "GroupQueryAttention input upload");
     if (in_place) {
         rkd = const_cast<void*>(pkd);
@@ -1203,7 +1225,7 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
         rkd = ob + o_rk;
         rvd = ob + o_rv;
     }
-    rc = mnb_gqa(&p, qd, pkd, pvd, sd, c->cos, c->sin, od, rkd, rvd, s->ws, s->ws_cap, s->stream);
+    rc = mnb_gqa(&p, qd, pkd, pvd, sd, cd, snd, od, rkd, rvd, s->ws, s->ws_cap, s->stream);
     if (rc) return rc;
     if (!out_dev) e = hipMemcpyAsync(attn_out, od, out_b, hipMemcpyDeviceToHost, s->stream);
     if (e == hipSuccess && !pres_dev && p.present_len) {

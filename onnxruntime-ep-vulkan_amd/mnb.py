@@ -91,7 +91,7 @@ class GqaProblem(C.Structure):
 
 
 GQA_ON_DEVICE_QKV, GQA_ON_DEVICE_PAST, GQA_ON_DEVICE_SEQLENS = 1, 2, 4
-GQA_ON_DEVICE_OUT, GQA_ON_DEVICE_PRESENT = 8, 16
+GQA_ON_DEVICE_OUT, GQA_ON_DEVICE_PRESENT, GQA_ON_DEVICE_CACHES = 8, 16, 32
 
 
 class MnbError(RuntimeError):
@@ -163,7 +163,7 @@ def load() -> C.CDLL:
                                             C.POINTER(vp)]),
         "mnb_gqa_caches_release": (C.c_int, [vp]),
         "mnb_session_run_gqa": (C.c_int, [vp, vp, C.POINTER(GqaProblem), vp, vp, vp, vp, vp, vp,
-                                          vp, C.c_uint32]),
+                                          vp, vp, vp, C.c_uint32]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)

@@ -299,3 +299,46 @@ def add_norm(h: Host, name: str, inp: dict, x_shape, *, skip=True, bias=False, w
     op = "SkipSimplifiedLayerNormalization" if skip else "SimplifiedLayerNormalization"
     h.node(op, domain, name, ins, outputs, attrs)
     return x_name, k_name, y_name, s_name
+
+
+def add_gqa(h: Host, name: str, inp: dict, *, num_heads: int, kv_num_heads: int, B, S,
+            past_shape_len, present_len, max_seq: int, rotary_dim: int, head_dim: int,
+            const_caches=True, attrs_over: dict | None = None, separate_kv=False,
+            extra_inputs=(), outputs=None, qkv_elem=FLOAT16, seqlens_elem=INT32,
+            cos_rank2=True):
+    """Adds a com.microsoft::GroupQueryAttention node in the packed-QKV form (the reference's
+    tests/ops/test_gqa.py model).  B, S, past_shape_len and present_len are declared extents
+    (-1 = symbolic); `inp` holds cos/sin when `const_caches` (then initializers)."""
+    D = head_dim
+    P = (num_heads + 2 * kv_num_heads) * D
+    n = lambda s: f"{name}_{s}"
+    h.value(n("qkv"), qkv_elem, (B, S, P))
+    h.value(n("past_k"), FLOAT16, (B, kv_num_heads, past_shape_len, D))
+    h.value(n("past_v"), FLOAT16, (B, kv_num_heads, past_shape_len, D))
+    h.value(n("seqlens"), seqlens_elem, (B,))
+    h.value(n("total"), INT32, ())
+    cshape = (max_seq, rotary_dim // 2) if cos_rank2 else (max_seq * rotary_dim // 2,)
+    h.value(n("cos"), FLOAT16, cshape, inp["cos"] if const_caches else None)
+    h.value(n("sin"), FLOAT16, cshape, inp["sin"] if const_caches else None)
+    ins = [n("qkv"), "", "", n("past_k"), n("past_v"), n("seqlens"), n("total"), n("cos"),
+           n("sin")]
+    if separate_kv:
+        h.value(n("k"), FLOAT16, (B, S, kv_num_heads * D))
+        ins[1] = n("k")
+    for nm, elem, shape in extra_inputs:
+        while len(ins) < 16 and len(ins) < int(nm.split("@")[1]):
+            ins.append("")
+        h.value(nm.split("@")[0], elem, shape)
+        ins.append(nm.split("@")[0])
+    h.value(n("out"), FLOAT16, (B, S, num_heads * D))
+    h.value(n("present_k"), FLOAT16, (B, kv_num_heads, present_len, D))
+    h.value(n("present_v"), FLOAT16, (B, kv_num_heads, present_len, D))
+    if outputs is None:
+        outputs = [n("out"), n("present_k"), n("present_v")]
+    attrs = {"num_heads": num_heads, "kv_num_heads": kv_num_heads, "do_rotary": 1,
+             "rotary_interleaved": 0, "local_window_size": -1}
+    attrs.update(attrs_over or {})
+    attrs = {k: v for k, v in attrs.items() if v is not None}
+    h.node("GroupQueryAttention", "com.microsoft", name, ins, outputs, attrs)
+    return {k: n(k) for k in ("qkv", "past_k", "past_v", "seqlens", "total", "cos", "sin", "out",
+                              "present_k", "present_v")}

@@ -165,8 +165,8 @@ def test_session_host_io(cuda):
         shape = mnb.gqa_problem(B, S, 8, 8 + S, 64, Nq, Nkv, D, 16)
         mnb.check(lib.mnb_session_run_gqa(sess, caches, C.byref(shape), inp["qkv"].ctypes.data,
                                           inp["past_k"].ctypes.data, inp["past_v"].ctypes.data,
-                                          inp["seqlens_k"].ctypes.data, attn.ctypes.data,
-                                          prk.ctypes.data, prv.ctypes.data, 0))
+                                          inp["seqlens_k"].ctypes.data, None, None,
+                                          attn.ctypes.data, prk.ctypes.data, prv.ctypes.data, 0))
         _check(inp, attn, prk, prv, Nq, Nkv)
         # shared buffer, host memory, in place
         pk, pv = inp["past_k"].copy(), inp["past_v"].copy()
@@ -174,10 +174,51 @@ def test_session_host_io(cuda):
         inp2 = dict(inp, seqlens_k=np.array([4, 2], np.int32))
         mnb.check(lib.mnb_session_run_gqa(sess, caches, C.byref(shape), inp["qkv"].ctypes.data,
                                           pk.ctypes.data, pv.ctypes.data,
-                                          inp2["seqlens_k"].ctypes.data, attn.ctypes.data,
-                                          pk.ctypes.data, pv.ctypes.data, 0))
+                                          inp2["seqlens_k"].ctypes.data, None, None,
+                                          attn.ctypes.data, pk.ctypes.data, pv.ctypes.data, 0))
         _check(inp2, attn, pk, pv, Nq, Nkv)
     finally:
         if caches.value:
             lib.mnb_gqa_caches_release(caches)
+        lib.mnb_session_destroy(sess)
+
+
+def test_session_per_call_caches(cuda):
+    """A node without resident caches (cos/sin are graph inputs, as in the reference's
+    tests/ops/test_gqa.py): the caches come with each call, from host or device memory."""
+    import mnb
+    import torch
+
+    lib = mnb.load()
+    Nq, Nkv, D = 8, 2, 32
+    inp = _inputs(1, 1, [4], Nq, Nkv, D, past_buffer=4, rotary_dim=16, max_seq=64, seed=11)
+    sess = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(sess)))
+    rec = C.c_void_p()
+    try:
+        node = mnb.gqa_problem(0, 0, 0, 0, 64, Nq, Nkv, D, 16)
+        mnb.check(lib.mnb_gqa_caches_upload(sess, C.byref(node), None, 0, None, 0, C.byref(rec)))
+        shape = mnb.gqa_problem(1, 1, 4, 5, 64, Nq, Nkv, D, 16)
+        attn = np.empty((1, 1, Nq * D), np.float16)
+        prk = np.zeros((1, Nkv, 5, D), np.float16)
+        prv = np.zeros((1, Nkv, 5, D), np.float16)
+        args = [inp["qkv"].ctypes.data, inp["past_k"].ctypes.data, inp["past_v"].ctypes.data,
+                inp["seqlens_k"].ctypes.data]
+        # resident caches absent and none passed: refused
+        assert lib.mnb_session_run_gqa(sess, rec, C.byref(shape), *args, None, None,
+                                       attn.ctypes.data, prk.ctypes.data, prv.ctypes.data, 0) != 0
+        mnb.check(lib.mnb_session_run_gqa(sess, rec, C.byref(shape), *args, inp["cos"].ctypes.data,
+                                          inp["sin"].ctypes.data, attn.ctypes.data,
+                                          prk.ctypes.data, prv.ctypes.data, 0))
+        _check(inp, attn, prk, prv, Nq, Nkv)
+        cd, sd = _t(inp["cos"], cuda), _t(inp["sin"], cuda)
+        attn2 = np.empty_like(attn)
+        mnb.check(lib.mnb_session_run_gqa(sess, rec, C.byref(shape), *args, cd.data_ptr(),
+                                          sd.data_ptr(), attn2.ctypes.data, prk.ctypes.data,
+                                          prv.ctypes.data, mnb.GQA_ON_DEVICE_CACHES))
+        torch.cuda.synchronize()
+        assert np.array_equal(attn, attn2)
+    finally:
+        if rec.value:
+            lib.mnb_gqa_caches_release(rec)
         lib.mnb_session_destroy(sess)
