@@ -406,7 +406,7 @@ def main() -> int:
     acc4 = {"config": "M=16 K=8192 N=3072 int4 bs128 zp, accuracy_level=4", "bytes": a_bytes,
             "us": round(a_us, 3), "GB/s": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
             "int_TOPS": round(2.0 * am * an * ak / (a_us * 1e-6) / 1e12, 2),
-            "kernel": "quantize_a_int8 + group_gemv<i8>",
+            "kernel": "quantize_a_int8 + strip_gemv<i8>",
             "roofline": {"bound": "hbm", "achieved": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(a_bytes / (a_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
@@ -488,7 +488,7 @@ def main() -> int:
                       "int4 bs32, biases, SwiGLU alpha 1.702 beta 1 limit 7",
             "bytes": q_bytes, "us": round(q_us, 2),
             "GB/s": round(q_bytes / (q_us * 1e-6) / 1e9, 1),
-            "kernels": "qmoe_route + group_gemv (fc1) + qmoe_swiglu + group_gemv (fc2) + "
+            "kernels": "qmoe_route + strip_gemv (fc1) + qmoe_swiglu + strip_gemv (fc2) + "
                        "qmoe_combine",
             "roofline": {"bound": "hbm", "achieved": round(q_bytes / (q_us * 1e-6) / 1e9, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -55,6 +55,8 @@ extern "C" {
 #define MNB_KERNEL_ACC4_I8 4     /* accuracy_level 4: int8 A, int8 MFMA, int32 block dots */
 #define MNB_KERNEL_GEMV_STREAM 5 /* fp16, M <= 4: coalesced 16-byte-chunk streaming GEMV */
 #define MNB_KERNEL_GROUP_MFMA 6  /* fp16, int4, block >= 32: row-tiled 16x16x32 MFMA GEMV */
+#define MNB_KERNEL_STRIP_MFMA 7  /* fp16, int4, block >= 32, 5..16 rows: activations held in
+                                    registers across a run of 16-column strips */
 
 /* One MatMulNBits node: the attributes plus the row count of this call. */
 typedef struct mnb_problem {

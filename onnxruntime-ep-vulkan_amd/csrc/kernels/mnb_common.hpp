@@ -23,6 +23,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f16x2 as_h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
 __device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
@@ -143,6 +144,33 @@ __device__ __forceinline__ float group_sum(float v, int G) {
         v = __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
     }
     return v;
+}
+
+// 4 x 4 transpose of dwords across the lane rows (16 lanes each) of a wavefront: on return,
+// v[t] of a lane in row g is what v[g] of the same column lane in row t held.
+__device__ __forceinline__ void transpose_rows(uint32_t& v0, uint32_t& v1, uint32_t& v2,
+                                               uint32_t& v3) {
+    auto a = __builtin_amdgcn_permlane32_swap(v0, v2, false, false);
+    v0 = a[0];
+    v2 = a[1];
+    auto b = __builtin_amdgcn_permlane32_swap(v1, v3, false, false);
+    v1 = b[0];
+    v3 = b[1];
+    auto c = __builtin_amdgcn_permlane16_swap(v0, v1, false, false);
+    v0 = c[0];
+    v1 = c[1];
+    auto d = __builtin_amdgcn_permlane16_swap(v2, v3, false, false);
+    v2 = d[0];
+    v3 = d[1];
+}
+
+// Eight int4 weights (one dword, natural order e0..e7) as int8 (q - z) in the order
+// [e0, e2, e4, e6, e1, e3, e5, e7]; zb = (128 - z) in every byte.
+__device__ __forceinline__ i32x2 qz_i8(uint32_t w, uint32_t zb) {
+    // per byte: (q + 128 - z) has no carry for q, z in 0..15; XOR 0x80 gives (q - z) mod 256
+    const uint32_t lo = ((w & 0x0F0F0F0Fu) + zb) ^ 0x80808080u;
+    const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) + zb) ^ 0x80808080u;
+    return i32x2{(int32_t)lo, (int32_t)hi};
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

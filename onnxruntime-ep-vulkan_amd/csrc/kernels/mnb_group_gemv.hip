@@ -32,38 +32,7 @@
 namespace mnb {
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
 
-namespace {
-
-// 4 x 4 transpose of dwords across the lane rows (16 lanes each) of a wavefront: on return,
-// v[t] of a lane in row g is what v[g] of the same column lane in row t held.
-__device__ __forceinline__ void transpose_rows(uint32_t& v0, uint32_t& v1, uint32_t& v2,
-                                               uint32_t& v3) {
-    auto a = __builtin_amdgcn_permlane32_swap(v0, v2, false, false);
-    v0 = a[0];
-    v2 = a[1];
-    auto b = __builtin_amdgcn_permlane32_swap(v1, v3, false, false);
-    v1 = b[0];
-    v3 = b[1];
-    auto c = __builtin_amdgcn_permlane16_swap(v0, v1, false, false);
-    v0 = c[0];
-    v1 = c[1];
-    auto d = __builtin_amdgcn_permlane16_swap(v2, v3, false, false);
-    v2 = d[0];
-    v3 = d[1];
-}
-
-// Eight int4 weights (one dword, natural order e0..e7) as int8 (q - z) in the order
-// [e0, e2, e4, e6, e1, e3, e5, e7] (the order quantize_a_int8 writes activations in).
-__device__ __forceinline__ i32x2 qz_i8(uint32_t w, uint32_t zb) {
-    // per byte: (q + 128 - z) has no carry for q, z in 0..15; XOR 0x80 gives (q - z) mod 256
-    const uint32_t lo = ((w & 0x0F0F0F0Fu) + zb) ^ 0x80808080u;
-    const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) + zb) ^ 0x80808080u;
-    return i32x2{(int32_t)lo, (int32_t)hi};
-}
-
-}  // namespace
 
 // T: activation / scale / output type (f16, or float for the int8 path's fp32 nodes).
 // I8: false = fp16 activations (A is f16 [a_rows][K]); true = int8 activations (A is the
@@ -577,6 +546,16 @@ hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const 
                                  int64_t k, int bits, int bs, hipStream_t st) {
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
     if (m == 0 || groups == 0) return hipSuccess;
+    // Up to 16 rows per group (by the mean for grouped rows): the strip GEMV, one 16-row tile
+    // per group plus more tiles for the groups that exceed it.
+    const int64_t ng = offsets ? groups : 1;
+    const int64_t bound = offsets ? max_rows : m;
+    const int64_t hint = offsets ? std::min<int64_t>(bound, 2 * ((m + ng - 1) / ng)) : m;
+    StripGeom sg;
+    if (hint <= 16 && !strip_gemv_forced_off() &&
+        strip_geometry(n, k, ng, bound, false, bs, z != nullptr, &sg))
+        return launch_strip_gemv(sg, false, a, nullptr, row_index, offsets, b, s, z, y, m, n, k,
+                                 bs, st);
     const GroupGeom g =
         group_geometry(offsets ? max_rows : m, n, k, offsets ? groups : 1, false, bs, false);
     return group_bs<f16, false>(bs, g, a, nullptr, row_index, offsets, b, s, z, y, m, n, k,
@@ -590,6 +569,11 @@ hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index
                                          int64_t n, int64_t k, int bits, int bs, hipStream_t st) {
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
     if (m == 0 || groups == 0) return hipSuccess;
+    StripGeom sg;
+    if (rows_hint <= 16 && !strip_gemv_forced_off() &&
+        strip_geometry(n, k, groups, rows_bound, false, bs, z != nullptr, &sg))
+        return launch_strip_gemv(sg, false, a, nullptr, row_index, offsets, b, s, z, y, m, n, k,
+                                 bs, st);
     // Tile height from the expected rows per group; enough row tiles for the bound (tiles past
     // a group's last row leave at once).
     GroupGeom g = group_geometry(std::max<int64_t>(1, std::min(rows_hint, rows_bound)), n, k,
@@ -678,6 +662,18 @@ hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* 
     if (m == 0) return hipSuccess;
     const GroupGeom g = group_geometry(m, n, k, 1, true, bs, true);
     const Acc4Layout l = acc4_layout(g, m, k, bs);
+    // fp16 with at most 16 rows: the quantiser's codes and scales (the workspace's first two
+    // parts) feed the strip GEMV.
+    StripGeom sg;
+    if (a_f16 && m <= 16 && !strip_gemv_forced_off() &&
+        strip_geometry(n, k, 1, m, true, bs, z != nullptr, &sg)) {
+        uint8_t* ws = static_cast<uint8_t*>(workspace);
+        int8_t* qa = reinterpret_cast<int8_t*>(ws + l.qa);
+        float* sa = reinterpret_cast<float*>(ws + l.sa);
+        hipError_t e = launch_quantize_a_int8(a, true, qa, sa, nullptr, true, m, k, bs, st);
+        if (e != hipSuccess) return e;
+        return launch_strip_gemv(sg, true, qa, sa, nullptr, nullptr, b, s, z, y, m, n, k, bs, st);
+    }
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     int8_t* qa = reinterpret_cast<int8_t*>(ws + l.qa);
     float* sa = reinterpret_cast<float*>(ws + l.sa);

@@ -85,6 +85,27 @@ hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index
                                          const void* s, const uint8_t* z, void* y, int64_t m,
                                          int64_t n, int64_t k, int bits, int bs,
                                          hipStream_t stream);
+// Launch shape of the strip GEMV (mnb_strip_gemv.hip): at most 16 rows per group, the
+// activations of a wavefront's K share held in registers across a run of column strips.
+struct StripGeom {
+    int waves;           // wavefronts per workgroup (split K)
+    int qw;              // 128-k quads per wavefront (register arrays of the instantiation)
+    int strips;          // 16-column strips per workgroup
+    int64_t gx, gy, gz;  // runs of strips, groups, 16-row tiles
+    size_t lds;
+};
+bool strip_geometry(int64_t n, int64_t k, int64_t groups, int64_t rows_bound, bool i8, int bs,
+                    bool has_zp, StripGeom* out);
+// True when MNB_FORCE_KERNEL=group asks for the row-tiled GEMV instead.
+bool strip_gemv_forced_off();
+// fp16 scales and Y; A is fp16, or for i8 (accuracy_level = 4) the permuted int8 codes of
+// quantize_a_int8 with their fp32 scales a_scale [rows][K / bs].
+hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const float* a_scale,
+                             const int32_t* row_index,
+                             const int32_t* offsets, const uint8_t* b, const void* s,
+                             const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bs,
+                             hipStream_t stream);
+
 // cnt / ncnt: split-K counters of a following int8 GEMV, cleared by the quantiser (may be null).
 hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,

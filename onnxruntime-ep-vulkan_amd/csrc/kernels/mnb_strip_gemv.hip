@@ -1,0 +1,438 @@
+// Strip GEMV: MatMulNBits with at most 16 rows per group on gfx950 MFMA -- dense decode batches,
+// routed experts (rows grouped by expert) and the accuracy_level = 4 int8 path.  int4 weights,
+// block_size >= 32, fp16 activations (or their int8 codes) and fp16 output.
+//
+// Work split.  A workgroup of W wavefronts owns one group (expert), one 16-row tile and a run of
+// S strips of 16 output columns.  K is cut into 128-k quads that are split over the W
+// wavefronts; each wavefront loads the MFMA A operands of its quads once, keeps them in
+// registers for the whole run and streams the weights of its quads strip after strip, so the
+// activations are read once per workgroup rather than once per strip.
+//
+// Loads.  For quad q, lane (n = l % 16, g = l / 16) reads the 16 bytes of chunk 4q + g (32 int4
+// weights) of column n: one instruction covers 16 runs of 64 contiguous bytes.  A 4 x 4 dword
+// transpose across the lane rows turns the four chunks of a quad into the B operands of four
+// 16x16x32 MFMAs (lane (n, g) supplies k = 8g .. 8g + 7 of each chunk).  The weights of the
+// next two strips (one, where registers are short) are in flight while a strip is computed.  The run's scales and zero points
+// are one contiguous byte range per tensor (ORT's [N][K/bs] layouts); the workgroup copies them
+// into LDS with 16-byte loads issued behind the first strip's weights.
+//
+// Arithmetic.  fp16: exact (q - zp) operands on v_mfma_f32_16x16x32_f16, the fp32 partial of a
+// block scaled once by the block's scale (the reference kernel's per-block fp32 partial,
+// rust/shaders/glsl/templates/q_gemv.comp:571-579).  int8: the activations arrive as the codes
+// and per-(row, block) scales of quantize_a_int8 (written in the weights' [0,2,4,6,1,3,5,7]
+// order once per call -- quantising inside every workgroup would repeat it per run of strips);
+// v_mfma_i32_16x16x32_i8 gives exact int32 block dots, scaled by a_scale * b_scale in fp32.
+//
+// Reduction.  Each wavefront's 16 x 16 partial tile of a strip goes to LDS; every four strips
+// the W partials are summed in wavefront order (run-to-run deterministic) and stored, so the
+// LDS buffer does not grow with the run and runs can be long.
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "mnb_common.hpp"
+#include "mnb_launch.hpp"
+
+namespace mnb {
+
+// Threads per workgroup the instantiation is compiled for: the register arrays grow with QW
+// (A operands 16 VGPRs per quad in fp16, 8 in int8; the strips of weights in flight 4 per quad
+// each), and 1024 threads leave each wavefront 128 VGPRs.
+constexpr int strip_max_threads(bool i8, int bs, int qw) {
+    return (i8 ? (qw <= 3 || (qw <= 4 && bs == 128)) : qw <= 2) ? 1024 : 512;
+}
+
+// Strips whose partial tiles are summed together: W x period KB of LDS, 32 KB.
+__host__ __device__ constexpr int strip_period(int waves) { return waves >= 32 ? 1 : 32 / waves; }
+
+namespace {
+
+// Copies `bytes` bytes from global memory into LDS with 16-byte loads (when `vec`: both ends
+// 16-byte aligned but for the byte tail), a batch of loads in flight per thread.
+__device__ __forceinline__ void copy_to_lds(uint8_t* __restrict__ dst,
+                                            const uint8_t* __restrict__ src, int bytes, bool vec) {
+    int done = 0;
+    if (vec) {
+        constexpr int kB = 4;
+        const int nvec = bytes >> 4;
+        const u32x4* __restrict__ s4 = reinterpret_cast<const u32x4*>(src);
+        u32x4* __restrict__ d4 = reinterpret_cast<u32x4*>(dst);
+        for (int base = (int)threadIdx.x; base < nvec; base += kB * (int)blockDim.x) {
+            u32x4 v[kB];
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                const int i = base + b * (int)blockDim.x;
+                v[b] = s4[i < nvec ? i : nvec - 1];
+            }
+#pragma unroll
+            for (int b = 0; b < kB; ++b) {
+                const int i = base + b * (int)blockDim.x;
+                if (i < nvec) d4[i] = v[b];
+            }
+        }
+        done = nvec << 4;
+    }
+    for (int i = done + (int)threadIdx.x; i < bytes; i += (int)blockDim.x) dst[i] = src[i];
+}
+
+}  // namespace
+
+template <bool I8, int BS, bool HAS_ZP, int QW>
+__global__ void __launch_bounds__(strip_max_threads(I8, BS, QW))
+strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
+           const int32_t* __restrict__ row_index,
+           const int32_t* __restrict__ offsets, const uint8_t* __restrict__ B,
+           const f16* __restrict__ Sc, const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M,
+           int N, int K, int S, int vec_s, int vec_z) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
+    constexpr int BPQ = 4 / CPB;                         // blocks per quad
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int W = blockDim.x >> 6;
+    const int kPeriod = strip_period(W);
+    const int nl = lane & 15;
+    const int g = lane >> 4;
+    const int chunks = K >> 5;
+    const int Q = (chunks + 3) >> 2;
+    const int bpc = K / BS;
+    const int zpb = (bpc + 1) >> 1;
+    const int n0 = blockIdx.x * S * 16;
+    const int ns = min(S, (N - n0 + 15) >> 4);           // strips of this run (>= 1)
+
+    int row_lo = 0, row_hi = M;
+    int64_t wb = 0, ws = 0, wz = 0;
+    if (offsets) {
+        const int e = blockIdx.y;
+        row_lo = offsets[e];
+        row_hi = offsets[e + 1];
+        wb = (int64_t)e * N * (K / 2);
+        ws = (int64_t)e * N * bpc;
+        wz = (int64_t)e * N * zpb;
+    }
+    const int r0 = row_lo + blockIdx.z * 16;
+    if (r0 >= row_hi) return;                            // the whole workgroup, before a barrier
+
+    const int q_lo = (wave * Q) / W;
+    const int q_n = ((wave + 1) * Q) / W - q_lo;         // quads of this wavefront, <= QW
+    const uint8_t* __restrict__ Bg = B + wb;
+
+    auto fetch = [&](int s, u32x4(&buf)[QW]) {
+        const int col = min(n0 + 16 * s + nl, N - 1);
+        const uint8_t* bc = Bg + (int64_t)col * (K / 2);
+#pragma unroll
+        for (int j = 0; j < QW; ++j) {
+            if (j < q_n) {                               // wave-uniform
+                const int c = min(4 * (q_lo + j) + g, chunks - 1);
+                buf[j] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(bc + 16 * (int64_t)c));
+            }
+        }
+    };
+
+    // Strips in flight ahead of the one computed: two, fewer where the registers are short
+    // (the int8 path's runs are usually a single strip).
+    constexpr int AHEAD = I8 ? (QW >= 4 ? 0 : 1) : (QW > 3 ? 1 : 2);
+    u32x4 b0[QW], b1[AHEAD > 0 ? QW : 1], b2[AHEAD > 1 ? QW : 1];
+    fetch(0, b0);
+    if constexpr (AHEAD > 1) {
+        if (ns > 1) fetch(1, b1);
+    }
+
+    // ---- A operands of this wavefront's quads: row nl of the tile, k = 32c + 8g .. + 8 ----
+    int rr = r0 + nl;
+    rr = rr < row_hi ? rr : row_hi - 1;
+    const int arow = row_index ? row_index[rr] : rr;
+    f16x8 af[I8 ? 1 : QW][4];
+    i32x2 aq[I8 ? QW : 1][4];
+    float sar[I8 ? QW : 1][I8 ? BPQ : 1];                // int8: a_scale of (row nl, block)
+#pragma unroll
+    for (int j = 0; j < QW; ++j) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int c = 4 * (q_lo + j) + t;
+            const bool live = j < q_n && c < chunks;
+            const int64_t off = (int64_t)arow * K + 32 * (int64_t)min(c, chunks - 1) + 8 * g;
+            if constexpr (!I8) {
+                const f16x8 v = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(Av) + off);
+                af[j][t] = live ? v : f16x8{};
+            } else {
+                const u32x2 v = *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(Av) + off);
+                aq[j][t] = live ? i32x2{(int32_t)v.x, (int32_t)v.y} : i32x2{0, 0};
+            }
+        }
+        if constexpr (I8) {
+#pragma unroll
+            for (int b = 0; b < BPQ; ++b) {
+                const int blk = min((128 * (q_lo + j) + BS * b) / BS, bpc - 1);
+                const float v = a_scale[(int64_t)arow * bpc + blk];
+                sar[j][b] = j < q_n ? v : 0.f;
+            }
+        }
+    }
+
+    // ---- the run's scales and zero points into LDS ----
+    const int ncols = min(16 * S, N - n0);
+    const int s_bytes = (16 * S * bpc * 2 + 15) & ~15;
+    const int z_bytes = HAS_ZP ? ((16 * S * zpb + 15) & ~15) : 0;
+    f16* const sS = reinterpret_cast<f16*>(smem);
+    uint8_t* const sZ = smem + s_bytes;
+    f32x4* const red = reinterpret_cast<f32x4*>(smem + s_bytes + z_bytes);
+    copy_to_lds(smem, reinterpret_cast<const uint8_t*>(Sc + ws + (int64_t)n0 * bpc),
+                ncols * bpc * 2, vec_s != 0);
+    if constexpr (HAS_ZP)
+        copy_to_lds(sZ, Z + wz + (int64_t)n0 * zpb, ncols * zpb, vec_z != 0);
+
+    __syncthreads();
+
+    auto compute = [&](int s, const u32x4(&buf)[QW]) {
+        const int cl = 16 * s + nl;                      // column within the run
+        const f16* __restrict__ ls = sS + cl * bpc;
+        const uint8_t* __restrict__ lz = sZ + cl * zpb;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < QW; ++j) {
+            if (j >= q_n) break;                         // wave-uniform
+            uint32_t v0 = buf[j].x, v1 = buf[j].y, v2 = buf[j].z, v3 = buf[j].w;
+            transpose_rows(v0, v1, v2, v3);
+            const uint32_t wt[4] = {v0, v1, v2, v3};
+            if constexpr (!I8) {
+                f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int c = 4 * (q_lo + j) + t;
+                    const int blk = min((32 * c) / BS, bpc - 1);
+                    int z = 8;
+                    if constexpr (HAS_ZP) z = (int)((lz[blk >> 1] >> ((blk & 1) * 4)) & 0xFu);
+                    const f16x2 zo = zoff4(z);
+                    f16x8 bop;
+                    bop.s01 = nib_pair<0>(wt[t], zo);
+                    bop.s23 = nib_pair<1>(wt[t], zo);
+                    bop.s45 = nib_pair<2>(wt[t], zo);
+                    bop.s67 = nib_pair<3>(wt[t], zo);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[j][t], bop, d, 0, 0, 0);
+                    if ((t + 1) % CPB == 0) {            // block end: scale its partial once
+                        const float sc = (float)ls[blk];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(d[q], sc, acc[q]);
+                        d = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+                }
+            } else {
+                i32x4 dot = {0, 0, 0, 0};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int c = 4 * (q_lo + j) + t;
+                    const int blk = min((32 * c) / BS, bpc - 1);
+                    int z = 8;
+                    if constexpr (HAS_ZP) z = (int)((lz[blk >> 1] >> ((blk & 1) * 4)) & 0xFu);
+                    const uint32_t zb = (uint32_t)(128 - z) * 0x01010101u;
+                    const i32x2 bop = qz_i8(wt[t], zb);
+                    dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, aq[j][t]),
+                                                                __builtin_bit_cast(long, bop), dot,
+                                                                0, 0, 0);
+                    if ((t + 1) % CPB == 0) {
+                        const float sb = (float)ls[blk];
+                        const int b = t / CPB;
+                        // output rows 4g .. 4g + 3 take the scales of lanes 4g .. 4g + 3
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float sa = __shfl(sar[j][b], 4 * g + q, 64);
+                            acc[q] = __builtin_fmaf((float)dot[q], sa * sb, acc[q]);
+                        }
+                        dot = i32x4{0, 0, 0, 0};
+                    }
+                }
+            }
+        }
+        red[(wave * kPeriod + s % kPeriod) * 64 + lane] = acc;
+    };
+
+    for (int s = 0; s < ns; ++s) {
+        if constexpr (AHEAD > 1) {
+            if (s + 2 < ns) fetch(s + 2, b2);
+        } else if constexpr (AHEAD == 1) {
+            if (s + 1 < ns) fetch(s + 1, b1);
+        } else {
+            if (s > 0) fetch(s, b0);
+        }
+        compute(s, b0);
+        if constexpr (AHEAD > 0) {
+#pragma unroll
+            for (int j = 0; j < QW; ++j) {
+                b0[j] = b1[j];
+                if constexpr (AHEAD > 1) b1[j] = b2[j];
+            }
+        }
+        // Every kPeriod strips (and at the end of the run): fixed-order sum of the W partial
+        // tiles of those strips, stored, then the partial buffer is free again.  The weights
+        // of the next strips stay in flight across the two barriers.
+        if ((s + 1) % kPeriod == 0 || s + 1 == ns) {
+            const int p0 = s - s % kPeriod;
+            const int np = s + 1 - p0;
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < np * 64; idx += blockDim.x) {
+                const int i = idx >> 6;
+                const int ll = idx & 63;
+                f32x4 sum = red[i * 64 + ll];
+                for (int w = 1; w < W; ++w) sum += red[(w * kPeriod + i) * 64 + ll];
+                const int col = n0 + 16 * (p0 + i) + (ll & 15);
+                if (col >= N) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = r0 + 4 * (ll >> 4) + q;
+                    if (r < row_hi) Y[(int64_t)r * N + col] = (f16)sum[q];
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Host side
+// ------------------------------------------------------------------------------------------
+
+namespace {
+
+constexpr int kQW[] = {1, 2, 3, 4, 6};
+
+int round_qw(int64_t q) {
+    for (int v : kQW)
+        if (q <= v) return v;
+    return 0;
+}
+
+}  // namespace
+
+bool strip_gemv_forced_off() {
+    const char* v = std::getenv("MNB_FORCE_KERNEL");
+    return v && !std::strcmp(v, "group");
+}
+
+bool strip_geometry(int64_t n, int64_t k, int64_t groups, int64_t rows_bound, bool i8, int bs,
+                    bool has_zp, StripGeom* out) {
+    if (bs != 32 && bs != 64 && bs != 128) return false;
+    if (k <= 0 || k % 32 || k % bs || n <= 0 || groups <= 0) return false;
+    const int64_t q = (k / 32 + 3) / 4;
+    StripGeom g{};
+    // The fewest wavefronts that keep a wavefront's quads at 4 or fewer, else the most that
+    // the instantiation's register budget allows.
+    for (int pass = 0; pass < 2 && g.waves == 0; ++pass) {
+        for (int w : {4, 8, 16}) {
+            const int ww = pass == 0 ? w : 20 - w;       // second pass: 16, 12, 8, 4
+            const int qw = round_qw((q + ww - 1) / ww);
+            if (qw == 0 || (pass == 0 && qw > 4)) continue;
+            if (64 * ww > strip_max_threads(i8, bs, qw)) continue;
+            g.waves = ww;
+            g.qw = qw;
+            break;
+        }
+    }
+    if (g.waves == 0) return false;
+    const int64_t nstrips = (n + 15) / 16;
+    const int64_t bpc = k / bs;
+    const int64_t zpb = (bpc + 1) / 2;
+    // Runs as long as the 64 KB of LDS (partial tiles, then staged scales and zero points)
+    // allow, sized so that the launch fills whole rounds of resident workgroups (by registers
+    // and LDS).
+    const int64_t per_strip = 16 * (bpc * 2 + (has_zp ? zpb : 0)) + 32;
+    const int64_t red_bytes = (int64_t)g.waves * strip_period(g.waves) * 64 * sizeof(f32x4);
+    const int64_t s_max =
+        std::max<int64_t>(1, std::min<int64_t>(32, (64 * 1024 - red_bytes) / per_strip));
+    const int waves_per_simd = g.qw <= 3 ? 4 : (g.qw == 4 ? 3 : 2);
+    const int64_t by_regs = std::max(1, 4 * waves_per_simd / g.waves);
+    const int64_t by_lds = std::max<int64_t>(1, (160 * 1024) / (s_max * per_strip + red_bytes + 64));
+    const int64_t slots = 256 * std::min(by_regs, by_lds);
+    const int64_t total = groups * nstrips;
+    const int64_t rounds = std::max<int64_t>(1, (total + slots * s_max - 1) / (slots * s_max));
+    int64_t s = (total + rounds * slots - 1) / (rounds * slots);
+    s = std::max<int64_t>(1, std::min<int64_t>(s, std::min<int64_t>(s_max, nstrips)));
+    g.strips = (int)s;
+    g.gx = (nstrips + s - 1) / s;
+    g.gy = groups;
+    g.gz = (std::max<int64_t>(rows_bound, 1) + 15) / 16;
+    g.lds = (size_t)((16 * s * bpc * 2 + 15) & ~15) + (has_zp ? (size_t)((16 * s * zpb + 15) & ~15) : 0) +
+            (size_t)red_bytes;
+    if (g.lds > 64 * 1024) return false;
+    if (g.gx > 0x7fffffff || g.gy > 65535 || g.gz > 65535) return false;
+    *out = g;
+    return true;
+}
+
+namespace {
+
+template <bool I8, int BS, bool HAS_ZP, int QW>
+hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
+                    const int32_t* row_index,
+                    const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
+                    void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
+                    hipStream_t st) {
+    auto kern = strip_gemv<I8, BS, HAS_ZP, QW>;
+    if (g.lds > 64 * 1024) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)g.gx, (unsigned)g.gy, (unsigned)g.gz);
+    const dim3 block((unsigned)(64 * g.waves), 1, 1);
+    hipLaunchKernelGGL(kern, grid, block, g.lds, st, a, a_scale, row_index,
+                       offsets, b, static_cast<const f16*>(s), z, static_cast<f16*>(y), (int)m,
+                       (int)n, (int)k, g.strips, vec_s, vec_z);
+    return hipGetLastError();
+}
+
+template <bool I8, int BS, bool HAS_ZP>
+hipError_t strip_qw(const StripGeom& g, const void* a, const float* a_scale,
+                    const int32_t* row_index,
+                    const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
+                    void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
+                    hipStream_t st) {
+    switch (g.qw) {
+        case 1: return strip_go<I8, BS, HAS_ZP, 1>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+        case 2: return strip_go<I8, BS, HAS_ZP, 2>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+        case 3: return strip_go<I8, BS, HAS_ZP, 3>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+        case 4: return strip_go<I8, BS, HAS_ZP, 4>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+        case 6: return strip_go<I8, BS, HAS_ZP, 6>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <bool I8>
+hipError_t strip_bs(int bs, const StripGeom& g, const void* a, const float* a_scale,
+                    const int32_t* row_index,
+                    const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
+                    void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
+                    hipStream_t st) {
+#define MNB_STRIP_ZP(BS_)                                                                          \
+    return z ? strip_qw<I8, BS_, true>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st) \
+             : strip_qw<I8, BS_, false>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st)
+    switch (bs) {
+        case 32: MNB_STRIP_ZP(32);
+        case 64: MNB_STRIP_ZP(64);
+        case 128: MNB_STRIP_ZP(128);
+        default: return hipErrorInvalidValue;
+    }
+#undef MNB_STRIP_ZP
+}
+
+}  // namespace
+
+hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const float* a_scale,
+                             const int32_t* row_index,
+                             const int32_t* offsets, const uint8_t* b, const void* s,
+                             const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bs,
+                             hipStream_t st) {
+    if (m == 0) return hipSuccess;
+    if (reinterpret_cast<uintptr_t>(a) % (i8 ? 8 : 16) || reinterpret_cast<uintptr_t>(b) % 16 ||
+        (i8 && !a_scale))
+        return hipErrorInvalidValue;
+    const int64_t bpc = k / bs;
+    const int64_t zpb = (bpc + 1) / 2;
+    // 16-byte copies of the scales / zero points need every run's first byte aligned: the
+    // tensor base, and each group's slice when there are several groups.
+    const bool multi = offsets != nullptr && g.gy > 1;
+    const int vec_s = reinterpret_cast<uintptr_t>(s) % 16 == 0 && (!multi || (n * bpc * 2) % 16 == 0);
+    const int vec_z = z && reinterpret_cast<uintptr_t>(z) % 16 == 0 && (!multi || (n * zpb) % 16 == 0);
+    if (i8) return strip_bs<true>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+    return strip_bs<false>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+}
+
+}  // namespace mnb

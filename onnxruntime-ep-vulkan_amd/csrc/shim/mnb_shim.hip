@@ -62,6 +62,7 @@ int forced_kernel() {
     if (!std::strcmp(v, "generic")) return MNB_KERNEL_GENERIC;
     if (!std::strcmp(v, "stream")) return MNB_KERNEL_GEMV_STREAM;
     if (!std::strcmp(v, "group")) return MNB_KERNEL_GROUP_MFMA;
+    if (!std::strcmp(v, "strip")) return MNB_KERNEL_STRIP_MFMA;
     return 0;
 }
 
@@ -147,6 +148,11 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     if (fast) kern = MNB_KERNEL_GEMV_MFMA;               // bits 8, block 16: 16-row MFMA GEMV
     if (group) kern = MNB_KERNEL_GROUP_MFMA;             // int4, block >= 32: any row count
     if (gemm && p->m > kGemmMinRows) kern = MNB_KERNEL_GEMM_MFMA;
+    mnb::StripGeom sg{};
+    const bool strip = group && p->m <= 16 &&
+                       mnb::strip_geometry(p->n, p->k, 1, p->m, false, p->block_size,
+                                           p->has_zero_points != 0, &sg);
+    if (strip) kern = MNB_KERNEL_STRIP_MFMA;             // 5..16 rows
     if (stream) kern = MNB_KERNEL_GEMV_STREAM;           // M <= 4
     const int forced = forced_kernel();
     if (forced == MNB_KERNEL_GENERIC) kern = MNB_KERNEL_GENERIC;
@@ -154,6 +160,7 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     if (forced == MNB_KERNEL_GEMV_STREAM && stream) kern = MNB_KERNEL_GEMV_STREAM;
     if (forced == MNB_KERNEL_GEMM_MFMA && gemm) kern = MNB_KERNEL_GEMM_MFMA;
     if (forced == MNB_KERNEL_GROUP_MFMA && group) kern = MNB_KERNEL_GROUP_MFMA;
+    if (forced == MNB_KERNEL_STRIP_MFMA && strip) kern = MNB_KERNEL_STRIP_MFMA;
     out->kernel = kern;
     if (kern == MNB_KERNEL_GEMM_MFMA) {
         const mnb::GemmConfig c = mnb::gemm_config(p->m, p->n);
@@ -170,6 +177,12 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
         out->tile_m = c.mr;
         out->grid_x = (c.total_waves + c.waves_per_group - 1) / c.waves_per_group;
         out->grid_y = (p->m + c.mr - 1) / c.mr;
+    } else if (kern == MNB_KERNEL_STRIP_MFMA) {
+        out->waves_per_group = sg.waves;
+        out->tile_n = 16 * sg.strips;
+        out->tile_m = 16;
+        out->grid_x = sg.gx;
+        out->grid_y = sg.gz;
     } else if (kern == MNB_KERNEL_GROUP_MFMA) {
         const mnb::GroupGeom g =
             mnb::group_geometry(p->m, p->n, p->k, 1, false, p->block_size, false);
@@ -226,7 +239,8 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
     // The MFMA path loads A in 16-byte and B in 16-byte units; fall back when a caller hands
     // over a sub-aligned view.
     if ((kern == MNB_KERNEL_GEMV_MFMA || kern == MNB_KERNEL_GEMV_STREAM ||
-         kern == MNB_KERNEL_GEMM_MFMA || kern == MNB_KERNEL_GROUP_MFMA) &&
+         kern == MNB_KERNEL_GEMM_MFMA || kern == MNB_KERNEL_GROUP_MFMA ||
+         kern == MNB_KERNEL_STRIP_MFMA) &&
         (!aligned(a, 16) || !aligned(b, 16)))
         kern = MNB_KERNEL_GENERIC;
     // The GEMM's LDS DMA also fetches scales and zero points as aligned dwords; the row-tiled
@@ -242,6 +256,13 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
                                          "256-byte aligned");
         e = mnb::launch_acc4(a, p->dtype == MNB_DTYPE_F16, b, scales, zero_points, y, p->m,
                              p->n, p->k, p->bits, p->block_size, workspace, st);
+    } else if (kern == MNB_KERNEL_STRIP_MFMA) {
+        mnb::StripGeom sg{};
+        if (!mnb::strip_geometry(p->n, p->k, 1, p->m, false, p->block_size,
+                                 zero_points != nullptr, &sg))
+            return fail(MNB_ERR_UNSUPPORTED, "strip GEMV geometry");
+        e = mnb::launch_strip_gemv(sg, false, a, nullptr, nullptr, nullptr, b, scales, zero_points, y,
+                                   p->m, p->n, p->k, p->block_size, st);
     } else if (kern == MNB_KERNEL_GROUP_MFMA) {
         e = mnb::launch_group_gemv_f16(a, nullptr, nullptr, 1, p->m, b, scales, zero_points, y,
                                        p->m, p->n, p->k, p->bits, p->block_size, st);
