@@ -378,7 +378,8 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
 template <typename T, int BS, bool PERMUTED, bool VEC>
 __global__ void __launch_bounds__(256)
 quantize_a_int8(const T* __restrict__ A, int8_t* __restrict__ qa, float* __restrict__ scale,
-                int32_t* __restrict__ qsum, int M, int K, int* __restrict__ cnt, int ncnt) {
+                int32_t* __restrict__ qsum, int M, int K, int* __restrict__ cnt, int ncnt,
+                int s_row, int s_blk) {
     constexpr int G = BS / 8;                            // threads per block: 2..16
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     // the split-K counters of the int8 GEMV that follows start at zero
@@ -440,7 +441,7 @@ quantize_a_int8(const T* __restrict__ A, int8_t* __restrict__ qa, float* __restr
 #pragma unroll
         for (int e = 0; e < 8; ++e) out[e] = o[e];
     }
-    if (k0 % BS == 0) scale[(int64_t)row * bpc + blk] = amax / 127.0f;
+    if (k0 % BS == 0) scale[(int64_t)row * s_row + (int64_t)blk * s_blk] = amax / 127.0f;
     if (qsum) {
         // block sum: the G partial sums meet in the block's first thread
         int bs_sum = s;
@@ -552,7 +553,7 @@ hipError_t launch_group_gemv_f16(const void* a, const int32_t* row_index, const 
     const int64_t bound = offsets ? max_rows : m;
     const int64_t hint = offsets ? std::min<int64_t>(bound, 2 * ((m + ng - 1) / ng)) : m;
     StripGeom sg;
-    if (hint <= 16 && !strip_gemv_forced_off() &&
+    if (hint <= 16 && !strip_gemv_forced_off() && strip_gemv_aligned(a, b, s, z, false) &&
         strip_geometry(n, k, ng, bound, false, bs, z != nullptr, &sg))
         return launch_strip_gemv(sg, false, a, nullptr, row_index, offsets, b, s, z, y, m, n, k,
                                  bs, st);
@@ -570,7 +571,7 @@ hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
     if (m == 0 || groups == 0) return hipSuccess;
     StripGeom sg;
-    if (rows_hint <= 16 && !strip_gemv_forced_off() &&
+    if (rows_hint <= 16 && !strip_gemv_forced_off() && strip_gemv_aligned(a, b, s, z, false) &&
         strip_geometry(n, k, groups, rows_bound, false, bs, z != nullptr, &sg))
         return launch_strip_gemv(sg, false, a, nullptr, row_index, offsets, b, s, z, y, m, n, k,
                                  bs, st);
@@ -585,11 +586,14 @@ hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index
 
 hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
-                                  hipStream_t st, int* cnt, int64_t ncnt) {
+                                  hipStream_t st, int* cnt, int64_t ncnt, int64_t scale_rows) {
     if (m == 0) return hipSuccess;
     if (k % bs || (bs != 16 && bs != 32 && bs != 64 && bs != 128)) return hipErrorInvalidValue;
     const int64_t groups = m * (k / 8);
     const dim3 grid((unsigned)((groups + 255) / 256));
+    // scales [m][k/bs], or block-major [k/bs][scale_rows] when scale_rows > 0
+    const int s_row = scale_rows > 0 ? 1 : (int)(k / bs);
+    const int s_blk = scale_rows > 0 ? (int)scale_rows : 1;
     const bool vec = (reinterpret_cast<uintptr_t>(a) % 16 == 0) &&
                      (reinterpret_cast<uintptr_t>(qa) % 8 == 0);
 #define MNB_Q(T_, BS_)                                                                            \
@@ -597,19 +601,19 @@ hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* 
         if (permuted && vec)                                                                      \
             hipLaunchKernelGGL((quantize_a_int8<T_, BS_, true, true>), grid, dim3(256), 0, st,    \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
-                               (int)ncnt);                                                        \
+                               (int)ncnt, s_row, s_blk);                                                        \
         else if (vec)                                                                             \
             hipLaunchKernelGGL((quantize_a_int8<T_, BS_, false, true>), grid, dim3(256), 0, st,   \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
-                               (int)ncnt);                                                        \
+                               (int)ncnt, s_row, s_blk);                                                        \
         else if (permuted)                                                                        \
             hipLaunchKernelGGL((quantize_a_int8<T_, BS_, true, false>), grid, dim3(256), 0, st,   \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
-                               (int)ncnt);                                                        \
+                               (int)ncnt, s_row, s_blk);                                                        \
         else                                                                                      \
             hipLaunchKernelGGL((quantize_a_int8<T_, BS_, false, false>), grid, dim3(256), 0, st,  \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
-                               (int)ncnt);                                                        \
+                               (int)ncnt, s_row, s_blk);                                                        \
     } while (0)
 #define MNB_QBS(T_)                                                                               \
     switch (bs) {                                                                                 \
@@ -640,7 +644,7 @@ Acc4Layout acc4_layout(const GroupGeom& g, int64_t m, int64_t k, int bs) {
     Acc4Layout l{};
     l.qa = 0;
     l.sa = align256((size_t)m * (size_t)k);
-    l.part = l.sa + align256((size_t)m * (size_t)(k / bs) * sizeof(float));
+    l.part = l.sa + align256((size_t)std::max<int64_t>(m, 16) * (size_t)(k / bs) * sizeof(float));
     l.nsid = g.gx * g.gy * g.gz;
     const size_t part_bytes = g.ksplit > 1
         ? (size_t)l.nsid * g.ksplit * g.mt * 64 * sizeof(f32x4) : 0;
@@ -665,12 +669,16 @@ hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* 
     // fp16 with at most 16 rows: the quantiser's codes and scales (the workspace's first two
     // parts) feed the strip GEMV.
     StripGeom sg;
+    uint8_t* const wsp = static_cast<uint8_t*>(workspace);
     if (a_f16 && m <= 16 && !strip_gemv_forced_off() &&
+        strip_gemv_aligned(wsp + l.qa, b, s, z, true) &&
         strip_geometry(n, k, 1, m, true, bs, z != nullptr, &sg)) {
-        uint8_t* ws = static_cast<uint8_t*>(workspace);
+        uint8_t* ws = wsp;
         int8_t* qa = reinterpret_cast<int8_t*>(ws + l.qa);
         float* sa = reinterpret_cast<float*>(ws + l.sa);
-        hipError_t e = launch_quantize_a_int8(a, true, qa, sa, nullptr, true, m, k, bs, st);
+        // block-major scales over 16 rows: an output lane's four rows are one 16-byte load
+        hipError_t e = launch_quantize_a_int8(a, true, qa, sa, nullptr, true, m, k, bs, st,
+                                              nullptr, 0, 16);
         if (e != hipSuccess) return e;
         return launch_strip_gemv(sg, true, qa, sa, nullptr, nullptr, b, s, z, y, m, n, k, bs, st);
     }

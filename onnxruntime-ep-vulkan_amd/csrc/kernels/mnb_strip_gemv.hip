@@ -19,9 +19,10 @@
 // Arithmetic.  fp16: exact (q - zp) operands on v_mfma_f32_16x16x32_f16, the fp32 partial of a
 // block scaled once by the block's scale (the reference kernel's per-block fp32 partial,
 // rust/shaders/glsl/templates/q_gemv.comp:571-579).  int8: the activations arrive as the codes
-// and per-(row, block) scales of quantize_a_int8 (written in the weights' [0,2,4,6,1,3,5,7]
-// order once per call -- quantising inside every workgroup would repeat it per run of strips);
-// v_mfma_i32_16x16x32_i8 gives exact int32 block dots, scaled by a_scale * b_scale in fp32.
+// of quantize_a_int8 (written in the weights' [0,2,4,6,1,3,5,7] order once per call --
+// quantising inside every workgroup would repeat it per run of strips) with block-major scales
+// over 16 rows; v_mfma_i32_16x16x64_i8 (x32 for block 32) gives exact int32 block dots, scaled
+// by a_scale * b_scale in fp32.
 //
 // Reduction.  Each wavefront's 16 x 16 partial tile of a strip goes to LDS; every four strips
 // the W partials are summed in wavefront order (run-to-run deterministic) and stored, so the
@@ -35,11 +36,15 @@
 
 namespace mnb {
 
-// Threads per workgroup the instantiation is compiled for: the register arrays grow with QW
-// (A operands 16 VGPRs per quad in fp16, 8 in int8; the strips of weights in flight 4 per quad
-// each), and 1024 threads leave each wavefront 128 VGPRs.
-constexpr int strip_max_threads(bool i8, int bs, int qw) {
-    return (i8 ? (qw <= 3 || (qw <= 4 && bs == 128)) : qw <= 2) ? 1024 : 512;
+// Threads per workgroup the instantiation is compiled for, 0 where it would not fit its
+// registers without spilling: the arrays grow with QW (A operands 16 VGPRs per quad in fp16, 8
+// in int8 plus a 4-row scale vector per block; the strips of weights in flight 4 per quad
+// each), and 1024 threads leave each wavefront 128 VGPRs, 512 threads 256.
+__host__ __device__ constexpr int strip_max_threads(bool i8, int bs, int qw) {
+    if (!i8) return qw <= 2 ? 1024 : (qw <= 6 ? 512 : 0);
+    if (bs == 32) return qw <= 2 ? 1024 : (qw <= 4 ? 512 : 0);
+    if (bs == 64) return qw <= 3 ? 1024 : (qw <= 6 ? 512 : 0);
+    return qw <= 4 ? 1024 : 512;
 }
 
 // Strips whose partial tiles are summed together: W x period KB of LDS, 32 KB.
@@ -47,38 +52,42 @@ __host__ __device__ constexpr int strip_period(int waves) { return waves >= 32 ?
 
 namespace {
 
-// Copies `bytes` bytes from global memory into LDS with 16-byte loads (when `vec`: both ends
-// 16-byte aligned but for the byte tail), a batch of loads in flight per thread.
-__device__ __forceinline__ void copy_to_lds(uint8_t* __restrict__ dst,
-                                            const uint8_t* __restrict__ src, int bytes, bool vec) {
-    int done = 0;
-    if (vec) {
-        constexpr int kB = 4;
-        const int nvec = bytes >> 4;
+// A copy of `bytes` bytes from global memory into LDS in two halves: issue() requests the first
+// kEarly 16-byte pieces of each thread (when `vec`: source 16-byte aligned), so the requests
+// are in flight while other loads are issued; finish() stores them and copies the rest.
+template <int kEarly>
+struct LdsCopy {
+    u32x4 v[kEarly];
+    __device__ __forceinline__ void issue(const uint8_t* __restrict__ src, int bytes, bool vec) {
+        const int nvec = vec ? bytes >> 4 : 0;
         const u32x4* __restrict__ s4 = reinterpret_cast<const u32x4*>(src);
-        u32x4* __restrict__ d4 = reinterpret_cast<u32x4*>(dst);
-        for (int base = (int)threadIdx.x; base < nvec; base += kB * (int)blockDim.x) {
-            u32x4 v[kB];
 #pragma unroll
-            for (int b = 0; b < kB; ++b) {
-                const int i = base + b * (int)blockDim.x;
-                v[b] = s4[i < nvec ? i : nvec - 1];
-            }
-#pragma unroll
-            for (int b = 0; b < kB; ++b) {
-                const int i = base + b * (int)blockDim.x;
-                if (i < nvec) d4[i] = v[b];
-            }
+        for (int b = 0; b < kEarly; ++b) {
+            const int i = (int)threadIdx.x + b * (int)blockDim.x;
+            if (i < nvec) v[b] = s4[i];
         }
-        done = nvec << 4;
     }
-    for (int i = done + (int)threadIdx.x; i < bytes; i += (int)blockDim.x) dst[i] = src[i];
-}
+    __device__ __forceinline__ void finish(uint8_t* __restrict__ dst,
+                                           const uint8_t* __restrict__ src, int bytes, bool vec) {
+        const int nvec = vec ? bytes >> 4 : 0;
+        u32x4* __restrict__ d4 = reinterpret_cast<u32x4*>(dst);
+#pragma unroll
+        for (int b = 0; b < kEarly; ++b) {
+            const int i = (int)threadIdx.x + b * (int)blockDim.x;
+            if (i < nvec) d4[i] = v[b];
+        }
+        const u32x4* __restrict__ s4 = reinterpret_cast<const u32x4*>(src);
+        for (int i = (int)threadIdx.x + kEarly * (int)blockDim.x; i < nvec; i += (int)blockDim.x)
+            d4[i] = s4[i];
+        for (int i = (nvec << 4) + (int)threadIdx.x; i < bytes; i += (int)blockDim.x)
+            dst[i] = src[i];
+    }
+};
 
 }  // namespace
 
 template <bool I8, int BS, bool HAS_ZP, int QW>
-__global__ void __launch_bounds__(strip_max_threads(I8, BS, QW))
+__global__ void __launch_bounds__(strip_max_threads(I8, BS, QW) ? strip_max_threads(I8, BS, QW) : 256)
 strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
            const int32_t* __restrict__ row_index,
            const int32_t* __restrict__ offsets, const uint8_t* __restrict__ B,
@@ -100,19 +109,10 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     const int n0 = blockIdx.x * S * 16;
     const int ns = min(S, (N - n0 + 15) >> 4);           // strips of this run (>= 1)
 
-    int row_lo = 0, row_hi = M;
-    int64_t wb = 0, ws = 0, wz = 0;
-    if (offsets) {
-        const int e = blockIdx.y;
-        row_lo = offsets[e];
-        row_hi = offsets[e + 1];
-        wb = (int64_t)e * N * (K / 2);
-        ws = (int64_t)e * N * bpc;
-        wz = (int64_t)e * N * zpb;
-    }
-    const int r0 = row_lo + blockIdx.z * 16;
-    if (r0 >= row_hi) return;                            // the whole workgroup, before a barrier
-
+    const int e = offsets ? (int)blockIdx.y : 0;
+    const int64_t wb = (int64_t)e * N * (K / 2);
+    const int64_t ws = (int64_t)e * N * bpc;
+    const int64_t wz = (int64_t)e * N * zpb;
     const int q_lo = (wave * Q) / W;
     const int q_n = ((wave + 1) * Q) / W - q_lo;         // quads of this wavefront, <= QW
     const uint8_t* __restrict__ Bg = B + wb;
@@ -134,10 +134,40 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     // (the int8 path's runs are usually a single strip).
     constexpr int AHEAD = I8 ? (QW >= 4 ? 0 : 1) : (QW > 3 ? 1 : 2);
     u32x4 b0[QW], b1[AHEAD > 0 ? QW : 1], b2[AHEAD > 1 ? QW : 1];
-    fetch(0, b0);
-    if constexpr (AHEAD > 1) {
-        if (ns > 1) fetch(1, b1);
+
+    // The run's scales and zero points (LDS copies), requested with the first strips' weights.
+    const int ncols = min(16 * S, N - n0);
+    const int s_bytes = (16 * S * bpc * 2 + 15) & ~15;
+    const int z_bytes = HAS_ZP ? ((16 * S * zpb + 15) & ~15) : 0;
+    f16* const sS = reinterpret_cast<f16*>(smem);
+    uint8_t* const sZ = smem + s_bytes;
+    f32x4* const red = reinterpret_cast<f32x4*>(smem + s_bytes + z_bytes);
+    const uint8_t* const s_src = reinterpret_cast<const uint8_t*>(Sc + ws + (int64_t)n0 * bpc);
+    const uint8_t* const z_src = HAS_ZP ? Z + wz + (int64_t)n0 * zpb : nullptr;
+    LdsCopy<4> scopy;
+    LdsCopy<1> zcopy;
+    auto request = [&]() {
+        fetch(0, b0);
+        if constexpr (AHEAD > 1) {
+            if (ns > 1) fetch(1, b1);
+        }
+        scopy.issue(s_src, ncols * bpc * 2, vec_s != 0);
+        if constexpr (HAS_ZP) zcopy.issue(z_src, ncols * zpb, vec_z != 0);
+    };
+
+    // Rows of this workgroup.  The first row tile of a group almost always has rows, so its
+    // requests go out before the group's row range is read (a dependent round trip, and for
+    // gathered rows a second one before the activations); later tiles read it first.
+    const bool eager = blockIdx.z == 0;
+    if (eager) request();
+    int row_lo = 0, row_hi = M;
+    if (offsets) {
+        row_lo = offsets[e];
+        row_hi = offsets[e + 1];
     }
+    const int r0 = row_lo + blockIdx.z * 16;
+    if (r0 >= row_hi) return;                            // the whole workgroup, before a barrier
+    if (!eager) request();
 
     // ---- A operands of this wavefront's quads: row nl of the tile, k = 32c + 8g .. + 8 ----
     int rr = r0 + nl;
@@ -145,7 +175,7 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     const int arow = row_index ? row_index[rr] : rr;
     f16x8 af[I8 ? 1 : QW][4];
     i32x2 aq[I8 ? QW : 1][4];
-    float sar[I8 ? QW : 1][I8 ? BPQ : 1];                // int8: a_scale of (row nl, block)
+    f32x4 sao[I8 ? QW : 1][I8 ? BPQ : 1];                // int8: a_scale of rows 4g .. 4g + 3
 #pragma unroll
     for (int j = 0; j < QW; ++j) {
 #pragma unroll
@@ -162,26 +192,17 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
             }
         }
         if constexpr (I8) {
+            // block-major scales over the 16 rows of the tile: rows 4g .. 4g + 3 in one load
 #pragma unroll
             for (int b = 0; b < BPQ; ++b) {
                 const int blk = min((128 * (q_lo + j) + BS * b) / BS, bpc - 1);
-                const float v = a_scale[(int64_t)arow * bpc + blk];
-                sar[j][b] = j < q_n ? v : 0.f;
+                sao[j][b] = *reinterpret_cast<const f32x4*>(a_scale + (int64_t)blk * 16 + 4 * g);
             }
         }
     }
 
-    // ---- the run's scales and zero points into LDS ----
-    const int ncols = min(16 * S, N - n0);
-    const int s_bytes = (16 * S * bpc * 2 + 15) & ~15;
-    const int z_bytes = HAS_ZP ? ((16 * S * zpb + 15) & ~15) : 0;
-    f16* const sS = reinterpret_cast<f16*>(smem);
-    uint8_t* const sZ = smem + s_bytes;
-    f32x4* const red = reinterpret_cast<f32x4*>(smem + s_bytes + z_bytes);
-    copy_to_lds(smem, reinterpret_cast<const uint8_t*>(Sc + ws + (int64_t)n0 * bpc),
-                ncols * bpc * 2, vec_s != 0);
-    if constexpr (HAS_ZP)
-        copy_to_lds(sZ, Z + wz + (int64_t)n0 * zpb, ncols * zpb, vec_z != 0);
+    scopy.finish(smem, s_src, ncols * bpc * 2, vec_s != 0);
+    if constexpr (HAS_ZP) zcopy.finish(sZ, z_src, ncols * zpb, vec_z != 0);
 
     __syncthreads();
 
@@ -220,26 +241,37 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
                 }
             } else {
                 i32x4 dot = {0, 0, 0, 0};
+                i32x2 bq[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const int c = 4 * (q_lo + j) + t;
                     const int blk = min((32 * c) / BS, bpc - 1);
                     int z = 8;
                     if constexpr (HAS_ZP) z = (int)((lz[blk >> 1] >> ((blk & 1) * 4)) & 0xFu);
-                    const uint32_t zb = (uint32_t)(128 - z) * 0x01010101u;
-                    const i32x2 bop = qz_i8(wt[t], zb);
-                    dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, aq[j][t]),
-                                                                __builtin_bit_cast(long, bop), dot,
-                                                                0, 0, 0);
-                    if ((t + 1) % CPB == 0) {
-                        const float sb = (float)ls[blk];
-                        const int b = t / CPB;
-                        // output rows 4g .. 4g + 3 take the scales of lanes 4g .. 4g + 3
+                    bq[t] = qz_i8(wt[t], (uint32_t)(128 - z) * 0x01010101u);
+                }
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const float sa = __shfl(sar[j][b], 4 * g + q, 64);
-                            acc[q] = __builtin_fmaf((float)dot[q], sa * sb, acc[q]);
-                        }
+                for (int t = 0; t < 4; t += (CPB >= 2 ? 2 : 1)) {
+                    if constexpr (CPB >= 2) {
+                        // two chunks of one block in one 16x16x64 MFMA: A and B place the
+                        // same k in the same (lane row, slot)
+                        const i32x4 a4 = {aq[j][t].x, aq[j][t].y, aq[j][t + 1].x, aq[j][t + 1].y};
+                        const i32x4 b4 = {bq[t].x, bq[t].y, bq[t + 1].x, bq[t + 1].y};
+                        dot = __builtin_amdgcn_mfma_i32_16x16x64_i8(a4, b4, dot, 0, 0, 0);
+                    } else {
+                        dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                            __builtin_bit_cast(long, aq[j][t]), __builtin_bit_cast(long, bq[t]), dot,
+                            0, 0, 0);
+                    }
+                    const int te = t + (CPB >= 2 ? 1 : 0);   // last chunk covered so far
+                    if ((te + 1) % CPB == 0) {               // block end: scale it
+                        const int c = 4 * (q_lo + j) + te;
+                        const int blk = min((32 * c) / BS, bpc - 1);
+                        const float sb = (float)ls[blk];
+                        const int b = te / CPB;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            acc[q] = __builtin_fmaf((float)dot[q], sao[j][b][q] * sb, acc[q]);
                         dot = i32x4{0, 0, 0, 0};
                     }
                 }
@@ -295,7 +327,7 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
 
 namespace {
 
-constexpr int kQW[] = {1, 2, 3, 4, 6};
+constexpr int kQW[] = {1, 2, 3, 4, 6, 8};
 
 int round_qw(int64_t q) {
     for (int v : kQW)
@@ -315,6 +347,7 @@ bool strip_geometry(int64_t n, int64_t k, int64_t groups, int64_t rows_bound, bo
     if (bs != 32 && bs != 64 && bs != 128) return false;
     if (k <= 0 || k % 32 || k % bs || n <= 0 || groups <= 0) return false;
     const int64_t q = (k / 32 + 3) / 4;
+    if (i8 && rows_bound > 16) return false;             // block-major scales cover 16 rows
     StripGeom g{};
     // The fewest wavefronts that keep a wavefront's quads at 4 or fewer, else the most that
     // the instantiation's register budget allows.
@@ -340,7 +373,7 @@ bool strip_geometry(int64_t n, int64_t k, int64_t groups, int64_t rows_bound, bo
     const int64_t red_bytes = (int64_t)g.waves * strip_period(g.waves) * 64 * sizeof(f32x4);
     const int64_t s_max =
         std::max<int64_t>(1, std::min<int64_t>(32, (64 * 1024 - red_bytes) / per_strip));
-    const int waves_per_simd = g.qw <= 3 ? 4 : (g.qw == 4 ? 3 : 2);
+    const int waves_per_simd = g.qw <= 3 ? 4 : (g.qw == 4 ? 3 : (g.qw == 6 ? 2 : 1));
     const int64_t by_regs = std::max(1, 4 * waves_per_simd / g.waves);
     const int64_t by_lds = std::max<int64_t>(1, (160 * 1024) / (s_max * per_strip + red_bytes + 64));
     const int64_t slots = 256 * std::min(by_regs, by_lds);
@@ -368,14 +401,19 @@ hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
                     const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
                     void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
                     hipStream_t st) {
+    if constexpr (strip_max_threads(I8, BS, QW) == 0) {
+        return hipErrorInvalidValue;                     // not instantiated (see above)
+    } else {
     auto kern = strip_gemv<I8, BS, HAS_ZP, QW>;
-    if (g.lds > 64 * 1024) return hipErrorInvalidValue;
+    if (g.lds > 64 * 1024 || 64 * g.waves > strip_max_threads(I8, BS, QW))
+        return hipErrorInvalidValue;
     const dim3 grid((unsigned)g.gx, (unsigned)g.gy, (unsigned)g.gz);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     hipLaunchKernelGGL(kern, grid, block, g.lds, st, a, a_scale, row_index,
                        offsets, b, static_cast<const f16*>(s), z, static_cast<f16*>(y), (int)m,
                        (int)n, (int)k, g.strips, vec_s, vec_z);
     return hipGetLastError();
+    }
 }
 
 template <bool I8, int BS, bool HAS_ZP>
@@ -390,6 +428,7 @@ hipError_t strip_qw(const StripGeom& g, const void* a, const float* a_scale,
         case 3: return strip_go<I8, BS, HAS_ZP, 3>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
         case 4: return strip_go<I8, BS, HAS_ZP, 4>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
         case 6: return strip_go<I8, BS, HAS_ZP, 6>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+        case 8: return strip_go<I8, BS, HAS_ZP, 8>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
 
         default: return hipErrorInvalidValue;
     }
@@ -415,6 +454,14 @@ hipError_t strip_bs(int bs, const StripGeom& g, const void* a, const float* a_sc
 
 }  // namespace
 
+bool strip_gemv_aligned(const void* a, const uint8_t* b, const void* s, const uint8_t* z,
+                        bool i8) {
+    (void)s;
+    (void)z;                                             // staged element-wise when sub-aligned
+    return reinterpret_cast<uintptr_t>(a) % (i8 ? 8 : 16) == 0 &&
+           reinterpret_cast<uintptr_t>(b) % 16 == 0;
+}
+
 hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const float* a_scale,
                              const int32_t* row_index,
                              const int32_t* offsets, const uint8_t* b, const void* s,
@@ -436,3 +483,4 @@ hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const f
 }
 
 }  // namespace mnb
+

@@ -245,6 +245,8 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
         kern = MNB_KERNEL_GENERIC;
     // The GEMM's LDS DMA also fetches scales and zero points as aligned dwords; the row-tiled
     // GEMV takes any other case of the same form.
+    if (kern == MNB_KERNEL_STRIP_MFMA && !mnb::strip_gemv_aligned(a, b, scales, zero_points, false))
+        kern = MNB_KERNEL_GROUP_MFMA;
     if (kern == MNB_KERNEL_GEMM_MFMA &&
         (!aligned(scales, 4) || !aligned(zero_points, 4) ||
          !mnb::gemm_supported(p->m, p->n, p->k, p->bits, p->block_size, zero_points != nullptr)))

@@ -37,26 +37,27 @@ def _check(y, ref, what, tol=F16_TOL):
 
 
 STRIP_SHAPES = [
-    # (M, N, K, bs, zp)
-    (5, 64, 256, 32, True),
-    (8, 100, 2880, 32, True),        # gpt-oss K: a partial last quad, ragged last strip
-    (16, 3072, 3072, 32, False),
-    (12, 48, 512, 64, True),
-    (16, 96, 1024, 128, False),
-    (9, 130, 384, 128, True),
-    (6, 64, 128, 32, True),          # one quad: three of four wavefronts hold no K share
-    (16, 9216, 3072, 32, True),      # Phi-3.5 qkv at a 16-row batch
-    (7, 40000, 256, 32, False),      # runs of two strips per workgroup
+    # (M, N, K, bs, zp, strip): strip = the planner picks the strip kernel
+    (5, 64, 256, 32, True, True),
+    (8, 104, 2880, 32, False, True),     # gpt-oss K: a partial last quad; N ragged (6.5 strips)
+    (8, 100, 2880, 32, True, True),      # 45-byte zero-point rows: staged without 16-byte pieces
+    (16, 3072, 3072, 32, False, True),
+    (12, 48, 512, 64, True, True),
+    (16, 96, 1024, 128, False, True),
+    (9, 130, 384, 128, True, True),
+    (6, 64, 128, 32, True, True),        # one quad: three of four wavefronts hold no K share
+    (16, 9216, 3072, 32, True, True),    # Phi-3.5 qkv at a 16-row batch
+    (7, 40000, 256, 32, False, True),    # runs of several strips per workgroup
 ]
 
 
-@pytest.mark.parametrize("M,N,K,bs,zp", STRIP_SHAPES)
-def test_strip_gemv_parity(cuda, M, N, K, bs, zp):
+@pytest.mark.parametrize("M,N,K,bs,zp,strip", STRIP_SHAPES)
+def test_strip_gemv_parity(cuda, M, N, K, bs, zp, strip):
     import mnb
     import torch
     print(f"[gpu] strip M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
     info = mnb.plan(mnb.problem(M, N, K, 4, bs, zp))
-    assert info.kernel == mnb.KERNEL_STRIP_MFMA
+    assert info.kernel == (mnb.KERNEL_STRIP_MFMA if strip else mnb.KERNEL_GROUP_MFMA)
     inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=M + 7 * N)
     y = mnb.matmul_nbits(_dev(inp["A"], cuda), _dev(inp["B"], cuda), _dev(inp["scales"], cuda),
                          _dev(inp["zp"], cuda), N, K, 4, bs)
@@ -68,7 +69,8 @@ def test_strip_gemv_parity(cuda, M, N, K, bs, zp):
 def test_strip_runs_of_several_strips():
     import mnb
     # the planner groups strips into runs when there are many more strips than workgroups
-    assert mnb.plan(mnb.problem(7, 40000, 256, 4, 32, False)).tile_n >= 32
+    info = mnb.plan(mnb.problem(7, 40000, 256, 4, 32, False))
+    assert info.kernel == mnb.KERNEL_STRIP_MFMA and info.tile_n >= 32
 
 
 def test_strip_bit_identical_runs(cuda):
