@@ -132,6 +132,11 @@ def main() -> int:
                     help="counter-collection mode: launch only this decode node (qkv_proj, o_proj, "
                          "gate_up_proj, down_proj) --steps times over rotated weights, then one "
                          "plain 256 MiB device copy for calibrating FETCH_SIZE/WRITE_SIZE; no JSON")
+    ap.add_argument("--pmc-launch", default=None, choices=["moe_gate_up", "moe_down", "acc4"],
+                    help="counter-collection mode: launch only the MoE expert GEMV (BASELINE "
+                         "configs[3], weights rotated over two copies) or the accuracy_level=4 "
+                         "call (configs[4]) --steps times, then one plain 256 MiB device copy "
+                         "for calibrating FETCH_SIZE/WRITE_SIZE; no JSON")
     ap.add_argument("--pmc-prefill", type=int, default=None, metavar="M",
                     help="counter-collection mode: launch only the prefill GEMM (K=3072, N=8192) "
                          "at M rows --steps times; no JSON")
@@ -186,6 +191,50 @@ def main() -> int:
         torch.cuda.synchronize()
         print(f"pmc mode: {args.steps} launches of the prefill GEMM M={pm} K={pk} N={pn} "
               f"({mnb.KERNEL_NAMES.get(mnb.plan(pprob).kernel)})")
+        return 0
+
+    if args.pmc_launch:
+        if args.pmc_launch == "acc4":
+            ak, an, am, abs_ = 8192, 3072, 16, 128
+            a_copies = max(2, -(-2 * MALL_BYTES // node_bytes(am, ak, an, bs=abs_)))
+            a_w = [make_weights(torch, dev, ak, an, gen, bs=abs_) for _ in range(a_copies)]
+            a_A = torch.randn(am, ak, device=dev, generator=gen).to(torch.float16)
+            a_Y = torch.empty(am, an, dtype=torch.float16, device=dev)
+            a_prob = mnb.problem(am, an, ak, BITS, abs_, True, mnb.DTYPE_F16, 4)
+            a_ws = torch.empty(mnb.workspace_bytes(a_prob), dtype=torch.uint8, device=dev)
+            for r in range(args.steps):
+                B, S, Z = a_w[r % a_copies]
+                mnb.check(lib.mnb_matmul_nbits(C.byref(a_prob), a_A.data_ptr(), B.data_ptr(),
+                                               S.data_ptr(), Z.data_ptr(), a_Y.data_ptr(),
+                                               a_ws.data_ptr(), a_ws.numel(), sptr))
+            what = f"accuracy_level=4 M={am} K={ak} N={an} bs{abs_} ({node_bytes(am, ak, an, bs=abs_)} algorithmic bytes)"
+        else:
+            E, T, TOPK, MK = 32, 64, 4, 2880
+            mn = 5760 if args.pmc_launch == "moe_gate_up" else 2880
+            top = np.argsort(-np.random.default_rng(20260801).standard_normal((T, E)), axis=1,
+                             kind="stable")[:, :TOPK].reshape(-1)
+            rows = torch.from_numpy((np.argsort(top, kind="stable") // TOPK).astype(np.int32)).to(dev)
+            cnt = np.bincount(top, minlength=E)
+            off = torch.from_numpy(np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32)).to(dev)
+            mA = torch.randn(T, MK, device=dev, generator=gen).to(torch.float16)
+            bpc = MK // BS
+            wB = [torch.randint(0, 256, (E, mn, bpc, BS // 2), dtype=torch.uint8, device=dev,
+                                generator=gen) for _ in range(2)]
+            wS = [(torch.randn(E, mn * bpc, device=dev, generator=gen).abs() * 0.02).to(torch.float16)
+                  for _ in range(2)]
+            mY = torch.empty(T * TOPK, mn, dtype=torch.float16, device=dev)
+            mp = mnb.MoeProblem(E, T * TOPK, int(cnt.max()), T, mn, MK, BITS, BS, 0, mnb.DTYPE_F16)
+            for r in range(args.steps):
+                mnb.check(lib.mnb_moe_grouped(C.byref(mp), mA.data_ptr(), rows.data_ptr(),
+                                              off.data_ptr(), wB[r % 2].data_ptr(),
+                                              wS[r % 2].data_ptr(), None, mY.data_ptr(), sptr))
+            what = f"MoE {args.pmc_launch} ({E * (mn * MK // 2 + 2 * mn * bpc)} bytes of expert weights and scales)"
+        torch.cuda.synchronize()
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"pmc mode: {args.steps} launches of {what}, then one copy of {src.numel()} bytes")
         return 0
 
     if args.pmc_node:

@@ -366,13 +366,13 @@ bool strip_geometry(int64_t n, int64_t k, int64_t groups, int64_t rows_bound, bo
     const int64_t nstrips = (n + 15) / 16;
     const int64_t bpc = k / bs;
     const int64_t zpb = (bpc + 1) / 2;
-    // Runs as long as the 64 KB of LDS (partial tiles, then staged scales and zero points)
-    // allow, sized so that the launch fills whole rounds of resident workgroups (by registers
+    // Runs as long as 80 KB of LDS (partial tiles, then staged scales and zero points: two
+    // workgroups per CU) allow, sized so that the launch fills whole rounds of resident workgroups (by registers
     // and LDS).
     const int64_t per_strip = 16 * (bpc * 2 + (has_zp ? zpb : 0)) + 32;
     const int64_t red_bytes = (int64_t)g.waves * strip_period(g.waves) * 64 * sizeof(f32x4);
     const int64_t s_max =
-        std::max<int64_t>(1, std::min<int64_t>(32, (64 * 1024 - red_bytes) / per_strip));
+        std::max<int64_t>(1, std::min<int64_t>(32, (80 * 1024 - red_bytes) / per_strip));
     const int waves_per_simd = g.qw <= 3 ? 4 : (g.qw == 4 ? 3 : (g.qw == 6 ? 2 : 1));
     const int64_t by_regs = std::max(1, 4 * waves_per_simd / g.waves);
     const int64_t by_lds = std::max<int64_t>(1, (160 * 1024) / (s_max * per_strip + red_bytes + 64));
@@ -387,7 +387,7 @@ bool strip_geometry(int64_t n, int64_t k, int64_t groups, int64_t rows_bound, bo
     g.gz = (std::max<int64_t>(rows_bound, 1) + 15) / 16;
     g.lds = (size_t)((16 * s * bpc * 2 + 15) & ~15) + (has_zp ? (size_t)((16 * s * zpb + 15) & ~15) : 0) +
             (size_t)red_bytes;
-    if (g.lds > 64 * 1024) return false;
+    if (g.lds > 80 * 1024) return false;
     if (g.gx > 0x7fffffff || g.gy > 65535 || g.gz > 65535) return false;
     *out = g;
     return true;
@@ -405,8 +405,13 @@ hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
         return hipErrorInvalidValue;                     // not instantiated (see above)
     } else {
     auto kern = strip_gemv<I8, BS, HAS_ZP, QW>;
-    if (g.lds > 64 * 1024 || 64 * g.waves > strip_max_threads(I8, BS, QW))
+    if (g.lds > 80 * 1024 || 64 * g.waves > strip_max_threads(I8, BS, QW))
         return hipErrorInvalidValue;
+    if (g.lds > 64 * 1024) {                             // above the default dynamic LDS limit
+        const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)g.lds);
+        if (ea != hipSuccess) return ea;
+    }
     const dim3 grid((unsigned)g.gx, (unsigned)g.gy, (unsigned)g.gz);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     hipLaunchKernelGGL(kern, grid, block, g.lds, st, a, a_scale, row_index,
