@@ -146,6 +146,22 @@ __device__ __forceinline__ float group_sum(float v, int G) {
     return v;
 }
 
+// Maximum over the 64 lanes of a wavefront, received by every lane (the exchanges of
+// group_sum; fmaxf ignores a NaN operand).
+__device__ __forceinline__ float wave_max64(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    uint32_t x = __builtin_bit_cast(uint32_t, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    v = fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+    x = __builtin_bit_cast(uint32_t, v);
+    const auto r2 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)r2[0]),
+                 __builtin_bit_cast(float, (uint32_t)r2[1]));
+}
+
 // 4 x 4 transpose of dwords across the lane rows (16 lanes each) of a wavefront: on return,
 // v[t] of a lane in row g is what v[g] of the same column lane in row t held.
 __device__ __forceinline__ void transpose_rows(uint32_t& v0, uint32_t& v1, uint32_t& v2,

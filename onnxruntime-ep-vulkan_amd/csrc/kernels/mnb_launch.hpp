@@ -101,13 +101,22 @@ bool strip_gemv_aligned(const void* a, const uint8_t* b, const void* s, const ui
                         bool i8);
 // True when MNB_FORCE_KERNEL=group asks for the row-tiled GEMV instead.
 bool strip_gemv_forced_off();
+// SwiGLU applied by the strip GEMV as it stores interleaved (gate, linear) column pairs
+// (QMoE fc1 with swiglu_fusion = 1): y[r][c / 2] = act(h[r][c] + b[c], h[r][c + 1] + b[c + 1])
+// for even c, h rounded to fp16 before the bias, y row stride N / 2 (N even).
+struct StripSwiglu {
+    const void* bias;    // fp16 [groups][N] or null
+    float alpha, beta, limit;
+    int has_limit;
+};
 // fp16 scales and Y; A is fp16, or for i8 (accuracy_level = 4) the permuted int8 codes of
-// quantize_a_int8 with their fp32 scales a_scale [rows][K / bs].
+// quantize_a_int8 with their fp32 scales block-major over 16 rows, a_scale [K / bs][16].
+// swiglu (fp16 A, no zero points) stores the activation instead of Y.
 hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const float* a_scale,
                              const int32_t* row_index,
                              const int32_t* offsets, const uint8_t* b, const void* s,
                              const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bs,
-                             hipStream_t stream);
+                             hipStream_t stream, const StripSwiglu* swiglu = nullptr);
 
 // cnt / ncnt: split-K counters of a following int8 GEMV, cleared by the quantiser (may be null).
 // scale_rows > 0 writes the scales block-major, [k/bs][scale_rows] (rows >= m untouched).

@@ -11,11 +11,14 @@
 //      qmoe_group      one workgroup: counting sort of the T*k (token, slot) assignments by
 //                      expert: offsets[E+1], the token of every grouped row, the grouped row of
 //                      every assignment.
+//      qmoe_group_small the same for T*k <= 1024 and E <= 64 (decode batches), stable.
 //   2. group_gemv      h = x W1_e^T for every grouped row (the MatMulNBits expert-grouped GEMV,
 //                      rows gathered through the sort), fp16 out.
 //   3. qmoe_swiglu     act = SwiGLU(h + b1_e): gate/linear interleaved or concatenated,
 //                      gate <= limit, |linear| <= limit, gate * sigmoid(alpha gate) * (linear + beta)
-//                      in fp32, fp16 out.
+//                      in fp32, fp16 out.  For interleaved pairs on the strip GEMV (at most 16
+//                      expected rows per expert) steps 2 and 3 are one kernel: the strip GEMV
+//                      applies SwiGLU to each (gate, linear) pair as it stores fc1's tiles.
 //   4. group_gemv      o = act W2_e^T, fp16 out.
 //   5. qmoe_combine    y[t] = sum over the token's k slots of w * (o + b2_e), fp32, in slot order
 //                      (deterministic), fp16 out.
@@ -40,9 +43,59 @@ __device__ __forceinline__ float ld(const L* p, int64_t i) {
 
 }  // namespace
 
-// Routing, part 1: one wavefront per token (four per workgroup), the logits of experts
-// e = lane + 64 j in registers: wave-wide max and sum for the softmax, then k rounds of a
-// wave-wide arg-max (the lower id wins a tie) over the experts not yet chosen.
+// One token's routing by a wavefront when E <= 64: lane e holds logit e.  An expert's rank is
+// the number of experts ahead of it (a larger logit, or an equal one with a lower id); the
+// experts of rank < k are the k rounds of arg-max with ties to the lower id, in slot order.
+// Each lane writes the 64-bit key (logit order, then 63 - lane) to the wavefront's LDS row and
+// counts the larger keys of that row, read as broadcasts (lanes past E write 0, below every
+// key); logits order as totally ordered keys (-0 as +0, a NaN above +inf or below -inf by its
+// sign) so the ranks are always a permutation of 0 .. E-1.  The chosen probabilities pass
+// through LDS by slot and are summed in slot order.  Returns the lane's rank (64 past E) and
+// routing weight (softmax, renormalised over the k slots when asked).
+struct Routed {
+    int rank;
+    float w;
+};
+
+template <int NP>
+__device__ __forceinline__ int count_above(const uint64_t* __restrict__ kb, uint64_t mine) {
+    typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        const u64x2 v = reinterpret_cast<const u64x2*>(kb)[j];
+        n += (v.x > mine ? 1 : 0) + (v.y > mine ? 1 : 0);
+    }
+    return n;
+}
+
+__device__ __forceinline__ Routed route_wave64(float v, int lane, int E, int k, int normalize,
+                                               uint64_t* __restrict__ kb,
+                                               float* __restrict__ kp) {
+    const bool live = lane < E;
+    v = live ? v + 0.f : -INFINITY;
+    const float mx = wave_max64(v);
+    const float ev = live ? expf(v - mx) : 0.f;
+    const float p = ev / group_sum(ev, 64);
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const uint32_t key = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const uint64_t mine = ((uint64_t)key << 6) | (uint64_t)(63 - lane);
+    kb[lane] = live ? mine : 0;
+    __builtin_amdgcn_wave_barrier();
+    const int rank = !live ? 64 : E <= 16 ? count_above<8>(kb, mine)
+                                : E <= 32 ? count_above<16>(kb, mine) : count_above<32>(kb, mine);
+    if (rank < k) kp[rank] = p;
+    __builtin_amdgcn_wave_barrier();
+    float psum = 0.f;
+    for (int s = 0; s < k; ++s) psum += kp[s];
+    __builtin_amdgcn_wave_barrier();                     // kb / kp are rewritten by the next token
+    return Routed{rank, normalize ? p / psum : p};
+}
+
+// Routing, part 1: one wavefront per token (four per workgroup).  E <= 64: route_wave64.
+// Otherwise the logits of experts e = lane + 64 j in registers: wave-wide max and sum for the
+// softmax, then k rounds of a wave-wide arg-max (the lower id wins a tie) over the experts not
+// yet chosen.
 template <typename L>
 __global__ void __launch_bounds__(256)
 qmoe_topk(const L* __restrict__ logits, int T, int E, int k, int normalize,
@@ -50,14 +103,27 @@ qmoe_topk(const L* __restrict__ logits, int T, int E, int k, int normalize,
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= T) return;                                  // whole wavefront
-    const int nj = (E + 63) / 64;                        // <= 16
     const L* lg = logits + (int64_t)t * E;
+    if (E <= 64) {
+        __shared__ __align__(16) uint64_t kb[4][64];
+        __shared__ float kp[4][8];
+        const int w = threadIdx.x >> 6;
+        const Routed r = route_wave64(ld(lg, min(lane, E - 1)), lane, E, k, normalize, kb[w],
+                                      kp[w]);
+        if (r.rank < k) {
+            expert_of[t * k + r.rank] = lane;
+            weight_of[t * k + r.rank] = r.w;
+        }
+        return;
+    }
+    const int nj = (E + 63) / 64;                        // <= 16
     float v[16];
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const int e = lane + 64 * j;
-        v[j] = (j < nj && e < E) ? ld(lg, e) : -INFINITY;
+        const float x = ld(lg, min(e, E - 1));          // clamped, unpredicated: issued together
+        v[j] = (j < nj && e < E) ? x : -INFINITY;
         mx = fmaxf(mx, v[j]);
     }
 #pragma unroll
@@ -124,7 +190,8 @@ qmoe_group(const int32_t* __restrict__ expert_of, int R, int E, int k,
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int a = tid + kRouteThreads * j;
-        ex[j] = a < R ? expert_of[a] : -1;
+        const int xv = expert_of[min(a, R - 1)];        // clamped, unpredicated: issued together
+        ex[j] = a < R ? xv : -1;
         sl[j] = ex[j] >= 0 ? atomicAdd(&cnt[ex[j]], 1) : 0;
     }
     __syncthreads();
@@ -151,6 +218,68 @@ qmoe_group(const int32_t* __restrict__ expert_of, int R, int E, int k,
         row_token[pos] = a / k;
         pos_of[a] = pos;
         expert_of_row[pos] = ex[j];
+    }
+}
+
+// Routing, part 2 for T * k <= kSmallR and E <= 64 (decode batches; one workgroup, one
+// assignment per thread): a stable counting sort by expert.  Within a wavefront the rank of an
+// assignment among those of its expert comes from one ballot per expert; wavefront 0 scans the
+// per-wavefront counts in (expert, wavefront) order.  The grouped rows of an expert keep token
+// order, independent of timing.
+constexpr int kSmallR = 1024;
+
+__global__ void __launch_bounds__(kSmallR)
+qmoe_group_small(const int32_t* __restrict__ expert_of, int R, int E, int k,
+                 int32_t* __restrict__ offsets, int32_t* __restrict__ row_token,
+                 int32_t* __restrict__ pos_of, int32_t* __restrict__ expert_of_row) {
+    constexpr int kWaves = kSmallR / 64;
+    __shared__ int32_t s_cnt[kWaves][64];                // per wavefront and expert
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int a = threadIdx.x;
+    const int x0 = expert_of[min(a, R - 1)];
+    const int ex = a < R ? x0 : -1;
+    int local = 0;
+    if (wave * 64 < R) {                                 // wave-uniform
+        for (int x = 0; x < E; ++x) {
+            const uint64_t m = __ballot(ex == x);
+            const int below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+            local = ex == x ? below : local;
+            if (lane == 0) s_cnt[wave][x] = __popcll(m);
+        }
+    } else if (lane < E) {
+        s_cnt[wave][lane] = 0;
+    }
+    __syncthreads();
+    if (wave == 0) {                                     // offsets, first row of (wave, expert)
+        int tot = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) tot += lane < E ? s_cnt[w][lane] : 0;
+        int incl = tot;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d);
+            incl += lane >= d ? o : 0;
+        }
+        int off = incl - tot;
+        if (lane < E) {
+            offsets[lane] = off;
+            if (lane == E - 1) offsets[E] = incl;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const int c = s_cnt[w][lane];
+                s_cnt[w][lane] = off;
+                off += c;
+            }
+        }
+    }
+    __syncthreads();
+    if (a < R) {
+        const int pos = s_cnt[wave][ex] + local;
+        row_token[pos] = a / k;
+        pos_of[a] = pos;
+        expert_of_row[pos] = ex;
     }
 }
 
@@ -304,20 +433,37 @@ hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, con
         hipLaunchKernelGGL(qmoe_topk<f16>, dim3(tk_grid), dim3(256), 0, st,
                            static_cast<const f16*>(logits), (int)q.rows, (int)q.experts, q.k,
                            q.normalize, expert_of, weight_of);
-    hipLaunchKernelGGL(qmoe_group, dim3(1), dim3(kRouteThreads), 0, st, expert_of, (int)R,
-                       (int)q.experts, q.k, offsets, row_token, pos_of, expert_of_row);
+    if (R <= kSmallR && q.experts <= 64)
+        hipLaunchKernelGGL(qmoe_group_small, dim3(1), dim3(kSmallR), 0, st, expert_of, (int)R,
+                           (int)q.experts, q.k, offsets, row_token, pos_of, expert_of_row);
+    else
+        hipLaunchKernelGGL(qmoe_group, dim3(1), dim3(kRouteThreads), 0, st, expert_of, (int)R,
+                           (int)q.experts, q.k, offsets, row_token, pos_of, expert_of_row);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // expected rows per expert (twice the mean, at least one) sets the GEMV tile height
     const int64_t hint = std::max<int64_t>(1, 2 * ((R + q.experts - 1) / q.experts));
-    e = launch_group_gemv_f16_bounded(x, row_token, offsets, q.experts, q.rows, hint, fc1, fc1_s,
-                                      nullptr, h, R, 2 * q.inter, q.hidden, 4, q.block_size, st);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(qmoe_swiglu, dim3(grid_for(R * q.inter / 4)), dim3(256), 0, st, h,
-                       static_cast<const f16*>(fc1_b), expert_of_row, act, R, q.inter, q.fusion,
-                       q.alpha, q.beta, q.limit, q.has_limit);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    // Interleaved gate/linear pairs on the strip GEMV: SwiGLU as fc1's tiles are stored.
+    StripGeom sg;
+    if (q.fusion == 1 && hint <= 16 && !strip_gemv_forced_off() &&
+        strip_gemv_aligned(x, fc1, fc1_s, nullptr, false) &&
+        strip_geometry(2 * q.inter, q.hidden, q.experts, q.rows, false, q.block_size, false,
+                       &sg)) {
+        const StripSwiglu sw{fc1_b, q.alpha, q.beta, q.limit, q.has_limit};
+        e = launch_strip_gemv(sg, false, x, nullptr, row_token, offsets, fc1, fc1_s, nullptr, act,
+                              R, 2 * q.inter, q.hidden, q.block_size, st, &sw);
+        if (e != hipSuccess) return e;
+    } else {
+        e = launch_group_gemv_f16_bounded(x, row_token, offsets, q.experts, q.rows, hint, fc1,
+                                          fc1_s, nullptr, h, R, 2 * q.inter, q.hidden, 4,
+                                          q.block_size, st);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(qmoe_swiglu, dim3(grid_for(R * q.inter / 4)), dim3(256), 0, st, h,
+                           static_cast<const f16*>(fc1_b), expert_of_row, act, R, q.inter,
+                           q.fusion, q.alpha, q.beta, q.limit, q.has_limit);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     e = launch_group_gemv_f16_bounded(act, nullptr, offsets, q.experts, q.rows, hint, fc2, fc2_s,
                                       nullptr, o, R, q.hidden, q.inter, 4, q.block_size, st);
     if (e != hipSuccess) return e;

@@ -86,13 +86,14 @@ struct LdsCopy {
 
 }  // namespace
 
-template <bool I8, int BS, bool HAS_ZP, int QW>
+// SWIGLU: the stored tile is SwiGLU of its interleaved (gate, linear) column pairs (StripSwiglu).
+template <bool I8, int BS, bool HAS_ZP, int QW, bool SWIGLU>
 __global__ void __launch_bounds__(strip_max_threads(I8, BS, QW) ? strip_max_threads(I8, BS, QW) : 256)
 strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
            const int32_t* __restrict__ row_index,
            const int32_t* __restrict__ offsets, const uint8_t* __restrict__ B,
            const f16* __restrict__ Sc, const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M,
-           int N, int K, int S, int vec_s, int vec_z) {
+           int N, int K, int S, int vec_s, int vec_z, StripSwiglu sw) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
     constexpr int BPQ = 4 / CPB;                         // blocks per quad
@@ -309,11 +310,35 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
                 f32x4 sum = red[i * 64 + ll];
                 for (int w = 1; w < W; ++w) sum += red[(w * kPeriod + i) * 64 + ll];
                 const int col = n0 + 16 * (p0 + i) + (ll & 15);
-                if (col >= N) continue;
+                if constexpr (SWIGLU) {
+                    // the odd column's (linear) sums from lane ll ^ 1, with every lane active
+                    f32x4 lin;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = r0 + 4 * (ll >> 4) + q;
-                    if (r < row_hi) Y[(int64_t)r * N + col] = (f16)sum[q];
+                    for (int q = 0; q < 4; ++q) lin[q] = dpp_f<0xB1>(sum[q]);
+                    if (col >= N || (ll & 1)) continue;
+                    const f16* bb = static_cast<const f16*>(sw.bias);
+                    const float bg = bb ? (float)bb[(int64_t)e * N + col] : 0.f;
+                    const float bl = bb ? (float)bb[(int64_t)e * N + col + 1] : 0.f;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int r = r0 + 4 * (ll >> 4) + q;
+                        // h is rounded to fp16 before its bias, as where h is stored
+                        float gt = (float)(f16)sum[q] + bg;
+                        float lt = (float)(f16)lin[q] + bl;
+                        if (sw.has_limit) {
+                            gt = fminf(gt, sw.limit);
+                            lt = fminf(fmaxf(lt, -sw.limit), sw.limit);
+                        }
+                        const float a = gt / (1.f + expf(-sw.alpha * gt)) * (lt + sw.beta);
+                        if (r < row_hi) Y[(int64_t)r * (N >> 1) + (col >> 1)] = (f16)a;
+                    }
+                } else {
+                    if (col >= N) continue;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int r = r0 + 4 * (ll >> 4) + q;
+                        if (r < row_hi) Y[(int64_t)r * N + col] = (f16)sum[q];
+                    }
                 }
             }
             __syncthreads();
@@ -395,16 +420,16 @@ bool strip_geometry(int64_t n, int64_t k, int64_t groups, int64_t rows_bound, bo
 
 namespace {
 
-template <bool I8, int BS, bool HAS_ZP, int QW>
+template <bool I8, int BS, bool HAS_ZP, int QW, bool SWIGLU>
 hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
                     const int32_t* row_index,
                     const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
                     void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
-                    hipStream_t st) {
-    if constexpr (strip_max_threads(I8, BS, QW) == 0) {
+                    const StripSwiglu& sw, hipStream_t st) {
+    if constexpr (strip_max_threads(I8, BS, QW) == 0 || (SWIGLU && (I8 || HAS_ZP))) {
         return hipErrorInvalidValue;                     // not instantiated (see above)
     } else {
-    auto kern = strip_gemv<I8, BS, HAS_ZP, QW>;
+    auto kern = strip_gemv<I8, BS, HAS_ZP, QW, SWIGLU>;
     if (g.lds > 80 * 1024 || 64 * g.waves > strip_max_threads(I8, BS, QW))
         return hipErrorInvalidValue;
     if (g.lds > 64 * 1024) {                             // above the default dynamic LDS limit
@@ -416,27 +441,31 @@ hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     hipLaunchKernelGGL(kern, grid, block, g.lds, st, a, a_scale, row_index,
                        offsets, b, static_cast<const f16*>(s), z, static_cast<f16*>(y), (int)m,
-                       (int)n, (int)k, g.strips, vec_s, vec_z);
+                       (int)n, (int)k, g.strips, vec_s, vec_z, sw);
     return hipGetLastError();
     }
 }
 
-template <bool I8, int BS, bool HAS_ZP>
+template <bool I8, int BS, bool HAS_ZP, bool SWIGLU>
 hipError_t strip_qw(const StripGeom& g, const void* a, const float* a_scale,
                     const int32_t* row_index,
                     const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
                     void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
-                    hipStream_t st) {
+                    const StripSwiglu& sw, hipStream_t st) {
+#define MNB_STRIP_GO(QW_)                                                                          \
+    case QW_:                                                                                      \
+        return strip_go<I8, BS, HAS_ZP, QW_, SWIGLU>(g, a, a_scale, row_index, offsets, b, s, z, y, \
+                                                     m, n, k, vec_s, vec_z, sw, st)
     switch (g.qw) {
-        case 1: return strip_go<I8, BS, HAS_ZP, 1>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
-        case 2: return strip_go<I8, BS, HAS_ZP, 2>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
-        case 3: return strip_go<I8, BS, HAS_ZP, 3>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
-        case 4: return strip_go<I8, BS, HAS_ZP, 4>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
-        case 6: return strip_go<I8, BS, HAS_ZP, 6>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
-        case 8: return strip_go<I8, BS, HAS_ZP, 8>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
-
+        MNB_STRIP_GO(1);
+        MNB_STRIP_GO(2);
+        MNB_STRIP_GO(3);
+        MNB_STRIP_GO(4);
+        MNB_STRIP_GO(6);
+        MNB_STRIP_GO(8);
         default: return hipErrorInvalidValue;
     }
+#undef MNB_STRIP_GO
 }
 
 template <bool I8>
@@ -444,10 +473,15 @@ hipError_t strip_bs(int bs, const StripGeom& g, const void* a, const float* a_sc
                     const int32_t* row_index,
                     const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
                     void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
-                    hipStream_t st) {
+                    const StripSwiglu* sw, hipStream_t st) {
+    const StripSwiglu none{};
 #define MNB_STRIP_ZP(BS_)                                                                          \
-    return z ? strip_qw<I8, BS_, true>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st) \
-             : strip_qw<I8, BS_, false>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st)
+    if (sw) return strip_qw<I8, BS_, false, true>(g, a, a_scale, row_index, offsets, b, s, z, y,   \
+                                                  m, n, k, vec_s, vec_z, *sw, st);                 \
+    return z ? strip_qw<I8, BS_, true, false>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, \
+                                              k, vec_s, vec_z, none, st)                           \
+             : strip_qw<I8, BS_, false, false>(g, a, a_scale, row_index, offsets, b, s, z, y, m,   \
+                                               n, k, vec_s, vec_z, none, st)
     switch (bs) {
         case 32: MNB_STRIP_ZP(32);
         case 64: MNB_STRIP_ZP(64);
@@ -471,10 +505,10 @@ hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const f
                              const int32_t* row_index,
                              const int32_t* offsets, const uint8_t* b, const void* s,
                              const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bs,
-                             hipStream_t st) {
+                             hipStream_t st, const StripSwiglu* swiglu) {
     if (m == 0) return hipSuccess;
     if (reinterpret_cast<uintptr_t>(a) % (i8 ? 8 : 16) || reinterpret_cast<uintptr_t>(b) % 16 ||
-        (i8 && !a_scale))
+        (i8 && !a_scale) || (swiglu && (i8 || z || n % 2)))
         return hipErrorInvalidValue;
     const int64_t bpc = k / bs;
     const int64_t zpb = (bpc + 1) / 2;
@@ -483,8 +517,8 @@ hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const f
     const bool multi = offsets != nullptr && g.gy > 1;
     const int vec_s = reinterpret_cast<uintptr_t>(s) % 16 == 0 && (!multi || (n * bpc * 2) % 16 == 0);
     const int vec_z = z && reinterpret_cast<uintptr_t>(z) % 16 == 0 && (!multi || (n * zpb) % 16 == 0);
-    if (i8) return strip_bs<true>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
-    return strip_bs<false>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, st);
+    if (i8) return strip_bs<true>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, nullptr, st);
+    return strip_bs<false>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, swiglu, st);
 }
 
 }  // namespace mnb

@@ -35,6 +35,11 @@ CASES = [
     (17, 384, 192, 16, 1, 64, 2, True, None, True, False),
     (33, 256, 256, 4, 4, 128, 1, True, 7.0, True, False),
     (8, 2880, 2880, 32, 4, 32, 1, True, 7.0, True, False),
+    # T*k > 1024: per-token routing kernel and the separate counting sort; row-tiled GEMVs
+    (300, 256, 128, 16, 4, 32, 1, True, 7.0, True, False),
+    # E > 64: the k-round arg-max routing; SwiGLU in the strip GEMV's stores
+    (20, 256, 128, 96, 4, 32, 1, True, 7.0, True, True),
+    (3, 512, 256, 64, 8, 64, 1, False, None, False, False),
 ]
 
 
@@ -73,6 +78,8 @@ def test_qmoe_matches_oracle(cuda, case):
         inp["logits"] = inp["logits"].astype(np.float32)
     if T >= 5:
         inp["logits"][1] = 0                     # a token whose logits all tie
+        inp["logits"][2, ::2] = -0.0             # ... and one whose ties mix -0 and +0
+        inp["logits"][2, 1::2] = 0.0
     ref16, ref = _refs(inp, k, I, bs, fusion, limit, normalize)
     d = {key: _t(v, cuda) for key, v in inp.items()}
     y = mnb.qmoe(d["x"], d["logits"], d["fc1"], d["fc1_scales"], d["fc2"], d["fc2_scales"], k=k,
