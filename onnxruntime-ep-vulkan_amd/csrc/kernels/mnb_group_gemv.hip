@@ -375,7 +375,7 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
 // qa = clamp(rint(a * (127 / amax)), -127, 127) (0 when amax == 0), all in fp32 with
 // round-half-even.  PERMUTED writes each group of eight as [0,2,4,6,1,3,5,7] (the order
 // qz_i8 produces weights in); otherwise natural order plus the block sums of qa.
-template <typename T, int BS, bool PERMUTED, bool VEC>
+template <typename T, int BS, int LAYOUT, bool VEC>
 __global__ void __launch_bounds__(256)
 quantize_a_int8(const T* __restrict__ A, int8_t* __restrict__ qa, float* __restrict__ scale,
                 int32_t* __restrict__ qsum, int M, int K, int* __restrict__ cnt, int ncnt,
@@ -425,7 +425,20 @@ quantize_a_int8(const T* __restrict__ A, int8_t* __restrict__ qa, float* __restr
     if (!live) return;
     const int blk = k0 / BS;
     const int bpc = K / BS;
-    int8_t* out = qa + (int64_t)row * K + k0;
+    constexpr bool PERMUTED = LAYOUT >= 1;
+    int kd = k0;
+    if constexpr (LAYOUT == 2) {
+        // quad-interleaved: in every whole 128-k quad, the 8-byte group of chunk t and lane row
+        // g (4t + g in natural order) goes to (t / 2) * 64 + 16 g + (t % 2) * 8, so that a lane
+        // row's four chunks are two 16-byte pieces and one 16-byte load per lane covers 64
+        // contiguous bytes of each of 16 rows; a partial last quad keeps natural order
+        const int qs = k0 & ~127;
+        if (qs + 128 <= K) {
+            const int t4 = (k0 & 127) >> 5, g4 = (k0 & 31) >> 3;
+            kd = qs + (t4 >> 1) * 64 + g4 * 16 + (t4 & 1) * 8;
+        }
+    }
+    int8_t* out = qa + (int64_t)row * K + kd;
     constexpr int order_p[8] = {0, 2, 4, 6, 1, 3, 5, 7};
     int8_t o[8];
 #pragma unroll
@@ -586,7 +599,8 @@ hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index
 
 hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
-                                  hipStream_t st, int* cnt, int64_t ncnt, int64_t scale_rows) {
+                                  hipStream_t st, int* cnt, int64_t ncnt, int64_t scale_rows,
+                                  bool quads) {
     if (m == 0) return hipSuccess;
     if (k % bs || (bs != 16 && bs != 32 && bs != 64 && bs != 128)) return hipErrorInvalidValue;
     const int64_t groups = m * (k / 8);
@@ -598,22 +612,30 @@ hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* 
                      (reinterpret_cast<uintptr_t>(qa) % 8 == 0);
 #define MNB_Q(T_, BS_)                                                                            \
     do {                                                                                          \
-        if (permuted && vec)                                                                      \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, true, true>), grid, dim3(256), 0, st,    \
-                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
-                               (int)ncnt, s_row, s_blk);                                                        \
+        if (quads && vec)                                                                         \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 2, true>), grid, dim3(256), 0, st,       \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
+                               (int)ncnt, s_row, s_blk);                                          \
+        else if (quads)                                                                           \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 2, false>), grid, dim3(256), 0, st,      \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
+                               (int)ncnt, s_row, s_blk);                                          \
+        else if (permuted && vec)                                                                 \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 1, true>), grid, dim3(256), 0, st,       \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
+                               (int)ncnt, s_row, s_blk);                                          \
         else if (vec)                                                                             \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, false, true>), grid, dim3(256), 0, st,   \
-                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
-                               (int)ncnt, s_row, s_blk);                                                        \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 0, true>), grid, dim3(256), 0, st,       \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
+                               (int)ncnt, s_row, s_blk);                                          \
         else if (permuted)                                                                        \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, true, false>), grid, dim3(256), 0, st,   \
-                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
-                               (int)ncnt, s_row, s_blk);                                                        \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 1, false>), grid, dim3(256), 0, st,      \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
+                               (int)ncnt, s_row, s_blk);                                          \
         else                                                                                      \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, false, false>), grid, dim3(256), 0, st,  \
-                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt, \
-                               (int)ncnt, s_row, s_blk);                                                        \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 0, false>), grid, dim3(256), 0, st,      \
+                               static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
+                               (int)ncnt, s_row, s_blk);                                          \
     } while (0)
 #define MNB_QBS(T_)                                                                               \
     switch (bs) {                                                                                 \
@@ -678,7 +700,7 @@ hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* 
         float* sa = reinterpret_cast<float*>(ws + l.sa);
         // block-major scales over 16 rows: an output lane's four rows are one 16-byte load
         hipError_t e = launch_quantize_a_int8(a, true, qa, sa, nullptr, true, m, k, bs, st,
-                                              nullptr, 0, 16);
+                                              nullptr, 0, 16, true);
         if (e != hipSuccess) return e;
         return launch_strip_gemv(sg, true, qa, sa, nullptr, nullptr, b, s, z, y, m, n, k, bs, st);
     }

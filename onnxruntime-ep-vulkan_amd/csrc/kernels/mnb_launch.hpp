@@ -96,7 +96,7 @@ struct StripGeom {
 };
 bool strip_geometry(int64_t n, int64_t k, int64_t groups, int64_t rows_bound, bool i8, int bs,
                     bool has_zp, StripGeom* out);
-// The pointer alignment the strip GEMV needs (A and B 16 bytes; int8 A 8 bytes).
+// The pointer alignment the strip GEMV needs (A and B 16 bytes).
 bool strip_gemv_aligned(const void* a, const uint8_t* b, const void* s, const uint8_t* z,
                         bool i8);
 // True when MNB_FORCE_KERNEL=group asks for the row-tiled GEMV instead.
@@ -109,8 +109,9 @@ struct StripSwiglu {
     float alpha, beta, limit;
     int has_limit;
 };
-// fp16 scales and Y; A is fp16, or for i8 (accuracy_level = 4) the permuted int8 codes of
-// quantize_a_int8 with their fp32 scales block-major over 16 rows, a_scale [K / bs][16].
+// fp16 scales and Y; A is fp16, or for i8 (accuracy_level = 4) the int8 codes of
+// quantize_a_int8 in its quad-interleaved layout (quads = true) with their fp32 scales
+// block-major over 16 rows, a_scale [K / bs][16].
 // swiglu (fp16 A, no zero points) stores the activation instead of Y.
 hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const float* a_scale,
                              const int32_t* row_index,
@@ -120,10 +121,12 @@ hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const f
 
 // cnt / ncnt: split-K counters of a following int8 GEMV, cleared by the quantiser (may be null).
 // scale_rows > 0 writes the scales block-major, [k/bs][scale_rows] (rows >= m untouched).
+// quads: the strip GEMV's layout -- permuted, and within every whole 128-k quad the 8-byte group
+// of chunk t, lane row g stored at (t / 2) * 64 + 16 g + (t % 2) * 8.
 hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* scale,
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
                                   hipStream_t stream, int* cnt = nullptr, int64_t ncnt = 0,
-                                  int64_t scale_rows = 0);
+                                  int64_t scale_rows = 0, bool quads = false);
 size_t acc4_workspace_bytes(int64_t m, int64_t n, int64_t k, int bs);
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,

@@ -19,10 +19,11 @@
 // Arithmetic.  fp16: exact (q - zp) operands on v_mfma_f32_16x16x32_f16, the fp32 partial of a
 // block scaled once by the block's scale (the reference kernel's per-block fp32 partial,
 // rust/shaders/glsl/templates/q_gemv.comp:571-579).  int8: the activations arrive as the codes
-// of quantize_a_int8 (written in the weights' [0,2,4,6,1,3,5,7] order once per call --
-// quantising inside every workgroup would repeat it per run of strips) with block-major scales
-// over 16 rows; v_mfma_i32_16x16x64_i8 (x32 for block 32) gives exact int32 block dots, scaled
-// by a_scale * b_scale in fp32.
+// of quantize_a_int8 (written once per call in the weights' [0,2,4,6,1,3,5,7] order, and within
+// each whole quad with a lane row's four chunks as two 16-byte pieces, so one load covers 64
+// contiguous bytes of each row -- quantising inside every workgroup would repeat it per run of
+// strips) with block-major scales over 16 rows; v_mfma_i32_16x16x64_i8 (x32 for block 32) gives
+// exact int32 block dots, scaled by a_scale * b_scale in fp32.
 //
 // Reduction.  Each wavefront's 16 x 16 partial tile of a strip goes to LDS; every four strips
 // the W partials are summed in wavefront order (run-to-run deterministic) and stored, so the
@@ -98,7 +99,9 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
     constexpr int BPQ = 4 / CPB;                         // blocks per quad
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform by construction; in an SGPR, the K share, its quad count and every
+    // per-quad condition below are scalar (branches, not lane masks) and address bases scalar
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int W = blockDim.x >> 6;
     const int kPeriod = strip_period(W);
     const int nl = lane & 15;
@@ -179,17 +182,32 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     f32x4 sao[I8 ? QW : 1][I8 ? BPQ : 1];                // int8: a_scale of rows 4g .. 4g + 3
 #pragma unroll
     for (int j = 0; j < QW; ++j) {
+        if (I8 && j < q_n && 4 * (q_lo + j) + 3 < chunks) {
+            // whole quad in the quantiser's quad-interleaved layout: chunks 0, 1 of this lane
+            // row at 16 g, chunks 2, 3 at 64 + 16 g -- two loads, each 64 contiguous bytes of
+            // every row of the tile
+            const int8_t* p = static_cast<const int8_t*>(Av) + (int64_t)arow * K +
+                              128 * (q_lo + j) + 16 * g;
+            const u32x4 v0 = *reinterpret_cast<const u32x4*>(p);
+            const u32x4 v1 = *reinterpret_cast<const u32x4*>(p + 64);
+            aq[j][0] = i32x2{(int32_t)v0.x, (int32_t)v0.y};
+            aq[j][1] = i32x2{(int32_t)v0.z, (int32_t)v0.w};
+            aq[j][2] = i32x2{(int32_t)v1.x, (int32_t)v1.y};
+            aq[j][3] = i32x2{(int32_t)v1.z, (int32_t)v1.w};
+        } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int c = 4 * (q_lo + j) + t;
-            const bool live = j < q_n && c < chunks;
-            const int64_t off = (int64_t)arow * K + 32 * (int64_t)min(c, chunks - 1) + 8 * g;
-            if constexpr (!I8) {
-                const f16x8 v = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(Av) + off);
-                af[j][t] = live ? v : f16x8{};
-            } else {
-                const u32x2 v = *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(Av) + off);
-                aq[j][t] = live ? i32x2{(int32_t)v.x, (int32_t)v.y} : i32x2{0, 0};
+            for (int t = 0; t < 4; ++t) {
+                const int c = 4 * (q_lo + j) + t;
+                const bool live = j < q_n && c < chunks;
+                const int64_t off = (int64_t)arow * K + 32 * (int64_t)min(c, chunks - 1) + 8 * g;
+                if constexpr (!I8) {
+                    const f16x8 v = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(Av) + off);
+                    af[j][t] = live ? v : f16x8{};
+                } else {
+                    // a partial last quad (natural order) or a quad past this wavefront's share
+                    const u32x2 v = *reinterpret_cast<const u32x2*>(static_cast<const int8_t*>(Av) + off);
+                    aq[j][t] = live ? i32x2{(int32_t)v.x, (int32_t)v.y} : i32x2{0, 0};
+                }
             }
         }
         if constexpr (I8) {
@@ -497,8 +515,7 @@ bool strip_gemv_aligned(const void* a, const uint8_t* b, const void* s, const ui
                         bool i8) {
     (void)s;
     (void)z;                                             // staged element-wise when sub-aligned
-    return reinterpret_cast<uintptr_t>(a) % (i8 ? 8 : 16) == 0 &&
-           reinterpret_cast<uintptr_t>(b) % 16 == 0;
+    return reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0;
 }
 
 hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const float* a_scale,
@@ -507,7 +524,7 @@ hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const f
                              const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bs,
                              hipStream_t st, const StripSwiglu* swiglu) {
     if (m == 0) return hipSuccess;
-    if (reinterpret_cast<uintptr_t>(a) % (i8 ? 8 : 16) || reinterpret_cast<uintptr_t>(b) % 16 ||
+    if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(b) % 16 ||
         (i8 && !a_scale) || (swiglu && (i8 || z || n % 2)))
         return hipErrorInvalidValue;
     const int64_t bpc = k / bs;
