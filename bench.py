@@ -184,10 +184,13 @@ def main() -> int:
         pA = torch.randn(pm, pk, device=dev, generator=gen).to(torch.float16)
         pY = torch.empty(pm, pn, dtype=torch.float16, device=dev)
         pprob = mnb.problem(pm, pn, pk, BITS, BS, False)
+        pwsb = mnb.workspace_bytes(pprob)
+        pws = torch.empty(max(pwsb, 1), dtype=torch.uint8, device=dev)
         for r in range(args.steps):
             pB, pS, _ = pw[r % 2]
             mnb.check(lib.mnb_matmul_nbits(C.byref(pprob), pA.data_ptr(), pB.data_ptr(),
-                                           pS.data_ptr(), None, pY.data_ptr(), None, 0, sptr))
+                                           pS.data_ptr(), None, pY.data_ptr(), pws.data_ptr(),
+                                           pwsb, sptr))
         torch.cuda.synchronize()
         print(f"pmc mode: {args.steps} launches of the prefill GEMM M={pm} K={pk} N={pn} "
               f"({mnb.KERNEL_NAMES.get(mnb.plan(pprob).kernel)})")
@@ -383,11 +386,15 @@ def main() -> int:
         pY = torch.empty(pm, pn, dtype=torch.float16, device=dev)
         pprob = mnb.problem(pm, pn, pk, BITS, BS, False)
         pinfo = mnb.plan(pprob)
+        # the K-split partials of the GEMM at M < 1024 (fewer row tiles than CUs)
+        pwsb = mnb.workspace_bytes(pprob)
+        pws = torch.empty(max(pwsb, 1), dtype=torch.uint8, device=dev)
 
-        def plaunch(r, sp, pA=pA, pY=pY, pprob=pprob):
+        def plaunch(r, sp, pA=pA, pY=pY, pprob=pprob, pws=pws, pwsb=pwsb):
             pB, pS, _ = pw[r % 2]
             rc = lib.mnb_matmul_nbits(C.byref(pprob), pA.data_ptr(), pB.data_ptr(),
-                                      pS.data_ptr(), None, pY.data_ptr(), None, 0, sp)
+                                      pS.data_ptr(), None, pY.data_ptr(), pws.data_ptr(), pwsb,
+                                      sp)
             if rc:
                 mnb.check(rc)
 
@@ -408,6 +415,8 @@ def main() -> int:
         prefill.append({"M": pm, "K": pk, "N": pn, "us": round(pus, 2), "TFLOP/s": round(ptf, 2),
                         "kernel": mnb.KERNEL_NAMES.get(pinfo.kernel, "?"),
                         "tile": [pinfo.tile_m, pinfo.tile_n],
+                        "k_split": pinfo.grid_x // ((pm + pinfo.tile_m - 1) // pinfo.tile_m
+                                                    * ((pn + pinfo.tile_n - 1) // pinfo.tile_n)),
                         "roofline": {"bound": "mfma", "achieved": round(ptf, 2),
                                      "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                                      "frac": round(ptf / F16_MFMA_PEAK_TFLOPS, 4),

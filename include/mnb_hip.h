@@ -79,7 +79,8 @@ typedef struct mnb_plan_info {
     int32_t tile_m;         /* output rows per workgroup */
     int64_t grid_x;
     int64_t grid_y;
-    int64_t workspace_bytes;/* device scratch the launch needs (0 for all but accuracy_level 4) */
+    int64_t workspace_bytes;/* device scratch: accuracy_level 4 (needed), or the fp32 partials
+                             * of a prefill GEMM split along K (optional; 0 elsewhere) */
 } mnb_plan_info;
 
 const char* mnb_last_error(void);
@@ -89,11 +90,14 @@ int mnb_version(void);
 int mnb_check_problem(const mnb_problem* p);
 /* Fills `out` with the launch the planner would make for `p`. */
 int mnb_plan(const mnb_problem* p, mnb_plan_info* out);
-/* Device scratch in bytes that mnb_matmul_nbits needs for `p` (0 except accuracy_level 4). */
+/* Device scratch in bytes for `p`: required for accuracy_level 4; for a prefill GEMM whose row
+ * tiles alone would leave CUs idle (e.g. M = 256) it holds the fp32 partials of a split along K,
+ * and a smaller workspace (or none) runs the GEMM unsplit; 0 otherwise. */
 int mnb_workspace_bytes(const mnb_problem* p, size_t* bytes);
 
-/* Y = A @ dequant(B)^T on device pointers.  `workspace` may be NULL when
- * mnb_workspace_bytes() reports 0; otherwise it must hold at least that many bytes. */
+/* Y = A @ dequant(B)^T on device pointers.  `workspace` (16-byte aligned) may be NULL when
+ * mnb_workspace_bytes() reports 0 or the plan's kernel is MNB_KERNEL_GEMM_MFMA; otherwise it must
+ * hold at least that many bytes. */
 int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, const void* scales,
                      const uint8_t* zero_points, void* y, void* workspace,
                      size_t workspace_bytes, void* stream);

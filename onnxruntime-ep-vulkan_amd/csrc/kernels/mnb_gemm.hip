@@ -28,6 +28,8 @@
 // scaled by the block's scale.  The scaled add of one sub-block is spread between the MFMAs of
 // the next, so that it runs on the VALU while the matrix core works.  For blocks of 64 or 128
 // the partial of each 64-k step is scaled on its own (the same scale twice for a 128 block).
+#include <algorithm>
+
 #include "mnb_common.hpp"
 #include "mnb_launch.hpp"
 
@@ -81,7 +83,7 @@ template <int BS, bool HAS_ZP>
 __global__ void __launch_bounds__(512)
 gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ S,
               const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K,
-              int tiles_m, int tiles_n) {
+              int tiles_m, int tiles_n, int ksplit, float* __restrict__ part) {
     static_assert(BS == 32 || BS == 64 || BS == 128, "block size");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* const sA = smem;
@@ -94,17 +96,24 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
     const int wm = wave >> 1;
     const int wn = wave & 1;
 
-    const int T = tiles_m * tiles_n;
-    const int per_xcd = (T + 7) >> 3;
-    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (tile >= T) return;                           // whole workgroup: before any barrier
+    // (tile, K split) items, each XCD taking a contiguous run of them
+    const int V = tiles_m * tiles_n * ksplit;
+    const int per_xcd = (V + 7) >> 3;
+    const int item = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (item >= V) return;                           // whole workgroup: before any barrier
+    const int tile = item / ksplit;
+    const int split = item - tile * ksplit;
     const int tile_m = tile / tiles_n;
     const int tile_n = tile - tile_m * tiles_n;
     const int m0 = tile_m * kBM;
     const int n0 = tile_n * kBN;
     const int bpc = K / BS;
     const int zpb = (bpc + 1) >> 1;
-    const int steps = K / kKS;
+    // this split's 64-k steps s0 .. s0 + steps - 1 (the host keeps every split non-empty); the
+    // pipeline below counts steps from 0 and the loaders add s0
+    const int per_split = (K / kKS + ksplit - 1) / ksplit;
+    const int s0 = split * per_split;
+    const int steps = min(K / kKS - s0, per_split);
     const int64_t col_bytes = K / 2;
     auto gcol = [&](int c) { const int g = n0 + c; return g < N ? g : N - 1; };
 
@@ -128,14 +137,14 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
     auto issue_a = [&](int step, int st) {
         uint8_t* dst = sA + st * kAStage + wave * 4 * 1024;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dma16(a_src[j] + step * kKS, dst + j * 1024);
+        for (int j = 0; j < 4; ++j) dma16(a_src[j] + (s0 + step) * kKS, dst + j * 1024);
     };
     auto issue_r = [&](int step, int st) {
         uint8_t* base = sR + st * kRStage;
         if (wave < 4) {
-            dma16(b_src + step * (kKS / 2), base + wave * 1024);
+            dma16(b_src + (s0 + step) * (kKS / 2), base + wave * 1024);
         } else {
-            const int blk0 = (step * kKS) / BS;
+            const int blk0 = ((s0 + step) * kKS) / BS;
             const int gc = gcol(aux & 127);
             const void* src;
             if (HAS_ZP && aux >= 128)
@@ -154,7 +163,7 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
         const u32x2 w = *reinterpret_cast<const u32x2*>(base + dq_col * 32 + dq_seg * 8);
         int z = 8;
         if constexpr (HAS_ZP) {
-            const int blk = (step * kKS + 16 * dq_seg) / BS;
+            const int blk = ((s0 + step) * kKS + 16 * dq_seg) / BS;
             const uint32_t zw = *reinterpret_cast<const uint32_t*>(base + kRawB + (128 + dq_col) * 4);
             const int byte = (int)(((int64_t)gcol(dq_col) * zpb + (blk >> 1)) & 3);
             z = (int)((zw >> (8 * byte + 4 * (blk & 1))) & 0xFu);
@@ -202,7 +211,7 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
                 sc[j][0] = (float)__builtin_bit_cast(f16, (uint16_t)(sw & 0xFFFFu));
                 sc[j][1] = (float)__builtin_bit_cast(f16, (uint16_t)(sw >> 16));
             } else {
-                const int64_t idx = (int64_t)gcol(c) * bpc + (step * kKS) / BS;
+                const int64_t idx = (int64_t)gcol(c) * bpc + ((s0 + step) * kKS) / BS;
                 const uint16_t h = (idx & 1) ? (uint16_t)(sw >> 16) : (uint16_t)(sw & 0xFFFFu);
                 sc[j][0] = sc[j][1] = (float)__builtin_bit_cast(f16, h);
             }
@@ -284,7 +293,9 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
 #pragma unroll
     for (int t = 0; t < 4; ++t) retire(t);
 
-    // ---- store: lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + r%4 of each tile ----
+    // ---- store: lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + r%4 of each tile; a K
+    // split stores its fp32 partial tile instead, summed by gemm_splitk_sum ----
+    float* const pbase = part ? part + (int64_t)split * M * N : nullptr;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const int i = t & 1, j = t >> 1;
@@ -293,8 +304,28 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (row < M) Y[(int64_t)row * N + col] = (f16)acc[t][r];
+            if (row >= M) continue;
+            if (pbase)
+                pbase[(int64_t)row * N + col] = acc[t][r];
+            else
+                Y[(int64_t)row * N + col] = (f16)acc[t][r];
         }
+    }
+}
+
+// Y = the sum of the ksplit fp32 partials, in split order (run-to-run deterministic); four
+// consecutive outputs per thread (M * N % 4 == 0, Y 8-byte aligned).
+__global__ void __launch_bounds__(256)
+gemm_splitk_sum(const float* __restrict__ part, f16* __restrict__ Y, int64_t mn, int ksplit) {
+    typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+    for (int64_t i = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x); i < mn;
+         i += 4 * (int64_t)gridDim.x * 256) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(part + i);
+        for (int sp = 1; sp < ksplit; ++sp) v += *reinterpret_cast<const f32x4*>(part + sp * mn + i);
+        f16x4_t o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = (f16)v[q];
+        *reinterpret_cast<f16x4_t*>(Y + i) = o;
     }
 }
 
@@ -313,57 +344,86 @@ bool gemm_supported(int64_t m, int64_t n, int64_t k, int bits, int bs, bool has_
     return true;
 }
 
-GemmConfig gemm_config(int64_t m, int64_t n) {
+GemmConfig gemm_config(int64_t m, int64_t n, int64_t k) {
     GemmConfig c{};
     c.bm = kBM;
     c.bn = kBN;
     c.tiles_m = (m + kBM - 1) / kBM;
     c.tiles_n = (n + kBN - 1) / kBN;
+    // Fewer tiles than the 256 CUs (M = 256: 64 tiles of 8192 columns): split K over up to four
+    // workgroups per tile, each split at least eight 64-k steps and none empty.
+    const int64_t tiles = c.tiles_m * c.tiles_n;
+    const int64_t steps = k / kKS;
+    int ks = 1;
+    if (tiles < 256 && (m * n) % 4 == 0)
+        ks = (int)std::max<int64_t>(1, std::min<int64_t>({4, 256 / tiles, steps / 8}));
+    while (ks > 1 && ((steps + ks - 1) / ks) * (ks - 1) >= steps) --ks;
+    c.ksplit = ks;
     return c;
+}
+
+size_t gemm_workspace_bytes(const GemmConfig& c, int64_t m, int64_t n) {
+    return c.ksplit > 1 ? (size_t)c.ksplit * (size_t)m * (size_t)n * sizeof(float) : 0;
 }
 
 template <int BS, bool HAS_ZP>
 static hipError_t gemm_go(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                           const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
-                          hipStream_t st) {
+                          float* part, hipStream_t st) {
     auto kern = gemm_f16_mfma<BS, HAS_ZP>;
     // More than 64 KB of dynamic LDS must be allowed explicitly (for the current device).
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     if (e != hipSuccess) return e;
-    const int64_t tiles = c.tiles_m * c.tiles_n;
-    const dim3 grid((unsigned)(8 * ((tiles + 7) / 8)), 1, 1);
+    const int ks = part ? c.ksplit : 1;
+    const int64_t items = c.tiles_m * c.tiles_n * ks;
+    const dim3 grid((unsigned)(8 * ((items + 7) / 8)), 1, 1);
     hipLaunchKernelGGL(kern, grid, dim3(512), kLds, st, static_cast<const f16*>(a), b,
                        static_cast<const f16*>(s), z, static_cast<f16*>(y), (int)m, (int)n,
-                       (int)k, (int)c.tiles_m, (int)c.tiles_n);
+                       (int)k, (int)c.tiles_m, (int)c.tiles_n, ks, ks > 1 ? part : nullptr);
+    if (ks > 1) {
+        const int64_t mn = m * n;
+        const unsigned blocks = (unsigned)std::min<int64_t>((mn / 4 + 255) / 256, 4096);
+        hipLaunchKernelGGL(gemm_splitk_sum, dim3(blocks), dim3(256), 0, st, part,
+                           static_cast<f16*>(y), mn, ks);
+    }
     return hipGetLastError();
 }
 
 template <int BS>
 static hipError_t gemm_zp(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                           const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
-                          hipStream_t st) {
-    if (z) return gemm_go<BS, true>(c, a, b, s, z, y, m, n, k, st);
-    return gemm_go<BS, false>(c, a, b, s, z, y, m, n, k, st);
+                          float* part, hipStream_t st) {
+    if (z) return gemm_go<BS, true>(c, a, b, s, z, y, m, n, k, part, st);
+    return gemm_go<BS, false>(c, a, b, s, z, y, m, n, k, part, st);
 }
 
 hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                            const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
-                           int bs, hipStream_t st) {
+                           int bs, hipStream_t st, void* workspace, size_t workspace_bytes) {
     if (m == 0) return hipSuccess;
     if (!gemm_supported(m, n, k, bits, bs, z != nullptr)) return hipErrorInvalidValue;
-    if (c.bm != kBM || c.bn != kBN) return hipErrorInvalidValue;
+    if (c.bm != kBM || c.bn != kBN || c.ksplit < 1) return hipErrorInvalidValue;
+    // the K split needs the partial buffer and 8-byte aligned output; without them, one pass
+    const size_t need = gemm_workspace_bytes(c, m, n);
+    float* part = need && workspace && workspace_bytes >= need &&
+                          reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                          reinterpret_cast<uintptr_t>(y) % 8 == 0
+                      ? static_cast<float*>(workspace)
+                      : nullptr;
     switch (bs) {
-        case 32: return gemm_zp<32>(c, a, b, s, z, y, m, n, k, st);
-        case 64: return gemm_zp<64>(c, a, b, s, z, y, m, n, k, st);
-        case 128: return gemm_zp<128>(c, a, b, s, z, y, m, n, k, st);
+        case 32: return gemm_zp<32>(c, a, b, s, z, y, m, n, k, part, st);
+        case 64: return gemm_zp<64>(c, a, b, s, z, y, m, n, k, part, st);
+        case 128: return gemm_zp<128>(c, a, b, s, z, y, m, n, k, part, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemm(const void* a, const uint8_t* b, const void* s, const uint8_t* z, void* y,
-                       int64_t m, int64_t n, int64_t k, int bits, int bs, hipStream_t st) {
-    return launch_gemm_cfg(gemm_config(m, n), a, b, s, z, y, m, n, k, bits, bs, st);
+                       int64_t m, int64_t n, int64_t k, int bits, int bs, hipStream_t st,
+                       void* workspace, size_t workspace_bytes) {
+    return launch_gemm_cfg(gemm_config(m, n, k), a, b, s, z, y, m, n, k, bits, bs, st, workspace,
+                           workspace_bytes);
 }
 
 }  // namespace mnb

@@ -40,15 +40,21 @@ hipError_t launch_gemv_stream_cfg(const StreamConfig& c, const void* a, const ui
 struct GemmConfig {
     int bm, bn;          // workgroup tile
     int64_t tiles_m, tiles_n;
+    int ksplit;          // workgroups per tile along K (fp32 partials summed by a second launch)
 };
 
 bool gemm_supported(int64_t m, int64_t n, int64_t k, int bits, int bs, bool has_zp);
-GemmConfig gemm_config(int64_t m, int64_t n);
+GemmConfig gemm_config(int64_t m, int64_t n, int64_t k);
+// fp32 partials of a K split (0 when the config does not split)
+size_t gemm_workspace_bytes(const GemmConfig& c, int64_t m, int64_t n);
+// With less workspace than gemm_workspace_bytes (or none) the launch runs without the K split.
 hipError_t launch_gemm(const void* a, const uint8_t* b, const void* s, const uint8_t* z, void* y,
-                       int64_t m, int64_t n, int64_t k, int bits, int bs, hipStream_t stream);
+                       int64_t m, int64_t n, int64_t k, int bits, int bs, hipStream_t stream,
+                       void* workspace = nullptr, size_t workspace_bytes = 0);
 hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                            const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
-                           int bs, hipStream_t stream);
+                           int bs, hipStream_t stream, void* workspace = nullptr,
+                           size_t workspace_bytes = 0);
 
 // Launch shape of the row-tiled MFMA GEMV (mnb_group_gemv.hip).
 struct GroupGeom {

@@ -163,12 +163,14 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     if (forced == MNB_KERNEL_STRIP_MFMA && strip) kern = MNB_KERNEL_STRIP_MFMA;
     out->kernel = kern;
     if (kern == MNB_KERNEL_GEMM_MFMA) {
-        const mnb::GemmConfig c = mnb::gemm_config(p->m, p->n);
+        const mnb::GemmConfig c = mnb::gemm_config(p->m, p->n, p->k);
         out->waves_per_group = 8;
         out->tile_n = c.bn;
         out->tile_m = c.bm;
-        out->grid_x = c.tiles_m * c.tiles_n;
+        out->grid_x = c.tiles_m * c.tiles_n * c.ksplit;
         out->grid_y = 1;
+        out->workspace_bytes = (int64_t)mnb::gemm_workspace_bytes(c, p->m, p->n);
+        return MNB_OK;
     } else if (kern == MNB_KERNEL_GEMV_STREAM) {
         const mnb::StreamConfig c =
             mnb::gemv_stream_config(p->m, p->n, p->k, p->bits, p->block_size);
@@ -229,8 +231,10 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
     if (p->has_zero_points && !zero_points)
         return fail(MNB_ERR_INVALID, "has_zero_points is set but zero_points is NULL");
     if (!p->has_zero_points) zero_points = nullptr;
-    if ((size_t)info.workspace_bytes > workspace_bytes ||
-        (info.workspace_bytes > 0 && !workspace))
+    // The prefill GEMM's workspace is optional: with less, it runs without splitting K.
+    if (info.kernel != MNB_KERNEL_GEMM_MFMA &&
+        ((size_t)info.workspace_bytes > workspace_bytes ||
+         (info.workspace_bytes > 0 && !workspace)))
         return fail(MNB_ERR_INVALID, "workspace of %zu bytes is smaller than the %lld needed",
                     workspace_bytes, (long long)info.workspace_bytes);
     const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -270,7 +274,7 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
                                        p->m, p->n, p->k, p->bits, p->block_size, st);
     } else if (kern == MNB_KERNEL_GEMM_MFMA) {
         e = mnb::launch_gemm(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
-                             p->block_size, st);
+                             p->block_size, st, workspace, workspace_bytes);
     } else if (kern == MNB_KERNEL_GEMV_STREAM) {
         e = mnb::launch_gemv_stream(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
                                     p->block_size, st);

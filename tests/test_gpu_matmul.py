@@ -195,6 +195,45 @@ def test_prefill_config_full_size(cuda, M):
     _check_f16(y, ref, f"prefill M={M}")
 
 
+def test_gemm_k_split_plan():
+    import mnb
+    # M=256 and 512 (64 and 128 row tiles of 256 x 128 for 256 CUs) split K over 4 and 2
+    # workgroups per tile, with fp32 partials in the workspace; M=2048 fills the GPU unsplit
+    for m, ks in ((256, 4), (512, 2), (2048, 1)):
+        info = mnb.plan(mnb.problem(m, 8192, 3072, 4, 32, False))
+        assert info.kernel == mnb.KERNEL_GEMM_MFMA
+        assert info.grid_x == (m + 255) // 256 * 64 * ks
+        assert info.workspace_bytes == (ks * m * 8192 * 4 if ks > 1 else 0)
+
+
+@pytest.mark.parametrize("M,N,K,bs,zp", [(256, 8192, 3072, 32, False), (300, 130, 2048, 128, True),
+                                         (129, 300, 1024, 64, False)])
+def test_gemm_k_split_and_unsplit_runs(cuda, M, N, K, bs, zp):
+    # the split launch (workspace given) and the one-pass launch (no workspace) both meet the
+    # bar against the oracle, and the split is run-to-run bit-identical
+    import ctypes as C
+    import mnb
+    import torch
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=5 + M)
+    p = mnb.problem(M, N, K, 4, bs, zp)
+    assert mnb.workspace_bytes(p) > 0
+    print(f"[gpu] gemm split/unsplit M={M} N={N} K={K}", flush=True)
+    t = {k: _dev(inp[k], cuda) for k in ("A", "B", "scales", "zp")}
+    ys = [mnb.matmul_nbits(t["A"], t["B"], t["scales"], t["zp"], N, K, 4, bs) for _ in range(2)]
+    y1 = torch.empty(M, N, dtype=torch.float16, device=cuda)
+    s = int(torch.cuda.current_stream().cuda_stream)
+    mnb.check(mnb.load().mnb_matmul_nbits(C.byref(p), t["A"].data_ptr(), t["B"].data_ptr(),
+                                          t["scales"].data_ptr(),
+                                          t["zp"].data_ptr() if zp else None, y1.data_ptr(),
+                                          None, 0, s))
+    torch.cuda.synchronize()
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
+    split = [y.cpu().numpy() for y in ys]
+    assert np.array_equal(split[0].view(np.uint16), split[1].view(np.uint16))
+    _check_f16(split[0], ref, f"split M={M}")
+    _check_f16(y1.cpu().numpy(), ref, f"unsplit M={M}")
+
+
 def test_three_runs_bit_identical(cuda):
     # tests/ops/test_matmulnbits.py:558-653: repeated runs in one session are bit-identical
     inp = orc.make_inputs(4, 1000, 3072, bits=4, block_size=32, with_zp=True, seed=42)
