@@ -142,7 +142,9 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
     constexpr int DW_PER_SEG = 4 / SEGS;                 // dwords of a chunk per block segment
     const int G = 1 << log2g;
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    // wave-uniform: in a scalar register, the task loop and its column base stay scalar
+    const int wave = __builtin_amdgcn_readfirstlane(
+        (int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
     const int grp = lane >> log2g;
     const int gi = lane & (G - 1);
     const int ng = 64 >> log2g;

@@ -409,9 +409,13 @@ quantize_a_int8(const T* __restrict__ A, int8_t* __restrict__ qa, float* __restr
     float amax = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(a[e]));
-    // G consecutive threads share a block (G divides 64 and blocks start at multiples of G).
-#pragma unroll
-    for (int off = G >> 1; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    // G consecutive threads share a block (G divides 64 and blocks start at multiples of G);
+    // their maximum through DPP exchanges within the lane row (G <= 16)
+    static_assert(G <= 16, "block of at most 16 threads");
+    if constexpr (G >= 2) amax = fmaxf(amax, dpp_f<0xB1>(amax));     // lane ^ 1
+    if constexpr (G >= 4) amax = fmaxf(amax, dpp_f<0x4E>(amax));     // lane ^ 2
+    if constexpr (G >= 8) amax = fmaxf(amax, dpp_f<0x141>(amax));    // 7 - i within 8
+    if constexpr (G >= 16) amax = fmaxf(amax, dpp_f<0x140>(amax));   // 15 - i within 16
     const float inv = amax > 0.f ? 127.0f / amax : 0.f;
     int q[8];
     int s = 0;
