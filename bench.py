@@ -546,8 +546,9 @@ def main() -> int:
                       "int4 bs32, biases, SwiGLU alpha 1.702 beta 1 limit 7",
             "bytes": q_bytes, "us": round(q_us, 2),
             "GB/s": round(q_bytes / (q_us * 1e-6) / 1e9, 1),
-            "kernels": "qmoe_topk + qmoe_group_small + strip_gemv (fc1, SwiGLU applied as "
-                       "its tiles are stored) + strip_gemv (fc2) + qmoe_combine",
+            "kernels": "qmoe_topk + strip_gemv (fc1: finds its expert's rows from the "
+                       "routing, SwiGLU applied as its tiles are stored) + strip_gemv (fc2) + "
+                       "qmoe_combine",
             "roofline": {"bound": "hbm", "achieved": round(q_bytes / (q_us * 1e-6) / 1e9, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(q_bytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}

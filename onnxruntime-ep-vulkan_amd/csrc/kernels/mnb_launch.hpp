@@ -110,10 +110,19 @@ bool strip_gemv_forced_off();
 // SwiGLU applied by the strip GEMV as it stores interleaved (gate, linear) column pairs
 // (QMoE fc1 with swiglu_fusion = 1): y[r][c / 2] = act(h[r][c] + b[c], h[r][c + 1] + b[c + 1])
 // for even c, h rounded to fp16 before the bias, y row stride N / 2 (N even).
+// With expert_of set (QMoE decode batches: R = T * k <= 1024 assignments, groups <= 64) the
+// kernel also finds each expert's rows itself: expert e's rows are the assignments a with
+// expert_of[a] == e in order (token a / k), at grouped positions from #{a : expert_of[a] < e};
+// the first workgroup of each expert publishes offsets[e] (and offsets[E] = R) and pos_of[a]
+// of its assignments for the launches that follow.  row_index is then unused.
 struct StripSwiglu {
     const void* bias;    // fp16 [groups][N] or null
     float alpha, beta, limit;
     int has_limit;
+    const int32_t* expert_of;   // [R] or null
+    int32_t* offsets;           // [groups + 1], written
+    int32_t* pos_of;            // [R], written
+    int R, k;
 };
 // fp16 scales and Y; A is fp16, or for i8 (accuracy_level = 4) the int8 codes of
 // quantize_a_int8 in its quad-interleaved layout (quads = true) with their fp32 scales

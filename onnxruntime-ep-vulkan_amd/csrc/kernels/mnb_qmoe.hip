@@ -11,7 +11,9 @@
 //      qmoe_group      one workgroup: counting sort of the T*k (token, slot) assignments by
 //                      expert: offsets[E+1], the token of every grouped row, the grouped row of
 //                      every assignment.
-//      qmoe_group_small the same for T*k <= 1024 and E <= 64 (decode batches), stable.
+//      qmoe_group_small the same for T*k <= 1024 and E <= 64 (decode batches), stable; when
+//                      fc1 runs on the strip GEMV with SwiGLU it finds its rows itself
+//                      (StripSwiglu) and no sort launch runs.
 //   2. group_gemv      h = x W1_e^T for every grouped row (the MatMulNBits expert-grouped GEMV,
 //                      rows gathered through the sort), fp16 out.
 //   3. qmoe_swiglu     act = SwiGLU(h + b1_e): gate/linear interleaved or concatenated,
@@ -433,7 +435,20 @@ hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, con
         hipLaunchKernelGGL(qmoe_topk<f16>, dim3(tk_grid), dim3(256), 0, st,
                            static_cast<const f16*>(logits), (int)q.rows, (int)q.experts, q.k,
                            q.normalize, expert_of, weight_of);
-    if (R <= kSmallR && q.experts <= 64)
+    // expected rows per expert (twice the mean, at least one) sets the GEMV tile height
+    const int64_t hint = std::max<int64_t>(1, 2 * ((R + q.experts - 1) / q.experts));
+    // Interleaved gate/linear pairs on the strip GEMV: SwiGLU as fc1's tiles are stored; for
+    // decode batches fc1 also sorts its own rows out of expert_of and publishes offsets and
+    // pos_of, so no sort launch runs.
+    StripGeom sg;
+    const bool fused = q.fusion == 1 && hint <= 16 && !strip_gemv_forced_off() &&
+                       strip_gemv_aligned(x, fc1, fc1_s, nullptr, false) &&
+                       strip_geometry(2 * q.inter, q.hidden, q.experts, q.rows, false,
+                                      q.block_size, false, &sg);
+    const bool self_sort = fused && R <= kSmallR && q.experts <= 64;
+    if (self_sort) {
+        // sorted inside fc1
+    } else if (R <= kSmallR && q.experts <= 64)
         hipLaunchKernelGGL(qmoe_group_small, dim3(1), dim3(kSmallR), 0, st, expert_of, (int)R,
                            (int)q.experts, q.k, offsets, row_token, pos_of, expert_of_row);
     else
@@ -441,15 +456,16 @@ hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, con
                            (int)q.experts, q.k, offsets, row_token, pos_of, expert_of_row);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // expected rows per expert (twice the mean, at least one) sets the GEMV tile height
-    const int64_t hint = std::max<int64_t>(1, 2 * ((R + q.experts - 1) / q.experts));
-    // Interleaved gate/linear pairs on the strip GEMV: SwiGLU as fc1's tiles are stored.
-    StripGeom sg;
-    if (q.fusion == 1 && hint <= 16 && !strip_gemv_forced_off() &&
-        strip_gemv_aligned(x, fc1, fc1_s, nullptr, false) &&
-        strip_geometry(2 * q.inter, q.hidden, q.experts, q.rows, false, q.block_size, false,
-                       &sg)) {
-        const StripSwiglu sw{fc1_b, q.alpha, q.beta, q.limit, q.has_limit};
+    if (fused) {
+        StripSwiglu sw{fc1_b, q.alpha, q.beta, q.limit, q.has_limit, nullptr, nullptr, nullptr,
+                       0, 0};
+        if (self_sort) {
+            sw.expert_of = expert_of;
+            sw.offsets = offsets;
+            sw.pos_of = pos_of;
+            sw.R = (int)R;
+            sw.k = q.k;
+        }
         e = launch_strip_gemv(sg, false, x, nullptr, row_token, offsets, fc1, fc1_s, nullptr, act,
                               R, 2 * q.inter, q.hidden, q.block_size, st, &sw);
         if (e != hipSuccess) return e;

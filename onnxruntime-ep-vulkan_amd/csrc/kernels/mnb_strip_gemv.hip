@@ -163,20 +163,81 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     // requests go out before the group's row range is read (a dependent round trip, and for
     // gathered rows a second one before the activations); later tiles read it first.
     const bool eager = blockIdx.z == 0;
+    // Rows from the routing itself (StripSwiglu): the expert ids are requested before the
+    // weights, so that waiting for them does not wait for the weights (loads complete in order)
+    constexpr int kChunks = 16;                          // R <= 1024
+    const bool routed = SWIGLU && sw.expert_of;
+    int xv[SWIGLU ? kChunks : 1];
+    if constexpr (SWIGLU) {
+        if (routed) {
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c)            // clamped, unpredicated: issued together
+                xv[c] = sw.expert_of[min(64 * c + lane, sw.R - 1)];
+        }
+    }
     if (eager) request();
     int row_lo = 0, row_hi = M;
-    if (offsets) {
-        row_lo = offsets[e];
-        row_hi = offsets[e + 1];
+    int arow;
+    if constexpr (SWIGLU) {
+      if (routed) {
+        // Every wavefront scans the R assignments in 64-lane chunks -- a ballot for "expert
+        // below e" counts row_lo, one for "expert e" ranks this expert's assignments -- and
+        // keeps the tokens of this tile's rows in its own 16 LDS slots (the partial-tile
+        // buffer, not used before the first strip).
+        int32_t* const s_tok = reinterpret_cast<int32_t*>(smem + s_bytes + z_bytes) + 16 * wave;
+        int n_lt = 0, n_eq = 0;
+        const int t0 = 16 * (int)blockIdx.z;
+        const bool publish = blockIdx.x == 0 && blockIdx.z == 0 && wave == 0;
+        int rank[kChunks];
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) {
+            if (64 * c >= sw.R) break;                   // wave-uniform
+            const bool valid = 64 * c + lane < sw.R;
+            const uint64_t m_lt = __ballot(valid && xv[c] < e);
+            const uint64_t m_eq = __ballot(valid && xv[c] == e);
+            rank[c] = n_eq + (int)__builtin_amdgcn_mbcnt_hi(
+                                 (uint32_t)(m_eq >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m_eq, 0));
+            if (valid && xv[c] == e && rank[c] >= t0 && rank[c] < t0 + 16)
+                s_tok[rank[c] - t0] = (64 * c + lane) / sw.k;
+            n_lt += __popcll(m_lt);
+            n_eq += __popcll(m_eq);
+        }
+        row_lo = n_lt;
+        row_hi = n_lt + n_eq;
+        if (publish) {                                   // before any early exit
+            if (lane == 0) {
+                sw.offsets[e] = row_lo;
+                if (e == (int)gridDim.y - 1) sw.offsets[e + 1] = sw.R;
+            }
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) {
+                if (64 * c >= sw.R) break;
+                if (64 * c + lane < sw.R && xv[c] == e) sw.pos_of[64 * c + lane] = row_lo + rank[c];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int r0 = row_lo + t0;
+        if (r0 >= row_hi) return;                        // the whole workgroup, before a barrier
+        if (!eager) request();
+        arow = s_tok[min(nl, row_hi - r0 - 1)];
+      }
+    }
+    if (!routed) {
+        if (offsets) {
+            row_lo = offsets[e];
+            row_hi = offsets[e + 1];
+        }
+        const int r0 = row_lo + blockIdx.z * 16;
+        if (r0 >= row_hi) return;                        // the whole workgroup, before a barrier
+        if (!eager) request();
+        // ---- this lane's row of the tile (row nl) ----
+        int rr = r0 + nl;
+        rr = rr < row_hi ? rr : row_hi - 1;
+        arow = row_index ? row_index[rr] : rr;
     }
     const int r0 = row_lo + blockIdx.z * 16;
-    if (r0 >= row_hi) return;                            // the whole workgroup, before a barrier
-    if (!eager) request();
 
     // ---- A operands of this wavefront's quads: row nl of the tile, k = 32c + 8g .. + 8 ----
-    int rr = r0 + nl;
-    rr = rr < row_hi ? rr : row_hi - 1;
-    const int arow = row_index ? row_index[rr] : rr;
     f16x8 af[I8 ? 1 : QW][4];
     i32x2 aq[I8 ? QW : 1][4];
     f32x4 sao[I8 ? QW : 1][I8 ? BPQ : 1];                // int8: a_scale of rows 4g .. 4g + 3
