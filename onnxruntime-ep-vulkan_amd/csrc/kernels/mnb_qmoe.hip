@@ -352,19 +352,29 @@ qmoe_combine(const f16* __restrict__ o, const f16* __restrict__ b2,
         float acc[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-        for (int s = 0; s < k; ++s) {
-            const int64_t a = t * k + s;
-            const float w = weight_of[a];
-            const f16x8 v = *reinterpret_cast<const f16x8*>(o + (int64_t)pos_of[a] * hidden + c);
-            if (b2) {
-                const f16x8 bb =
-                    *reinterpret_cast<const f16x8*>(b2 + (int64_t)expert_of[a] * hidden + c);
+        // all slots' indices first, then all their rows (k <= 8; slots past k re-read slot k-1
+        // and are not added): two dependent round trips instead of two per slot
+        int pos[8], ex[8];
+        float w[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] += w * ((float)v[j] + (float)bb[j]);
-            } else {
+        for (int s = 0; s < 8; ++s) {
+            const int64_t a = t * k + min(s, k - 1);
+            pos[s] = pos_of[a];
+            ex[s] = expert_of[a];
+            w[s] = weight_of[a];
+        }
+        f16x8 v[8], bb[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] += w * (float)v[j];
-            }
+        for (int s = 0; s < 8; ++s) {
+            v[s] = *reinterpret_cast<const f16x8*>(o + (int64_t)pos[s] * hidden + c);
+            bb[s] = b2 ? *reinterpret_cast<const f16x8*>(b2 + (int64_t)ex[s] * hidden + c)
+                       : f16x8{};
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            if (s >= k) break;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] += w[s] * ((float)v[s][j] + (float)bb[s][j]);
         }
         f16x8 out;
 #pragma unroll
