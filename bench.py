@@ -81,6 +81,62 @@ def measured_traffic(node: str, algorithmic: int):
     return d["traffic_bytes_per_launch"]
 
 
+# Launch shapes over which the read floor is the least time: 1 KB runs per wavefront, wavefronts
+# per workgroup, contiguous (1) or grid-stride (0) runs.
+READ_SHAPES = [(l, w, c) for l in (1, 2, 4, 8, 16) for w in (4, 8, 16) for c in (1, 0)]
+
+
+def graph_us(torch, stream, fn, reps: int, tries: int = 3) -> float:
+    """Least average device time per call of `fn(r, stream_ptr)` over `tries` replays of one HIP
+    graph of `reps` calls (HIP events on the stream the graph is replayed on)."""
+    for r in range(2):
+        fn(r, int(stream.cuda_stream))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(stream)
+    with torch.cuda.graph(g, stream=cs):
+        sp = int(torch.cuda.current_stream().cuda_stream)
+        for r in range(reps):
+            fn(r, sp)
+    torch.cuda.synchronize()
+    g.replay()
+    best = float("inf")
+    for _ in range(tries):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, 1e3 * a.elapsed_time(b) / reps)
+    del g
+    return best
+
+
+def read_floor(lib, torch, dev, stream, nbytes: int, region, shapes=READ_SHAPES, reps: int = 40):
+    """The least per-launch time (us) of mnb_calibrate_read over `shapes` for `nbytes`, reading a
+    different copy of `region` (>= 2x the Infinity Cache) on every launch, and the best shape."""
+    import mnb
+
+    stride = -(-nbytes // 65536) * 65536
+    copies = region.numel() // stride
+    assert copies * nbytes >= 2 * MALL_BYTES, "region too small to rotate past the Infinity Cache"
+    out = torch.zeros(1024, dtype=torch.int32, device=dev)
+    best, best_shape = float("inf"), None
+    for (l, w, c) in shapes:
+        def f(r, sp, l=l, w=w, c=c):
+            rc = lib.mnb_calibrate_read(region.data_ptr() + (r % copies) * stride, nbytes, l, w,
+                                        c, out.data_ptr(), sp)
+            if rc:
+                mnb.check(rc)
+        us = graph_us(torch, stream, f, max(reps, 2 * copies // 3))
+        if us < best:
+            best, best_shape = us, {"loads_per_lane": l, "waves_per_group": w,
+                                    "contiguous": bool(c)}
+    return best, best_shape
+
+
 def cpu_baseline(seconds: float = 10.0) -> dict:
     """The oracle's C restatement on the host cores, over the same layer set at M=1."""
     import numpy as np
@@ -137,6 +193,10 @@ def main() -> int:
                          "configs[3], weights rotated over two copies) or the accuracy_level=4 "
                          "call (configs[4]) --steps times, then one plain 256 MiB device copy "
                          "for calibrating FETCH_SIZE/WRITE_SIZE; no JSON")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="print, one JSON line per size, the least time one launch needs to read "
+                         "that many bytes (mnb_calibrate_read over launch shapes), for the decode "
+                         "nodes' byte counts and larger sizes; no benchmark line")
     ap.add_argument("--pmc-prefill", type=int, default=None, metavar="M",
                     help="counter-collection mode: launch only the prefill GEMM (K=3072, N=8192) "
                          "at M rows --steps times; no JSON")
@@ -177,6 +237,20 @@ def main() -> int:
     def step(s, sp=sptr):
         for i in range(len(LAYER)):
             launch(i, s % copies, sp)
+
+    if args.read_floor:
+        region = torch.empty(1536 << 20, dtype=torch.uint8, device=dev)
+        region.random_(generator=gen)
+        sizes = [(name, node_bytes(1, k, n)) for name, k, n in LAYER]
+        sizes += [("acc4", node_bytes(16, 8192, 3072, bs=128))]
+        sizes += [(f"{mb} MiB", mb << 20) for mb in (1, 2, 4, 8, 32, 64, 128, 256, 512)]
+        for name, nb in sizes:
+            us, shape = read_floor(lib, torch, dev, stream, nb, region)
+            print(json.dumps({"size": name, "bytes": nb, "floor_us": round(us, 3),
+                              "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
+                              "frac_of_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                              "shape": shape}), flush=True)
+        return 0
 
     if args.pmc_prefill:
         pm, pk, pn = args.pmc_prefill, 3072, 8192
@@ -325,11 +399,23 @@ def main() -> int:
         kern_us.append(1e3 * a.elapsed_time(b) / reps)
         del g1
 
+    # The read floor of each node's byte count: the least time one launch of a kernel that does
+    # nothing but read that many bytes (all loads issued up front) needs on this device, over
+    # launch shapes, reading a fresh copy on every launch as the decode launches do.
+    region = torch.empty(768 << 20, dtype=torch.uint8, device=dev)
+    region.random_(generator=gen)
+    floors = [read_floor(lib, torch, dev, stream, node_bytes(1, k, n), region)
+              for _, k, n in LAYER]
+    del region
+
     per_kernel = []
     for i, ((name, k, n), us) in enumerate(zip(LAYER, kern_us)):
         nb = node_bytes(1, k, n)
         per_kernel.append({"node": name, "K": k, "N": n, "bytes": nb, "us": round(us, 3),
                            "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
+                           "frac_hbm": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                           "read_floor_us": round(floors[i][0], 3),
+                           "frac_of_read_floor": round(floors[i][0] / us, 4),
                            "kernel": mnb.KERNEL_NAMES.get(mnb.plan(probs[i]).kernel, "?")})
     dom = max(range(len(LAYER)), key=lambda i: kern_us[i])
     dom_bytes = node_bytes(1, LAYER[dom][1], LAYER[dom][2])
@@ -338,7 +424,10 @@ def main() -> int:
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(LAYER[dom][0], dom_bytes),
                 "kernel": f"MatMulNBits {LAYER[dom][0]} M=1 K={LAYER[dom][1]} N={LAYER[dom][2]}",
-                "per_launch_bytes": dom_bytes, "launch_us": round(kern_us[dom], 3)}
+                "per_launch_bytes": dom_bytes, "launch_us": round(kern_us[dom], 3),
+                "read_floor_us": round(floors[dom][0], 3),
+                "read_floor_shape": floors[dom][1],
+                "frac_of_read_floor": round(floors[dom][0] / kern_us[dom], 4)}
 
     # Prefill: M in {256, 512, 2048}, K=3072, N=8192, implicit zero point
     # (not part of `value`).  HIP events around a graph of `preps` launches; weights rotate over

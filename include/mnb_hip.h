@@ -356,6 +356,16 @@ uint64_t mnb_launch_count(void);
 int mnb_calibrate_mfma(int32_t workgroups, int32_t iters, const void* operands_f16, float* out,
                        void* stream);
 
+/* Read floor; no counterpart in the reference (a measurement utility for bench.py).  Reads
+ * `bytes` (a positive multiple of 16) at `src` (16-byte aligned) once: every wavefront issues
+ * `loads_per_lane` (1, 2, 4, 8 or 16) non-temporal 16-byte loads per lane, 1 KB per instruction,
+ * all before using any, over contiguous runs (contiguous != 0) or runs strided by the number of
+ * wavefronts; `waves_per_group` 1..16.  `out` holds 1024 uint32 and is written only in a case
+ * no real data produces.  The shortest time over launch shapes is the least time any kernel
+ * needs to stream that many bytes in one launch. */
+int mnb_calibrate_read(const void* src, size_t bytes, int32_t loads_per_lane,
+                       int32_t waves_per_group, int32_t contiguous, uint32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

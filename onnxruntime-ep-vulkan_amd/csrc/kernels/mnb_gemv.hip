@@ -98,7 +98,7 @@ constexpr int gemv_group_blocks() {
 }
 
 template <int BITS, int BS, bool HAS_ZP, int MT>
-__global__ void __launch_bounds__(1024)
+__global__ void __launch_bounds__(kGemvMaxThreads)
 gemv_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ S,
               const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K) {
     using Chunk = LaneChunk<BITS, BS>;
@@ -338,6 +338,7 @@ template <int BITS, int BS, bool HAS_ZP>
 static hipError_t gemv_dispatch_mt(const GemvGeom& g, const void* a, const uint8_t* b,
                                    const void* s, const uint8_t* z, void* y, int64_t m,
                                    int64_t n, int64_t k, hipStream_t stream) {
+    if (g.waves < 1 || 64 * g.waves > kGemvMaxThreads) return hipErrorInvalidValue;
     const dim3 grid((unsigned)g.gx, (unsigned)g.gy, 1);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     const f16* A = static_cast<const f16*>(a);

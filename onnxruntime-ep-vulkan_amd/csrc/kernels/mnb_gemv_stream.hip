@@ -76,6 +76,11 @@ hipError_t launch_gemv_stream_cfg(const StreamConfig& c, const void* a, const ui
                                   const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
                                   int64_t k, int bits, int bs, hipStream_t st) {
     if (m == 0) return hipSuccess;
+    // the kernel is compiled for kStreamMaxThreads threads per workgroup
+    if (c.waves_per_group < 1 || 64 * c.waves_per_group > kStreamMaxThreads)
+        return hipErrorInvalidValue;
+    if (c.mr < 1 || c.mr > 4 || (c.u != 1 && c.u != 2) || c.tasks < 1 || c.total_waves < 1)
+        return hipErrorInvalidValue;
     if (c.g != 16 && c.g != 32 && c.g != 64) return hipErrorInvalidValue;
     if ((int64_t)c.g * c.cpl * (128 / bits) < k) return hipErrorInvalidValue;
     if (bits == 4) return stream_bits<4>(c, a, b, s, z, y, m, n, k, bs, st);

@@ -132,7 +132,7 @@ __device__ __forceinline__ void stream_fetch(StreamPass<chunk_segs<BITS, BS>(), 
 // rows of A (rows m0 .. m0+MR-1, m0 = blockIdx.y * MR) are held in registers for the lane's
 // chunk set; CPL chunks per lane at most.  G is a power of two passed as log2(G).
 template <int BITS, int BS, bool HAS_ZP, int MR, int CPL, int U, bool NT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kStreamMaxThreads)
 gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ S,
             const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K, int log2g,
             int tasks, int total_waves) {

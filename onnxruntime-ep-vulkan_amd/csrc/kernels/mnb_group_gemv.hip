@@ -38,7 +38,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 // I8: false = fp16 activations (A is f16 [a_rows][K]); true = int8 activations (A is the
 // quantiser's qa [a_rows][K] in permuted order, a_scale fp32 [a_rows][K/BS]).
 template <typename T, bool I8, int BS, bool HAS_ZP, int MT>
-__global__ void __launch_bounds__(512)
+__global__ void __launch_bounds__(kGroupMaxThreads)
 group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
            const int32_t* __restrict__ row_index, const int32_t* __restrict__ offsets,
            const uint8_t* __restrict__ B, const T* __restrict__ S, const uint8_t* __restrict__ Z,
@@ -512,6 +512,7 @@ static hipError_t group_mt(const GroupGeom& g, const void* a, const float* a_sca
                            const int32_t* row_index, const int32_t* offsets, const uint8_t* b,
                            const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
                            int64_t k, f32x4* part, int* cnt, hipStream_t st) {
+    if (g.waves < 1 || 64 * g.waves > kGroupMaxThreads) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(g.gx * g.ksplit), (unsigned)g.gy, (unsigned)g.gz);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     const T* S = static_cast<const T*>(s);

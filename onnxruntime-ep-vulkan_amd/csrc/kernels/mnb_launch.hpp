@@ -6,6 +6,13 @@
 
 namespace mnb {
 
+// Threads per workgroup each kernel family is compiled for (its __launch_bounds__).  A launcher
+// refuses a launch shape above its kernel's limit before anything reaches the device: a
+// workgroup larger than the compiled bound fails as an unspecified launch failure.
+constexpr int kStreamMaxThreads = 256;   // gemv_stream
+constexpr int kGroupMaxThreads = 512;    // group_gemv
+constexpr int kGemvMaxThreads = 1024;    // gemv_f16_mfma
+
 // Geometry shared by the planner (host) and the launchers.
 struct GemvGeom {
     int mt;        // 16-row M tiles per workgroup (1, 2 or 4)
@@ -201,5 +208,9 @@ hipError_t launch_gqa(const GqaArgs& a, const void* qkv, const void* past_k, con
 // Roofline calibration (mnb_calibrate.hip): workgroups x 4 wavefronts x iters x 16 MFMAs.
 hipError_t launch_mfma_calibrate(const void* operands, float* out, int workgroups, int iters,
                                  hipStream_t stream);
+// Read floor (mnb_calibrate.hip): n16 16-byte units, loads_per_lane in {1,2,4,8,16} 1 KB runs
+// per wavefront, wpg wavefronts per workgroup (1..16), contiguous or grid-stride runs.
+hipError_t launch_read_floor(const void* src, int64_t n16, int loads_per_lane, int wpg,
+                             bool contig, uint32_t* out, hipStream_t stream);
 
 }  // namespace mnb

@@ -89,6 +89,25 @@ int mnb_calibrate_mfma(int32_t workgroups, int32_t iters, const void* operands_f
     return MNB_OK;
 }
 
+int mnb_calibrate_read(const void* src, size_t bytes, int32_t loads_per_lane,
+                       int32_t waves_per_group, int32_t contiguous, uint32_t* out, void* stream) {
+    if (!src || !out) return fail(MNB_ERR_INVALID, "src and out must not be NULL");
+    if (!aligned(src, 16) || bytes == 0 || bytes % 16)
+        return fail(MNB_ERR_INVALID, "src must be 16-byte aligned and bytes a positive multiple "
+                                     "of 16 (got %zu)", bytes);
+    if (loads_per_lane != 1 && loads_per_lane != 2 && loads_per_lane != 4 &&
+        loads_per_lane != 8 && loads_per_lane != 16)
+        return fail(MNB_ERR_INVALID, "loads_per_lane = %d; 1, 2, 4, 8 or 16", loads_per_lane);
+    if (waves_per_group < 1 || waves_per_group > 16)
+        return fail(MNB_ERR_INVALID, "waves_per_group = %d; 1..16 (the kernel is compiled for "
+                                     "1024 threads)", waves_per_group);
+    hipError_t e = mnb::launch_read_floor(src, (int64_t)(bytes / 16), loads_per_lane,
+                                          waves_per_group, contiguous != 0, out,
+                                          static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "read-floor launch");
+    return MNB_OK;
+}
+
 int mnb_check_problem(const mnb_problem* p) {
     if (!p) return fail(MNB_ERR_INVALID, "problem is NULL");
     if (p->bits != 4 && p->bits != 8)

@@ -141,6 +141,7 @@ def load() -> C.CDLL:
         "mnb_memcpy": (C.c_int, [C.c_int, vp, vp, sz, C.c_int]),
         "mnb_launch_count": (C.c_uint64, []),
         "mnb_calibrate_mfma": (C.c_int, [i32, i32, vp, vp, vp]),
+        "mnb_calibrate_read": (C.c_int, [vp, sz, i32, i32, i32, vp, vp]),
         "mnb_qmoe_check": (C.c_int, [C.POINTER(QmoeProblem)]),
         "mnb_qmoe_workspace_bytes": (C.c_int, [C.POINTER(QmoeProblem), C.POINTER(sz)]),
         "mnb_qmoe": (C.c_int, [C.POINTER(QmoeProblem), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,

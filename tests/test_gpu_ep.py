@@ -69,6 +69,41 @@ def test_compute_matches_oracle(host, lead, N, K, bits, bs, zp):
     _check(y.reshape(M, N), ref, "ep")
 
 
+@pytest.mark.parametrize("lead,N,K,bs,zp,a_dtype", [
+    ((16,), 3072, 8192, 128, True, np.float16),
+    ((1,), 512, 1024, 32, True, np.float32),        # the shape of the reference's level-4 record
+    ((2, 3), 96, 512, 64, False, np.float16),       # leading dims fold into M = 6
+])
+def test_compute_accuracy_level_4(host, lead, N, K, bs, zp, a_dtype):
+    """A node with accuracy_level = 4 is claimed, compiled and computed with int8 activations
+    (the plugin's Compute runs the quantiser and the int8 MFMA GEMV), matching the oracle's
+    level-4 definition at the output dtype's bar."""
+    print(f"[gpu] ep acc4 lead={lead} N={N} K={K} bs={bs} zp={zp} {a_dtype.__name__}", flush=True)
+    M = int(np.prod(lead))
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=4 * M + N,
+                          a_dtype=a_dtype)
+    host.reset()
+    a_name, y_name = mh.add_matmul_nbits(host, "mm", inp, N, K, 4, bs, lead + (K,),
+                                         a_dtype=a_dtype, acc_level=4)
+    assert host.get_capability() == (1, ["mm:drop"])
+    assert host.compile() == 0, mh.err()
+    before = mh.EP_COUNT()
+    host.feed(a_name, inp["A"].reshape(lead + (K,)))
+    assert host.compute(0) == 0, mh.err()
+    assert mh.EP_COUNT() == before + 1
+    y = host.fetch(y_name, a_dtype, M * N).reshape(M, N)
+    ref4 = orc.matmul_nbits_acc4(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
+    if a_dtype == np.float16:
+        _check(y, ref4, "ep acc4")
+    else:
+        # fp32 output: only the fp32 combination of exact int32 block dots differs
+        assert orc.max_err_rms_normalised(y, ref4) <= 1e-5
+    # the level-1 result differs by the int8 quantisation noise of A (about 0.6 % of RMS(y))
+    ref1 = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
+    rms = float(np.sqrt(np.mean(ref1.astype(np.float64) ** 2)))
+    assert float(np.sqrt(np.mean((y.astype(np.float64) - ref1) ** 2))) <= 1.2e-2 * rms
+
+
 def test_three_runs_bit_identical_and_row_count_changes(host):
     N, K = 512, 2048
     inp = orc.make_inputs(4, N, K, with_zp=True, seed=5)

@@ -1,0 +1,80 @@
+"""Launch-shape guards of the HIP launchers (host-only: nothing reaches a device).
+
+A workgroup larger than the thread count a kernel was compiled for (its __launch_bounds__) does
+not run: the launch fails as an unspecified launch failure.  The launchers therefore refuse such
+a shape before any HIP call, returning hipErrorInvalidValue.  The decode launcher takes its shape
+as a StreamConfig (internal C++ API of libmnb_hip.so, bound here by its mangled name).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+HIP_ERROR_INVALID_VALUE = 1
+LAUNCH_STREAM_CFG = "_ZN3mnb22launch_gemv_stream_cfgERKNS_12StreamConfigEPKvPKhS4_S6_PvllliiP12ihipStream_t"
+
+
+class StreamConfig(C.Structure):
+    # mnb::StreamConfig (csrc/kernels/mnb_launch.hpp)
+    _fields_ = [("mr", C.c_int), ("g", C.c_int), ("cpl", C.c_int), ("u", C.c_int),
+                ("waves_per_group", C.c_int), ("nontemporal", C.c_int),
+                ("tasks", C.c_int64), ("total_waves", C.c_int64)]
+
+
+def _launcher():
+    import mnb
+
+    f = getattr(mnb.load(), LAUNCH_STREAM_CFG)
+    f.restype = C.c_int
+    f.argtypes = [C.POINTER(StreamConfig)] + [C.c_void_p] * 5 + [C.c_int64] * 3 + \
+        [C.c_int, C.c_int, C.c_void_p]
+    return f
+
+
+def _cfg(**kw) -> StreamConfig:
+    # the planner's shape for qkv at M=1 (K=3072, N=9216): 32 lanes per column, 3 chunks each
+    base = dict(mr=1, g=32, cpl=3, u=1, waves_per_group=4, nontemporal=1, tasks=4608,
+                total_waves=2048)
+    base.update(kw)
+    return StreamConfig(**base)
+
+
+def _call(cfg: StreamConfig) -> int:
+    fake = C.c_void_p(0x1000)          # never dereferenced: the guard returns first
+    return _launcher()(C.byref(cfg), fake, fake, fake, fake, fake, 1, 9216, 3072, 4, 32, None)
+
+
+def test_stream_launch_refuses_workgroups_above_compiled_bound():
+    # 8 wavefronts = 512 threads; gemv_stream is compiled for 256
+    assert _call(_cfg(waves_per_group=8)) == HIP_ERROR_INVALID_VALUE
+    assert _call(_cfg(waves_per_group=5)) == HIP_ERROR_INVALID_VALUE
+    assert _call(_cfg(waves_per_group=0)) == HIP_ERROR_INVALID_VALUE
+
+
+def test_stream_launch_refuses_malformed_shapes():
+    assert _call(_cfg(g=8)) == HIP_ERROR_INVALID_VALUE
+    assert _call(_cfg(cpl=2)) == HIP_ERROR_INVALID_VALUE          # 32 * 2 chunks < 96
+    assert _call(_cfg(mr=5)) == HIP_ERROR_INVALID_VALUE
+    assert _call(_cfg(u=3)) == HIP_ERROR_INVALID_VALUE
+    assert _call(_cfg(total_waves=0)) == HIP_ERROR_INVALID_VALUE
+
+
+def test_planner_shapes_stay_within_compiled_bounds():
+    """Every plan the planner makes for the decode, strip, group and GEMV kernels uses a
+    workgroup no larger than that kernel family's compiled bound."""
+    import mnb
+
+    bounds = {mnb.KERNEL_GEMV_STREAM: 256, mnb.KERNEL_GROUP_MFMA: 512,
+              mnb.KERNEL_GEMV_MFMA: 1024, mnb.KERNEL_GEMM_MFMA: 512, mnb.KERNEL_ACC4_I8: 1024,
+              mnb.KERNEL_STRIP_MFMA: 1024, mnb.KERNEL_GENERIC: 256}
+    for m in (1, 2, 3, 4, 5, 8, 16, 17, 33, 64, 65, 256, 2048):
+        for k, n in ((3072, 9216), (8192, 3072), (2880, 2880), (128, 48)):
+            for bits in (4, 8):
+                for bs in (16, 32, 64, 128):
+                    for level in (0, 4):
+                        p = mnb.problem(m, n, k, bits, bs, True, mnb.DTYPE_F16, level)
+                        try:
+                            info = mnb.plan(p)
+                        except mnb.MnbError:
+                            continue
+                        assert 64 * info.waves_per_group <= bounds[info.kernel], (m, k, n, bits, bs, level, info.kernel, info.waves_per_group)
