@@ -1,13 +1,9 @@
 // Launch configuration of the streaming decode GEMV (kernel in mnb_gemv_stream.hpp, instantiated
 // per bit width in mnb_gemv_stream_b4.hip / mnb_gemv_stream_b8.hip).
-#include "mnb_launch.hpp"
+#include "mnb_gemv_stream.hpp"
 
 namespace mnb {
 
-template <int BITS>
-hipError_t stream_bits(const StreamConfig& c, const void* a, const uint8_t* b, const void* s,
-                       const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bs,
-                       hipStream_t st);
 extern template hipError_t stream_bits<4>(const StreamConfig&, const void*, const uint8_t*,
                                           const void*, const uint8_t*, void*, int64_t, int64_t,
                                           int64_t, int, hipStream_t);
@@ -18,74 +14,97 @@ extern template hipError_t stream_bits<8>(const StreamConfig&, const void*, cons
 namespace {
 
 constexpr int kNumCUs = 256;
+// Largest dynamic LDS a decode workgroup may take: with more the decode shapes would fit one
+// workgroup per CU and the launch is left to the row-tiled kernels.
+constexpr int64_t kStreamMaxLds = 96 * 1024;
 
-// Chunks-per-lane capacity for MR rows held in registers.
-int cpl_cap(int mr) { return mr == 1 ? 8 : (mr == 2 ? 4 : 2); }
+// Chunks per lane the kernel is instantiated for: 8 for one row and one column per lane group,
+// 4 with two columns or with several rows (two columns only for one row).
+int cpl_cap(int u, int mr) { return u == 1 && mr == 1 ? 8 : 4; }
 
-int rows_tile(int64_t m) { return m <= 1 ? 1 : (m == 2 ? 2 : (m == 3 ? 3 : 4)); }
+// Fills the derived fields (workgroups along N, LDS bytes) of a shape; false when the shape is
+// malformed or exceeds what the kernel is compiled for.
+bool derive(StreamConfig& c, int64_t n, int64_t k, int bits, int bs) {
+    if (c.waves_per_group < 1 || 64 * c.waves_per_group > kStreamMaxThreads) return false;
+    if (c.mr < 1 || c.mr > 4 || (c.u != 1 && c.u != 2)) return false;
+    if (c.g != 16 && c.g != 32 && c.g != 64) return false;
+    if (bits != 4 && bits != 8) return false;
+    const int64_t wpc = 128 / bits;
+    if (k <= 0 || k % wpc || k % bs || n <= 0) return false;
+    const int64_t cpc = k / wpc;
+    if (c.mr > 1 && c.u != 1) return false;
+    if (c.cpl < 1 || c.cpl > cpl_cap(c.u, c.mr) || (int64_t)c.g * c.cpl < cpc) return false;
+    const int64_t cols = (int64_t)c.waves_per_group * (64 / c.g) * c.u;
+    const int64_t bpc = k / bs;
+    const int64_t zpb = (bpc * bits + 7) / 8;
+    c.groups = (n + cols - 1) / cols;
+    c.lds = c.mr * cpc * (bits == 4 ? stream_chunk_stride<4>() : stream_chunk_stride<8>()) +
+            ((cols * bpc * 2 + 15) & ~15) + ((cols * zpb + 15) & ~15);
+    return c.groups <= 0x7fffffff && c.lds <= kStreamMaxLds;
+}
 
 }  // namespace
+
+StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int bs) {
+    StreamConfig c{};
+    c.mr = m <= 1 ? 1 : (int)(m < 4 ? m : 4);
+    const int64_t cpc = k / (128 / bits);
+    // Lane-group width: the widest group whose lanes are best filled (G * CPL chunk slots for
+    // cpc chunks), so each load instruction reads the longest contiguous runs.
+    double best = -1.0;
+    int g = 64;
+    for (int cand : {64, 32, 16}) {
+        const int64_t cpl = (cpc + cand - 1) / cand;
+        if (cpl > cpl_cap(1, c.mr)) continue;
+        const double fill = (double)cpc / (double)(cand * cpl);
+        if (fill > best + 1e-9) { best = fill; g = cand; }
+    }
+    c.g = g;
+    c.cpl = (int)((cpc + g - 1) / g);
+    // Workgroups: every one stages the whole activation vector (2*K bytes per row) before it
+    // streams weights, so more workgroups mean more of that traffic ahead of the weights.
+    // Measured on MI355X (Phi-3.5 decode shapes): about three workgroups per CU for K <= 4096,
+    // one per CU for K = 8192; 4..16 wavefronts each, one column per lane group.
+    const int64_t target_groups = (k <= 4096 ? 3 : 1) * kNumCUs;
+    const int64_t cols_per_group = (n + target_groups - 1) / target_groups;
+    const int64_t per_wave = 64 / g;
+    int64_t w = (cols_per_group + per_wave - 1) / per_wave;
+    const int64_t wmax = kStreamMaxThreads / 64;
+    c.u = 1;
+    if (w > wmax && c.mr == 1 && c.cpl <= cpl_cap(2, 1)) {
+        c.u = 2;
+        w = (cols_per_group + 2 * per_wave - 1) / (2 * per_wave);
+    }
+    c.waves_per_group = (int)(w < 4 ? 4 : (w > wmax ? wmax : w));
+    derive(c, n, k, bits, bs);
+    return c;
+}
 
 bool gemv_stream_supported(int64_t m, int64_t k, int bits, int bs) {
     if (bits != 4 && bits != 8) return false;
     if (bs != 16 && bs != 32 && bs != 64 && bs != 128) return false;
+    if (m < 1 || m > 4) return false;
     const int wpc = 128 / bits;
     if (k <= 0 || k % wpc || k % bs) return false;
-    const int mr = rows_tile(m);
-    if (m < 1 || m > 4) return false;
-    const int64_t cpc = k / wpc;
-    return cpc <= (int64_t)64 * cpl_cap(mr);
+    StreamConfig c = gemv_stream_config(m, 1 << 20, k, bits, bs);
+    return derive(c, 1 << 20, k, bits, bs);
 }
 
-StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int bs) {
-    (void)bs;
-    StreamConfig c{};
-    c.mr = rows_tile(m);
-    const int64_t cpc = k / (128 / bits);
-    const int cap = cpl_cap(c.mr);
-    // Lane-group width: weigh the fraction of lane slots that hold a chunk against having enough
-    // wavefronts in flight (about 16 per CU) to cover HBM latency.  Measured on MI355X for the
-    // Phi-3.5 shapes: 96 chunks per column -> G = 32 when N >= 9216, G = 64 for N = 3072;
-    // 256 chunks -> G = 64.
-    double best = -1.0;
-    int g = 64;
-    for (int cand : {64, 32, 16}) {                 // ties go to the wider group
-        const int64_t cpl = (cpc + cand - 1) / cand;
-        if (cpl > cap) continue;
-        const double fill = (double)cpc / (double)(cand * cpl);
-        const double waves = (double)n * cand / 64.0;
-        const double par = waves >= 16.0 * kNumCUs ? 1.0 : waves / (16.0 * kNumCUs);
-        const double score = fill * __builtin_sqrt(par);
-        if (score > best + 1e-9) { best = score; g = cand; }
-    }
-    c.g = g;
-    c.cpl = (int)((cpc + g - 1) / g);
-    c.u = 1;
-    c.waves_per_group = 4;
-    c.nontemporal = 1;
-    const int ng = 64 / g;
-    const int64_t tasks = (n + (int64_t)ng * c.u - 1) / ((int64_t)ng * c.u);
-    c.tasks = tasks;
-    // Up to 8 wavefronts per CU; the rest of the columns are covered by looping, which keeps
-    // the next pass's loads in flight while the current one is reduced.
-    c.total_waves = tasks < 8 * kNumCUs ? tasks : 8 * kNumCUs;
-    return c;
-}
-
-hipError_t launch_gemv_stream_cfg(const StreamConfig& c, const void* a, const uint8_t* b,
+hipError_t launch_gemv_stream_cfg(const StreamConfig& cfg, const void* a, const uint8_t* b,
                                   const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
                                   int64_t k, int bits, int bs, hipStream_t st) {
     if (m == 0) return hipSuccess;
-    // the kernel is compiled for kStreamMaxThreads threads per workgroup
-    if (c.waves_per_group < 1 || 64 * c.waves_per_group > kStreamMaxThreads)
-        return hipErrorInvalidValue;
-    if (c.mr < 1 || c.mr > 4 || (c.u != 1 && c.u != 2) || c.tasks < 1 || c.total_waves < 1)
-        return hipErrorInvalidValue;
-    if (c.g != 16 && c.g != 32 && c.g != 64) return hipErrorInvalidValue;
-    if ((int64_t)c.g * c.cpl * (128 / bits) < k) return hipErrorInvalidValue;
+    StreamConfig c = cfg;
+    // the shape is checked (the kernel is compiled for kStreamMaxThreads threads per workgroup,
+    // U <= 2, CPL <= 8) and its derived fields recomputed before anything is launched
+    if (m < 0 || c.mr < (m < 4 ? m : 4) || !derive(c, n, k, bits, bs)) return hipErrorInvalidValue;
+    const int64_t cols = (int64_t)c.waves_per_group * (64 / c.g) * c.u;
+    const int64_t bpc = k / bs;
+    const int64_t zpb = (bpc * bits + 7) / 8;
+    c.vec_s = (reinterpret_cast<uintptr_t>(s) % 16 == 0) && (cols * bpc * 2) % 16 == 0;
+    c.vec_z = z && (reinterpret_cast<uintptr_t>(z) % 16 == 0) && (cols * zpb) % 16 == 0;
     if (bits == 4) return stream_bits<4>(c, a, b, s, z, y, m, n, k, bs, st);
-    if (bits == 8) return stream_bits<8>(c, a, b, s, z, y, m, n, k, bs, st);
-    return hipErrorInvalidValue;
+    return stream_bits<8>(c, a, b, s, z, y, m, n, k, bs, st);
 }
 
 hipError_t launch_gemv_stream(const void* a, const uint8_t* b, const void* s, const uint8_t* z,

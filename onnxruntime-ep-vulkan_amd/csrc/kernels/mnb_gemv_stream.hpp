@@ -1,12 +1,26 @@
 // Streaming decode GEMV for MatMulNBits on gfx950 (fp16 A, M <= 4 rows, K % (128/bits) == 0).
 //
-// Design.  The packed weight of column n is K*bits/8 contiguous bytes (B is [N][K/bs][bs*bits/8]),
-// so the kernel reads it in 16-byte "chunks" (32 int4 or 16 int8 weights) with one dwordx4 load
-// per lane: a lane group of G lanes (G = 16, 32 or 64) owns one column at a time and lane i of the
-// group takes chunks i, i+G, i+2G, ... .  One load instruction therefore covers 64/G runs of
-// G*16 contiguous bytes, the coalescing HBM wants, and the chunk set of a lane is the same for
-// every column, so the activation values it multiplies are loaded once into registers and reused
-// for every column the wavefront visits.
+// Design.  At M <= 4 one launch streams 5-30 MB of weights, and once the whole chip has its
+// weight loads in flight every memory request -- an L2 hit included -- waits behind that burst
+// (measured on MI355X: a 6 KB L2-resident read takes 0.4 us alone and 1.6-2.7 us while the other
+// workgroups stream).  Whatever a wavefront needs besides its own weights must therefore arrive
+// before the burst starts.  The launch is one to three workgroups per CU (up to 16 wavefronts
+// each); a workgroup first requests what its wavefronts share -- the MR activation rows (an L2 /
+// MALL hit) and its columns' scale and zero-point bytes (cold in HBM) -- stages the activations
+// in LDS as soon as they arrive, and only then issues its weights; the scale and zero-point
+// bytes, requested earlier, reach LDS behind a second barrier while the weights are in flight.
+// Each wavefront makes exactly one pass: it owns U
+// columns per lane group and issues all of their 16-byte weight loads at once.  The packed weight
+// of column n is K*bits/8 contiguous bytes (B is [N][K/bs][bs*bits/8]); a lane group of G lanes
+// (G = 16, 32 or 64) owns a column and lane i of the group takes chunks i, i+G, i+2G, ... (a
+// "chunk" is 16 bytes: 32 int4 or 16 int8 weights), so one load instruction covers 64/G runs of
+// G*16 contiguous bytes, the coalescing HBM wants.
+//
+// Staged in LDS: the activations in the pair order the unpack produces, each chunk with the fp32
+// sum of its activations per quant-block segment, and the workgroup's scale and zero-point bytes,
+// which for its C consecutive columns are one contiguous byte range each, copied with 16-byte
+// loads.  A lane reads its chunks' activations, scales and zero points from LDS (broadcast reads,
+// a padded chunk stride that keeps 8 consecutive chunks in 8 different bank groups).
 //
 // Arithmetic.  The reference forms, per (column, quant block), the fp32 sum of a * (q - zp) and
 // scales it once (rust/shaders/glsl/templates/q_gemv.comp:571-579).  Here each chunk's weights are
@@ -14,7 +28,7 @@
 // an exponent-zero half), multiplied by the fp16 activations with v_dot2_f32_f16 (products are
 // exact in fp32), and the chunk's block partial is recovered exactly as
 //     sum a*(q - zp) = 2^24 * sum a*(q*2^-24) - zp * sum a,
-// with sum a over the chunk's block segment computed once per lane when A is loaded.  The block
+// with sum a over the chunk's block segment taken from the staged activations.  The block
 // partial is then scaled by the block's scale in fp32 and added to the lane's accumulator; the G
 // lane accumulators of a column are summed by a fixed butterfly, so results are run-to-run
 // deterministic.  A chunk that lies inside one quant block (bs >= 32 for int4) contributes a
@@ -51,290 +65,355 @@ __device__ __forceinline__ f16x2 sub_pair(uint32_t w) {
     }
 }
 
-// Rearranges 8 (int4) or 4 (int8) consecutive fp16 activations, given as dwords x[0..] of
-// natural pairs, into the pair order sub_pair produces.
+// Rearranges 8 consecutive fp16 activations, given as 4 dwords x[0..3] of natural pairs, into
+// the pair order sub_pair produces: int4 (a0,a4) (a1,a5) (a2,a6) (a3,a7); int8 (a0,a2) (a1,a3)
+// (a4,a6) (a5,a7).
 template <int BITS>
-__device__ __forceinline__ void pair_activations(const uint32_t* x, f16x2* out) {
+__device__ __forceinline__ u32x4 pair_activations(u32x4 x) {
     if constexpr (BITS == 4) {
-        // x0 = (a0,a1) x1 = (a2,a3) x2 = (a4,a5) x3 = (a6,a7) -> (a0,a4) (a1,a5) (a2,a6) (a3,a7)
-        out[0] = as_h2(__builtin_amdgcn_perm(x[2], x[0], 0x05040100u));
-        out[1] = as_h2(__builtin_amdgcn_perm(x[2], x[0], 0x07060302u));
-        out[2] = as_h2(__builtin_amdgcn_perm(x[3], x[1], 0x05040100u));
-        out[3] = as_h2(__builtin_amdgcn_perm(x[3], x[1], 0x07060302u));
+        return u32x4{__builtin_amdgcn_perm(x.z, x.x, 0x05040100u),
+                     __builtin_amdgcn_perm(x.z, x.x, 0x07060302u),
+                     __builtin_amdgcn_perm(x.w, x.y, 0x05040100u),
+                     __builtin_amdgcn_perm(x.w, x.y, 0x07060302u)};
     } else {
-        // x0 = (a0,a1) x1 = (a2,a3) -> (a0,a2) (a1,a3)
-        out[0] = as_h2(__builtin_amdgcn_perm(x[1], x[0], 0x05040100u));
-        out[1] = as_h2(__builtin_amdgcn_perm(x[1], x[0], 0x07060302u));
+        return u32x4{__builtin_amdgcn_perm(x.y, x.x, 0x05040100u),
+                     __builtin_amdgcn_perm(x.y, x.x, 0x07060302u),
+                     __builtin_amdgcn_perm(x.w, x.z, 0x05040100u),
+                     __builtin_amdgcn_perm(x.w, x.z, 0x07060302u)};
     }
 }
 
 }  // namespace
 
-// Weight-side registers of one pass: U columns x CPL chunks per lane.  Scales and zero points
-// are kept raw (the fp16 bits and the packed byte) so that issuing the loads never waits for
-// them; they are decoded when the pass is computed.
-template <int SEGS, int CPL, int U>
-struct StreamPass {
-    u32x4 bw[U][CPL];
-    uint16_t sraw[U][CPL][SEGS];
-    uint32_t zraw[U][CPL][SEGS];
-    int cols[U];
-};
+// LDS bytes of one staged activation chunk: its fp16 pairs (64 bytes int4, 32 bytes int8) and
+// the fp32 segment sums, padded to 80 / 48 bytes so that 8 consecutive chunks start in 8
+// distinct 16-byte bank groups (5c mod 8 and 3c mod 8 are permutations of 0..7).
+template <int BITS>
+__host__ __device__ constexpr int stream_chunk_stride() { return BITS == 4 ? 80 : 48; }
 
-// Loads of one pass.  Out-of-range chunks and columns read a clamped, in-bounds address; their
-// contribution is removed at compute time (scale forced to zero), so no load sits behind a
-// branch and every request of the pass is in flight at once.
-template <int BITS, int BS, bool HAS_ZP, int CPL, int U, bool NT>
-__device__ __forceinline__ void stream_fetch(StreamPass<chunk_segs<BITS, BS>(), CPL, U>& p,
-                                             const uint8_t* __restrict__ B,
-                                             const f16* __restrict__ S,
-                                             const uint8_t* __restrict__ Z, int task, int ng,
-                                             int grp, int gi, int G, int N, int K) {
-    constexpr int WPC = chunk_weights<BITS>();
-    constexpr int SEGS = chunk_segs<BITS, BS>();
-    const int cpc = K / WPC;
-    const int bpc = K / BS;
-    const int zpb = (bpc * BITS + 7) / 8;
-    const int64_t col_bytes = (int64_t)K * BITS / 8;
-    const int base = task * ng * U;
-    const uint16_t* __restrict__ Sr = reinterpret_cast<const uint16_t*>(S);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int col = base + grp * U + u;
-        p.cols[u] = col;
-        const int cc = col < N ? col : N - 1;
-        const uint8_t* bcol = B + (int64_t)cc * col_bytes;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            int c = gi + j * G;
-            c = c < cpc ? c : cpc - 1;
-            const u32x4* q = reinterpret_cast<const u32x4*>(bcol + (int64_t)c * 16);
-            p.bw[u][j] = NT ? __builtin_nontemporal_load(q) : *q;
-#pragma unroll
-            for (int s = 0; s < SEGS; ++s) {
-                const int blk = (c * WPC + s * BS) / BS;
-                p.sraw[u][j][s] = Sr[(int64_t)cc * bpc + blk];
-                if constexpr (HAS_ZP) {
-                    p.zraw[u][j][s] = BITS == 4 ? (uint32_t)Z[(int64_t)cc * zpb + (blk >> 1)]
-                                                : (uint32_t)Z[(int64_t)cc * zpb + blk];
-                } else {
-                    p.zraw[u][j][s] = 0u;
-                }
-            }
-        }
-    }
-}
+// Units (16 bytes) a thread loads per staging batch: activations, scale bytes, zero-point bytes.
+constexpr int kStreamAU = 2;
+constexpr int kStreamSU = 2;
+constexpr int kStreamZU = 1;
 
-// One wavefront = 64/G lane groups; a "task" is the NG*U consecutive columns a wavefront
-// handles in one pass (group g takes columns base + g*U + u, u < U).  Waves loop over tasks with
-// a grid stride, fetching the next pass's weights before computing the current one; the first
-// pass's weights are requested before the activations, so the HBM stream starts at once.  MR
-// rows of A (rows m0 .. m0+MR-1, m0 = blockIdx.y * MR) are held in registers for the lane's
-// chunk set; CPL chunks per lane at most.  G is a power of two passed as log2(G).
-template <int BITS, int BS, bool HAS_ZP, int MR, int CPL, int U, bool NT>
+// One workgroup = `waves` wavefronts (blockDim.x / 64) = C = waves * (64/G) * U consecutive
+// columns, col0 = blockIdx.x * C; MR rows of A (m0 = blockIdx.y * MR).  vec_s / vec_z: the
+// workgroup's scale / zero-point byte ranges may be copied with 16-byte loads (the host checked
+// the base alignment and that C * row bytes is a multiple of 16); otherwise 2-byte / 1-byte loads.
+template <int BITS, int BS, bool HAS_ZP, int MR, int CPL, int U>
 __global__ void __launch_bounds__(kStreamMaxThreads)
 gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ S,
             const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K, int log2g,
-            int tasks, int total_waves) {
+            int vec_s, int vec_z) {
     constexpr int WPC = chunk_weights<BITS>();
     constexpr int NP = chunk_pairs<BITS>();
     constexpr int SEGS = chunk_segs<BITS, BS>();
     constexpr int DW_PER_SEG = 4 / SEGS;                 // dwords of a chunk per block segment
+    constexpr int UPC = WPC / 8;                         // 16-byte activation units per chunk
+    constexpr int CST = stream_chunk_stride<BITS>();
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int T = (int)blockDim.x;
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = 1 << log2g;
-    const int lane = threadIdx.x & 63;
-    // wave-uniform: in a scalar register, the task loop and its column base stay scalar
-    const int wave = __builtin_amdgcn_readfirstlane(
-        (int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+    const int ng = 64 >> log2g;
     const int grp = lane >> log2g;
     const int gi = lane & (G - 1);
-    const int ng = 64 >> log2g;
     const int cpc = K / WPC;                             // chunks per column
-    const int m0 = blockIdx.y * MR;
-    int task = wave;
-    if (task >= tasks) return;                           // no barriers below: safe to leave
+    const int bpc = K / BS;
+    const int zpb = (bpc * BITS + 7) / 8;
+    const int C = (T >> 6) * ng * U;
+    const int col0 = (int)blockIdx.x * C;
+    const int ncols = min(C, N - col0);
+    const int m0 = (int)blockIdx.y * MR;
+    const int64_t col_bytes = (int64_t)K * BITS / 8;
 
-    StreamPass<SEGS, CPL, U> cur;
-    stream_fetch<BITS, BS, HAS_ZP, CPL, U, NT>(cur, B, S, Z, task, ng, grp, gi, G, N, K);
+    uint8_t* sA = smem;
+    uint8_t* sS = smem + MR * cpc * CST;
+    uint8_t* sZ = sS + ((C * bpc * 2 + 15) & ~15);
+    const int s_bytes = ncols * bpc * 2;
+    const int z_bytes = HAS_ZP ? ncols * zpb : 0;
+    const uint8_t* gS = reinterpret_cast<const uint8_t*>(S) + (int64_t)col0 * bpc * 2;
+    const uint8_t* gZ = HAS_ZP ? Z + (int64_t)col0 * zpb : nullptr;
 
-    // ---- activations for this lane's chunks, paired to match sub_pair, plus segment sums ----
-    f16x2 ap[MR][CPL][NP];
-    float asum[MR][CPL][SEGS];
-    bool live[CPL];
+    // ---- first staging batch: activation units, scale and zero-point units --------------------
+    const int upr = K / 8;                               // activation units per row
+    const int a_units = MR * upr;
+    // Every load of this batch is made by every thread (indices past the end are clamped to an
+    // in-bounds unit whose value is not used), so the number of loads in flight is the same on
+    // every path and waiting for the activations does not wait for the later requests.
+    u32x4 av[kStreamAU];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int c0 = gi + j * G;
-        live[j] = c0 < cpc;
-        const int c = live[j] ? c0 : cpc - 1;
+    for (int i = 0; i < kStreamAU; ++i) {
+        const int u = min(tid + i * T, a_units - 1);
+        const int r = u / upr;
+        const int row = min(m0 + r, M - 1);
+        av[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)row * K + (int64_t)(u - r * upr) * 8);
+    }
+    const int s_units = vec_s ? s_bytes / 16 : 0;
+    const int z_units = vec_z ? z_bytes / 16 : 0;
+    const u32x4* s4 = reinterpret_cast<const u32x4*>(s_units > 0 ? gS : reinterpret_cast<const uint8_t*>(A));
+    const u32x4* z4 = reinterpret_cast<const u32x4*>(z_units > 0 ? gZ : reinterpret_cast<const uint8_t*>(A));
+    u32x4 sv[kStreamSU], zv[kStreamZU];
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            const int row = (m0 + r) < M ? (m0 + r) : M - 1;
-            const uint32_t* src =
-                reinterpret_cast<const uint32_t*>(A + (int64_t)row * K + (int64_t)c * WPC);
+    for (int i = 0; i < kStreamSU; ++i) sv[i] = s4[min(tid + i * T, max(s_units - 1, 0))];
+    if constexpr (HAS_ZP) {
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                uint32_t x[4] = {0u, 0u, 0u, 0u};
-                if constexpr (BITS == 4) {               // 8 activations = 16 bytes
-                    const u32x4 v = *reinterpret_cast<const u32x4*>(src + 4 * d);
-                    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
-                    pair_activations<4>(x, &ap[r][j][4 * d]);
-                } else {                                 // 4 activations = 8 bytes
-                    const u32x2 v = *reinterpret_cast<const u32x2*>(src + 2 * d);
-                    x[0] = v.x; x[1] = v.y;
-                    pair_activations<8>(x, &ap[r][j][2 * d]);
-                }
-            }
-            const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+        for (int i = 0; i < kStreamZU; ++i) zv[i] = z4[min(tid + i * T, max(z_units - 1, 0))];
+    }
+
+    // ---- stage the first batch into LDS ------------------------------------------------------
+    const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
+    // Unit u: row r, chunk c, quarter (int4) or half (int8) q of the chunk.  The pairing and the
+    // unit's sum are computed on every lane (a clamped unit past the end included, so that the
+    // loads above are used unconditionally and stay where they are); only real units are stored.
+    auto stage_a = [&](int u, u32x4 x) {
+        const u32x4 p = pair_activations<BITS>(x);
+        if (u < a_units) {
+            const int r = u / upr;
+            const int w = u - r * upr;
+            const int c = w / UPC;
+            const int q = w - c * UPC;
+            *reinterpret_cast<u32x4*>(sA + (r * cpc + c) * CST + 16 * q) = p;
+        }
+        float t = 0.f;
+        t = __builtin_amdgcn_fdot2(as_h2(p.x), one2, t, false);
+        t = __builtin_amdgcn_fdot2(as_h2(p.y), one2, t, false);
+        t = __builtin_amdgcn_fdot2(as_h2(p.z), one2, t, false);
+        t = __builtin_amdgcn_fdot2(as_h2(p.w), one2, t, false);
+        return u < a_units ? t : 0.f;
+    };
+    // Segment sums across the units of a chunk: the units of one chunk sit in UPC consecutive
+    // threads (T and the units per row are multiples of UPC), combined in a fixed order.
+    auto store_sums = [&](int u, float t) {
+        const int r = u / upr;
+        const int w = u - r * upr;
+        const int c = w / UPC;
+        const int q = w - c * UPC;
+        float* dst = reinterpret_cast<float*>(sA + (r * cpc + c) * CST + 4 * NP);
+        if constexpr (BITS == 4 && SEGS == 2) {          // block 16: two units per segment
+            if ((q & 1) == 0) dst[q >> 1] = t;
+        } else {
+            if (q == 0) dst[0] = t;
+        }
+    };
 #pragma unroll
-            for (int s = 0; s < SEGS; ++s) {
-                float t = 0.f;
+    for (int i = 0; i < kStreamAU; ++i) {
+        const int u = tid + i * T;
+        float t = stage_a(u, av[i]);
+        // partner sums over the lane's quad (int4) or pair (int8); out-of-range units add 0
+        t += dpp_f<0xB1>(t);                             // lane ^ 1
+        if constexpr (BITS == 4 && SEGS == 1) t += dpp_f<0x4E>(t);   // lane ^ 2
+        if (u < a_units) store_sums(u, t);
+    }
+    // ---- what the first batch did not cover (long K, several rows, unaligned tensors) -------
+    for (int base = tid + kStreamAU * T; base < a_units; base += kStreamAU * T) {
+        u32x4 x[kStreamAU];
 #pragma unroll
-                for (int p = s * (NP / SEGS); p < (s + 1) * (NP / SEGS); ++p)
-                    t = __builtin_amdgcn_fdot2(ap[r][j][p], one2, t, false);
-                asum[r][j][s] = t;
-            }
+        for (int i = 0; i < kStreamAU; ++i) {
+            const int u = base + i * T;
+            const int r = u / upr;
+            const int row = min(m0 + min(r, MR - 1), M - 1);
+            if (u < a_units)
+                x[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)row * K + (int64_t)(u - r * upr) * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < kStreamAU; ++i) {
+            const int u = base + i * T;
+            float t = u < a_units ? stage_a(u, x[i]) : 0.f;
+            t += dpp_f<0xB1>(t);
+            if constexpr (BITS == 4 && SEGS == 1) t += dpp_f<0x4E>(t);
+            if (u < a_units) store_sums(u, t);
+        }
+    }
+    for (int u = tid + kStreamSU * T; u < s_units; u += T)
+        reinterpret_cast<u32x4*>(sS)[u] = reinterpret_cast<const u32x4*>(gS)[u];
+    for (int i = 2 * (tid + s_units * 8); i < s_bytes; i += 2 * T)   // 2-byte remainder / path
+        *reinterpret_cast<uint16_t*>(sS + i) = *reinterpret_cast<const uint16_t*>(gS + i);
+    if constexpr (HAS_ZP) {
+        for (int u = tid + kStreamZU * T; u < z_units; u += T)
+            reinterpret_cast<u32x4*>(sZ)[u] = reinterpret_cast<const u32x4*>(gZ)[u];
+        for (int i = tid + z_units * 16; i < z_bytes; i += T) sZ[i] = gZ[i];
+    }
+    __syncthreads();
+
+    // ---- the wavefront's weights: every load of the pass, issued at once --------------------
+    u32x4 bw[U][CPL];
+    int lcol[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int lc = (wave * ng + grp) * U + u;        // column within the workgroup
+        lcol[u] = lc;
+        const int cc = min(col0 + lc, N - 1);
+        const uint8_t* bcol = B + (int64_t)cc * col_bytes;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = min(gi + j * G, cpc - 1);
+            bw[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bcol + (int64_t)c * 16));
         }
     }
 
-    while (true) {
-        const int next = task + total_waves;
-        const bool more = next < tasks;                  // wave-uniform
-        StreamPass<SEGS, CPL, U> nxt;
-        if (more) stream_fetch<BITS, BS, HAS_ZP, CPL, U, NT>(nxt, B, S, Z, next, ng, grp, gi, G, N, K);
+    // ---- the scale and zero-point bytes (requested before the weights, from HBM) ------------
+#pragma unroll
+    for (int i = 0; i < kStreamSU; ++i) {
+        const int u = tid + i * T;
+        if (u < s_units) reinterpret_cast<u32x4*>(sS)[u] = sv[i];
+    }
+    if constexpr (HAS_ZP) {
+#pragma unroll
+        for (int i = 0; i < kStreamZU; ++i) {
+            const int u = tid + i * T;
+            if (u < z_units) reinterpret_cast<u32x4*>(sZ)[u] = zv[i];
+        }
+    }
+    __syncthreads();
 
-        float acc[MR][U];
+    // ---- compute: chunk by chunk, its activations read from LDS once for all U columns ------
+    float acc[MR][U];
 #pragma unroll
-        for (int r = 0; r < MR; ++r)
+    for (int r = 0; r < MR; ++r)
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc[r][u] = 0.f;
+        for (int u = 0; u < U; ++u) acc[r][u] = 0.f;
+    const uint16_t* sSr = reinterpret_cast<const uint16_t*>(sS);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        // With several rows, keep the scheduler from hoisting every chunk's activation reads
+        // to the top (MR * 16 registers per chunk); one row's are cheap to hold.
+        if constexpr (MR > 1) __builtin_amdgcn_sched_barrier(0);
+        const int c0 = gi + j * G;
+        const bool live = c0 < cpc;
+        const int c = live ? c0 : cpc - 1;
+        f16x2 ap[MR][NP];
+        float asum[MR][SEGS];
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+            const uint8_t* src = sA + (r * cpc + c) * CST;
+#pragma unroll
+            for (int q = 0; q < NP / 4; ++q) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * q);
+                ap[r][4 * q + 0] = as_h2(v.x);
+                ap[r][4 * q + 1] = as_h2(v.y);
+                ap[r][4 * q + 2] = as_h2(v.z);
+                ap[r][4 * q + 3] = as_h2(v.w);
+            }
+#pragma unroll
+            for (int s = 0; s < SEGS; ++s)
+                asum[r][s] = reinterpret_cast<const float*>(src + 4 * NP)[s];
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            const int lc = min(lcol[u], C - 1);
+            const uint32_t w[4] = {bw[u][j].x, bw[u][j].y, bw[u][j].z, bw[u][j].w};
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const uint32_t w[4] = {cur.bw[u][j].x, cur.bw[u][j].y, cur.bw[u][j].z,
-                                       cur.bw[u][j].w};
+            for (int s = 0; s < SEGS; ++s) {
+                const int blk = (c * WPC + s * BS) / BS;
+                float sv1 = (float)__builtin_bit_cast(f16, sSr[lc * bpc + blk]);
+                sv1 = live ? sv1 : 0.f;
+                float zf;
+                if constexpr (!HAS_ZP) {
+                    zf = (float)(1 << (BITS - 1));
+                } else if constexpr (BITS == 4) {
+                    zf = (float)((sZ[lc * zpb + (blk >> 1)] >> ((blk & 1) * 4)) & 0xF);
+                } else {
+                    zf = (float)sZ[lc * zpb + blk];
+                }
+                const float s24 = sv1 * 16777216.0f;
+                const float sz = -sv1 * zf;
 #pragma unroll
-                for (int s = 0; s < SEGS; ++s) {
-                    const int blk = ((gi + j * G) * WPC + s * BS) / BS;
-                    float sv = (float)__builtin_bit_cast(f16, cur.sraw[u][j][s]);
-                    sv = live[j] ? sv : 0.f;
-                    float zv;
-                    if constexpr (!HAS_ZP) {
-                        zv = (float)(1 << (BITS - 1));
-                    } else if constexpr (BITS == 4) {
-                        zv = (float)((cur.zraw[u][j][s] >> ((blk & 1) * 4)) & 0xFu);
-                    } else {
-                        zv = (float)cur.zraw[u][j][s];
-                    }
-                    const float s24 = sv * 16777216.0f;
-                    const float sz = -sv * zv;
+                for (int r = 0; r < MR; ++r) {
+                    float t = 0.f;
+                    float t16 = 0.f;
 #pragma unroll
-                    for (int r = 0; r < MR; ++r) {
-                        float t = 0.f;
-                        float t16 = 0.f;
-#pragma unroll
-                        for (int d = s * DW_PER_SEG; d < (s + 1) * DW_PER_SEG; ++d) {
-                            if constexpr (BITS == 4) {
-                                // Nibble pairs 0 and 2 sit in bits 0-3 of each half (q * 2^-24);
-                                // pairs 1 and 3 are masked in place at bits 4-7 (16q * 2^-24,
-                                // still subnormal) and summed apart, scaled by 1/16 below:
-                                // one shift per dword instead of three.
-                                const uint32_t wh = w[d] >> 8;
-                                t = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x000F000Fu), ap[r][j][4 * d + 0], t, false);
-                                t = __builtin_amdgcn_fdot2(as_h2(wh & 0x000F000Fu), ap[r][j][4 * d + 2], t, false);
-                                t16 = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x00F000F0u), ap[r][j][4 * d + 1], t16, false);
-                                t16 = __builtin_amdgcn_fdot2(as_h2(wh & 0x00F000F0u), ap[r][j][4 * d + 3], t16, false);
-                            } else {
-                                t = __builtin_amdgcn_fdot2(sub_pair<8, 0>(w[d]), ap[r][j][2 * d + 0], t, false);
-                                t = __builtin_amdgcn_fdot2(sub_pair<8, 1>(w[d]), ap[r][j][2 * d + 1], t, false);
-                            }
+                    for (int d = s * DW_PER_SEG; d < (s + 1) * DW_PER_SEG; ++d) {
+                        if constexpr (BITS == 4) {
+                            // Nibble pairs 0 and 2 sit in bits 0-3 of each half (q * 2^-24);
+                            // pairs 1 and 3 are masked in place at bits 4-7 (16q * 2^-24, still
+                            // subnormal) and summed apart, scaled by 1/16 below: one shift per
+                            // dword instead of three.
+                            const uint32_t wh = w[d] >> 8;
+                            t = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x000F000Fu), ap[r][4 * d + 0], t, false);
+                            t = __builtin_amdgcn_fdot2(as_h2(wh & 0x000F000Fu), ap[r][4 * d + 2], t, false);
+                            t16 = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x00F000F0u), ap[r][4 * d + 1], t16, false);
+                            t16 = __builtin_amdgcn_fdot2(as_h2(wh & 0x00F000F0u), ap[r][4 * d + 3], t16, false);
+                        } else {
+                            t = __builtin_amdgcn_fdot2(sub_pair<8, 0>(w[d]), ap[r][2 * d + 0], t, false);
+                            t = __builtin_amdgcn_fdot2(sub_pair<8, 1>(w[d]), ap[r][2 * d + 1], t, false);
                         }
-                        t = __builtin_fmaf(t16, 0.0625f, t);
-                        acc[r][u] = __builtin_fmaf(s24, t, acc[r][u]);
-                        acc[r][u] = __builtin_fmaf(sz, asum[r][j][s], acc[r][u]);
                     }
+                    t = __builtin_fmaf(t16, 0.0625f, t);
+                    acc[r][u] = __builtin_fmaf(s24, t, acc[r][u]);
+                    acc[r][u] = __builtin_fmaf(sz, asum[r][s], acc[r][u]);
                 }
             }
         }
+    }
 #pragma unroll
-        for (int r = 0; r < MR; ++r)
+    for (int r = 0; r < MR; ++r)
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc[r][u] = group_sum(acc[r][u], G);
-        if (gi == 0) {
+        for (int u = 0; u < U; ++u) acc[r][u] = group_sum(acc[r][u], G);
+    if (gi == 0) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (cur.cols[u] >= N) continue;
+        for (int u = 0; u < U; ++u) {
+            if (lcol[u] >= ncols) continue;
 #pragma unroll
-                for (int r = 0; r < MR; ++r)
-                    if (m0 + r < M) Y[(int64_t)(m0 + r) * N + cur.cols[u]] = (f16)acc[r][u];
-            }
+            for (int r = 0; r < MR; ++r)
+                if (m0 + r < M) Y[(int64_t)(m0 + r) * N + col0 + lcol[u]] = (f16)acc[r][u];
         }
-        if (!more) break;
-        cur = nxt;
-        task = next;
     }
 }
 
-template <int BITS, int BS, bool HAS_ZP, int MR, int CPL, int U, bool NT>
+template <int BITS, int BS, bool HAS_ZP, int MR, int CPL, int U>
 hipError_t stream_go(const StreamConfig& c, const f16* A, const uint8_t* B, const f16* S,
-                            const uint8_t* Z, f16* Y, int64_t m, int64_t n, int64_t k,
-                            hipStream_t st) {
-    const int64_t wpg = c.waves_per_group;
-    const dim3 grid((unsigned)((c.total_waves + wpg - 1) / wpg), (unsigned)((m + MR - 1) / MR), 1);
-    const dim3 block((unsigned)(64 * wpg), 1, 1);
-    hipLaunchKernelGGL((gemv_stream<BITS, BS, HAS_ZP, MR, CPL, U, NT>), grid, block, 0, st, A, B,
-                       S, Z, Y, (int)m, (int)n, (int)k, __builtin_ctz((unsigned)c.g), (int)c.tasks,
-                       (int)(grid.x * wpg));
+                     const uint8_t* Z, f16* Y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+    auto kern = gemv_stream<BITS, BS, HAS_ZP, MR, CPL, U>;
+    if (c.lds > 64 * 1024) {                             // above the default dynamic LDS limit
+        const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
+        if (ea != hipSuccess) return ea;
+    }
+    const dim3 grid((unsigned)c.groups, (unsigned)((m + MR - 1) / MR), 1);
+    const dim3 block((unsigned)(64 * c.waves_per_group), 1, 1);
+    hipLaunchKernelGGL(kern, grid, block, (size_t)c.lds, st, A, B, S, Z, Y, (int)m, (int)n, (int)k,
+                       __builtin_ctz((unsigned)c.g), c.vec_s, c.vec_z);
     return hipGetLastError();
 }
 
-template <int BITS, int BS, bool HAS_ZP, int MR, int U, bool NT>
+template <int BITS, int BS, bool HAS_ZP, int MR, int U>
 hipError_t stream_cpl(const StreamConfig& c, const f16* A, const uint8_t* B, const f16* S,
-                             const uint8_t* Z, f16* Y, int64_t m, int64_t n, int64_t k,
-                             hipStream_t st) {
+                      const uint8_t* Z, f16* Y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
     // Register arrays are sized by the instantiated CPL; the runtime count selects the
     // smallest instantiation that holds it.
-    if (c.cpl <= 1) return stream_go<BITS, BS, HAS_ZP, MR, 1, U, NT>(c, A, B, S, Z, Y, m, n, k, st);
-    if (c.cpl <= 2) return stream_go<BITS, BS, HAS_ZP, MR, 2, U, NT>(c, A, B, S, Z, Y, m, n, k, st);
-    if constexpr (MR <= 2) {
-        if (c.cpl <= 3) return stream_go<BITS, BS, HAS_ZP, MR, 3, U, NT>(c, A, B, S, Z, Y, m, n, k, st);
-        if (c.cpl <= 4) return stream_go<BITS, BS, HAS_ZP, MR, 4, U, NT>(c, A, B, S, Z, Y, m, n, k, st);
-    }
-    if constexpr (MR == 1) {
-        if (c.cpl <= 6) return stream_go<BITS, BS, HAS_ZP, MR, 6, U, NT>(c, A, B, S, Z, Y, m, n, k, st);
-        if (c.cpl <= 8) return stream_go<BITS, BS, HAS_ZP, MR, 8, U, NT>(c, A, B, S, Z, Y, m, n, k, st);
+    if (c.cpl <= 1) return stream_go<BITS, BS, HAS_ZP, MR, 1, U>(c, A, B, S, Z, Y, m, n, k, st);
+    if (c.cpl <= 2) return stream_go<BITS, BS, HAS_ZP, MR, 2, U>(c, A, B, S, Z, Y, m, n, k, st);
+    if (c.cpl <= 3) return stream_go<BITS, BS, HAS_ZP, MR, 3, U>(c, A, B, S, Z, Y, m, n, k, st);
+    if (c.cpl <= 4) return stream_go<BITS, BS, HAS_ZP, MR, 4, U>(c, A, B, S, Z, Y, m, n, k, st);
+    if constexpr (U == 1 && MR == 1) {
+        if (c.cpl <= 6) return stream_go<BITS, BS, HAS_ZP, MR, 6, U>(c, A, B, S, Z, Y, m, n, k, st);
+        if (c.cpl <= 8) return stream_go<BITS, BS, HAS_ZP, MR, 8, U>(c, A, B, S, Z, Y, m, n, k, st);
     }
     return hipErrorInvalidValue;
 }
 
 template <int BITS, int BS, bool HAS_ZP>
-hipError_t stream_rows(const StreamConfig& c, const f16* A, const uint8_t* B,
-                              const f16* S, const uint8_t* Z, f16* Y, int64_t m, int64_t n,
-                              int64_t k, hipStream_t st) {
-    const bool nt = c.nontemporal != 0;
-#define MNB_STREAM_U(MR_)                                                                         \
-    do {                                                                                          \
-        if (c.u == 1)                                                                             \
-            return nt ? stream_cpl<BITS, BS, HAS_ZP, MR_, 1, true>(c, A, B, S, Z, Y, m, n, k, st) \
-                      : stream_cpl<BITS, BS, HAS_ZP, MR_, 1, false>(c, A, B, S, Z, Y, m, n, k, st); \
-        if (c.u == 2)                                                                             \
-            return nt ? stream_cpl<BITS, BS, HAS_ZP, MR_, 2, true>(c, A, B, S, Z, Y, m, n, k, st) \
-                      : stream_cpl<BITS, BS, HAS_ZP, MR_, 2, false>(c, A, B, S, Z, Y, m, n, k, st); \
-        return hipErrorInvalidValue;                                                              \
-    } while (0)
+hipError_t stream_rows(const StreamConfig& c, const f16* A, const uint8_t* B, const f16* S,
+                       const uint8_t* Z, f16* Y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+    // two columns per lane group only for one row (with more rows the registers would not fit)
     switch (c.mr) {
-        case 1: MNB_STREAM_U(1);
-        case 2: MNB_STREAM_U(2);
-        case 3: MNB_STREAM_U(3);
-        case 4: MNB_STREAM_U(4);
+        case 1:
+            if (c.u == 2) return stream_cpl<BITS, BS, HAS_ZP, 1, 2>(c, A, B, S, Z, Y, m, n, k, st);
+            return stream_cpl<BITS, BS, HAS_ZP, 1, 1>(c, A, B, S, Z, Y, m, n, k, st);
+        case 2: return stream_cpl<BITS, BS, HAS_ZP, 2, 1>(c, A, B, S, Z, Y, m, n, k, st);
+        case 3: return stream_cpl<BITS, BS, HAS_ZP, 3, 1>(c, A, B, S, Z, Y, m, n, k, st);
+        case 4: return stream_cpl<BITS, BS, HAS_ZP, 4, 1>(c, A, B, S, Z, Y, m, n, k, st);
         default: return hipErrorInvalidValue;
     }
-#undef MNB_STREAM_U
 }
 
 template <int BITS, int BS>
 hipError_t stream_zp(const StreamConfig& c, const void* a, const uint8_t* b, const void* s,
-                            const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
-                            hipStream_t st) {
+                     const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
     const f16* A = static_cast<const f16*>(a);
     const f16* S = static_cast<const f16*>(s);
     f16* Y = static_cast<f16*>(y);

@@ -9,7 +9,7 @@ namespace mnb {
 // Threads per workgroup each kernel family is compiled for (its __launch_bounds__).  A launcher
 // refuses a launch shape above its kernel's limit before anything reaches the device: a
 // workgroup larger than the compiled bound fails as an unspecified launch failure.
-constexpr int kStreamMaxThreads = 256;   // gemv_stream
+constexpr int kStreamMaxThreads = 1024;  // gemv_stream
 constexpr int kGroupMaxThreads = 512;    // group_gemv
 constexpr int kGemvMaxThreads = 1024;    // gemv_f16_mfma
 
@@ -22,16 +22,18 @@ struct GemvGeom {
     size_t lds;    // dynamic LDS bytes
 };
 
-// Launch shape of the streaming decode GEMV (mnb_gemv_stream.hip).
+// Launch shape of the streaming decode GEMV (mnb_gemv_stream.hip).  Each wavefront makes one
+// pass over u columns per lane group; a workgroup covers waves_per_group * (64/g) * u columns
+// (about one workgroup per CU).
 struct StreamConfig {
     int mr;              // rows of A per workgroup row-tile (1..4)
     int g;               // lanes per column (16, 32, 64)
     int cpl;             // 16-byte chunks per lane (ceil(chunks per column / g))
-    int u;               // columns per lane group per pass (1 or 2)
-    int waves_per_group; // wavefronts per workgroup
-    int nontemporal;     // stream weights with non-temporal loads
-    int64_t tasks;       // passes over (64/g)*u columns
-    int64_t total_waves; // wavefronts launched (<= tasks; waves loop over tasks)
+    int u;               // columns per lane group (1 or 2)
+    int waves_per_group; // wavefronts per workgroup (1..16)
+    int vec_s, vec_z;    // scale / zero-point bytes staged with 16-byte loads (set at launch)
+    int64_t groups;      // workgroups along N (derived)
+    int64_t lds;         // dynamic LDS bytes (derived)
 };
 
 bool gemv_stream_supported(int64_t m, int64_t k, int bits, int bs);

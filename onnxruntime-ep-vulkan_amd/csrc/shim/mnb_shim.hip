@@ -194,9 +194,9 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
         const mnb::StreamConfig c =
             mnb::gemv_stream_config(p->m, p->n, p->k, p->bits, p->block_size);
         out->waves_per_group = c.waves_per_group;
-        out->tile_n = (64 / c.g) * c.u;
+        out->tile_n = c.waves_per_group * (64 / c.g) * c.u;
         out->tile_m = c.mr;
-        out->grid_x = (c.total_waves + c.waves_per_group - 1) / c.waves_per_group;
+        out->grid_x = c.groups;
         out->grid_y = (p->m + c.mr - 1) / c.mr;
     } else if (kern == MNB_KERNEL_STRIP_MFMA) {
         out->waves_per_group = sg.waves;

@@ -17,8 +17,8 @@ LAUNCH_STREAM_CFG = "_ZN3mnb22launch_gemv_stream_cfgERKNS_12StreamConfigEPKvPKhS
 class StreamConfig(C.Structure):
     # mnb::StreamConfig (csrc/kernels/mnb_launch.hpp)
     _fields_ = [("mr", C.c_int), ("g", C.c_int), ("cpl", C.c_int), ("u", C.c_int),
-                ("waves_per_group", C.c_int), ("nontemporal", C.c_int),
-                ("tasks", C.c_int64), ("total_waves", C.c_int64)]
+                ("waves_per_group", C.c_int), ("vec_s", C.c_int), ("vec_z", C.c_int),
+                ("groups", C.c_int64), ("lds", C.c_int64)]
 
 
 def _launcher():
@@ -32,9 +32,8 @@ def _launcher():
 
 
 def _cfg(**kw) -> StreamConfig:
-    # the planner's shape for qkv at M=1 (K=3072, N=9216): 32 lanes per column, 3 chunks each
-    base = dict(mr=1, g=32, cpl=3, u=1, waves_per_group=4, nontemporal=1, tasks=4608,
-                total_waves=2048)
+    # a shape for qkv at M=1 (K=3072, N=9216): 32 lanes per column, 3 chunks each
+    base = dict(mr=1, g=32, cpl=3, u=1, waves_per_group=4, vec_s=0, vec_z=0, groups=0, lds=0)
     base.update(kw)
     return StreamConfig(**base)
 
@@ -45,9 +44,9 @@ def _call(cfg: StreamConfig) -> int:
 
 
 def test_stream_launch_refuses_workgroups_above_compiled_bound():
-    # 8 wavefronts = 512 threads; gemv_stream is compiled for 256
-    assert _call(_cfg(waves_per_group=8)) == HIP_ERROR_INVALID_VALUE
-    assert _call(_cfg(waves_per_group=5)) == HIP_ERROR_INVALID_VALUE
+    # 17 wavefronts = 1088 threads; gemv_stream is compiled for 1024
+    assert _call(_cfg(waves_per_group=17)) == HIP_ERROR_INVALID_VALUE
+    assert _call(_cfg(waves_per_group=32)) == HIP_ERROR_INVALID_VALUE
     assert _call(_cfg(waves_per_group=0)) == HIP_ERROR_INVALID_VALUE
 
 
@@ -56,7 +55,9 @@ def test_stream_launch_refuses_malformed_shapes():
     assert _call(_cfg(cpl=2)) == HIP_ERROR_INVALID_VALUE          # 32 * 2 chunks < 96
     assert _call(_cfg(mr=5)) == HIP_ERROR_INVALID_VALUE
     assert _call(_cfg(u=3)) == HIP_ERROR_INVALID_VALUE
-    assert _call(_cfg(total_waves=0)) == HIP_ERROR_INVALID_VALUE
+    assert _call(_cfg(cpl=9)) == HIP_ERROR_INVALID_VALUE          # above the instantiated 8
+    assert _call(_cfg(u=2, cpl=6)) == HIP_ERROR_INVALID_VALUE     # two columns: at most 4
+    assert _call(_cfg(mr=2, u=2)) == HIP_ERROR_INVALID_VALUE      # two columns: one row only
 
 
 def test_planner_shapes_stay_within_compiled_bounds():
@@ -64,7 +65,7 @@ def test_planner_shapes_stay_within_compiled_bounds():
     workgroup no larger than that kernel family's compiled bound."""
     import mnb
 
-    bounds = {mnb.KERNEL_GEMV_STREAM: 256, mnb.KERNEL_GROUP_MFMA: 512,
+    bounds = {mnb.KERNEL_GEMV_STREAM: 1024, mnb.KERNEL_GROUP_MFMA: 512,
               mnb.KERNEL_GEMV_MFMA: 1024, mnb.KERNEL_GEMM_MFMA: 512, mnb.KERNEL_ACC4_I8: 1024,
               mnb.KERNEL_STRIP_MFMA: 1024, mnb.KERNEL_GENERIC: 256}
     for m in (1, 2, 3, 4, 5, 8, 16, 17, 33, 64, 65, 256, 2048):
