@@ -102,6 +102,22 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
                      const uint8_t* zero_points, void* y, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* mnb_matmul_nbits with no allocation and no workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory at call time (code under HIP
+ * graph capture, tight serving loops, hosts that forbid hipMalloc).  The scratch the kernels need
+ * (the accuracy_level 4 int8 activations and split-K partials, the prefill GEMM's K-split
+ * partials) comes from a device array of mnb_noalloc_scratch_bytes() bytes (48 MiB) inside the
+ * library, one per GPU, held until the process ends; nothing is allocated and no library routine
+ * that allocates is called.  accuracy_level 4 problems whose workspace exceeds it are rejected
+ * with MNB_ERR_UNSUPPORTED; a prefill GEMM whose K-split partials exceed it runs unsplit.  Every
+ * call on one GPU uses that GPU's array, so calls that overlap in time on one GPU (other streams
+ * or host threads) race; what must start at zero is cleared by the call itself.  The GPU is the
+ * stream's (the current device for the NULL stream).  Stream-ordered, like mnb_matmul_nbits. */
+int mnb_matmul_nbits_noalloc(const mnb_problem* p, const void* a, const uint8_t* b,
+                             const void* scales, const uint8_t* zero_points, void* y,
+                             void* stream);
+size_t mnb_noalloc_scratch_bytes(void);
+
 /* W[n][k] = fp16_rne(fp32(q - zp) * fp32(scale)), written as fp16 [N][K]. */
 int mnb_dequantize_f16(int64_t n, int64_t k, int32_t bits, int32_t block_size,
                        const uint8_t* b, const void* scales_f16, const uint8_t* zero_points,

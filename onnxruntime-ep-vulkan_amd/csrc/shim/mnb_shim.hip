@@ -310,6 +310,85 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
     return MNB_OK;
 }
 
+}  // extern "C"
+
+// ---- allocation-free MatMulNBits ------------------------------------------------------------
+//
+// Scratch for mnb_matmul_nbits_noalloc: a file-scope device array, one copy per GPU the library
+// runs on (held until the process ends).  Host code never passes `scratch` itself to a kernel or
+// a copy -- in host code the name is a stand-in, not a device address -- but the address
+// hipGetSymbolAddress returns for it on that device, looked up once per device.
+namespace {
+constexpr size_t kScratchBytes = (size_t)48 << 20;
+constexpr int kScratchDevices = 64;
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kScratchDevices];
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+// The scratch array's address on `device` (made current for the lookup, then restored).
+int scratch_on(int device, void** out) {
+    if (device < 0 || device >= kScratchDevices)
+        return fail(MNB_ERR_UNSUPPORTED, "device %d is beyond the %d devices the scratch table "
+                                         "covers", device, kScratchDevices);
+    ScratchSlot& slot = g_scratch[device];
+    std::call_once(slot.once, [&] {
+        int prev = -1;
+        hipError_t e = hipGetDevice(&prev);
+        if (e == hipSuccess && prev != device) e = hipSetDevice(device);
+        if (e == hipSuccess) e = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch));
+        if (prev >= 0 && prev != device) {
+            const hipError_t r = hipSetDevice(prev);
+            if (e == hipSuccess) e = r;
+        }
+        if (e == hipSuccess && !slot.ptr) e = hipErrorInvalidSymbol;
+        slot.err = e;
+    });
+    if (slot.err != hipSuccess) return hip_fail(slot.err, "scratch address (hipGetSymbolAddress)");
+    *out = slot.ptr;
+    return MNB_OK;
+}
+}  // namespace
+
+extern "C" {
+
+size_t mnb_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int mnb_matmul_nbits_noalloc(const mnb_problem* p, const void* a, const uint8_t* b,
+                             const void* scales, const uint8_t* zero_points, void* y,
+                             void* stream) {
+    mnb_plan_info info;
+    int rc = mnb_plan(p, &info);
+    if (rc) return rc;
+    const size_t need = (size_t)info.workspace_bytes;
+    // accuracy_level 4 needs its workspace; the prefill GEMM's is optional (without it the GEMM
+    // runs unsplit along K)
+    if (info.kernel == MNB_KERNEL_ACC4_I8 && need > kScratchBytes)
+        return fail(MNB_ERR_UNSUPPORTED, "accuracy_level 4 at M = %lld, N = %lld, K = %lld needs "
+                    "%zu bytes of scratch; the allocation-free entry point holds %zu (call "
+                    "mnb_matmul_nbits with a workspace instead)", (long long)p->m,
+                    (long long)p->n, (long long)p->k, need, kScratchBytes);
+    if (p->m == 0) return MNB_OK;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    if (need > 0 && need <= kScratchBytes) {
+        int device = -1;
+        const hipStream_t st = static_cast<hipStream_t>(stream);
+        const hipError_t e = st ? hipStreamGetDevice(st, &device) : hipGetDevice(&device);
+        if (e != hipSuccess) return hip_fail(e, "device of the stream");
+        rc = scratch_on(device, &ws);
+        if (rc) return rc;
+        ws_bytes = need;
+    }
+    return mnb_matmul_nbits(p, a, b, scales, zero_points, y, ws, ws_bytes, stream);
+}
+
 int mnb_dequantize_f16(int64_t n, int64_t k, int32_t bits, int32_t block_size,
                        const uint8_t* b, const void* scales_f16, const uint8_t* zero_points,
                        void* w_out_f16, void* stream) {

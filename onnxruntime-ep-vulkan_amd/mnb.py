@@ -121,6 +121,8 @@ def load() -> C.CDLL:
         "mnb_plan": (C.c_int, [C.POINTER(Problem), C.POINTER(PlanInfo)]),
         "mnb_workspace_bytes": (C.c_int, [C.POINTER(Problem), C.POINTER(sz)]),
         "mnb_matmul_nbits": (C.c_int, [C.POINTER(Problem), vp, vp, vp, vp, vp, vp, sz, vp]),
+        "mnb_matmul_nbits_noalloc": (C.c_int, [C.POINTER(Problem), vp, vp, vp, vp, vp, vp]),
+        "mnb_noalloc_scratch_bytes": (sz, []),
         "mnb_dequantize_f16": (C.c_int, [i64, i64, i32, i32, vp, vp, vp, vp, vp]),
         "mnb_quantize_a_int8": (C.c_int, [i64, i64, i32, i32, vp, vp, vp, vp, vp]),
         "mnb_moe_grouped": (C.c_int, [C.POINTER(MoeProblem), vp, vp, vp, vp, vp, vp, vp, vp]),

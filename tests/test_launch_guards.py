@@ -79,3 +79,16 @@ def test_planner_shapes_stay_within_compiled_bounds():
                         except mnb.MnbError:
                             continue
                         assert 64 * info.waves_per_group <= bounds[info.kernel], (m, k, n, bits, bs, level, info.kernel, info.waves_per_group)
+
+
+def test_noalloc_refuses_level_4_beyond_its_scratch():
+    """The allocation-free entry point refuses an accuracy_level 4 problem whose workspace is
+    larger than its scratch array, before any device work (the pointers are never read)."""
+    import mnb
+
+    lib = mnb.load()
+    p = mnb.problem(8192, 64, 8192, 4, 32, False, mnb.DTYPE_F16, 4)
+    assert mnb.workspace_bytes(p) > lib.mnb_noalloc_scratch_bytes() == 48 << 20
+    assert lib.mnb_matmul_nbits_noalloc(C.byref(p), None, None, None, None, None, None) == \
+        mnb.MNB_ERR_UNSUPPORTED
+    assert b"scratch" in lib.mnb_last_error()
