@@ -49,32 +49,41 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     StreamConfig c{};
     c.mr = m <= 1 ? 1 : (int)(m < 4 ? m : 4);
     const int64_t cpc = k / (128 / bits);
-    // Lane-group width: the widest group whose lanes are best filled (G * CPL chunk slots for
-    // cpc chunks), so each load instruction reads the longest contiguous runs.
-    double best = -1.0;
+    // Lane-group width: the best-filled group (G * CPL chunk slots for cpc chunks); among equally
+    // filled ones, the one that puts closest to 16 wavefronts on each CU (one per 64/G columns).
+    // Measured on MI355X for the Phi-3.5 decode shapes: qkv G=32 (18 per CU), gate_up G=16 (16
+    // per CU) rather than G=32 (32 per CU).
+    auto waves_per_cu = [&](int cand) {
+        return (double)((n + 64 / cand - 1) / (64 / cand)) / kNumCUs;
+    };
+    double best_fill = -1.0, best_dist = 0.0;
     int g = 64;
     for (int cand : {64, 32, 16}) {
         const int64_t cpl = (cpc + cand - 1) / cand;
         if (cpl > cpl_cap(1, c.mr)) continue;
         const double fill = (double)cpc / (double)(cand * cpl);
-        if (fill > best + 1e-9) { best = fill; g = cand; }
+        const double dist = __builtin_fabs(waves_per_cu(cand) - 16.0);
+        if (fill > best_fill + 1e-9 || (fill > best_fill - 1e-9 && dist < best_dist)) {
+            best_fill = fill;
+            best_dist = dist;
+            g = cand;
+        }
     }
     c.g = g;
     c.cpl = (int)((cpc + g - 1) / g);
-    // Workgroups: every one stages the whole activation vector (2*K bytes per row) before it
-    // streams weights, so more workgroups mean more of that traffic ahead of the weights.
-    // Measured on MI355X (Phi-3.5 decode shapes): about three workgroups per CU for K <= 4096,
-    // one per CU for K = 8192; 4..16 wavefronts each, one column per lane group.
-    const int64_t target_groups = (k <= 4096 ? 3 : 1) * kNumCUs;
-    const int64_t cols_per_group = (n + target_groups - 1) / target_groups;
-    const int64_t per_wave = 64 / g;
-    int64_t w = (cols_per_group + per_wave - 1) / per_wave;
-    const int64_t wmax = kStreamMaxThreads / 64;
+    // One column per lane group unless that needs more than 32 wavefronts per CU.
     c.u = 1;
-    if (w > wmax && c.mr == 1 && c.cpl <= cpl_cap(2, 1)) {
+    double wpc = waves_per_cu(g);
+    if (wpc > 32.0 && c.mr == 1 && c.cpl <= cpl_cap(2, 1)) {
         c.u = 2;
-        w = (cols_per_group + 2 * per_wave - 1) / (2 * per_wave);
+        wpc /= 2.0;
     }
+    // Workgroups: each stages the whole activation vector (2*K bytes per row) before it streams
+    // weights, so more workgroups mean more of that traffic ahead of the weights.  Measured:
+    // about three workgroups per CU for K <= 4096, one for K = 8192; 4..16 wavefronts each.
+    const double groups_per_cu = k <= 4096 ? 3.0 : 1.0;
+    int64_t w = (int64_t)(wpc / groups_per_cu + 0.5);
+    const int64_t wmax = kStreamMaxThreads / 64;
     c.waves_per_group = (int)(w < 4 ? 4 : (w > wmax ? wmax : w));
     derive(c, n, k, bits, bs);
     return c;
