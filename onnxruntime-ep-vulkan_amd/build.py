@@ -26,11 +26,11 @@ CSRC = PKG / "csrc"
 LIB = PKG / "lib"
 OBJ = PKG / "_build"
 INCLUDE = REPO / "include"
-# ORT's plugin-EP C headers (ONNX Runtime v1.28.0, MIT) as vendored in the reference checkout;
-# read at build time only.  The built library is what travels.
+# ORT's plugin-EP C headers (ONNX Runtime v1.28.0, MIT), vendored under third_party/onnxruntime
+# (ORT_INCLUDE_DIR overrides them).
 ORT_INCLUDE_CANDIDATES = [
     Path(os.environ.get("ORT_INCLUDE_DIR", "")),
-    Path("/root/reference/third_party/onnxruntime/include"),
+    REPO / "third_party" / "onnxruntime" / "include",
 ]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
