@@ -8,13 +8,17 @@ nodes, run GetCapability / Compile / Compute, and read the output tensors.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 import numpy as np
 
 ROOT = Path(__file__).resolve().parents[1]
-MOCK_SO = Path(__file__).resolve().parent / "mock_ort" / "build" / "libmock_ort.so"
-EP_SO = ROOT / "onnxruntime-ep-vulkan_amd" / "lib" / "libonnxruntime_mi355x_ep.so"
+# The sanitizer lane (tests/test_ep_sanitizers.py) points these at its ASan/UBSan builds.
+MOCK_SO = Path(os.environ.get("MI355X_TEST_MOCK_SO") or
+               Path(__file__).resolve().parent / "mock_ort" / "build" / "libmock_ort.so")
+EP_SO = Path(os.environ.get("MI355X_TEST_EP_SO") or
+             ROOT / "onnxruntime-ep-vulkan_amd" / "lib" / "libonnxruntime_mi355x_ep.so")
 
 FLOAT, UINT8, INT32, FLOAT16 = 1, 2, 6, 10
 NP_ELEM = {np.dtype(np.float32): FLOAT, np.dtype(np.uint8): UINT8, np.dtype(np.int32): INT32,
