@@ -17,8 +17,9 @@ The line also carries, measured in the same run:
   moe           configs[3] (32 experts, top-4 of 64 tokens, gate_up and down) in GB/s
   qmoe          configs[3] as one fused QMoE op (routing, both expert GEMVs, SwiGLU, combine)
   mfma_calibration  the fp16 MFMA rate the chip sustains on random and on constant operands
-  cpu_baseline  the C restatement in oracle/ (kind "port"; stock ORT is not installed in this
-                image) on the host's cores, on a bounded sample of the same layer set
+  cpu_baseline  the C restatement in oracle/ (kind "port", not ORT) on the host's cores, on a
+                bounded sample of the same layer set; stock_ort_cpu_baseline says whether stock
+                ONNX Runtime (the reference's baseline) could be timed (it is not installed)
 `--pmc-node NODE` runs one node's launches and a 256 MiB copy only, for rocprofv3 --pmc passes
 (FETCH_SIZE, WRITE_SIZE) whose results give roofline.traffic (profiles/traffic_*.json).
 """
@@ -173,8 +174,19 @@ def cpu_baseline(seconds: float = 10.0) -> dict:
     return {"value": round(per_set * iters / el / 1e9, 3), "unit": "GB/s", "cores": cores,
             "kind": "port",
             "sample": f"{iters} passes of the 4-node Phi-3.5 decode layer set (M=1, int4 bs32, zp) "
-                      f"in {el:.1f} s; stock ORT CPUExecutionProvider is not installed in this "
-                      f"image, so the oracle's C restatement (fp32 accumulate, OpenMP) stands in"}
+                      f"in {el:.1f} s with the oracle's C restatement of MatMulNBits (fp32 "
+                      f"accumulate, OpenMP) -- this build's port, not ONNX Runtime"}
+
+
+def stock_ort_probe() -> str:
+    """Whether stock ONNX Runtime (the reference's CPU baseline) can be timed here."""
+    import importlib.util
+
+    if importlib.util.find_spec("onnxruntime") is None:
+        return ("stock ORT baseline unavailable: the onnxruntime package is not installed on "
+                "this machine (probed with importlib), and nothing can be installed")
+    return ("onnxruntime is importable but this build does not time it: building the one-node "
+            "model needs the onnx package")
 
 
 def main() -> int:
@@ -709,6 +721,7 @@ def main() -> int:
         "qmoe": qmoe,
         "session_io": session_io,
         "cpu_baseline": cpu,
+        "stock_ort_cpu_baseline": stock_ort_probe(),
     }
     print(json.dumps(line))
     return 0

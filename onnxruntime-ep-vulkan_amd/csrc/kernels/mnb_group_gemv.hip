@@ -309,8 +309,10 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     if (ksplit > 1) {
         // K split over workgroups: each writes its partial tile; the last to arrive (device-
         // scope counter) adds the partials in split order and stores Y, then re-arms the
-        // counter.  Partials move through device-coherent (agent-scope) atomic stores and
-        // loads, so no workgroup has to write back or invalidate its XCD's L2.
+        // counter.  Ordering follows the HIP memory model at agent scope: every thread's partial
+        // stores are followed by an agent-scope fence before the workgroup barrier, the arrival
+        // counter is an acquire-release read-modify-write, and the last workgroup fences again
+        // before it reads the other workgroups' partials.
         const int sid = (blockIdx.z * gridDim.y + blockIdx.y) * (gridDim.x / ksplit) + strip;
         float* mine = reinterpret_cast<float*>(part + ((int64_t)sid * ksplit + split) * (MT * 64));
         for (int idx = threadIdx.x; idx < 64 * MT; idx += blockDim.x) {
@@ -321,14 +323,15 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
                 __hip_atomic_store(mine + 4 * idx + q, sum[q], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
-        __builtin_amdgcn_s_waitcnt(0);                   // the partial has reached memory
+        __threadfence();                                 // release this thread's partial stores
         __syncthreads();
         __shared__ int last;
         if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(cnt + sid, 1, __ATOMIC_RELAXED,
+            last = __hip_atomic_fetch_add(cnt + sid, 1, __ATOMIC_ACQ_REL,
                                           __HIP_MEMORY_SCOPE_AGENT) == ksplit - 1;
         __syncthreads();
         if (!last) return;
+        __threadfence();                                 // acquire the other splits' partials
         const float* all = reinterpret_cast<const float*>(part + (int64_t)sid * ksplit * (MT * 64));
         for (int idx = threadIdx.x; idx < 64 * MT; idx += blockDim.x) {
             f32x4 sum;

@@ -34,6 +34,32 @@ def _dev(x, device):
     return None if x is None else torch.from_numpy(np.ascontiguousarray(x)).to(device)
 
 
+# MNB_FORCE_KERNEL values and the planner kernel each one selects.
+FORCED = {"stream": 5, "gemv": 1, "gemm": 2, "generic": 3, "group": 6, "strip": 7}
+
+
+def _forced_kernel(M, N, K, bits, bs, zp, kernel):
+    """The kernel the planner picks for this shape with MNB_FORCE_KERNEL=kernel (host only)."""
+    import mnb
+
+    old = os.environ.get("MNB_FORCE_KERNEL")
+    os.environ["MNB_FORCE_KERNEL"] = kernel
+    try:
+        return mnb.plan(mnb.problem(M, N, K, bits, bs, zp)).kernel
+    finally:
+        if old is None:
+            os.environ.pop("MNB_FORCE_KERNEL", None)
+        else:
+            os.environ["MNB_FORCE_KERNEL"] = old
+
+
+def _forcible(shapes):
+    """(shape..., kernel) for every forced kernel that really runs on the shape: a kernel that
+    cannot take a shape is left out instead of silently re-running the default kernel."""
+    return [(*sh, k) for sh in shapes for k in FORCED
+            if _forced_kernel(*sh, k) == FORCED[k]]
+
+
 def _run(inp, N, K, bits, bs, device, kernel=None, acc=0):
     import mnb
     import torch
@@ -41,6 +67,9 @@ def _run(inp, N, K, bits, bs, device, kernel=None, acc=0):
     try:
         if kernel:
             os.environ["MNB_FORCE_KERNEL"] = kernel
+            M = int(np.prod(inp["A"].shape[:-1]))
+            got = mnb.plan(mnb.problem(M, N, K, bits, bs, inp.get("zp") is not None)).kernel
+            assert got == FORCED[kernel], f"{kernel} forced, planner chose {got}"
         else:
             os.environ.pop("MNB_FORCE_KERNEL", None)
         y = mnb.matmul_nbits(_dev(inp["A"], device), _dev(inp["B"], device),
@@ -80,8 +109,15 @@ def test_dequant_bit_exact(cuda, name):
     assert np.array_equal(got, d["W_bits"]), f"{np.count_nonzero(got != d['W_bits'])} mismatches"
 
 
-@pytest.mark.parametrize("kernel", ["stream", "gemv", "gemm", "generic"])
-@pytest.mark.parametrize("name", KATS)
+def _kat_cases():
+    out = []
+    for name in KATS:
+        M, N, K, bits, bs, hz = (int(v) for v in _load(name)["meta"])
+        out += [(name, k) for k in FORCED if _forced_kernel(M, N, K, bits, bs, bool(hz), k) == FORCED[k]]
+    return out
+
+
+@pytest.mark.parametrize("name,kernel", _kat_cases())
 def test_integer_exact_kat(cuda, name, kernel):
     d = _load(name)
     M, N, K, bits, bs, hz = (int(v) for v in d["meta"])
@@ -119,8 +155,7 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("kernel", ["stream", "gemv", "gemm", "generic"])
-@pytest.mark.parametrize("M,N,K,bits,bs,zp", SHAPES)
+@pytest.mark.parametrize("M,N,K,bits,bs,zp,kernel", _forcible(SHAPES))
 def test_random_parity_f16(cuda, M, N, K, bits, bs, zp, kernel):
     inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=M * 1000 + N + K)
     print(f"[gpu] parity M={M} N={N} K={K} bits={bits} bs={bs} zp={zp} {kernel}", flush=True)
@@ -180,6 +215,34 @@ def test_gemm_parity(cuda, M, N, K, bs, zp):
     y = _run(inp, N, K, 4, bs, cuda, "gemm")
     ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
     _check_f16(y, ref, f"gemm M={M} N={N} K={K} bs={bs}")
+
+
+def test_gemm_uneven_k_split(cuda):
+    """K split whose last split is shorter: K = 1600 is 25 steps of 64, over 3 workgroups per tile
+    (9, 9 and 7 steps).  Checked against the oracle, and against the same GEMM run unsplit (no
+    workspace) at the same bar."""
+    import mnb
+    import torch
+
+    M, N, K = 129, 300, 1600
+    p = mnb.problem(M, N, K, 4, 32, False)
+    info = mnb.plan(p)
+    tiles = -(-M // info.tile_m) * -(-N // info.tile_n)
+    assert info.kernel == mnb.KERNEL_GEMM_MFMA and info.grid_x == 3 * tiles
+    assert mnb.workspace_bytes(p) == 3 * M * N * 4
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=32, with_zp=False, seed=1600)
+    print(f"[gpu] gemm uneven split M={M} N={N} K={K}", flush=True)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], None, N, K, 4, 32)
+    split = _run(inp, N, K, 4, 32, cuda)
+    _check_f16(split, ref, "uneven split")
+    t = {k: _dev(v, cuda) for k, v in inp.items() if v is not None}
+    unsplit = torch.empty(M, N, dtype=torch.float16, device=cuda)
+    import ctypes as C
+    mnb.check(mnb.load().mnb_matmul_nbits(C.byref(p), t["A"].data_ptr(), t["B"].data_ptr(),
+                                          t["scales"].data_ptr(), None, unsplit.data_ptr(), None,
+                                          0, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    _check_f16(unsplit.cpu().numpy(), ref, "unsplit")
 
 
 @pytest.mark.parametrize("M", [512, 2048])

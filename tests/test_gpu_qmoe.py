@@ -89,6 +89,47 @@ def test_qmoe_matches_oracle(cuda, case):
     _check(y.float().cpu().numpy(), ref16, ref)
 
 
+def _skewed_logits(T, E, heavy=3, heavy_rows=40, odd=7, odd_rows=17):
+    """Router logits under which expert `heavy` takes exactly `heavy_rows` tokens (three 16-row
+    tiles) and expert `odd` exactly `odd_rows` (one more than a tile); every other token's second
+    choice is spread over experts 8..12."""
+    rng = np.random.default_rng(4040)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    lg[:, heavy] = -8.0
+    lg[:, odd] = -8.0
+    for t in range(T):
+        lg[t, 8 + t % 5] = 4.0
+        if t < heavy_rows:
+            lg[t, heavy] = 8.0
+        elif t < heavy_rows + odd_rows:
+            lg[t, odd] = 8.0
+    return lg.astype(np.float16)
+
+
+@pytest.mark.gpu
+def test_qmoe_skewed_routing_spans_several_row_tiles(cuda):
+    """fc1 finds its own rows (interleaved SwiGLU, T*k <= 1024, E <= 64) with the row-tile hint at
+    T*k/E = 8: an expert with 40 rows spans three 16-row tiles (the tiles past the first read
+    their window of the expert's ranked rows) and one with 17 rows spans two."""
+    import mnb
+    import torch
+
+    T, H, I, E, k = 64, 256, 128, 16, 2
+    inp = oq.make_qmoe_inputs(T, H, I, E, block_size=32, bias=True, seed=4041)
+    inp["logits"] = _skewed_logits(T, E)
+    experts, _ = oq.route(inp["logits"], k)
+    counts = np.bincount(experts.reshape(-1), minlength=E)
+    assert counts[3] == 40 and counts[7] == 17 and counts.max() == 40
+    print(f"[gpu] qmoe skewed routing T={T} E={E} k={k} counts {counts.tolist()}", flush=True)
+    ref16, ref = _refs(inp, k, I, 32, 1, 7.0, True)
+    d = {key: _t(v, cuda) for key, v in inp.items()}
+    y = mnb.qmoe(d["x"], d["logits"], d["fc1"], d["fc1_scales"], d["fc2"], d["fc2_scales"], k=k,
+                 inter=I, block_size=32, fc1_bias=d["fc1_bias"], fc2_bias=d["fc2_bias"],
+                 fusion=1, normalize=True, limit=7.0)
+    torch.cuda.synchronize()
+    _check(y.float().cpu().numpy(), ref16, ref)
+
+
 @pytest.mark.gpu
 def test_qmoe_is_deterministic(cuda):
     import mnb

@@ -48,17 +48,20 @@ def residual_fp32(inp, skip=True, bias=False):
     return r
 
 
-@pytest.mark.parametrize("rows,hidden", [(1, 3072), (7, 2880), (64, 4096), (5, 8192), (3, 128),
-                                         (33, 3072)])
-@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+ROWS_HIDDEN = [(1, 3072), (7, 2880), (64, 4096), (5, 8192), (3, 128), (33, 3072)]
+# fp32 rows are held in registers up to 4096 elements (8192 for fp16); the wider fp32 form is
+# refused by the library (tests/test_launch_guards.py), not run.
+SHAPES = [(r, h, dt) for (r, h) in ROWS_HIDDEN for dt in (np.float16, np.float32)
+          if not (dt == np.float32 and h > 4096)]
+
+
+@pytest.mark.parametrize("rows,hidden,dtype", SHAPES)
 @pytest.mark.parametrize("skip,bias,want_sum", [(True, False, True), (True, True, True),
                                                 (False, False, False), (True, False, False)])
 def test_rmsnorm_matches_oracle(cuda, rows, hidden, dtype, skip, bias, want_sum):
     import mnb
     import torch
 
-    if dtype == np.float32 and hidden > 4096:
-        pytest.skip("fp32 rows are limited to 4096 elements")
     inp = rn.make_inputs(rows, hidden, dtype=dtype, seed=rows + hidden)
     d = {k: _t(v, cuda) for k, v in inp.items()}
     y, sm = mnb.skip_rmsnorm(d["x"], d["gamma"], skip=d["skip"] if skip else None,
@@ -93,3 +96,4 @@ def test_rmsnorm_session_host_io(cuda):
         if w.value:
             lib.mnb_rmsnorm_weights_release(w)
         lib.mnb_session_destroy(sess)
+

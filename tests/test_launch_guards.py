@@ -1,4 +1,5 @@
-"""Launch-shape guards of the HIP launchers (host-only: nothing reaches a device).
+"""Host-side guards of the HIP library (nothing here reaches a device): launch shapes against the
+workgroup sizes the kernels are compiled for, and forms the library refuses before launching.
 
 A workgroup larger than the thread count a kernel was compiled for (its __launch_bounds__) does
 not run: the launch fails as an unspecified launch failure.  The launchers therefore refuse such
@@ -92,3 +93,22 @@ def test_noalloc_refuses_level_4_beyond_its_scratch():
     assert lib.mnb_matmul_nbits_noalloc(C.byref(p), None, None, None, None, None, None) == \
         mnb.MNB_ERR_UNSUPPORTED
     assert b"scratch" in lib.mnb_last_error()
+
+
+def test_rmsnorm_refuses_wide_fp32_rows():
+    """fp32 rows above 4096 elements (and fp16 above 8192) are refused with a message, before
+    anything reaches a device."""
+    import mnb
+
+    lib = mnb.load()
+    for dtype, hidden, ok in ((mnb.DTYPE_F32, 4096, True), (mnb.DTYPE_F32, 8192, False),
+                              (mnb.DTYPE_F16, 8192, True), (mnb.DTYPE_F16, 8200, False)):
+        p = mnb.RmsNormProblem(5, hidden, 1e-5, 1, 0, 1, dtype)
+        rc = lib.mnb_rmsnorm_check(C.byref(p))
+        if ok:
+            assert rc == mnb.MNB_OK
+        else:
+            assert rc == mnb.MNB_ERR_UNSUPPORTED
+            assert b"hidden" in lib.mnb_last_error()
+        rc = lib.mnb_skip_rmsnorm(C.byref(p), None, None, None, None, None, None, None)
+        assert (rc == mnb.MNB_ERR_INVALID) if ok else (rc == mnb.MNB_ERR_UNSUPPORTED)
