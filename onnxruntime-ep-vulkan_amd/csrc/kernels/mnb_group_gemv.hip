@@ -309,10 +309,15 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     if (ksplit > 1) {
         // K split over workgroups: each writes its partial tile; the last to arrive (device-
         // scope counter) adds the partials in split order and stores Y, then re-arms the
-        // counter.  Ordering follows the HIP memory model at agent scope: every thread's partial
-        // stores are followed by an agent-scope fence before the workgroup barrier, the arrival
-        // counter is an acquire-release read-modify-write, and the last workgroup fences again
-        // before it reads the other workgroups' partials.
+        // counter.  Ordering relies on a property of gfx950 rather than on HIP memory-model
+        // fences: the partials are written with agent-scope atomic stores, which are performed
+        // at the device coherence point (written through the XCD's L2), s_waitcnt(0) waits
+        // until they have completed there, the arrival counter is an agent-scope atomic at the
+        // same point, and the last workgroup reads the partials with agent-scope atomic loads.
+        // An arriving workgroup that sees the final count therefore sees every partial.  The
+        // model-level alternative -- release / acquire fences at agent scope -- compiles on
+        // gfx950 to a write-back and an invalidate of the whole L2 (buffer_wbl2 / buffer_inv)
+        // per workgroup, which made this launch about ten times slower when measured.
         const int sid = (blockIdx.z * gridDim.y + blockIdx.y) * (gridDim.x / ksplit) + strip;
         float* mine = reinterpret_cast<float*>(part + ((int64_t)sid * ksplit + split) * (MT * 64));
         for (int idx = threadIdx.x; idx < 64 * MT; idx += blockDim.x) {
@@ -323,15 +328,14 @@ group_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
                 __hip_atomic_store(mine + 4 * idx + q, sum[q], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
-        __threadfence();                                 // release this thread's partial stores
+        __builtin_amdgcn_s_waitcnt(0);                   // the partial stores have completed
         __syncthreads();
         __shared__ int last;
         if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(cnt + sid, 1, __ATOMIC_ACQ_REL,
+            last = __hip_atomic_fetch_add(cnt + sid, 1, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT) == ksplit - 1;
         __syncthreads();
         if (!last) return;
-        __threadfence();                                 // acquire the other splits' partials
         const float* all = reinterpret_cast<const float*>(part + (int64_t)sid * ksplit * (MT * 64));
         for (int idx = threadIdx.x; idx < 64 * MT; idx += blockDim.x) {
             f32x4 sum;
