@@ -57,6 +57,8 @@ extern "C" {
 #define MNB_KERNEL_GROUP_MFMA 6  /* fp16, int4, block >= 32: row-tiled 16x16x32 MFMA GEMV */
 #define MNB_KERNEL_STRIP_MFMA 7  /* fp16, int4, block >= 32, 5..16 rows: activations held in
                                     registers across a run of 16-column strips */
+#define MNB_KERNEL_ACC4_STREAM 8 /* accuracy_level 4, fp16, <= 16 rows, K % 128 == 0 up to 8192:
+                                    int8 MFMA, one 16-column strip per workgroup over all of K */
 
 /* One MatMulNBits node: the attributes plus the row count of this call. */
 typedef struct mnb_problem {

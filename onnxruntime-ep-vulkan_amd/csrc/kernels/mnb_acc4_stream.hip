@@ -1,0 +1,287 @@
+// accuracy_level = 4 at up to 16 rows (batched decode): int8 activations x int4 weights on
+// gfx950 MFMA, one 16-column strip per workgroup over the whole of K.
+//
+// The launch follows the quantiser (quantize_a_int8: the activations' int8 codes in the strip
+// layout -- within every 128-k quad a lane row's chunks 0,1 and 2,3 are two 16-byte pieces --
+// and their fp32 scales block-major over 16 rows).  A workgroup of KW wavefronts owns one strip
+// of 16 columns; wavefront w owns quads [w R, w R + R) of K (KW R = K / 128):
+//   * every thread first requests its share of the 16 rows' codes and scales (2R 16-byte pieces
+//     and R * blocks-per-quad / 4 scales), then its wavefront's block scales and zero points,
+//     then its R quads of weights (lane (n, g): 16 bytes of column n, chunk 4q + g, streamed
+//     past the caches) -- so the activations, needed first, are not queued behind the weights;
+//   * the codes go to LDS (rows padded by 16 bytes: the 16 rows' reads start in distinct bank
+//     groups), one barrier, and each wavefront computes: a 4 x 4 dword transpose across the lane
+//     rows gives the B operands, weights become exact int8 (q - zp), v_mfma_i32_16x16x64_i8
+//     (16x16x32 for block 32) gives exact int32 block dots, scaled by a_scale * b_scale in fp32;
+//   * the KW partial tiles are added in LDS in wavefront order (run-to-run deterministic) and
+//     stored as fp16.
+// Nothing crosses workgroups: no counters and no partial tiles in memory.  Each workgroup reads
+// the codes of all of K (16 K bytes, from L2) -- the price of having no cross-workgroup
+// reduction, which measured slower on gfx950 (splitting K over 4..16 workgroups per strip adds
+// two serialised device-scope round trips, the counter and the partials, at the kernel's end).
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "mnb_common.hpp"
+#include "mnb_launch.hpp"
+
+namespace mnb {
+
+namespace {
+
+constexpr int kAcc4sMaxWaves = 16;
+constexpr size_t kAcc4sMaxLds = 160 * 1024;
+
+template <int BS, bool HAS_ZP, int R>
+__global__ void __launch_bounds__(64 * kAcc4sMaxWaves)
+acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
+            const uint8_t* __restrict__ B, const f16* __restrict__ Sc,
+            const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K) {
+    constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
+    constexpr int BPQ = 4 / CPB;                         // blocks per quad
+    constexpr int PA = 2 * R;                            // 16-byte code pieces per thread
+    constexpr int PS = (R * BPQ + 3) / 4;                // activation scales per thread
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int kw = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int KW = blockDim.x >> 6;
+    const int T = blockDim.x;
+    const int nl = lane & 15;
+    const int g = lane >> 4;
+    const int quads = K >> 7;                            // = KW * R
+    const int bpc = K / BS;                              // a multiple of 4
+    const int zpb = bpc >> 1;
+    const int strip = blockIdx.x;
+    const int q0 = kw * R;                               // this wavefront's first quad
+    const int RB = 128 * quads + 16;                     // LDS row stride of the codes
+    uint8_t* const sA = smem;
+    float* const sSa = reinterpret_cast<float*>(smem + 16 * RB);          // [bpc][16] + 4
+    f32x4* const sRed = reinterpret_cast<f32x4*>(smem + 16 * RB + bpc * 64 + 16);
+
+    // ---- 1. this thread's share of the codes and activation scales -------------------------
+    // 16 rows x quads x 8 pieces = T * PA exactly; rows past M repeat row M - 1 (never stored)
+    const int t = threadIdx.x;
+    const int ppr = 8 * quads;                           // pieces per row
+    u32x4 va[PA];
+#pragma unroll
+    for (int i = 0; i < PA; ++i) {
+        const int u = t + i * T;
+        const int row = min(u / ppr, M - 1);
+        va[i] = *reinterpret_cast<const u32x4*>(qa + (int64_t)row * K + 16 * (u % ppr));
+    }
+    const int nsc = bpc * 16;
+    float vs[PS];
+#pragma unroll
+    for (int i = 0; i < PS; ++i) vs[i] = a_scale[min(t + i * T, nsc - 1)];
+
+    // ---- 2. the wavefront's block scales and zero points (contiguous per column) -----------
+    const int col = min(16 * strip + nl, N - 1);
+    constexpr int NS = R * BPQ;                          // blocks of the wavefront's quads
+    constexpr int NZ = (NS + 1) / 2;
+    const int b0 = q0 * BPQ;                             // first block; even unless NS == 1
+    uint16_t sv[NS];
+    uint8_t zv[NZ];
+    const uint16_t* sp = reinterpret_cast<const uint16_t*>(Sc) + (int64_t)col * bpc + b0;
+    const uint8_t* zp = Z + (int64_t)col * zpb + (b0 >> 1);
+    if constexpr (NS % 4 == 0) {
+        // 8-byte and 2-byte aligned: bpc % 4 == 0, b0 % 4 == 0, the launcher checks the bases
+#pragma unroll
+        for (int i = 0; i < NS / 4; ++i) {
+            const u32x2 v = *reinterpret_cast<const u32x2*>(sp + 4 * i);
+            sv[4 * i] = (uint16_t)v.x;
+            sv[4 * i + 1] = (uint16_t)(v.x >> 16);
+            sv[4 * i + 2] = (uint16_t)v.y;
+            sv[4 * i + 3] = (uint16_t)(v.y >> 16);
+        }
+        if constexpr (HAS_ZP) {
+#pragma unroll
+            for (int i = 0; i < NZ / 2; ++i) {
+                const uint16_t v = *reinterpret_cast<const uint16_t*>(zp + 2 * i);
+                zv[2 * i] = (uint8_t)v;
+                zv[2 * i + 1] = (uint8_t)(v >> 8);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NS; ++i) sv[i] = sp[i];
+        if constexpr (HAS_ZP) {
+#pragma unroll
+            for (int i = 0; i < NZ; ++i) zv[i] = zp[i];
+        }
+    }
+
+    // ---- 3. the wavefront's weights ----------------------------------------------------------
+    const uint8_t* bc = B + (int64_t)col * (K / 2);
+    u32x4 bw[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+        bw[j] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(bc + 16 * (int64_t)(4 * (q0 + j) + g)));
+
+    // ---- 4. stage the codes and scales; unpredicated stores (a dummy slot for the scales
+    // past the end), so that only the activation loads are waited for here --------------------
+#pragma unroll
+    for (int i = 0; i < PA; ++i) {
+        const int u = t + i * T;
+        *reinterpret_cast<u32x4*>(sA + (u / ppr) * RB + 16 * (u % ppr)) = va[i];
+    }
+#pragma unroll
+    for (int i = 0; i < PS; ++i) {
+        const int u = t + i * T;
+        sSa[u < nsc ? u : nsc + (u & 3)] = vs[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 5. the strip's partial tile over this wavefront's quads -----------------------------
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const uint8_t* ar = sA + nl * RB + 128 * (q0 + j) + 16 * g;
+        const u32x4 a01 = *reinterpret_cast<const u32x4*>(ar);        // chunks 0, 1 of row nl
+        const u32x4 a23 = *reinterpret_cast<const u32x4*>(ar + 64);   // chunks 2, 3
+        const i32x2 aq[4] = {i32x2{(int32_t)a01.x, (int32_t)a01.y}, i32x2{(int32_t)a01.z, (int32_t)a01.w},
+                             i32x2{(int32_t)a23.x, (int32_t)a23.y}, i32x2{(int32_t)a23.z, (int32_t)a23.w}};
+        uint32_t v0 = bw[j].x, v1 = bw[j].y, v2 = bw[j].z, v3 = bw[j].w;
+        transpose_rows(v0, v1, v2, v3);
+        const uint32_t wt[4] = {v0, v1, v2, v3};
+        i32x2 bq[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int bi = j * BPQ + c / CPB;            // block within the wavefront's range
+            int z = 8;
+            if constexpr (HAS_ZP)
+                z = (int)((zv[(bi + (b0 & 1)) >> 1] >> (((b0 + bi) & 1) * 4)) & 0xFu);
+            bq[c] = qz_i8(wt[c], (uint32_t)(128 - z) * 0x01010101u);
+        }
+        i32x4 dot = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; c += (CPB >= 2 ? 2 : 1)) {
+            if constexpr (CPB >= 2) {
+                // two chunks of one block in one 16x16x64 MFMA: A and B place the same k in the
+                // same (lane row, slot)
+                const i32x4 a4 = {aq[c].x, aq[c].y, aq[c + 1].x, aq[c + 1].y};
+                const i32x4 b4 = {bq[c].x, bq[c].y, bq[c + 1].x, bq[c + 1].y};
+                dot = __builtin_amdgcn_mfma_i32_16x16x64_i8(a4, b4, dot, 0, 0, 0);
+            } else {
+                dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, aq[c]),
+                                                            __builtin_bit_cast(long, bq[c]), dot,
+                                                            0, 0, 0);
+            }
+            const int ce = c + (CPB >= 2 ? 1 : 0);       // last chunk covered so far
+            if ((ce + 1) % CPB == 0) {                   // block end: scale it
+                const int b = ce / CPB;
+                const float sb = (float)__builtin_bit_cast(f16, sv[j * BPQ + b]);
+                const f32x4 sa =
+                    *reinterpret_cast<const f32x4*>(sSa + ((q0 + j) * BPQ + b) * 16 + 4 * g);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf((float)dot[q], sa[q] * sb, acc[q]);
+                dot = i32x4{0, 0, 0, 0};
+            }
+        }
+    }
+
+    // ---- 6. the KW partial tiles in wavefront order, stored by wavefront 0 -----------------
+    if (kw > 0) sRed[kw * 64 + lane] = acc;
+    __syncthreads();
+    if (kw > 0) return;
+    for (int w = 1; w < KW; ++w) acc += sRed[w * 64 + lane];
+    const int cc = 16 * strip + nl;
+    if (cc >= N) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = 4 * g + q;                         // MFMA output: rows 4g .. 4g + 3
+        if (r < M) Y[(int64_t)r * N + cc] = (f16)acc[q];
+    }
+}
+
+template <int BS, bool HAS_ZP>
+hipError_t acc4s_go(const Acc4StreamGeom& g, const int8_t* qa, const float* sa, const uint8_t* b,
+                    const void* s, const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
+                    hipStream_t st) {
+    const dim3 grid((unsigned)g.gx, 1, 1);
+    const dim3 block((unsigned)(64 * g.waves), 1, 1);
+#define MNB_A4S(R_)                                                                               \
+    do {                                                                                          \
+        auto kern = acc4_stream<BS, HAS_ZP, R_>;                                                  \
+        if (g.lds > 64 * 1024) {                                                                  \
+            const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),      \
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)g.lds);                          \
+            if (ea != hipSuccess) return ea;                                                      \
+        }                                                                                         \
+        hipLaunchKernelGGL(kern, grid, block, g.lds, st, qa, sa, b, static_cast<const f16*>(s),   \
+                           z, static_cast<f16*>(y), (int)m, (int)n, (int)k);                      \
+    } while (0)
+    switch (g.r) {
+        case 1: MNB_A4S(1); break;
+        case 2: MNB_A4S(2); break;
+        case 4: MNB_A4S(4); break;
+        case 8: MNB_A4S(8); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef MNB_A4S
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool acc4_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, Acc4StreamGeom* out) {
+    if (m < 1 || m > 16 || n < 1 || k < 128 || k % 128 || (bs != 32 && bs != 64 && bs != 128))
+        return false;
+    if ((k / bs) % 4) return false;                      // whole 4-block groups of scales
+    const int64_t quads = k / 128;
+    Acc4StreamGeom g{};
+    // R quads per wavefront: the largest of 8, 4, 2, 1 that divides K into at least 8
+    // wavefronts (into all of its quads when there are fewer than 8), at most 16 wavefronts.
+    g.r = 0;
+    for (int r : {8, 4, 2, 1}) {
+        if (quads % r == 0 && (quads / r >= 8 || r == 1) && quads / r <= kAcc4sMaxWaves) {
+            g.r = r;
+            break;
+        }
+    }
+    if (g.r == 0) return false;
+    g.waves = (int)(quads / g.r);
+    g.gx = (n + 15) / 16;
+    g.lds = (size_t)16 * (size_t)(128 * quads + 16) + (size_t)(k / bs) * 64 + 16 +
+            (size_t)g.waves * 64 * sizeof(f32x4);
+    if (g.lds > kAcc4sMaxLds || g.gx > 0x7fffffff) return false;
+    *out = g;
+    return true;
+}
+
+bool acc4_stream_planned(bool a_f16, int64_t m, int64_t n, int64_t k, int bs,
+                         Acc4StreamGeom* out) {
+    const char* v = std::getenv("MNB_FORCE_KERNEL");
+    if (v && (!std::strcmp(v, "strip") || !std::strcmp(v, "group"))) return false;
+    return a_f16 && acc4_stream_geometry(m, n, k, bs, out);
+}
+
+bool acc4_stream_aligned(const void* qa, const uint8_t* b, const void* s, const uint8_t* z) {
+    return reinterpret_cast<uintptr_t>(qa) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(s) % 8 == 0 && reinterpret_cast<uintptr_t>(z) % 2 == 0;
+}
+
+hipError_t launch_acc4_stream(const Acc4StreamGeom& g, const int8_t* qa, const float* sa,
+                              const uint8_t* b, const void* s, const uint8_t* z, void* y,
+                              int64_t m, int64_t n, int64_t k, int bs, hipStream_t st) {
+    // the staging covers 16 rows x K exactly with 2R pieces per thread: waves * R == K / 128
+    Acc4StreamGeom want{};
+    if (!acc4_stream_geometry(m, n, k, bs, &want) || want.r != g.r || want.waves != g.waves ||
+        want.gx != g.gx || want.lds != g.lds || !acc4_stream_aligned(qa, b, s, z))
+        return hipErrorInvalidValue;
+#define MNB_A4S_ZP(BS_)                                                                           \
+    return z ? acc4s_go<BS_, true>(g, qa, sa, b, s, z, y, m, n, k, st)                           \
+             : acc4s_go<BS_, false>(g, qa, sa, b, s, z, y, m, n, k, st)
+    switch (bs) {
+        case 32: MNB_A4S_ZP(32);
+        case 64: MNB_A4S_ZP(64);
+        case 128: MNB_A4S_ZP(128);
+        default: return hipErrorInvalidValue;
+    }
+#undef MNB_A4S_ZP
+}
+
+}  // namespace mnb

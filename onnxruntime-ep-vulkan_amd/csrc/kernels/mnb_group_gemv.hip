@@ -666,31 +666,44 @@ hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* 
     return hipGetLastError();
 }
 
-// accuracy_level = 4 workspace: qa [m][k] int8 | a_scale [m][k/bs] fp32 | split-K partial
-// tiles | split-K counters, each part 256-byte aligned.
+// accuracy_level = 4 workspace: qa [m][k] int8 | a_scale fp32 ([m][k/bs], or block-major over
+// 16 rows) | the row-tiled GEMV's split-K partial tiles | its split-K counters, each part
+// 256-byte aligned (the last two empty when another int8 GEMV is planned).
 namespace {
 struct Acc4Layout {
     size_t qa, sa, part, cnt, total;
-    int64_t nsid;
+    int64_t ncnt;
 };
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-Acc4Layout acc4_layout(const GroupGeom& g, int64_t m, int64_t k, int bs) {
+Acc4Layout acc4_layout(bool a_f16, int64_t m, int64_t n, int64_t k, int bs, GroupGeom* gout,
+                       Acc4StreamGeom* sout, bool* stream, bool* strip) {
     Acc4Layout l{};
     l.qa = 0;
     l.sa = align256((size_t)m * (size_t)k);
     l.part = l.sa + align256((size_t)std::max<int64_t>(m, 16) * (size_t)(k / bs) * sizeof(float));
-    l.nsid = g.gx * g.gy * g.gz;
-    const size_t part_bytes = g.ksplit > 1
-        ? (size_t)l.nsid * g.ksplit * g.mt * 64 * sizeof(f32x4) : 0;
+    size_t part_bytes = 0;
+    *stream = acc4_stream_planned(a_f16, m, n, k, bs, sout);
+    StripGeom sg;
+    *strip = !*stream && a_f16 && m <= 16 && !strip_gemv_forced_off() &&
+             strip_geometry(n, k, 1, m, true, bs, true, &sg);   // zero points: the larger LDS
+    const GroupGeom g = group_geometry(m, n, k, 1, true, bs, true);
+    *gout = g;
+    if (!*stream && !*strip) {
+        const int64_t nsid = g.gx * g.gy * g.gz;
+        part_bytes = g.ksplit > 1 ? (size_t)nsid * g.ksplit * g.mt * 64 * sizeof(f32x4) : 0;
+        l.ncnt = g.ksplit > 1 ? nsid : 0;
+    }
     l.cnt = l.part + align256(part_bytes);
-    l.total = l.cnt + align256((size_t)(g.ksplit > 1 ? l.nsid : 0) * sizeof(int));
+    l.total = l.cnt + align256((size_t)l.ncnt * sizeof(int));
     return l;
 }
 }  // namespace
 
-size_t acc4_workspace_bytes(int64_t m, int64_t n, int64_t k, int bs) {
-    const GroupGeom g = group_geometry(m, n, k, 1, true, bs, true);
-    return acc4_layout(g, m, k, bs).total;
+size_t acc4_workspace_bytes(int64_t m, int64_t n, int64_t k, int bs, bool a_f16) {
+    GroupGeom g;
+    Acc4StreamGeom sg;
+    bool stream, strip;
+    return acc4_layout(a_f16, m, n, k, bs, &g, &sg, &stream, &strip).total;
 }
 
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
@@ -698,31 +711,38 @@ hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* 
                        int bs, void* workspace, hipStream_t st) {
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
-    const GroupGeom g = group_geometry(m, n, k, 1, true, bs, true);
-    const Acc4Layout l = acc4_layout(g, m, k, bs);
-    // fp16 with at most 16 rows: the quantiser's codes and scales (the workspace's first two
-    // parts) feed the strip GEMV.
+    GroupGeom g{};
+    Acc4StreamGeom ag{};
+    bool stream = false, strip = false;
+    const Acc4Layout l = acc4_layout(a_f16, m, n, k, bs, &g, &ag, &stream, &strip);
+    uint8_t* const ws = static_cast<uint8_t*>(workspace);
+    int8_t* const qa = reinterpret_cast<int8_t*>(ws + l.qa);
+    float* const sa = reinterpret_cast<float*>(ws + l.sa);
+    // fp16 with at most 16 rows: the quantiser's codes (quad-interleaved) and scales
+    // (block-major over 16 rows, the workspace's first two parts) feed the strip-per-workgroup
+    // GEMV, or the strip GEMV where that one does not apply
     StripGeom sg;
-    uint8_t* const wsp = static_cast<uint8_t*>(workspace);
-    if (a_f16 && m <= 16 && !strip_gemv_forced_off() &&
-        strip_gemv_aligned(wsp + l.qa, b, s, z, true) &&
-        strip_geometry(n, k, 1, m, true, bs, z != nullptr, &sg)) {
-        uint8_t* ws = wsp;
-        int8_t* qa = reinterpret_cast<int8_t*>(ws + l.qa);
-        float* sa = reinterpret_cast<float*>(ws + l.sa);
-        // block-major scales over 16 rows: an output lane's four rows are one 16-byte load
+    if (stream && acc4_stream_aligned(qa, b, s, z)) {
+        hipError_t e = launch_quantize_a_int8(a, true, qa, sa, nullptr, true, m, k, bs, st,
+                                              nullptr, 0, 16, true);
+        if (e != hipSuccess) return e;
+        return launch_acc4_stream(ag, qa, sa, b, s, z, y, m, n, k, bs, st);
+    }
+    if (stream || strip) {
+        // (the planned kernel, or the fallback of the strip-per-workgroup one for sub-aligned
+        // scales or zero points; the workspace has no split-K room for the row-tiled GEMV)
+        if (!strip_gemv_aligned(qa, b, s, z, true) ||
+            !strip_geometry(n, k, 1, m, true, bs, z != nullptr, &sg))
+            return hipErrorInvalidValue;
         hipError_t e = launch_quantize_a_int8(a, true, qa, sa, nullptr, true, m, k, bs, st,
                                               nullptr, 0, 16, true);
         if (e != hipSuccess) return e;
         return launch_strip_gemv(sg, true, qa, sa, nullptr, nullptr, b, s, z, y, m, n, k, bs, st);
     }
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
-    int8_t* qa = reinterpret_cast<int8_t*>(ws + l.qa);
-    float* sa = reinterpret_cast<float*>(ws + l.sa);
     f32x4* part = g.ksplit > 1 ? reinterpret_cast<f32x4*>(ws + l.part) : nullptr;
     int* cnt = g.ksplit > 1 ? reinterpret_cast<int*>(ws + l.cnt) : nullptr;
     hipError_t e = launch_quantize_a_int8(a, a_f16, qa, sa, nullptr, true, m, k, bs, st, cnt,
-                                          g.ksplit > 1 ? l.nsid : 0);
+                                          l.ncnt);
     if (e != hipSuccess) return e;
     if (a_f16)
         return group_bs<f16, true>(bs, g, qa, sa, nullptr, nullptr, b, s, z, y, m, n, k, part, cnt, st);

@@ -151,7 +151,26 @@ hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* 
                                   int32_t* qsum, bool permuted, int64_t m, int64_t k, int bs,
                                   hipStream_t stream, int* cnt = nullptr, int64_t ncnt = 0,
                                   int64_t scale_rows = 0, bool quads = false);
-size_t acc4_workspace_bytes(int64_t m, int64_t n, int64_t k, int bs);
+size_t acc4_workspace_bytes(int64_t m, int64_t n, int64_t k, int bs, bool a_f16);
+// accuracy_level = 4 at up to 16 fp16 rows (mnb_acc4_stream.hip): one 16-column strip per
+// workgroup over all of K, `waves` wavefronts of r quads each (waves * r == K / 128), the
+// workgroup's partial tiles added in LDS.  K % 128 == 0, (K / bs) % 4 == 0, K up to 8192.
+struct Acc4StreamGeom {
+    int r;               // 128-k quads per wavefront: 1, 2, 4 or 8
+    int waves;           // wavefronts per workgroup, K / (128 r), 1..16
+    int64_t gx;          // workgroups: 16-column strips
+    size_t lds;          // bytes: staged codes and activation scales, partial tiles
+};
+bool acc4_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, Acc4StreamGeom* out);
+// The geometry when the accuracy_level = 4 planner takes this kernel (fp16 A, and no
+// MNB_FORCE_KERNEL=strip or =group asking for the other int8 GEMVs).
+bool acc4_stream_planned(bool a_f16, int64_t m, int64_t n, int64_t k, int bs,
+                         Acc4StreamGeom* out);
+// Codes and B 16-byte, scales 8-byte, zero points 2-byte aligned.
+bool acc4_stream_aligned(const void* qa, const uint8_t* b, const void* s, const uint8_t* z);
+hipError_t launch_acc4_stream(const Acc4StreamGeom& g, const int8_t* qa, const float* a_scale,
+                              const uint8_t* b, const void* s, const uint8_t* z, void* y,
+                              int64_t m, int64_t n, int64_t k, int bs, hipStream_t stream);
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                        int bs, void* workspace, hipStream_t stream);

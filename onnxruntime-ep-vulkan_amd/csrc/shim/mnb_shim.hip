@@ -145,16 +145,27 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
                         "accuracy_level 4 is implemented for bits = 4, block_size >= 32 and "
                         "K %% 32 == 0 (got bits = %d, block_size = %d, K = %lld)",
                         p->bits, p->block_size, (long long)p->k);
-        const mnb::GroupGeom g =
-            mnb::group_geometry(p->m, p->n, p->k, 1, true, p->block_size, true);
+        const bool f16 = p->dtype == MNB_DTYPE_F16;
         out->kernel = MNB_KERNEL_ACC4_I8;
-        out->waves_per_group = g.waves;
         out->tile_n = 16;
-        out->tile_m = 16 * g.mt;
-        out->grid_x = g.gx * g.ksplit;
-        out->grid_y = g.gz;
+        mnb::Acc4StreamGeom ag{};
+        if (mnb::acc4_stream_planned(f16, p->m, p->n, p->k, p->block_size, &ag)) {
+            // up to 16 rows: one 16-column strip per workgroup over all of K
+            out->kernel = MNB_KERNEL_ACC4_STREAM;
+            out->waves_per_group = ag.waves;
+            out->tile_m = 16;
+            out->grid_x = ag.gx;
+            out->grid_y = 1;
+        } else {
+            const mnb::GroupGeom g =
+                mnb::group_geometry(p->m, p->n, p->k, 1, true, p->block_size, true);
+            out->waves_per_group = g.waves;
+            out->tile_m = 16 * g.mt;
+            out->grid_x = g.gx * g.ksplit;
+            out->grid_y = g.gz;
+        }
         out->workspace_bytes =
-            (int64_t)mnb::acc4_workspace_bytes(p->m, p->n, p->k, p->block_size);
+            (int64_t)mnb::acc4_workspace_bytes(p->m, p->n, p->k, p->block_size, f16);
         return MNB_OK;
     }
     const bool f16 = p->dtype == MNB_DTYPE_F16;
@@ -274,7 +285,7 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
         (!aligned(scales, 4) || !aligned(zero_points, 4) ||
          !mnb::gemm_supported(p->m, p->n, p->k, p->bits, p->block_size, zero_points != nullptr)))
         kern = MNB_KERNEL_GROUP_MFMA;
-    if (kern == MNB_KERNEL_ACC4_I8) {
+    if (kern == MNB_KERNEL_ACC4_I8 || kern == MNB_KERNEL_ACC4_STREAM) {
         // the int8 path reads B in 16-byte units and stages its own aligned copy of A
         if (!aligned(b, 16) || !aligned(workspace, 256))
             return fail(MNB_ERR_INVALID, "accuracy_level 4 needs B 16-byte and the workspace "
@@ -369,7 +380,8 @@ int mnb_matmul_nbits_noalloc(const mnb_problem* p, const void* a, const uint8_t*
     const size_t need = (size_t)info.workspace_bytes;
     // accuracy_level 4 needs its workspace; the prefill GEMM's is optional (without it the GEMM
     // runs unsplit along K)
-    if (info.kernel == MNB_KERNEL_ACC4_I8 && need > kScratchBytes)
+    if ((info.kernel == MNB_KERNEL_ACC4_I8 || info.kernel == MNB_KERNEL_ACC4_STREAM) &&
+        need > kScratchBytes)
         return fail(MNB_ERR_UNSUPPORTED, "accuracy_level 4 at M = %lld, N = %lld, K = %lld needs "
                     "%zu bytes of scratch; the allocation-free entry point holds %zu (call "
                     "mnb_matmul_nbits with a workspace instead)", (long long)p->m,

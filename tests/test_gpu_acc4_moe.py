@@ -121,7 +121,9 @@ def test_accuracy_level_4(cuda, M, N, K, bs, zp):
     import torch
     inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=20260801 + M)
     print(f"[gpu] acc4 M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
-    assert mnb.plan(mnb.problem(M, N, K, 4, bs, zp, mnb.DTYPE_F16, 4)).kernel == mnb.KERNEL_ACC4_I8
+    kern = mnb.plan(mnb.problem(M, N, K, 4, bs, zp, mnb.DTYPE_F16, 4)).kernel
+    # up to 16 rows the strip-per-workgroup int8 GEMV takes the shapes it supports
+    assert kern == mnb.KERNEL_ACC4_I8 or (M <= 16 and kern == mnb.KERNEL_ACC4_STREAM)
     y = mnb.matmul_nbits(_dev(inp["A"], cuda), _dev(inp["B"], cuda), _dev(inp["scales"], cuda),
                          _dev(inp["zp"], cuda), N, K, 4, bs, accuracy_level=4)
     torch.cuda.synchronize()
@@ -139,25 +141,37 @@ def test_accuracy_level_4(cuda, M, N, K, bs, zp):
 
 
 def test_accuracy_level_4_split_k_reuses_workspace(cuda):
-    # The K-split int8 GEMV hands partial tiles between workgroups through the workspace and a
-    # counter per strip that the quantiser clears: three calls on one workspace (inputs x, y, x)
-    # must each match the level-4 definition, and the first and third must be bit-identical.
+    # The row-tiled int8 GEMV (MNB_FORCE_KERNEL=group) hands partial tiles between workgroups
+    # through the workspace and a counter per strip that the quantiser clears: three calls on one
+    # workspace (inputs x, y, x) must each match the level-4 definition, and the first and third
+    # must be bit-identical.
     import mnb
+    import os
     import torch
     M, N, K, bs = 1, 256, 8192, 32
-    assert mnb.plan(mnb.problem(M, N, K, 4, bs, True, mnb.DTYPE_F16, 4)).grid_x > (N + 15) // 16
-    ins = [orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=True, seed=s) for s in (5, 6)]
-    ws = torch.zeros(mnb.workspace_bytes(mnb.problem(M, N, K, 4, bs, True, mnb.DTYPE_F16, 4)),
-                     dtype=torch.uint8, device=cuda)
-    outs = []
-    for inp in (ins[0], ins[1], ins[0]):
-        t = [_dev(inp[k], cuda) for k in ("A", "B", "scales", "zp")]
-        y = mnb.matmul_nbits(*t, N, K, 4, bs, accuracy_level=4, workspace=ws)
-        torch.cuda.synchronize()
-        y = y.cpu().numpy()
-        _check(y, orc.matmul_nbits_acc4(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs),
-               "acc4 split-K")
-        outs.append(y)
+    print("[gpu] acc4 split-K workspace reuse (row-tiled GEMV)", flush=True)
+    old = os.environ.get("MNB_FORCE_KERNEL")
+    os.environ["MNB_FORCE_KERNEL"] = "group"
+    try:
+        prob = mnb.problem(M, N, K, 4, bs, True, mnb.DTYPE_F16, 4)
+        info = mnb.plan(prob)
+        assert info.kernel == mnb.KERNEL_ACC4_I8 and info.grid_x > (N + 15) // 16
+        ins = [orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=True, seed=s) for s in (5, 6)]
+        ws = torch.zeros(mnb.workspace_bytes(prob), dtype=torch.uint8, device=cuda)
+        outs = []
+        for inp in (ins[0], ins[1], ins[0]):
+            t = [_dev(inp[k], cuda) for k in ("A", "B", "scales", "zp")]
+            y = mnb.matmul_nbits(*t, N, K, 4, bs, accuracy_level=4, workspace=ws)
+            torch.cuda.synchronize()
+            y = y.cpu().numpy()
+            _check(y, orc.matmul_nbits_acc4(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4,
+                                            bs), "acc4 split-K")
+            outs.append(y)
+    finally:
+        if old is None:
+            os.environ.pop("MNB_FORCE_KERNEL", None)
+        else:
+            os.environ["MNB_FORCE_KERNEL"] = old
     assert np.array_equal(outs[0].view(np.uint16), outs[2].view(np.uint16))
 
 

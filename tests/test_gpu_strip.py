@@ -151,14 +151,26 @@ def test_strip_moe_uneven_experts(cuda, N, K, bs, zp):
 ])
 def test_strip_accuracy_level_4(cuda, M, N, K, bs, zp):
     import mnb
+    import os
     import torch
     print(f"[gpu] strip acc4 M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
     inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=900 + M)
     # an all-zero activation block and a tiny value exercise the quantiser's edge cases
     inp["A"][0, :bs] = 0
     inp["A"][M - 1, 5] = np.float16(1e-3)
-    y = mnb.matmul_nbits(_dev(inp["A"], cuda), _dev(inp["B"], cuda), _dev(inp["scales"], cuda),
-                         _dev(inp["zp"], cuda), N, K, 4, bs, accuracy_level=4)
-    torch.cuda.synchronize()
+    # MNB_FORCE_KERNEL=strip: the strip GEMV instead of the strip-per-wavefront int8 kernel
+    old = os.environ.get("MNB_FORCE_KERNEL")
+    os.environ["MNB_FORCE_KERNEL"] = "strip"
+    try:
+        assert mnb.plan(mnb.problem(M, N, K, 4, bs, zp, mnb.DTYPE_F16, 4)).kernel == \
+            mnb.KERNEL_ACC4_I8
+        y = mnb.matmul_nbits(_dev(inp["A"], cuda), _dev(inp["B"], cuda), _dev(inp["scales"], cuda),
+                             _dev(inp["zp"], cuda), N, K, 4, bs, accuracy_level=4)
+        torch.cuda.synchronize()
+    finally:
+        if old is None:
+            os.environ.pop("MNB_FORCE_KERNEL", None)
+        else:
+            os.environ["MNB_FORCE_KERNEL"] = old
     ref4 = orc.matmul_nbits_acc4(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
     _check(y.cpu().numpy(), ref4, "strip acc4 vs level-4 definition")
