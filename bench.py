@@ -684,11 +684,42 @@ def main() -> int:
     dev_us = io_call_us(dA.data_ptr(), 1, dY.data_ptr(), 1)
     torch.cuda.synchronize()
     same = bool(np.array_equal(hY.view(np.uint16), dY.cpu().numpy().view(np.uint16)))
+
+    # Stream-aware Compute (the EP's OrtSyncStreamImpl: an async session per ORT stream): calls
+    # with device tensors return once enqueued; the wall clock of `reps` calls plus the one
+    # synchronisation at the end of the run, per call.
+    ssess = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(ssess)))
+    mnb.check(lib.mnb_session_set_async(ssess, 1))
+    dY2 = torch.empty_like(dY)
+
+    def stream_call_us(reps=300):
+        for _ in range(20):
+            mnb.check(lib.mnb_session_run(ssess, qw, 1, dA.data_ptr(), 1, dY2.data_ptr(), 1))
+        mnb.check(lib.mnb_session_synchronize(ssess))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            mnb.check(lib.mnb_session_run(ssess, qw, 1, dA.data_ptr(), 1, dY2.data_ptr(), 1))
+        t1 = time.perf_counter()
+        mnb.check(lib.mnb_session_synchronize(ssess))
+        t2 = time.perf_counter()
+        return (t2 - t0) / reps * 1e6, (t1 - t0) / reps * 1e6
+
+    stream_us, enqueue_us = stream_call_us()
+    same_stream = bool(np.array_equal(dY2.cpu().numpy().view(np.uint16),
+                                      dY.cpu().numpy().view(np.uint16)))
+    lib.mnb_session_destroy(ssess)
     lib.mnb_weights_release(qw)
     lib.mnb_session_destroy(sess)
     session_io = {"node": f"{LAYER[0][0]} M=1 K={qk} N={qn}", "host_io_us": round(host_us, 2),
                   "device_io_us": round(dev_us, 2), "outputs_identical": same,
-                  "note": "median wall clock of one synchronous EP Compute call (mnb_session_run)"}
+                  "device_io_stream_us": round(stream_us, 2),
+                  "device_io_stream_enqueue_us": round(enqueue_us, 2),
+                  "stream_outputs_identical": same_stream,
+                  "note": "host_io_us / device_io_us: median wall clock of one synchronous EP "
+                          "Compute call (mnb_session_run); device_io_stream_us: stream-aware "
+                          "Compute (async session, device tensors), wall clock per call over 300 "
+                          "calls plus the run-end synchronisation; _enqueue_us: the calls alone"}
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
 

@@ -274,6 +274,25 @@ int mnb_session_destroy(mnb_session* s);
 /* The session's hipStream_t (as void*). */
 void* mnb_session_stream(mnb_session* s);
 int mnb_session_synchronize(mnb_session* s);
+/* Async mode (off by default): a session call whose tensors all live in the session device's
+ * memory returns once its work is enqueued on the session's stream, without waiting for it;
+ * calls with a host tensor still return after the stream has finished.  Stream-ordered work
+ * that follows sees the results; the host sees them after mnb_session_synchronize or an event.
+ * Backs the EP's OrtSyncStreamImpl: ORT's stream-aware EPs enqueue Compute on the stream ORT
+ * hands them (onnxruntime_ep_c_api.h OrtSyncStreamImpl, OrtEpFactory::IsStreamAware /
+ * CreateSyncStreamForDevice); the reference declines streams (rust/src/factory.rs:1268-1280). */
+int mnb_session_set_async(mnb_session* s, int enabled);
+
+/* Streams and events for the EP's OrtSyncStreamImpl / OrtSyncNotificationImpl (hipStream_t and
+ * hipEvent_t as void*; events are created without timing).  No counterpart in the reference,
+ * which has no streams. */
+int mnb_stream_synchronize(int device_index, void* stream);
+int mnb_device_synchronize(int device_index);
+int mnb_event_create(int device_index, void** event);
+int mnb_event_destroy(void* event);
+int mnb_event_record(void* event, void* stream);        /* event completes after prior work */
+int mnb_stream_wait_event(void* stream, void* event);   /* later work on stream waits for it */
+int mnb_event_synchronize(void* event);                 /* host waits for it */
 
 /* Uploads one node's constant inputs to HBM (hipMalloc + copy), once.  Byte sizes are checked
  * against the problem's layout.  zero_points may be NULL (implied zero point). */
@@ -292,6 +311,10 @@ int mnb_weights_release(mnb_weights* w);
 int mnb_device_malloc(int device_index, size_t bytes, void** out);
 int mnb_device_free(int device_index, void* p);
 int mnb_memcpy(int device_index, void* dst, const void* src, size_t bytes, int kind);
+/* The same copy ordered on `stream` (a hipStream_t): device-to-device copies return once
+ * enqueued, copies that touch host memory once complete. */
+int mnb_memcpy_on_stream(int device_index, void* dst, const void* src, size_t bytes, int kind,
+                         void* stream);
 
 /* Compute with device-resident A and Y (stream-ordered on the session stream, no sync). */
 int mnb_session_run_device(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_dev,

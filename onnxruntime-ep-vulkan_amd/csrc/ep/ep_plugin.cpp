@@ -529,6 +529,66 @@ int32_t tensor_elem_type(const OrtApi* api, const OrtValue* v, std::vector<int64
     return (int32_t)et;
 }
 
+// ---- streams (device-memory mode) -------------------------------------------------------------
+// ORT's stream-aware EP contract (onnxruntime_ep_c_api.h: OrtEpFactory::IsStreamAware and
+// CreateSyncStreamForDevice, OrtSyncStreamImpl, OrtSyncNotificationImpl).  Each ORT stream on an
+// MI355X device is an async mnb_session of its own -- a hipStream_t with its own staging buffers
+// and workspace -- so Compute calls on different ORT streams share no buffer.  Compute enqueues
+// on the stream of its kernel context and returns without waiting when its tensors are in HBM;
+// ORT orders streams through notifications (hipEvents) and the run's end synchronises.  The
+// reference declines streams (rust/src/factory.rs:1268-1280: IsStreamAware false,
+// CreateSyncStreamForDevice null), so every one of its Computes waits for the GPU.
+struct SyncStream {
+    OrtSyncStreamImpl base;         // first member
+    Factory* factory = nullptr;
+    int device = 0;
+    mnb_session* session = nullptr;
+};
+
+struct SyncNote {
+    OrtSyncNotificationImpl base;   // first member
+    SyncStream* producer = nullptr;
+    void* event = nullptr;          // hipEvent_t
+};
+
+std::mutex g_stream_mu;
+std::map<void*, SyncStream*> g_streams;   // hipStream_t of each live SyncStream
+
+SyncStream* stream_of_handle(void* h) {
+    if (!h) return nullptr;
+    std::lock_guard<std::mutex> lk(g_stream_mu);
+    auto it = g_streams.find(h);
+    return it == g_streams.end() ? nullptr : it->second;
+}
+
+bool any_streams() {
+    std::lock_guard<std::mutex> lk(g_stream_mu);
+    return !g_streams.empty();
+}
+
+// The hipStream_t behind an ORT stream, when it is one of this EP's, else null.
+void* our_stream_handle(const OrtApi* api, OrtSyncStream* st) {
+    if (!st || !api->SyncStream_GetHandle) return nullptr;
+    void* h = api->SyncStream_GetHandle(st);
+    return stream_of_handle(h) ? h : nullptr;
+}
+
+// The session a Compute runs on: the async session of the ORT stream in its kernel context
+// (stream-aware mode), else the EP's own synchronous session.
+mnb_session* compute_session(Ep* ep, OrtKernelContext* ctx) {
+    if (ep->memory_device && ep->api->KernelContext_GetGPUComputeStream) {
+        void* h = nullptr;
+        OrtStatus* st = ep->api->KernelContext_GetGPUComputeStream(ctx, &h);
+        if (st) {
+            ep->api->ReleaseStatus(st);
+            h = nullptr;
+        }
+        SyncStream* ss = stream_of_handle(h);
+        if (ss && ss->device == ep->device) return ss->session;
+    }
+    return ep->session;
+}
+
 // Whether a tensor lives in this EP's HBM (device-memory mode), checking the device ordinal.
 bool on_our_device(Ep* ep, const OrtValue* v) {
     if (!ep->memory_device || !v) return false;
@@ -574,7 +634,7 @@ void compute_qmoe(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     ORT_OK(api, GetTensorMutableData(y, &ydata));
     const bool x_dev = on_our_device(ep, x), r_dev = on_our_device(ep, r), y_dev = on_our_device(ep, y);
     std::lock_guard<std::mutex> lk(k.mu);
-    mnb_ok(mnb_session_run_qmoe(ep->session, k.qweights, rows, tensor_data(api, x), x_dev ? 1 : 0,
+    mnb_ok(mnb_session_run_qmoe(compute_session(ep, ctx), k.qweights, rows, tensor_data(api, x), x_dev ? 1 : 0,
                                 tensor_data(api, r), r_dev ? 1 : 0, ydata, y_dev ? 1 : 0),
            "QMoE kernels");
     g_compute_count.fetch_add(1);
@@ -615,7 +675,7 @@ void compute_norm(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     ORT_OK(api, GetTensorMutableData(y, &yd));
     if (sum) ORT_OK(api, GetTensorMutableData(sum, &sd));
     std::lock_guard<std::mutex> lk(k.mu);
-    mnb_ok(mnb_session_run_rmsnorm(ep->session, k.nweights, rows, tensor_data(api, x),
+    mnb_ok(mnb_session_run_rmsnorm(compute_session(ep, ctx), k.nweights, rows, tensor_data(api, x),
                                    on_our_device(ep, x) ? 1 : 0, sk ? tensor_data(api, sk) : nullptr,
                                    on_our_device(ep, sk) ? 1 : 0, yd, on_our_device(ep, y) ? 1 : 0,
                                    sd, on_our_device(ep, sum) ? 1 : 0),
@@ -694,7 +754,7 @@ void compute_gqa(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
         if (on_our_device(ep, in[4])) flags |= MNB_GQA_ON_DEVICE_CACHES;
     }
     std::lock_guard<std::mutex> lk(k.mu);
-    mnb_ok(mnb_session_run_gqa(ep->session, k.gcaches, &p, tensor_data(api, in[0]),
+    mnb_ok(mnb_session_run_gqa(compute_session(ep, ctx), k.gcaches, &p, tensor_data(api, in[0]),
                                tensor_data(api, in[1]), tensor_data(api, in[2]),
                                static_cast<const int32_t*>(tensor_data(api, in[3])),
                                in[4] ? tensor_data(api, in[4]) : nullptr,
@@ -758,8 +818,12 @@ void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
     }
 
     std::lock_guard<std::mutex> lk(k.mu);
+    mnb_session* sess = compute_session(ep, ctx);
     if (!k.resident) {
-        // Weights that are not constant initializers arrive with every call: upload them.
+        // Weights that are not constant initializers arrive with every call: upload them.  The
+        // stream first finishes what it has enqueued (an earlier node may write a weight input,
+        // and the previous upload may still be read).
+        if (sess != ep->session) mnb_ok(mnb_session_synchronize(sess), "draining the stream");
         const void* host[3] = {nullptr, nullptr, nullptr};
         size_t bytes[3] = {0, 0, 0};
         std::vector<uint8_t> staged[3];
@@ -788,7 +852,7 @@ void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
                                   host[2], bytes[2], &k.weights),
                "uploading MatMulNBits weights");
     }
-    mnb_ok(mnb_session_run(ep->session, k.weights, m, adata, a_dev ? 1 : 0, ydata, y_dev ? 1 : 0),
+    mnb_ok(mnb_session_run(sess, k.weights, m, adata, a_dev ? 1 : 0, ydata, y_dev ? 1 : 0),
            "MatMulNBits kernel");
     g_compute_count.fetch_add(1);
 }
@@ -1244,7 +1308,11 @@ const char* ORT_API_CALL f_get_name(const OrtEpFactory*) noexcept { return kEpNa
 const char* ORT_API_CALL f_get_vendor(const OrtEpFactory*) noexcept { return kEpVendor; }
 uint32_t ORT_API_CALL f_get_vendor_id(const OrtEpFactory*) noexcept { return kAmdVendorId; }
 const char* ORT_API_CALL f_get_version(const OrtEpFactory*) noexcept { return kEpVersion; }
-bool ORT_API_CALL f_is_stream_aware(const OrtEpFactory*) noexcept { return false; }
+// Stream-aware in device-memory mode (host I/O has no streams to share).
+bool ORT_API_CALL f_is_stream_aware(const OrtEpFactory* self) noexcept {
+    const Factory* f = as_factory(self);
+    return f && f->device_memory;
+}
 
 // HIP devices this library can run on (gfx950), in HIP ordinal order.
 std::vector<int> usable_hip_devices() {
@@ -1444,7 +1512,7 @@ bool ORT_API_CALL dt_can_copy(const OrtDataTransferImpl* self, const OrtMemoryDe
 }
 
 OrtStatus* ORT_API_CALL dt_copy(OrtDataTransferImpl* self, const OrtValue** src, OrtValue** dst,
-                                OrtSyncStream**, size_t n) noexcept {
+                                OrtSyncStream** streams, size_t n) noexcept {
     auto* t = reinterpret_cast<DataTransfer*>(self);
     const OrtApi* api = t ? t->factory->api : nullptr;
     return guarded(api, "CopyTensors", [&] {
@@ -1462,7 +1530,17 @@ OrtStatus* ORT_API_CALL dt_copy(OrtDataTransferImpl* self, const OrtValue** src,
             const void* sp = tensor_data(api, src[i]);
             const int kind = s_hbm && d_hbm ? MNB_COPY_DEVICE_TO_DEVICE
                                             : (s_hbm ? MNB_COPY_DEVICE_TO_HOST : MNB_COPY_HOST_TO_DEVICE);
-            mnb_ok(mnb_memcpy(d_hbm ? dd : sd, dp, sp, sb, kind), "tensor copy");
+            const int dev = d_hbm ? dd : sd;
+            void* h = our_stream_handle(api, streams ? streams[i] : nullptr);
+            if (h) {
+                // ordered on the ORT stream: after the kernels that produced the source
+                mnb_ok(mnb_memcpy_on_stream(dev, dp, sp, sb, kind, h), "tensor copy");
+                continue;
+            }
+            // no stream: after everything enqueued on this EP's streams (they do not order
+            // with the synchronous copy)
+            if (any_streams()) mnb_ok(mnb_device_synchronize(dev), "draining the EP's streams");
+            mnb_ok(mnb_memcpy(dev, dp, sp, sb, kind), "tensor copy");
         }
     });
 }
@@ -1483,10 +1561,122 @@ OrtStatus* ORT_API_CALL f_create_data_transfer(OrtEpFactory* self, OrtDataTransf
     });
 }
 
-OrtStatus* ORT_API_CALL f_create_sync_stream(OrtEpFactory*, const OrtMemoryDevice*,
+void ORT_API_CALL sn_release(OrtSyncNotificationImpl* self) noexcept {
+    auto* n = reinterpret_cast<SyncNote*>(self);
+    if (!n) return;
+    (void)mnb_event_destroy(n->event);
+    delete n;
+}
+
+OrtStatus* ORT_API_CALL sn_activate(OrtSyncNotificationImpl* self) noexcept {
+    auto* n = reinterpret_cast<SyncNote*>(self);
+    const OrtApi* api = n ? n->producer->factory->api : nullptr;
+    return guarded(api, "Notification::Activate", [&] {
+        if (!n) fail(ORT_INVALID_ARGUMENT, "null notification");
+        mnb_ok(mnb_event_record(n->event, mnb_session_stream(n->producer->session)),
+               "recording the notification");
+    });
+}
+
+OrtStatus* ORT_API_CALL sn_wait_on_device(OrtSyncNotificationImpl* self,
+                                          OrtSyncStream* consumer) noexcept {
+    auto* n = reinterpret_cast<SyncNote*>(self);
+    const OrtApi* api = n ? n->producer->factory->api : nullptr;
+    return guarded(api, "Notification::WaitOnDevice", [&] {
+        if (!n) fail(ORT_INVALID_ARGUMENT, "null notification");
+        void* h = our_stream_handle(api, consumer);
+        if (h)
+            mnb_ok(mnb_stream_wait_event(h, n->event), "stream wait on the notification");
+        else                        // another EP's stream: wait on the host instead
+            mnb_ok(mnb_event_synchronize(n->event), "host wait on the notification");
+    });
+}
+
+OrtStatus* ORT_API_CALL sn_wait_on_host(OrtSyncNotificationImpl* self) noexcept {
+    auto* n = reinterpret_cast<SyncNote*>(self);
+    const OrtApi* api = n ? n->producer->factory->api : nullptr;
+    return guarded(api, "Notification::WaitOnHost", [&] {
+        if (!n) fail(ORT_INVALID_ARGUMENT, "null notification");
+        mnb_ok(mnb_event_synchronize(n->event), "host wait on the notification");
+    });
+}
+
+void ORT_API_CALL ss_release(OrtSyncStreamImpl* self) noexcept {
+    auto* ss = reinterpret_cast<SyncStream*>(self);
+    if (!ss) return;
+    {
+        std::lock_guard<std::mutex> lk(g_stream_mu);
+        g_streams.erase(mnb_session_stream(ss->session));
+    }
+    (void)mnb_session_destroy(ss->session);      // drains the stream first
+    delete ss;
+}
+
+void* ORT_API_CALL ss_get_handle(OrtSyncStreamImpl* self) noexcept {
+    auto* ss = reinterpret_cast<SyncStream*>(self);
+    return ss ? mnb_session_stream(ss->session) : nullptr;
+}
+
+OrtStatus* ORT_API_CALL ss_create_notification(OrtSyncStreamImpl* self,
+                                               OrtSyncNotificationImpl** out) noexcept {
+    if (out) *out = nullptr;
+    auto* ss = reinterpret_cast<SyncStream*>(self);
+    return guarded(ss ? ss->factory->api : nullptr, "CreateNotification", [&] {
+        if (!ss || !out) fail(ORT_INVALID_ARGUMENT, "null CreateNotification argument");
+        auto n = std::make_unique<SyncNote>();
+        std::memset(&n->base, 0, sizeof(n->base));
+        n->base.ort_version_supported = ss->factory->version;
+        n->base.Release = sn_release;
+        n->base.Activate = sn_activate;
+        n->base.WaitOnDevice = sn_wait_on_device;
+        n->base.WaitOnHost = sn_wait_on_host;
+        n->producer = ss;
+        mnb_ok(mnb_event_create(ss->device, &n->event), "creating a notification event");
+        *out = &n.release()->base;
+    });
+}
+
+// HIP streams need no flush: work is submitted as it is enqueued.
+OrtStatus* ORT_API_CALL ss_flush(OrtSyncStreamImpl*) noexcept { return nullptr; }
+
+// The end of a run: the stream's work is complete (and its errors reported) before Run returns.
+OrtStatus* ORT_API_CALL ss_on_session_run_end(OrtSyncStreamImpl* self) noexcept {
+    auto* ss = reinterpret_cast<SyncStream*>(self);
+    return guarded(ss ? ss->factory->api : nullptr, "OnSessionRunEnd", [&] {
+        if (ss) mnb_ok(mnb_session_synchronize(ss->session), "finishing the run's GPU work");
+    });
+}
+
+OrtStatus* ORT_API_CALL f_create_sync_stream(OrtEpFactory* self, const OrtMemoryDevice* md,
                                              const OrtKeyValuePairs*, OrtSyncStreamImpl** out) noexcept {
     if (out) *out = nullptr;
-    return nullptr;
+    Factory* f = as_factory(self);
+    return guarded(f ? f->api : nullptr, "CreateSyncStreamForDevice", [&] {
+        if (!f || !out || !f->device_memory) return;     // host I/O: no streams
+        int device = -1;
+        if (!is_our_hbm(f->ep_api, md, &device)) return; // not this EP's memory: no stream
+        auto ss = std::make_unique<SyncStream>();
+        std::memset(&ss->base, 0, sizeof(ss->base));
+        ss->base.ort_version_supported = f->version;
+        ss->base.Release = ss_release;
+        ss->base.GetHandle = ss_get_handle;
+        ss->base.CreateNotification = ss_create_notification;
+        ss->base.Flush = ss_flush;
+        ss->base.OnSessionRunEnd = ss_on_session_run_end;
+        ss->factory = f;
+        ss->device = device;
+        mnb_ok(mnb_session_create(device, &ss->session), "opening a HIP stream");
+        const int rc = mnb_session_set_async(ss->session, 1);
+        if (rc) {
+            (void)mnb_session_destroy(ss->session);
+            mnb_ok(rc, "async session");
+        }
+        {
+            std::lock_guard<std::mutex> lk(g_stream_mu);
+            g_streams[mnb_session_stream(ss->session)] = ss.get();
+        }
+        *out = &ss.release()->base;
+    });
 }
 
 // ---- ABI negotiation --------------------------------------------------------------------------

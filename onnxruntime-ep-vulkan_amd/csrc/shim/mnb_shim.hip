@@ -707,6 +707,7 @@ int mnb_gqa(const mnb_gqa_problem* p, const void* packed_qkv, const void* past_k
 struct mnb_session {
     int device = 0;
     hipStream_t stream = nullptr;
+    bool async = false;             // device-only calls return once enqueued
     std::mutex mu;
     void* a_dev = nullptr;
     size_t a_cap = 0;
@@ -828,6 +829,82 @@ int mnb_session_synchronize(mnb_session* s) {
     return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
+int mnb_session_set_async(mnb_session* s, int enabled) {
+    if (!s) return fail(MNB_ERR_INVALID, "session is NULL");
+    std::lock_guard<std::mutex> lk(s->mu);
+    s->async = enabled != 0;
+    return MNB_OK;
+}
+
+int mnb_memcpy_on_stream(int device_index, void* dst, const void* src, size_t bytes, int kind,
+                         void* stream) {
+    if (bytes == 0) return MNB_OK;
+    if (!dst || !src) return fail(MNB_ERR_INVALID, "a NULL copy pointer was passed");
+    hipMemcpyKind k;
+    switch (kind) {
+        case MNB_COPY_HOST_TO_DEVICE: k = hipMemcpyHostToDevice; break;
+        case MNB_COPY_DEVICE_TO_HOST: k = hipMemcpyDeviceToHost; break;
+        case MNB_COPY_DEVICE_TO_DEVICE: k = hipMemcpyDeviceToDevice; break;
+        default: return fail(MNB_ERR_INVALID, "copy kind %d", kind);
+    }
+    hipError_t e = hipSetDevice(device_index);
+    if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    e = hipMemcpyAsync(dst, src, bytes, k, st);
+    // host memory involved: complete before returning (the caller may reuse or read it)
+    if (e == hipSuccess && kind != MNB_COPY_DEVICE_TO_DEVICE) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipMemcpyAsync");
+}
+
+int mnb_stream_synchronize(int device_index, void* stream) {
+    hipError_t e = hipSetDevice(device_index);
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int mnb_device_synchronize(int device_index) {
+    hipError_t e = hipSetDevice(device_index);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipDeviceSynchronize");
+}
+
+int mnb_event_create(int device_index, void** event) {
+    if (!event) return fail(MNB_ERR_INVALID, "event is NULL");
+    *event = nullptr;
+    hipError_t e = hipSetDevice(device_index);
+    hipEvent_t ev = nullptr;
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags");
+    *event = ev;
+    return MNB_OK;
+}
+
+int mnb_event_destroy(void* event) {
+    if (!event) return MNB_OK;
+    const hipError_t e = hipEventDestroy(static_cast<hipEvent_t>(event));
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipEventDestroy");
+}
+
+int mnb_event_record(void* event, void* stream) {
+    if (!event) return fail(MNB_ERR_INVALID, "event is NULL");
+    const hipError_t e =
+        hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipEventRecord");
+}
+
+int mnb_stream_wait_event(void* stream, void* event) {
+    if (!event) return fail(MNB_ERR_INVALID, "event is NULL");
+    const hipError_t e =
+        hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event), 0);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamWaitEvent");
+}
+
+int mnb_event_synchronize(void* event) {
+    if (!event) return fail(MNB_ERR_INVALID, "event is NULL");
+    const hipError_t e = hipEventSynchronize(static_cast<hipEvent_t>(event));
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipEventSynchronize");
+}
+
 static int grow(void** p, size_t* cap, size_t need) {
     if (need <= *cap) return MNB_OK;
     if (*p) (void)hipFree(*p);
@@ -840,6 +917,25 @@ static int grow(void** p, size_t* cap, size_t need) {
     }
     *cap = need;
     return MNB_OK;
+}
+
+// A session buffer of at least `need` bytes.  In async mode, work already enqueued on the
+// session's stream may still use the old buffer: the stream is drained before it is freed.
+static int sgrow(mnb_session* s, void** p, size_t* cap, size_t need) {
+    if (need <= *cap) return MNB_OK;
+    if (s->async && *p) {
+        const hipError_t e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    }
+    return grow(p, cap, need);
+}
+
+// The end of a session call: host synchronisation, except for async sessions whose call read
+// and wrote device memory only (host tensors must be complete when the call returns).
+static int finish(mnb_session* s, bool host_io) {
+    if (s->async && !host_io) return MNB_OK;
+    const hipError_t e = hipStreamSynchronize(s->stream);
+    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
 int mnb_weights_upload(mnb_session* s, const mnb_problem* node, const void* b_host,
@@ -907,7 +1003,7 @@ static int run_locked(mnb_session* s, const mnb_weights* w, int64_t m, const voi
     int rc = mnb_workspace_bytes(&p, &ws);
     if (rc) return rc;
     if (ws) {
-        rc = grow(&s->ws, &s->ws_cap, ws);
+        rc = sgrow(s, &s->ws, &s->ws_cap, ws);
         if (rc) return rc;
     }
     return mnb_matmul_nbits(&p, a_dev, w->b, w->scales, w->zp, y_dev, s->ws, s->ws_cap,
@@ -937,14 +1033,14 @@ int mnb_session_run(mnb_session* s, const mnb_weights* w, int64_t m, const void*
     void* y_dev = y;
     int rc;
     if (!a_on_device) {                                  // stage A into HBM
-        rc = grow(&s->a_dev, &s->a_cap, a_bytes);
+        rc = sgrow(s, &s->a_dev, &s->a_cap, a_bytes);
         if (rc) return rc;
         hipError_t e = hipMemcpyAsync(s->a_dev, a, a_bytes, hipMemcpyHostToDevice, s->stream);
         if (e != hipSuccess) return hip_fail(e, "A upload");
         a_dev = s->a_dev;
     }
     if (!y_on_device) {
-        rc = grow(&s->y_dev, &s->y_cap, y_bytes);
+        rc = sgrow(s, &s->y_dev, &s->y_cap, y_bytes);
         if (rc) return rc;
         y_dev = s->y_dev;
     }
@@ -954,9 +1050,7 @@ int mnb_session_run(mnb_session* s, const mnb_weights* w, int64_t m, const void*
         hipError_t e = hipMemcpyAsync(y, s->y_dev, y_bytes, hipMemcpyDeviceToHost, s->stream);
         if (e != hipSuccess) return hip_fail(e, "Y download");
     }
-    hipError_t e = hipStreamSynchronize(s->stream);
-    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    return MNB_OK;
+    return finish(s, !a_on_device || !y_on_device);
 }
 
 struct mnb_qmoe_weights {
@@ -1074,11 +1168,11 @@ int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows
     // one staging buffer for x and the logits, one for y; the workspace after them
     const size_t x_off = 0, l_off = (x_bytes + 255) & ~(size_t)255;
     const size_t stage = l_off + l_bytes;
-    rc = grow(&s->a_dev, &s->a_cap, stage);
+    rc = sgrow(s, &s->a_dev, &s->a_cap, stage);
     if (rc) return rc;
-    rc = grow(&s->y_dev, &s->y_cap, x_bytes);
+    rc = sgrow(s, &s->y_dev, &s->y_cap, x_bytes);
     if (rc) return rc;
-    rc = grow(&s->ws, &s->ws_cap, ws);
+    rc = sgrow(s, &s->ws, &s->ws_cap, ws);
     if (rc) return rc;
     uint8_t* st = static_cast<uint8_t*>(s->a_dev);
     const void* xd = x;
@@ -1102,8 +1196,7 @@ int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows
         e = hipMemcpyAsync(y, s->y_dev, x_bytes, hipMemcpyDeviceToHost, s->stream);
         if (e != hipSuccess) return hip_fail(e, "QMoE output download");
     }
-    e = hipStreamSynchronize(s->stream);
-    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+    return finish(s, !x_on_device || !logits_on_device || !y_on_device);
 }
 
 struct mnb_rmsnorm_weights {
@@ -1178,9 +1271,9 @@ int mnb_session_run_rmsnorm(mnb_session* s, const mnb_rmsnorm_weights* w, int64_
     const size_t bytes = (size_t)rows * (size_t)p.hidden * (size_t)elem_bytes(p.dtype);
     const size_t slot = (bytes + 255) & ~(size_t)255;
     // inputs staged one after the other in the A buffer, outputs in the Y buffer
-    rc = grow(&s->a_dev, &s->a_cap, 2 * slot);
+    rc = sgrow(s, &s->a_dev, &s->a_cap, 2 * slot);
     if (rc) return rc;
-    rc = grow(&s->y_dev, &s->y_cap, 2 * slot);
+    rc = sgrow(s, &s->y_dev, &s->y_cap, 2 * slot);
     if (rc) return rc;
     uint8_t* in = static_cast<uint8_t*>(s->a_dev);
     uint8_t* outb = static_cast<uint8_t*>(s->y_dev);
@@ -1204,8 +1297,8 @@ int mnb_session_run_rmsnorm(mnb_session* s, const mnb_rmsnorm_weights* w, int64_
     if (e == hipSuccess && sum_out && !sum_on_device)
         e = hipMemcpyAsync(sum_out, qd, bytes, hipMemcpyDeviceToHost, s->stream);
     if (e != hipSuccess) return hip_fail(e, "RMSNorm output download");
-    e = hipStreamSynchronize(s->stream);
-    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+    return finish(s, !x_on_device || (p.has_skip && !skip_on_device) || !y_on_device ||
+                         (sum_out && !sum_on_device));
 }
 
 struct mnb_gqa_caches {
@@ -1321,11 +1414,11 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
     const size_t in_total = o_sin + al(cache_b);
     const size_t o_out = 0, o_rk = al(out_b), o_rv = o_rk + al(pres_b);
     const size_t out_total = o_rv + al(pres_b);
-    rc = grow(&s->a_dev, &s->a_cap, in_total);
-    if (!rc) rc = grow(&s->y_dev, &s->y_cap, out_total);
+    rc = sgrow(s, &s->a_dev, &s->a_cap, in_total);
+    if (!rc) rc = sgrow(s, &s->y_dev, &s->y_cap, out_total);
     size_t ws = 0;
     if (!rc) rc = mnb_gqa_workspace_bytes(&p, &ws);
-    if (!rc) rc = grow(&s->ws, &s->ws_cap, ws);
+    if (!rc) rc = sgrow(s, &s->ws, &s->ws_cap, ws);
     if (rc) return rc;
     uint8_t* in = static_cast<uint8_t*>(s->a_dev);
     uint8_t* ob = static_cast<uint8_t*>(s->y_dev);
@@ -1337,6 +1430,9 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
     void* rkd = present_key;
     void* rvd = present_value;
     hipError_t e = hipSuccess;
+    // any host tensor: the call returns only after the stream has finished
+    const bool host_io = !qkv_dev || (p.past_len_max && !past_dev) || !seq_dev || !out_dev ||
+                         (p.present_len && !pres_dev) || (own_caches && !cache_dev);
     auto up = [&](const void* src, size_t off, size_t bytes) -> const void* {
         if (e == hipSuccess && bytes)
             e = hipMemcpyAsync(in + off, src, bytes, hipMemcpyHostToDevice, s->stream);
@@ -1371,8 +1467,7 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
             e = hipMemcpyAsync(present_value, rvd, pres_b, hipMemcpyDeviceToHost, s->stream);
     }
     if (e != hipSuccess) return hip_fail(e, "GroupQueryAttention output download");
-    e = hipStreamSynchronize(s->stream);
-    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+    return finish(s, host_io);
 }
 
 int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,

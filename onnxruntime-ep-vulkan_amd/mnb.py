@@ -24,6 +24,10 @@ MNB_ERR_UNSUPPORTED = 2
 MNB_ERR_HIP = 3
 MNB_ERR_NOMEM = 4
 
+COPY_HOST_TO_DEVICE = 1
+COPY_DEVICE_TO_HOST = 2
+COPY_DEVICE_TO_DEVICE = 3
+
 DTYPE_F16 = 1
 DTYPE_F32 = 2
 
@@ -133,6 +137,15 @@ def load() -> C.CDLL:
         "mnb_session_destroy": (C.c_int, [vp]),
         "mnb_session_stream": (vp, [vp]),
         "mnb_session_synchronize": (C.c_int, [vp]),
+        "mnb_session_set_async": (C.c_int, [vp, C.c_int]),
+        "mnb_memcpy_on_stream": (C.c_int, [C.c_int, vp, vp, C.c_size_t, C.c_int, vp]),
+        "mnb_stream_synchronize": (C.c_int, [C.c_int, vp]),
+        "mnb_device_synchronize": (C.c_int, [C.c_int]),
+        "mnb_event_create": (C.c_int, [C.c_int, C.POINTER(vp)]),
+        "mnb_event_destroy": (C.c_int, [vp]),
+        "mnb_event_record": (C.c_int, [vp, vp]),
+        "mnb_stream_wait_event": (C.c_int, [vp, vp]),
+        "mnb_event_synchronize": (C.c_int, [vp]),
         "mnb_weights_upload": (C.c_int, [vp, C.POINTER(Problem), vp, sz, vp, sz, vp, sz,
                                          C.POINTER(vp)]),
         "mnb_weights_release": (C.c_int, [vp]),

@@ -71,6 +71,11 @@ def lib() -> C.CDLL:
             "mock_device_io_setup": (C.c_int, [C.c_int]),
             "mock_feed_device": (C.c_int, [C.c_char_p, C.c_int, C.c_int, i64p, C.c_void_p,
                                            C.c_size_t]),
+            "mock_is_stream_aware": (C.c_int, []),
+            "mock_stream_setup": (C.c_int, []),
+            "mock_stream_handle": (C.c_void_p, []),
+            "mock_run_end": (C.c_int, []),
+            "mock_notification_roundtrip": (C.c_int, []),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -201,6 +206,23 @@ class Host:
     def device_io_setup(self, i=0) -> int:
         return self.L.mock_device_io_setup(i)
 
+    def is_stream_aware(self) -> int:
+        return lib().mock_is_stream_aware()
+
+    def stream_setup(self) -> int:
+        """ORT's stream set-up for a stream-aware factory (after device_io_setup): 1 when a
+        stream was created, 0 when the factory is not stream-aware."""
+        return lib().mock_stream_setup()
+
+    def stream_handle(self):
+        return lib().mock_stream_handle()
+
+    def run_end(self) -> int:
+        return lib().mock_run_end()
+
+    def notification_roundtrip(self) -> int:
+        return lib().mock_notification_roundtrip()
+
     def compute(self, group=0) -> int:
         return self.L.mock_compute(group)
 
@@ -216,11 +238,14 @@ class Host:
 
 def add_matmul_nbits(h: Host, name: str, inp: dict, N: int, K: int, bits: int, bs: int,
                      a_shape, a_dtype=np.float16, const_weights=True, acc_level=None,
-                     extra_inputs=(), y_name=None):
-    """Adds one MatMulNBits node with inputs from an oracle make_inputs() dict."""
+                     extra_inputs=(), y_name=None, a_name=None):
+    """Adds one MatMulNBits node with inputs from an oracle make_inputs() dict; `a_name` names
+    an existing value (another node's output) as A."""
     el = FLOAT16 if np.dtype(a_dtype) == np.float16 else FLOAT
-    a_name, y_name = f"{name}_A", y_name or f"{name}_Y"
-    h.value(a_name, el, a_shape)
+    if a_name is None:
+        a_name = f"{name}_A"
+        h.value(a_name, el, a_shape)
+    y_name = y_name or f"{name}_Y"
     h.value(y_name, el, tuple(a_shape[:-1]) + (N,))
     ins = [a_name]
     for role, arr, elem in (("B", inp["B"], UINT8), ("scales", inp["scales"], el),

@@ -111,6 +111,11 @@ struct OrtKernelContext {
     std::vector<OrtValue*> inputs;
     std::vector<std::unique_ptr<OrtValue>> outputs;
     std::vector<int32_t> out_elem;
+    void* stream = nullptr;         // the EP stream's native handle (stream-aware EPs)
+};
+// ORT's framework stream wrapping an EP's OrtSyncStreamImpl.
+struct OrtSyncStream {
+    OrtSyncStreamImpl* impl = nullptr;
 };
 struct OrtLogger {};
 struct OrtNodeComputeContext {};
@@ -351,6 +356,15 @@ OrtStatus* ORT_API_CALL m_KernelContext_GetOutput(OrtKernelContext* c, size_t i,
     return nullptr;
 }
 
+OrtStatus* ORT_API_CALL m_KernelContext_GetGPUComputeStream(const OrtKernelContext* c, void** out) NX {
+    *out = c->stream;
+    return nullptr;
+}
+
+void* ORT_API_CALL m_SyncStream_GetHandle(OrtSyncStream* s) NX {
+    return s && s->impl ? s->impl->GetHandle(s->impl) : nullptr;
+}
+
 OrtHardwareDeviceType ORT_API_CALL m_HardwareDevice_Type(const OrtHardwareDevice* d) NX { return d->type; }
 uint32_t ORT_API_CALL m_HardwareDevice_VendorId(const OrtHardwareDevice* d) NX { return d->vendor_id; }
 uint32_t ORT_API_CALL m_HardwareDevice_DeviceId(const OrtHardwareDevice* d) NX { return d->device_id; }
@@ -501,6 +515,8 @@ void init_api() {
     g_api.KernelContext_GetOutputCount = m_KernelContext_GetOutputCount;
     g_api.KernelContext_GetInput = m_KernelContext_GetInput;
     g_api.KernelContext_GetOutput = m_KernelContext_GetOutput;
+    g_api.KernelContext_GetGPUComputeStream = m_KernelContext_GetGPUComputeStream;
+    g_api.SyncStream_GetHandle = m_SyncStream_GetHandle;
     g_api.HardwareDevice_Type = m_HardwareDevice_Type;
     g_api.HardwareDevice_VendorId = m_HardwareDevice_VendorId;
     g_api.HardwareDevice_DeviceId = m_HardwareDevice_DeviceId;
@@ -559,6 +575,8 @@ struct Host {
     OrtAllocator* dev_alloc = nullptr;
     OrtDataTransferImpl* dt = nullptr;
     const OrtMemoryDevice* dev_md = nullptr;
+    // stream-aware EPs: the one stream of the session's device (ORT's default for one device)
+    OrtSyncStream stream;
 };
 Host* g = nullptr;
 
@@ -880,8 +898,11 @@ int mock_compute(int i) {
     std::vector<std::unique_ptr<OrtValue>> init_vals;
     for (OrtValueInfo* v : gr.fused->inputs) {
         auto it = g->feeds.find(v->name);
+        auto ft = g->fetches.find(v->name);     // an earlier island's output, where it lives
         if (it != g->feeds.end()) {
             ctx.inputs.push_back(&it->second);
+        } else if (ft != g->fetches.end()) {
+            ctx.inputs.push_back(&ft->second);
         } else if (v->constant) {
             auto val = std::make_unique<OrtValue>();
             val->elem = v->type.tensor.elem;
@@ -896,6 +917,7 @@ int mock_compute(int i) {
         }
     }
     for (OrtValueInfo* v : gr.fused->outputs) ctx.out_elem.push_back(v->type.tensor.elem);
+    ctx.stream = g->stream.impl ? g->stream.impl->GetHandle(g->stream.impl) : nullptr;
     OrtNodeComputeInfo* info = gr.info;
     void* state = nullptr;
     int rc = 0;
@@ -941,7 +963,8 @@ int mock_fetch(const char* name, void* dst, size_t bytes, int64_t* dims, int max
         h.bytes = v.bytes;
         const OrtValue* src[1] = {&v};
         OrtValue* dsts[1] = {&h};
-        int rc = status_rc(g->dt->CopyTensors(g->dt, src, dsts, nullptr, 1));
+        OrtSyncStream* st[1] = {&g->stream};
+        int rc = status_rc(g->dt->CopyTensors(g->dt, src, dsts, g->stream.impl ? st : nullptr, 1));
         if (rc) return -1;
     } else {
         std::memcpy(dst, v.data, v.bytes);
@@ -1068,15 +1091,79 @@ int mock_feed_device(const char* name, int elem, int rank, const int64_t* dims, 
     d.md = g->dev_md;
     const OrtValue* src[1] = {&h};
     OrtValue* dst[1] = {&d};
-    int rc = status_rc(g->dt->CopyTensors(g->dt, src, dst, nullptr, 1));
+    OrtSyncStream* st[1] = {&g->stream};
+    int rc = status_rc(g->dt->CopyTensors(g->dt, src, dst, g->stream.impl ? st : nullptr, 1));
     if (rc) return rc;
     g->feeds[name] = d;
     return 0;
 }
 
+// Stream set-up the way ORT does it for a stream-aware EP (after mock_device_io_setup): one
+// OrtSyncStreamImpl for the device's memory, created through CreateSyncStreamForDevice; computes
+// and copies then carry it.  Returns 1 (stream created), 0 (the factory is not stream-aware),
+// or an error code.
+int mock_stream_setup(void) {
+    if (!g || !g->factory || !g->dev_md) {
+        set_err("device I/O is not set up");
+        return -1;
+    }
+    if (!g->factory->IsStreamAware || !g->factory->IsStreamAware(g->factory)) return 0;
+    OrtSyncStreamImpl* impl = nullptr;
+    int rc = status_rc(g->factory->CreateSyncStreamForDevice(g->factory, g->dev_md, nullptr, &impl));
+    if (rc) return rc;
+    if (!impl) {
+        set_err("a stream-aware factory created no stream");
+        return -1;
+    }
+    g->stream.impl = impl;
+    return 1;
+}
+
+// IsStreamAware of the loaded factory (-1 without one).
+int mock_is_stream_aware(void) {
+    if (!g || !g->factory) return -1;
+    return g->factory->IsStreamAware && g->factory->IsStreamAware(g->factory) ? 1 : 0;
+}
+
+// The stream's native handle (null without a stream).
+void* mock_stream_handle(void) {
+    return g && g->stream.impl ? g->stream.impl->GetHandle(g->stream.impl) : nullptr;
+}
+
+// What ORT does when a run ends: OnSessionRunEnd on the run's stream.
+int mock_run_end(void) {
+    if (!g || !g->stream.impl) return 0;
+    return status_rc(g->stream.impl->OnSessionRunEnd(g->stream.impl));
+}
+
+// A notification from the stream, activated, waited on by the stream itself and by the host,
+// released (ORT's cross-stream and stream-to-host synchronisation).
+int mock_notification_roundtrip(void) {
+    if (!g || !g->stream.impl) {
+        set_err("no stream");
+        return -1;
+    }
+    OrtSyncStreamImpl* impl = g->stream.impl;
+    OrtSyncNotificationImpl* n = nullptr;
+    int rc = status_rc(impl->CreateNotification(impl, &n));
+    if (rc) return rc;
+    if (!n) {
+        set_err("CreateNotification returned no notification");
+        return -1;
+    }
+    rc = status_rc(n->Activate(n));
+    if (!rc) rc = status_rc(n->WaitOnDevice(n, &g->stream));
+    if (!rc) rc = status_rc(n->WaitOnHost(n));
+    if (!rc) rc = status_rc(impl->Flush(impl));
+    n->Release(n);
+    return rc;
+}
+
 // Releases compute infos, the EP and the factory (in ORT's order) and unloads the library.
 int mock_shutdown(void) {
     if (!g) return 0;
+    if (g->stream.impl) g->stream.impl->Release(g->stream.impl);   // drains its work first
+    g->stream.impl = nullptr;
     free_device_buffers();
     if (g->dev_alloc && g->factory) g->factory->ReleaseAllocator(g->factory, g->dev_alloc);
     g->dev_alloc = nullptr;

@@ -236,6 +236,16 @@ def dm_host(monkeypatch):
     assert mh.lib().mock_live_memory_infos() == 0, "the factory leaked an OrtMemoryInfo"
 
 
+def test_stream_aware_only_in_device_memory_mode(dm_host):
+    # IsStreamAware: host I/O has no stream to share; device-memory mode enqueues Compute on the
+    # stream ORT creates through CreateSyncStreamForDevice (onnxruntime_ep_c_api.h)
+    assert dm_host.is_stream_aware() == 1
+
+
+def test_host_io_factory_is_not_stream_aware(host):
+    assert host.is_stream_aware() == 0
+
+
 def test_device_memory_is_off_by_default(host):
     # no allocator, no data transfer, no default memory device: ORT keeps every tensor on the host
     assert host.create_allocator_for(mh.MEM_GPU, mh.AMD, 0) == 0

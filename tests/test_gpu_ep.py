@@ -239,3 +239,42 @@ def test_device_resident_weights_as_graph_inputs(dm_host):
     y = dm_host.fetch(y_name, np.float16, 3 * N)
     _check(y, orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, 32),
            "device-resident weights")
+
+
+def test_stream_aware_chain_matches_oracle(dm_host):
+    """Stream-aware mode (ORT's OrtSyncStreamImpl): ORT creates one stream for the device through
+    CreateSyncStreamForDevice, the input copy, two chained MatMulNBits islands (the second reads
+    the first's HBM output) and the output copy are ordered on it with no host wait in between,
+    and OnSessionRunEnd finishes the run.  Three runs (x, y, x): each matches the oracle (the
+    second node against the oracle applied to the first node's own output), the first and third
+    are bit-identical."""
+    print("[gpu] ep stream-aware chain", flush=True)
+    M, K, N1, N2 = 4, 1024, 512, 256
+    w1 = orc.make_inputs(M, N1, K, bits=4, block_size=32, with_zp=True, seed=31)
+    w2 = orc.make_inputs(M, N2, N1, bits=4, block_size=64, with_zp=False, seed=32)
+    dm_host.reset()
+    a_name, y1_name = mh.add_matmul_nbits(dm_host, "mm1", w1, N1, K, 4, 32, (M, K))
+    # the second node's input is the first's output
+    _, y2_name = mh.add_matmul_nbits(dm_host, "mm2", w2, N2, N1, 4, 64, (M, N1), a_name=y1_name)
+    assert dm_host.get_capability()[0] == 2
+    assert dm_host.compile() == 0, mh.err()
+    assert dm_host.device_io_setup(0) == 0, mh.err()
+    assert dm_host.is_stream_aware() == 1
+    assert dm_host.stream_setup() == 1, mh.err()
+    assert dm_host.stream_handle()
+    rng = np.random.default_rng(33)
+    xs = [rng.standard_normal((M, K), dtype=np.float32).astype(np.float16) for _ in range(2)]
+    outs = []
+    for x in (xs[0], xs[1], xs[0]):
+        dm_host.feed_device(a_name, x)
+        assert dm_host.compute(0) == 0, mh.err()
+        assert dm_host.compute(1) == 0, mh.err()
+        assert dm_host.run_end() == 0, mh.err()
+        y1 = dm_host.fetch(y1_name, np.float16, M * N1).reshape(M, N1)
+        y2 = dm_host.fetch(y2_name, np.float16, M * N2).reshape(M, N2)
+        _check(y1, orc.matmul_nbits(x, w1["B"], w1["scales"], w1["zp"], N1, K, 4, 32), "stream mm1")
+        _check(y2, orc.matmul_nbits(y1, w2["B"], w2["scales"], None, N2, N1, 4, 64), "stream mm2")
+        outs.append(y2)
+    assert np.array_equal(outs[0].view(np.uint16), outs[2].view(np.uint16))
+    assert dm_host.notification_roundtrip() == 0, mh.err()
+
