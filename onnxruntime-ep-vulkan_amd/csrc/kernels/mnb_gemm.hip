@@ -1,4 +1,5 @@
-// Prefill MatMulNBits on gfx950: dequantise-into-LDS fp16 MFMA GEMM (fp16 A, int4, block >= 32).
+// Prefill MatMulNBits on gfx950: dequantise-into-LDS fp16 MFMA GEMM (fp16 A; 4- or 8-bit
+// weights; blocks of 16, 32, 64 or 128).
 //
 // Work split.  One workgroup of 8 wavefronts owns a 256 x 128 tile of Y; the wavefronts form a
 // 4 (M) x 2 (N) grid and each owns a 64 x 64 sub-tile of four 32 x 32 MFMA tiles.  K is walked in
@@ -8,27 +9,31 @@
 // column tile).
 //
 // Data movement.  Global -> LDS uses the gfx950 LDS DMA (global_load_lds_dwordx4 / _dword):
-// no registers, no LDS write instructions.  Three A stages and four raw-B stages form a ring;
-// step s + 2's A and step s + 3's raw B are requested while step s is multiplied, so every
-// load has two steps to land.  Each step's raw int4 B (128 columns x 32 bytes) is turned once
-// per workgroup into exact (q - zp) fp16 values in an LDS buffer (magic-number unpack,
-// mnb_common.hpp) that all four row-wavefronts then read as MFMA operands; the per-column
-// fp16 scales and packed zero points ride along in the raw stage.  One barrier per step.
+// no registers, no LDS write instructions.  Three A stages and three raw-B stages form a ring;
+// step s + 2's A and step s + 3's raw B are requested while step s is multiplied, so every load
+// has two steps to land.  Each step's raw B (128 columns x 32 or 64 bytes) and its per-column
+// scale and zero-point dwords are turned once per workgroup into exact (q - zp) fp16 values and
+// the step's block scales in an LDS buffer that all four row-wavefronts then read.  One barrier
+// per step.
 //
 // LDS layouts (16-byte slots):
 //   A stage  [256 rows][8 k-chunks], chunk kc of row r at slot 8r + (kc ^ swz(r)): one DMA
 //            instruction covers 8 whole rows (8 full 128-byte lines of A), and a wavefront's
 //            MFMA operand read (32 rows x one chunk, twice) touches every bank group once.
-//   raw B    [128 cols][2 x 16 B] + scale dword per column + zero-point dword per column.
-//   (q - z)  [8 k-chunks][128 cols]: an operand read is 2 x 512 contiguous bytes.
+//   raw B    [128 cols][32 B (4-bit) or 64 B (8-bit)], then the scale dwords (1 per column, 2
+//            for blocks of 16) and one zero-point dword per column.
+//   (q - z)  [8 k-chunks][128 cols] fp16 (an operand read is 2 x 512 contiguous bytes), then
+//            the step's block scales, 4 fp16 per column.
 //
 // Arithmetic.  Each 32 x 32 tile's partial over one quant block is accumulated by MFMAs over the
-// exact (q - zp) operands in fp32 -- the reference kernel's per-block fp32 partial
-// (rust/shaders/glsl/templates/q_gemv.comp:571-579) -- and added to the tile's accumulator
-// scaled by the block's scale.  The scaled add of one sub-block is spread between the MFMAs of
-// the next, so that it runs on the VALU while the matrix core works.  For blocks of 64 or 128
-// the partial of each 64-k step is scaled on its own (the same scale twice for a 128 block).
+// exact (q - zp) operands in fp32 (fp16 a x integer q - zp is exact in fp32) -- the reference
+// kernel's per-block fp32 partial (rust/shaders/glsl/templates/q_gemv.comp:571-579) -- and added
+// to the tile's accumulator scaled by the block's scale.  The scaled add of one sub-block is
+// spread between the MFMAs of the next, so that it runs on the VALU while the matrix core works.
+// Blocks of 16 are one MFMA each; blocks of 64 or 128 scale the partial of each 64-k step on
+// its own (the same scale twice for a 128 block).
 #include <algorithm>
+#include <type_traits>
 
 #include "mnb_common.hpp"
 #include "mnb_launch.hpp"
@@ -45,13 +50,26 @@ constexpr int kBM = 64 * kWM;                    // 256
 constexpr int kBN = 64 * kWN;                    // 128
 constexpr int kKS = 64;                          // K per step
 constexpr int kNA = 3;                           // A stages
-constexpr int kNR = 4;                           // raw-B stages
+constexpr int kNR = 3;                           // raw-B stages
 constexpr int kAStage = kBM * kKS * 2;           // 32 KB
-constexpr int kRawB = kBN * kKS / 2;             // 4 KB
-constexpr int kRStage = kRawB + 256 * 4;         // + scale and zero-point dwords
-constexpr int kFStage = kBN * kKS * 2;           // 16 KB of (q - z) fp16
-constexpr int kLds = kNA * kAStage + kNR * kRStage + 2 * kFStage;   // 151552 bytes
-constexpr int kDmaPerStep = 5;                   // DMA instructions per wavefront and step
+constexpr int kFQ = kBN * kKS * 2;               // 16 KB of (q - z) fp16
+constexpr int kFStage = kFQ + kBN * 4 * 2;       // + 4 fp16 block scales per column
+
+// Per-form sizes: raw B bytes per stage, scale dwords per column and step, aux dwords per stage
+// (scales then zero points, padded to the DMA count), DMAs per step by wavefronts 0-3 (raw B)
+// and 4-7 (aux), LDS bytes.
+template <int BITS, int BS>
+struct GemmForm {
+    static constexpr int kRawB = kBN * kKS * BITS / 8;          // 4 or 8 KB
+    static constexpr int kSD = BS == 16 ? 2 : 1;
+    static constexpr int kAuxUsed = kBN * (kSD + 1);            // 256 or 384 dwords
+    static constexpr int kAuxDma = (kAuxUsed + 255) / 256;      // per thread of waves 4-7
+    static constexpr int kAux = kAuxDma * 256;                  // dwords, DMA-padded
+    static constexpr int kRStage = kRawB + 4 * kAux;
+    static constexpr int kRawDma = BITS / 4;                    // per thread of waves 0-3
+    static constexpr int kLds = kNA * kAStage + kNR * kRStage + 2 * kFStage;
+    static_assert(kLds <= 160 * 1024, "LDS");
+};
 
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
@@ -70,25 +88,34 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 }
 
 // Workgroup barrier without the release/acquire fence of __syncthreads (which would wait for
-// every outstanding DMA); the waits that matter are explicit above.
+// every outstanding DMA); the waits that matter are explicit.
 __device__ __forceinline__ void wg_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
 
+// Two bytes of w (bytes I and I + 1) as the fp16 pair (1024 + b_I, 1024 + b_{I+1}).
+template <int I>
+__device__ __forceinline__ f16x2 byte_pair(uint32_t w) {
+    constexpr uint32_t sel = (uint32_t)I | (0x0Cu << 8) | ((uint32_t)(I + 1) << 16) | (0x0Cu << 24);
+    return as_h2(__builtin_amdgcn_perm(w, w, sel) | 0x64006400u);
+}
+
 }  // namespace
 
-template <int BS, bool HAS_ZP>
+template <int BITS, int BS, bool HAS_ZP>
 __global__ void __launch_bounds__(512)
 gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ S,
               const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K,
               int tiles_m, int tiles_n, int ksplit, float* __restrict__ part) {
-    static_assert(BS == 32 || BS == 64 || BS == 128, "block size");
+    static_assert(BITS == 4 || BITS == 8, "bits");
+    static_assert(BS == 16 || BS == 32 || BS == 64 || BS == 128, "block size");
+    using F = GemmForm<BITS, BS>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     uint8_t* const sA = smem;
     uint8_t* const sR = smem + kNA * kAStage;
-    uint8_t* const sF = sR + kNR * kRStage;
+    uint8_t* const sF = sR + kNR * F::kRStage;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -108,13 +135,13 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
     const int m0 = tile_m * kBM;
     const int n0 = tile_n * kBN;
     const int bpc = K / BS;
-    const int zpb = (bpc + 1) >> 1;
+    const int zpb = BITS == 8 ? bpc : (bpc + 1) >> 1;   // zero-point bytes per column
     // this split's 64-k steps s0 .. s0 + steps - 1 (the host keeps every split non-empty); the
     // pipeline below counts steps from 0 and the loaders add s0
     const int per_split = (K / kKS + ksplit - 1) / ksplit;
     const int s0 = split * per_split;
     const int steps = min(K / kKS - s0, per_split);
-    const int64_t col_bytes = K / 2;
+    const int64_t col_bytes = (int64_t)K * BITS / 8;
     auto gcol = [&](int c) { const int g = n0 + c; return g < N ? g : N - 1; };
 
     // ---- DMA sources: A (4 instructions per wavefront) ----
@@ -127,12 +154,18 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
         gm = gm < M ? gm : M - 1;                    // clamped rows are never stored
         a_src[j] = A + (int64_t)gm * K + 8 * kc;
     }
-    // raw B (wavefronts 0-3, thread t: column t/2, 16-byte half t%2) or the per-column scale /
-    // zero-point dwords (wavefronts 4-7)
-    const uint8_t* b_src = nullptr;
-    int aux = 0;
-    if (wave < 4) b_src = B + (int64_t)gcol(tid >> 1) * col_bytes + 16 * (tid & 1);
-    else aux = tid - 256;
+    // raw B (wavefronts 0-3; instruction j of lane l: the 16-byte piece that lands at
+    // 1 KB * (kRawDma * wave + j) + 16 l, i.e. column (that offset) / bytes-per-column) or the
+    // scale and zero-point dwords (wavefronts 4-7)
+    constexpr int kColStep = kKS * BITS / 8;         // raw bytes per column and step: 32 or 64
+    const uint8_t* b_src[F::kRawDma];
+    int b_piece[F::kRawDma];
+#pragma unroll
+    for (int j = 0; j < F::kRawDma; ++j) {
+        const int off = 1024 * (F::kRawDma * (wave & 3) + j) + 16 * lane;
+        b_src[j] = B + (int64_t)gcol(off / kColStep) * col_bytes;
+        b_piece[j] = off % kColStep;
+    }
 
     auto issue_a = [&](int step, int st) {
         uint8_t* dst = sA + st * kAStage + wave * 4 * 1024;
@@ -140,45 +173,98 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
         for (int j = 0; j < 4; ++j) dma16(a_src[j] + (s0 + step) * kKS, dst + j * 1024);
     };
     auto issue_r = [&](int step, int st) {
-        uint8_t* base = sR + st * kRStage;
+        uint8_t* base = sR + st * F::kRStage;
         if (wave < 4) {
-            dma16(b_src + (s0 + step) * (kKS / 2), base + wave * 1024);
+#pragma unroll
+            for (int j = 0; j < F::kRawDma; ++j)
+                dma16(b_src[j] + (s0 + step) * kColStep + b_piece[j],
+                      base + 1024 * (F::kRawDma * wave + j));
         } else {
             const int blk0 = ((s0 + step) * kKS) / BS;
-            const int gc = gcol(aux & 127);
-            const void* src;
-            if (HAS_ZP && aux >= 128)
-                src = Z + (((int64_t)gc * zpb + (blk0 >> 1)) & ~(int64_t)3);
-            else
-                src = S + (((int64_t)gc * bpc + blk0) & ~(int64_t)1);
-            dma4(src, base + kRawB + (wave - 4) * 256);
+#pragma unroll
+            for (int j = 0; j < F::kAuxDma; ++j) {
+                // aux dword a: scale dword a % kSD of column a / kSD, then zero-point dwords;
+                // dwords past the used ones re-read the last zero-point dword (padding)
+                const int a = min(256 * j + (tid - 256), F::kAuxUsed - 1);
+                const void* src;
+                if (HAS_ZP && a >= kBN * F::kSD) {
+                    const int gc = gcol(a - kBN * F::kSD);
+                    const int64_t zb = BITS == 8 ? (int64_t)gc * zpb + blk0
+                                                 : (int64_t)gc * zpb + (blk0 >> 1);
+                    src = Z + (zb & ~(int64_t)3);
+                } else {
+                    const int aa = min(a, kBN * F::kSD - 1);
+                    const int gc = gcol(aa / F::kSD);
+                    src = S + ((((int64_t)gc * bpc + blk0) & ~(int64_t)1) + 2 * (aa % F::kSD));
+                }
+                dma4(src, base + F::kRawB + 1024 * j + 4 * (tid - 256));
+            }
         }
     };
 
-    // ---- raw stage -> (q - z) fp16: thread t takes column t%128, k 16*(t/128) .. +15 ----
+    // ---- raw stage -> (q - z) fp16 and the step's block scales: thread t takes column
+    // t%128, k 16*(t/128) .. +15 ----
     const int dq_col = tid & 127;
     const int dq_seg = tid >> 7;
     auto dequant = [&](int step, int rst, int fst) {
-        const uint8_t* base = sR + rst * kRStage;
-        const u32x2 w = *reinterpret_cast<const u32x2*>(base + dq_col * 32 + dq_seg * 8);
-        int z = 8;
-        if constexpr (HAS_ZP) {
-            const int blk = ((s0 + step) * kKS + 16 * dq_seg) / BS;
-            const uint32_t zw = *reinterpret_cast<const uint32_t*>(base + kRawB + (128 + dq_col) * 4);
-            const int byte = (int)(((int64_t)gcol(dq_col) * zpb + (blk >> 1)) & 3);
-            z = (int)((zw >> (8 * byte + 4 * (blk & 1))) & 0xFu);
-        }
-        const f16x2 zo = zoff4(z);
-        f16x8 v0, v1;
-        v0.s01 = nib_pair<0>(w.x, zo);
-        v0.s23 = nib_pair<1>(w.x, zo);
-        v0.s45 = nib_pair<2>(w.x, zo);
-        v0.s67 = nib_pair<3>(w.x, zo);
-        v1.s01 = nib_pair<0>(w.y, zo);
-        v1.s23 = nib_pair<1>(w.y, zo);
-        v1.s45 = nib_pair<2>(w.y, zo);
-        v1.s67 = nib_pair<3>(w.y, zo);
+        const uint8_t* base = sR + rst * F::kRStage;
+        const uint32_t* aux = reinterpret_cast<const uint32_t*>(base + F::kRawB);
+        const int gk = (s0 + step) * kKS + 16 * dq_seg;          // first k of the 16
+        const int blk = gk / BS;
+        const int blk0 = ((s0 + step) * kKS) / BS;
         uint8_t* f = sF + fst * kFStage;
+        if ((16 * dq_seg) % BS == 0) {
+            // the first thread of each block in the step stores its scale (slot 16 seg / BS)
+            uint32_t sw;
+            int half;
+            if constexpr (BS == 16) {
+                sw = aux[dq_col * 2 + (dq_seg >> 1)];
+                half = dq_seg & 1;
+            } else {
+                sw = aux[dq_col];
+                half = (int)((((int64_t)gcol(dq_col) * bpc + blk0) & 1) + (blk - blk0));
+            }
+            reinterpret_cast<uint16_t*>(f + kFQ)[dq_col * 4 + blk - blk0] =
+                (uint16_t)(half ? (sw >> 16) : (sw & 0xFFFFu));
+        }
+        int z = 1 << (BITS - 1);
+        if constexpr (HAS_ZP) {
+            const uint32_t zw = aux[kBN * F::kSD + dq_col];
+            const int64_t zbase = (int64_t)gcol(dq_col) * zpb;
+            if constexpr (BITS == 8) {
+                const int byte = (int)((zbase + blk) & 3);
+                z = (int)((zw >> (8 * byte)) & 0xFFu);
+            } else {
+                const int byte = (int)((zbase + (blk >> 1)) & 3);
+                z = (int)((zw >> (8 * byte + 4 * (blk & 1))) & 0xFu);
+            }
+        }
+        f16x8 v0, v1;
+        if constexpr (BITS == 4) {
+            const u32x2 w = *reinterpret_cast<const u32x2*>(base + dq_col * 32 + dq_seg * 8);
+            const f16x2 zo = zoff4(z);
+            v0.s01 = nib_pair<0>(w.x, zo);
+            v0.s23 = nib_pair<1>(w.x, zo);
+            v0.s45 = nib_pair<2>(w.x, zo);
+            v0.s67 = nib_pair<3>(w.x, zo);
+            v1.s01 = nib_pair<0>(w.y, zo);
+            v1.s23 = nib_pair<1>(w.y, zo);
+            v1.s45 = nib_pair<2>(w.y, zo);
+            v1.s67 = nib_pair<3>(w.y, zo);
+        } else {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(base + dq_col * 64 + dq_seg * 16);
+            const f16 zf = (f16)(1024 + z);
+            const f16x2 zo = {zf, zf};
+            // (1024 + q) - (1024 + z) = q - z, exact
+            v0.s01 = byte_pair<0>(w.x) - zo;
+            v0.s23 = byte_pair<2>(w.x) - zo;
+            v0.s45 = byte_pair<0>(w.y) - zo;
+            v0.s67 = byte_pair<2>(w.y) - zo;
+            v1.s01 = byte_pair<0>(w.z) - zo;
+            v1.s23 = byte_pair<2>(w.z) - zo;
+            v1.s45 = byte_pair<0>(w.w) - zo;
+            v1.s67 = byte_pair<2>(w.w) - zo;
+        }
         *reinterpret_cast<f16x8*>(f + ((2 * dq_seg) * 128 + dq_col) * 16) = v0;
         *reinterpret_cast<f16x8*>(f + ((2 * dq_seg + 1) * 128 + dq_col) * 16) = v1;
     };
@@ -198,23 +284,19 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
         asm volatile("" : "+v"(acc[t]));             // keep the adds here, beside the MFMAs
     };
 
-    auto compute = [&](int step, int ast, int fst, int rst, auto&& between) {
+    auto compute = [&](int ast, int fst, auto&& between) {
         const uint8_t* a_base = sA + ast * kAStage;
         const uint8_t* f_base = sF + fst * kFStage;
-        const uint8_t* auxs = sR + rst * kRStage + kRawB;
-        float sc[2][2];                              // [j][sub]
+        // the step's block scales of the wavefront's two 32-column halves: [j][slot]
+        float sc[2][4];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int c = wn * 64 + 32 * j + (lane & 31);
-            const uint32_t sw = *reinterpret_cast<const uint32_t*>(auxs + c * 4);
-            if constexpr (BS == 32) {
-                sc[j][0] = (float)__builtin_bit_cast(f16, (uint16_t)(sw & 0xFFFFu));
-                sc[j][1] = (float)__builtin_bit_cast(f16, (uint16_t)(sw >> 16));
-            } else {
-                const int64_t idx = (int64_t)gcol(c) * bpc + ((s0 + step) * kKS) / BS;
-                const uint16_t h = (idx & 1) ? (uint16_t)(sw >> 16) : (uint16_t)(sw & 0xFFFFu);
-                sc[j][0] = sc[j][1] = (float)__builtin_bit_cast(f16, h);
-            }
+            const u32x2 sw = *reinterpret_cast<const u32x2*>(f_base + kFQ + c * 8);
+            sc[j][0] = (float)__builtin_bit_cast(f16, (uint16_t)(sw.x & 0xFFFFu));
+            sc[j][1] = (float)__builtin_bit_cast(f16, (uint16_t)(sw.x >> 16));
+            sc[j][2] = (float)__builtin_bit_cast(f16, (uint16_t)(sw.y & 0xFFFFu));
+            sc[j][3] = (float)__builtin_bit_cast(f16, (uint16_t)(sw.y >> 16));
         }
         // Operands of both sub-blocks are requested up front; LDS returns them in order.
         f16x8 a[2][2][2], b[2][2][2];                // [sub][tile half][k half]
@@ -239,6 +321,26 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             if (sub == 1) between();
+            if constexpr (BS == 16) {
+                // a block per MFMA: each partial is scaled as soon as the next MFMAs are issued
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    f32x16 c[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        c[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][t & 1][h],
+                                                                     b[sub][t >> 1][h], f32x16{},
+                                                                     0, 0, 0);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const float scv = sc[t >> 1][2 * sub + h];
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(c[t][r], scv, acc[t][r]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                continue;
+            }
             // A block of 32 starts at every sub-block; blocks of 64 and 128 are scaled per step.
             const bool fresh = BS == 32 || sub == 0;
             if (fresh) {
@@ -262,36 +364,51 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
                 }
             }
             if (BS == 32 || sub == 1) {              // the partial is complete: keep its scales
-                psc[0] = sc[0][sub];
-                psc[1] = sc[1][sub];
+                psc[0] = sc[0][BS == 32 ? sub : 0];
+                psc[1] = sc[1][BS == 32 ? sub : 0];
                 asm volatile("" : "+v"(psc[0]), "+v"(psc[1]));
             }
         }
     };
+
+    // DMAs per step of this wavefront (counted in issue order by vmcnt)
+    constexpr int kDmaLo = 4 + F::kRawDma, kDmaHi = 4 + F::kAuxDma;
+    auto wait_steps = [&](auto two) {                // two: 0, 1 or 2 steps may stay in flight
+        constexpr int n = decltype(two)::value;
+        if (wave < 4) wait_vm_lgkm0<n * kDmaLo>(); else wait_vm_lgkm0<n * kDmaHi>();
+    };
+    using Zero = std::integral_constant<int, 0>;
+    using One = std::integral_constant<int, 1>;
+    using Two = std::integral_constant<int, 2>;
 
     // ---- prologue: raw(0) | A(0) raw(1) | A(1) raw(2) ----
     issue_r(0, 0);
     issue_a(0, 0);
     if (steps > 1) { issue_r(1, 1); issue_a(1, 1); }
     if (steps > 2) issue_r(2, 2);
-    if (steps > 2) wait_vm_lgkm0<2 * kDmaPerStep>(); else wait_vm_lgkm0<0>();
+    if (steps > 2) wait_steps(Two{}); else wait_steps(Zero{});
     wg_barrier();
     dequant(0, 0, 0);
 
     for (int s = 0; s < steps; ++s) {
-        // A(s) and raw(s+1) were requested two steps ago; the previous step's five may still
-        // be in flight (all requests are counted in issue order).
-        if (s + 2 < steps) wait_vm_lgkm0<kDmaPerStep>(); else wait_vm_lgkm0<0>();
+        // A(s) and raw(s+1) were requested two steps ago; the previous step's requests may
+        // still be in flight (all requests are counted in issue order)
+        if (s + 2 < steps) wait_steps(One{}); else wait_steps(Zero{});
         wg_barrier();
         if (s + 2 < steps) issue_a(s + 2, (s + 2) % kNA);
+        // raw stage (s + 3) % 3 = s % 3: its dequantisation (for step s) finished before the
+        // barrier above
         if (s + 3 < steps) issue_r(s + 3, (s + 3) % kNR);
-        compute(s, s % kNA, s & 1, s % kNR, [&]() {
+        compute(s % kNA, s & 1, [&]() {
             if (s + 1 < steps) dequant(s + 1, (s + 1) % kNR, (s + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
         });
     }
+
+    if constexpr (BS != 16) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) retire(t);
+        for (int t = 0; t < 4; ++t) retire(t);
+    }
 
     // ---- store: lane l holds column l%32, rows 8*(r/4) + 4*(l/32) + r%4 of each tile; a K
     // split stores its fp32 partial tile instead, summed by gemm_splitk_sum ----
@@ -334,13 +451,14 @@ gemm_splitk_sum(const float* __restrict__ part, f16* __restrict__ Y, int64_t mn,
 // ------------------------------------------------------------------------------------------
 
 bool gemm_supported(int64_t m, int64_t n, int64_t k, int bits, int bs, bool has_zp) {
-    if (m <= 0 || n <= 0 || bits != 4 || k <= 0 || k % kKS) return false;
-    if (bs != 32 && bs != 64 && bs != 128) return false;
+    if (m <= 0 || n <= 0 || (bits != 4 && bits != 8) || k <= 0 || k % kKS) return false;
+    if (bs != 16 && bs != 32 && bs != 64 && bs != 128) return false;
     if (k % bs) return false;
     const int64_t bpc = k / bs;
     // The scale and zero-point dwords of the last column must not reach past the arrays.
     if (bs > 32 && (n * bpc) % 2) return false;
-    if (has_zp && (n * ((bpc + 1) / 2)) % 4) return false;
+    const int64_t zpb = bits == 8 ? bpc : (bpc + 1) / 2;
+    if (has_zp && (n * zpb) % 4) return false;
     return true;
 }
 
@@ -366,19 +484,20 @@ size_t gemm_workspace_bytes(const GemmConfig& c, int64_t m, int64_t n) {
     return c.ksplit > 1 ? (size_t)c.ksplit * (size_t)m * (size_t)n * sizeof(float) : 0;
 }
 
-template <int BS, bool HAS_ZP>
+template <int BITS, int BS, bool HAS_ZP>
 static hipError_t gemm_go(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                           const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
                           float* part, hipStream_t st) {
-    auto kern = gemm_f16_mfma<BS, HAS_ZP>;
+    auto kern = gemm_f16_mfma<BITS, BS, HAS_ZP>;
+    constexpr int lds = GemmForm<BITS, BS>::kLds;
     // More than 64 KB of dynamic LDS must be allowed explicitly (for the current device).
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (e != hipSuccess) return e;
     const int ks = part ? c.ksplit : 1;
     const int64_t items = c.tiles_m * c.tiles_n * ks;
     const dim3 grid((unsigned)(8 * ((items + 7) / 8)), 1, 1);
-    hipLaunchKernelGGL(kern, grid, dim3(512), kLds, st, static_cast<const f16*>(a), b,
+    hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, static_cast<const f16*>(a), b,
                        static_cast<const f16*>(s), z, static_cast<f16*>(y), (int)m, (int)n,
                        (int)k, (int)c.tiles_m, (int)c.tiles_n, ks, ks > 1 ? part : nullptr);
     if (ks > 1) {
@@ -390,12 +509,25 @@ static hipError_t gemm_go(const GemmConfig& c, const void* a, const uint8_t* b, 
     return hipGetLastError();
 }
 
-template <int BS>
+template <int BITS, int BS>
 static hipError_t gemm_zp(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
                           const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
                           float* part, hipStream_t st) {
-    if (z) return gemm_go<BS, true>(c, a, b, s, z, y, m, n, k, part, st);
-    return gemm_go<BS, false>(c, a, b, s, z, y, m, n, k, part, st);
+    if (z) return gemm_go<BITS, BS, true>(c, a, b, s, z, y, m, n, k, part, st);
+    return gemm_go<BITS, BS, false>(c, a, b, s, z, y, m, n, k, part, st);
+}
+
+template <int BITS>
+static hipError_t gemm_bs(int bs, const GemmConfig& c, const void* a, const uint8_t* b,
+                          const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
+                          int64_t k, float* part, hipStream_t st) {
+    switch (bs) {
+        case 16: return gemm_zp<BITS, 16>(c, a, b, s, z, y, m, n, k, part, st);
+        case 32: return gemm_zp<BITS, 32>(c, a, b, s, z, y, m, n, k, part, st);
+        case 64: return gemm_zp<BITS, 64>(c, a, b, s, z, y, m, n, k, part, st);
+        case 128: return gemm_zp<BITS, 128>(c, a, b, s, z, y, m, n, k, part, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b, const void* s,
@@ -411,12 +543,8 @@ hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b,
                           reinterpret_cast<uintptr_t>(y) % 8 == 0
                       ? static_cast<float*>(workspace)
                       : nullptr;
-    switch (bs) {
-        case 32: return gemm_zp<32>(c, a, b, s, z, y, m, n, k, part, st);
-        case 64: return gemm_zp<64>(c, a, b, s, z, y, m, n, k, part, st);
-        case 128: return gemm_zp<128>(c, a, b, s, z, y, m, n, k, part, st);
-        default: return hipErrorInvalidValue;
-    }
+    return bits == 8 ? gemm_bs<8>(bs, c, a, b, s, z, y, m, n, k, part, st)
+                     : gemm_bs<4>(bs, c, a, b, s, z, y, m, n, k, part, st);
 }
 
 hipError_t launch_gemm(const void* a, const uint8_t* b, const void* s, const uint8_t* z, void* y,

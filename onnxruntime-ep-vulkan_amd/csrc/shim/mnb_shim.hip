@@ -278,13 +278,20 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
         (!aligned(a, 16) || !aligned(b, 16)))
         kern = MNB_KERNEL_GENERIC;
     // The GEMM's LDS DMA also fetches scales and zero points as aligned dwords; the row-tiled
-    // GEMV takes any other case of the same form.
+    // GEMV (int4, block >= 32), else the 16-row MFMA GEMV or the generic kernel, takes any other
+    // case of the same form.
     if (kern == MNB_KERNEL_STRIP_MFMA && !mnb::strip_gemv_aligned(a, b, scales, zero_points, false))
         kern = MNB_KERNEL_GROUP_MFMA;
     if (kern == MNB_KERNEL_GEMM_MFMA &&
         (!aligned(scales, 4) || !aligned(zero_points, 4) ||
-         !mnb::gemm_supported(p->m, p->n, p->k, p->bits, p->block_size, zero_points != nullptr)))
-        kern = MNB_KERNEL_GROUP_MFMA;
+         !mnb::gemm_supported(p->m, p->n, p->k, p->bits, p->block_size, zero_points != nullptr))) {
+        if (mnb::group_gemv_supported(p->k, p->bits, p->block_size))
+            kern = MNB_KERNEL_GROUP_MFMA;
+        else if (mnb::gemv_supported(p->k, p->bits, p->block_size))
+            kern = MNB_KERNEL_GEMV_MFMA;
+        else
+            kern = MNB_KERNEL_GENERIC;
+    }
     if (kern == MNB_KERNEL_ACC4_I8 || kern == MNB_KERNEL_ACC4_STREAM) {
         // the int8 path reads B in 16-byte units and stages its own aligned copy of A
         if (!aligned(b, 16) || !aligned(workspace, 256))

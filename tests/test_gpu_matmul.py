@@ -197,24 +197,30 @@ def test_baseline_configs_full_size(cuda, name, M, N, K, zp):
 
 
 GEMM_SHAPES = [
-    # (M, N, K, bs, zp): tile edges in M and N, every block size of the GEMM path
-    (65, 64, 256, 32, False),
-    (128, 256, 512, 32, True),
-    (129, 300, 1024, 64, False),
-    (256, 8192, 3072, 32, False),      # BASELINE configs[2], M=256
-    (300, 130, 2048, 128, True),
-    (512, 512, 3072, 32, True),
-    (777, 1000, 768, 64, True),
+    # (M, N, K, bits, bs, zp): tile edges in M and N, every block size and both weight widths
+    (65, 64, 256, 4, 32, False),
+    (128, 256, 512, 4, 32, True),
+    (129, 300, 1024, 4, 64, False),
+    (256, 8192, 3072, 4, 32, False),   # BASELINE configs[2], M=256
+    (300, 130, 2048, 4, 128, True),
+    (512, 512, 3072, 4, 32, True),
+    (777, 1000, 768, 4, 64, True),
+    (100, 200, 512, 4, 16, True),      # block 16: two scale dwords per column and step
+    (300, 96, 1024, 4, 16, False),
+    (2048, 2880, 2880, 8, 32, True),   # gpt-oss 8-bit node at prefill size
+    (129, 136, 1024, 8, 16, True),     # 8-bit, block 16: a zero-point dword per step
+    (300, 260, 2048, 8, 64, False),
+    (65, 128, 1536, 8, 128, True),
 ]
 
 
-@pytest.mark.parametrize("M,N,K,bs,zp", GEMM_SHAPES)
-def test_gemm_parity(cuda, M, N, K, bs, zp):
-    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=M + 7 * N + K)
-    print(f"[gpu] gemm M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
-    y = _run(inp, N, K, 4, bs, cuda, "gemm")
-    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
-    _check_f16(y, ref, f"gemm M={M} N={N} K={K} bs={bs}")
+@pytest.mark.parametrize("M,N,K,bits,bs,zp", GEMM_SHAPES)
+def test_gemm_parity(cuda, M, N, K, bits, bs, zp):
+    inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=M + 7 * N + K)
+    print(f"[gpu] gemm M={M} N={N} K={K} bits={bits} bs={bs} zp={zp}", flush=True)
+    y = _run(inp, N, K, bits, bs, cuda, "gemm")
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
+    _check_f16(y, ref, f"gemm M={M} N={N} K={K} bits={bits} bs={bs}")
 
 
 def test_gemm_uneven_k_split(cuda):
