@@ -528,6 +528,40 @@ def main() -> int:
                                      "ceiling_random_operands": round(ceil_rand, 1),
                                      "frac_of_ceiling": round(ptf / ceil_rand, 4)}})
 
+    # 8-bit prefill: gpt-oss's 8-bit MatMulNBits nodes (bits 8, block 32, zero points) at the
+    # prefill GEMM's M=2048, K = N = 2880; weights rotate over two copies.
+    qk8, qn8, qm8, qbs8 = 2880, 2880, 2048, 32
+    bpc8 = qk8 // qbs8
+    w8 = [(torch.randint(0, 256, (qn8, bpc8, qbs8), dtype=torch.uint8, device=dev, generator=gen),
+           (torch.randn(qn8 * bpc8, device=dev, generator=gen).abs() * 0.02).to(torch.float16),
+           torch.randint(0, 256, (qn8, bpc8), dtype=torch.uint8, device=dev, generator=gen))
+          for _ in range(2)]
+    A8 = torch.randn(qm8, qk8, device=dev, generator=gen).to(torch.float16)
+    Y8 = torch.empty(qm8, qn8, dtype=torch.float16, device=dev)
+    p8 = mnb.problem(qm8, qn8, qk8, 8, qbs8, True)
+    ws8b = mnb.workspace_bytes(p8)
+    ws8 = torch.empty(max(ws8b, 1), dtype=torch.uint8, device=dev)
+
+    def launch8(r, sp):
+        B8, S8, Z8 = w8[r % 2]
+        rc = lib.mnb_matmul_nbits(C.byref(p8), A8.data_ptr(), B8.data_ptr(), S8.data_ptr(),
+                                  Z8.data_ptr(), Y8.data_ptr(), ws8.data_ptr(), ws8b, sp)
+        if rc:
+            mnb.check(rc)
+
+    us8 = graph_us(torch, stream, launch8, 20)
+    tf8 = 2.0 * qm8 * qn8 * qk8 / (us8 * 1e-6) / 1e12
+    prefill_8bit = {"M": qm8, "K": qk8, "N": qn8, "bits": 8, "block_size": qbs8,
+                    "zero_points": True, "us": round(us8, 2), "TFLOP/s": round(tf8, 2),
+                    "kernel": mnb.KERNEL_NAMES.get(mnb.plan(p8).kernel, "?"),
+                    "roofline": {"bound": "mfma", "achieved": round(tf8, 2),
+                                 "peak": F16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(tf8 / F16_MFMA_PEAK_TFLOPS, 4),
+                                 "traffic": None,
+                                 "ceiling_random_operands": round(ceil_rand, 1),
+                                 "frac_of_ceiling": round(tf8 / ceil_rand, 4)}}
+    del w8
+
     def graph_time_us(fn, reps):
         """Average device time per launch of `fn(r, stream)` over a graph of `reps` launches."""
         for r in range(2):
@@ -543,7 +577,7 @@ def main() -> int:
         return 1e3 * a.elapsed_time(b) / reps
 
     # accuracy_level = 4: M=16, K=8192, N=3072, int4 bs128 with zero points;
-    # one launch = the int8 quantiser of A + the int8 MFMA GEMV.  Weights rotated over >= 2x MALL.
+    # one call = the int8 quantiser of A + the int8 MFMA GEMV.  Weights rotated over >= 2x MALL.
     ak, an, am, abs_ = 8192, 3072, 16, 128
     a_bytes = node_bytes(am, ak, an, bs=abs_)
     a_copies = max(2, -(-2 * MALL_BYTES // a_bytes))
@@ -565,7 +599,10 @@ def main() -> int:
     acc4 = {"config": "M=16 K=8192 N=3072 int4 bs128 zp, accuracy_level=4", "bytes": a_bytes,
             "us": round(a_us, 3), "GB/s": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
             "int_TOPS": round(2.0 * am * an * ak / (a_us * 1e-6) / 1e12, 2),
-            "kernel": "quantize_a_int8 + strip_gemv<i8>",
+            "kernel": "quantize_a_int8 + " + {
+                mnb.KERNEL_ACC4_STREAM: "acc4_stream (one 16-column strip per workgroup over "
+                                        "all of K, int8 MFMA)",
+            }.get(mnb.plan(a_prob).kernel, mnb.KERNEL_NAMES.get(mnb.plan(a_prob).kernel, "?")),
             "roofline": {"bound": "hbm", "achieved": round(a_bytes / (a_us * 1e-6) / 1e9, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(a_bytes / (a_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
@@ -746,6 +783,7 @@ def main() -> int:
         "roofline": roofline,
         "per_kernel": per_kernel,
         "prefill": prefill,
+        "prefill_8bit": prefill_8bit,
         "mfma_calibration": mfma_cal,
         "accuracy_level_4": acc4,
         "moe": moe,

@@ -60,15 +60,19 @@ acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
     f32x4* const sRed = reinterpret_cast<f32x4*>(smem + 16 * RB + bpc * 64 + 16);
 
     // ---- 1. this thread's share of the codes and activation scales -------------------------
-    // 16 rows x quads x 8 pieces = T * PA exactly; rows past M repeat row M - 1 (never stored)
+    // 16 rows x quads x 8 pieces = T * PA exactly.  The workgroup's T = 64 KW threads cover 8 / R
+    // whole rows of ppr = 8 quads pieces, so piece i of thread t is piece p0 of row
+    // row0 + i * 8 / R; rows past M repeat row M - 1 (never stored).
     const int t = threadIdx.x;
     const int ppr = 8 * quads;                           // pieces per row
+    const int row0 = t / ppr;
+    const int p0 = t - row0 * ppr;
+    constexpr int kRowStep = 8 / R;
     u32x4 va[PA];
 #pragma unroll
     for (int i = 0; i < PA; ++i) {
-        const int u = t + i * T;
-        const int row = min(u / ppr, M - 1);
-        va[i] = *reinterpret_cast<const u32x4*>(qa + (int64_t)row * K + 16 * (u % ppr));
+        const int row = min(row0 + i * kRowStep, M - 1);
+        va[i] = *reinterpret_cast<const u32x4*>(qa + (int64_t)row * K + 16 * p0);
     }
     const int nsc = bpc * 16;
     float vs[PS];
@@ -122,10 +126,8 @@ acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
     // ---- 4. stage the codes and scales; unpredicated stores (a dummy slot for the scales
     // past the end), so that only the activation loads are waited for here --------------------
 #pragma unroll
-    for (int i = 0; i < PA; ++i) {
-        const int u = t + i * T;
-        *reinterpret_cast<u32x4*>(sA + (u / ppr) * RB + 16 * (u % ppr)) = va[i];
-    }
+    for (int i = 0; i < PA; ++i)
+        *reinterpret_cast<u32x4*>(sA + (row0 + i * kRowStep) * RB + 16 * p0) = va[i];
 #pragma unroll
     for (int i = 0; i < PS; ++i) {
         const int u = t + i * T;

@@ -287,21 +287,8 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
     auto compute = [&](int ast, int fst, auto&& between) {
         const uint8_t* a_base = sA + ast * kAStage;
         const uint8_t* f_base = sF + fst * kFStage;
-        // the step's block scales of the wavefront's two 32-column halves: [j][slot]
-        float sc[2][4];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int c = wn * 64 + 32 * j + (lane & 31);
-            const u32x2 sw = *reinterpret_cast<const u32x2*>(f_base + kFQ + c * 8);
-            sc[j][0] = (float)__builtin_bit_cast(f16, (uint16_t)(sw.x & 0xFFFFu));
-            sc[j][1] = (float)__builtin_bit_cast(f16, (uint16_t)(sw.x >> 16));
-            sc[j][2] = (float)__builtin_bit_cast(f16, (uint16_t)(sw.y & 0xFFFFu));
-            sc[j][3] = (float)__builtin_bit_cast(f16, (uint16_t)(sw.y >> 16));
-        }
-        // Operands of both sub-blocks are requested up front; LDS returns them in order.
         f16x8 a[2][2][2], b[2][2][2];                // [sub][tile half][k half]
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
+        auto load_sub = [&](int sub) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int kc = 2 * (2 * sub + h) + (lane >> 5);
@@ -317,23 +304,49 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
                     b[sub][j][h] = *reinterpret_cast<const f16x8*>(f_base + (kc * 128 + col) * 16);
                 }
             }
+        };
+        // the step's block scales of the wavefront's two 32-column halves, [j][slot]
+        u32x2 sw[2];
+        auto load_scales = [&]() {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int c = wn * 64 + 32 * j + (lane & 31);
+                sw[j] = *reinterpret_cast<const u32x2*>(f_base + kFQ + c * 8);
+            }
+        };
+        auto scale_of = [&](int j, int slot) {
+            const uint32_t w = slot < 2 ? sw[j].x : sw[j].y;
+            return (float)__builtin_bit_cast(f16, (uint16_t)((slot & 1) ? (w >> 16) : (w & 0xFFFFu)));
+        };
+        // Sub-block 0's operands first; sub-block 1's and the scales are requested behind the
+        // first MFMAs, so no more than about 15 LDS reads are ever outstanding (the counter the
+        // waits use) and the first MFMA waits only for its own operands.
+        load_sub(0);
         __builtin_amdgcn_sched_barrier(0);
+        auto after_first = [&](int sub, int t) {
+            if (sub == 0 && t == 0) {
+                load_sub(1);
+                load_scales();
+            }
+        };
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
             if (sub == 1) between();
             if constexpr (BS == 16) {
-                // a block per MFMA: each partial is scaled as soon as the next MFMAs are issued
+                // a block per MFMA: each partial is scaled once the next MFMAs are issued
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     f32x16 c[4];
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
+                    for (int t = 0; t < 4; ++t) {
                         c[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][t & 1][h],
                                                                      b[sub][t >> 1][h], f32x16{},
                                                                      0, 0, 0);
+                        if (h == 0) after_first(sub, t);
+                    }
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const float scv = sc[t >> 1][2 * sub + h];
+                        const float scv = scale_of(t >> 1, 2 * sub + h);
 #pragma unroll
                         for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(c[t][r], scv, acc[t][r]);
                     }
@@ -353,6 +366,7 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
                     f32x16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][i][0], b[sub][j][0], f32x16{}, 0, 0, 0);
                     pd[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[sub][i][1], b[sub][j][1], c, 0, 0, 0);
                     if (t < 3) retire(t + 1);
+                    after_first(sub, t);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             } else {
@@ -364,8 +378,8 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
                 }
             }
             if (BS == 32 || sub == 1) {              // the partial is complete: keep its scales
-                psc[0] = sc[0][BS == 32 ? sub : 0];
-                psc[1] = sc[1][BS == 32 ? sub : 0];
+                psc[0] = scale_of(0, BS == 32 ? sub : 0);
+                psc[1] = scale_of(1, BS == 32 ? sub : 0);
                 asm volatile("" : "+v"(psc[0]), "+v"(psc[1]));
             }
         }
