@@ -388,6 +388,12 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
 
 /* Number of MatMulNBits-family kernel launches made by this process (proves the GPU ran). */
 uint64_t mnb_launch_count(void);
+/* Number of device allocations the library has made on its own behalf in this process: weights
+ * and caches at upload, session staging and workspace when a call needs more than the session
+ * holds (mnb_device_malloc, the caller's allocator, is not counted).  Counterpart of the
+ * reference's AllocRecorder (rust/src/ops/quant.rs:1400-1547): a steady-state decode call leaves
+ * it unchanged, which shows that no dequantised weight or per-call buffer is ever created. */
+uint64_t mnb_device_alloc_count(void);
 
 /* Roofline calibration; no counterpart in the reference (a measurement utility for bench.py).
  * Runs `workgroups` x 4 wavefronts x `iters` x 16 v_mfma_f32_32x32x16_f16 (32768 flops each) on

@@ -121,9 +121,13 @@ inline ClaimDecision claim_matmul_nbits(const NodeFacts& f, bool int8_path) {
 // claims what it implements, which is the gpt-oss form the reference records
 // (docs/OP_COVERAGE.md:831-835) widened in top-k and narrowed in activation:
 //   * k in 1..8 (the reference: 1..2), k <= E;
-//   * activation_type "swiglu" only, with swiglu_fusion 1 (interleaved) or 2 (concatenated);
-//     fusion 0 means separate fc3 weights, which this EP does not implement (ORT's own CPU
-//     kernel refuses it as well, docs/OP_COVERAGE.md:2199-2204);
+//   * activation_type "swiglu" only, with swiglu_fusion 1 (interleaved) or 2 (concatenated),
+//     or 0 with no fc3 inputs: the form gpt-oss-20b ships (docs/OP_COVERAGE.md:831-835: 8 of 11
+//     inputs occupied, fc1 [E, 2I, H/2]).  Its fc1 channels are gpt-oss's gate/linear pairs,
+//     interleaved, and the reference's census asks only for the attribute to read 1 for ORT's
+//     CPU kernel to accept the same weights (tests/ops/test_phi35.py:1445-1453; ORT's CPU
+//     kernel refuses fusion 0, docs/OP_COVERAGE.md:2199-2204), so it runs as fusion 1.
+//     Fusion 0 with separate fc3 weights is declined by the rule on inputs 8 and above;
 //   * use_sparse_mixer 0; expert_weight_bits 4; quant_type absent or "int"; block_size absent
 //     or 0 (one scale per output channel) or 32/64/128;
 //   * x float16 [.., H]; router logits float16 or float [rows, E];
@@ -158,6 +162,7 @@ struct QmoeFacts {
 struct QmoeShape {
     int64_t experts = 0, hidden = 0, inter = 0;
     bool per_channel = false;
+    int32_t swiglu_fusion = 1;   // the layout the kernel runs: 1 interleaved, 2 concatenated
 };
 
 inline bool is_qmoe(const std::string& op_type, const std::string& domain) {
@@ -179,9 +184,10 @@ inline ClaimDecision claim_qmoe(const QmoeFacts& f, QmoeShape* shape = nullptr) 
     if (!f.has_k) return decline("the required attribute k is missing");
     if (f.activation_type != "swiglu")
         return decline("activation_type = " + f.activation_type + "; this EP implements swiglu");
-    if (f.swiglu_fusion != 1 && f.swiglu_fusion != 2)
+    if (f.swiglu_fusion < 0 || f.swiglu_fusion > 2)
         return decline("swiglu_fusion = " + std::to_string(f.swiglu_fusion) +
-                       "; this EP implements 1 (interleaved) and 2 (concatenated)");
+                       "; this EP implements 0 (gpt-oss, no fc3), 1 (interleaved) and 2 "
+                       "(concatenated)");
     if (f.use_sparse_mixer != 0) return decline("use_sparse_mixer changes the routing");
     if (f.expert_weight_bits != 4)
         return decline("expert_weight_bits = " + std::to_string(f.expert_weight_bits) +
@@ -256,6 +262,7 @@ inline ClaimDecision claim_qmoe(const QmoeFacts& f, QmoeShape* shape = nullptr) 
         shape->hidden = H;
         shape->inter = I;
         shape->per_channel = per_channel;
+        shape->swiglu_fusion = f.swiglu_fusion == 2 ? 2 : 1;
     }
     return ClaimDecision{true, {}};
 }

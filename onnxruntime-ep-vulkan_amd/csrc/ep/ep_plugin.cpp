@@ -1031,7 +1031,7 @@ std::unique_ptr<NodeKernel> compile_qmoe(Ep* ep, const OrtNode* node, const OrtN
     p.num_experts = shape.experts;
     p.k = (int32_t)f.k;
     p.block_size = f.block_size == 0 ? 32 : (int32_t)f.block_size;
-    p.swiglu_fusion = (int32_t)f.swiglu_fusion;
+    p.swiglu_fusion = shape.swiglu_fusion;
     p.normalize_routing = f.normalize_routing_weights != 0;
     p.activation_alpha = f.activation_alpha;
     p.activation_beta = f.activation_beta;

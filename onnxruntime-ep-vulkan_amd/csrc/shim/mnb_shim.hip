@@ -26,6 +26,18 @@ namespace {
 
 thread_local std::string g_last_error;
 std::atomic<uint64_t> g_launches{0};
+std::atomic<uint64_t> g_device_allocs{0};
+
+// Every device allocation the library makes on its own behalf (weights and caches at upload,
+// session staging and workspace as they grow) goes through here and is counted, so a test can
+// show that steady-state calls allocate nothing.  mnb_device_malloc, the caller's allocator,
+// is not counted.
+template <class T>
+hipError_t counted_malloc(T** p, size_t bytes) {
+    const hipError_t e = hipMalloc(reinterpret_cast<void**>(p), bytes);
+    if (e == hipSuccess) g_device_allocs.fetch_add(1);
+    return e;
+}
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -75,6 +87,8 @@ const char* mnb_last_error(void) { return g_last_error.c_str(); }
 int mnb_version(void) { return 1; }
 
 uint64_t mnb_launch_count(void) { return g_launches.load(); }
+
+uint64_t mnb_device_alloc_count(void) { return g_device_allocs.load(); }
 
 int mnb_calibrate_mfma(int32_t workgroups, int32_t iters, const void* operands_f16, float* out,
                        void* stream) {
@@ -917,7 +931,7 @@ static int grow(void** p, size_t* cap, size_t need) {
     if (*p) (void)hipFree(*p);
     *p = nullptr;
     *cap = 0;
-    hipError_t e = hipMalloc(p, need);
+    hipError_t e = counted_malloc(p, need);
     if (e != hipSuccess) {
         *p = nullptr;
         return fail(MNB_ERR_NOMEM, "hipMalloc(%zu): %s", need, hipGetErrorString(e));
@@ -971,9 +985,9 @@ int mnb_weights_upload(mnb_session* s, const mnb_problem* node, const void* b_ho
     if (!w) return fail(MNB_ERR_NOMEM, "weights allocation failed");
     w->s = s;
     w->node = p;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(&w->b), want_b);
-    if (e == hipSuccess) e = hipMalloc(&w->scales, want_s);
-    if (e == hipSuccess && p.has_zero_points) e = hipMalloc(reinterpret_cast<void**>(&w->zp), want_z);
+    hipError_t e = counted_malloc(&w->b, want_b);
+    if (e == hipSuccess) e = counted_malloc(&w->scales, want_s);
+    if (e == hipSuccess && p.has_zero_points) e = counted_malloc(&w->zp, want_z);
     if (e == hipSuccess) e = hipMemcpyAsync(w->b, b_host, want_b, hipMemcpyHostToDevice, s->stream);
     if (e == hipSuccess)
         e = hipMemcpyAsync(w->scales, scales_host, want_s, hipMemcpyHostToDevice, s->stream);
@@ -1141,7 +1155,7 @@ int mnb_qmoe_weights_upload(mnb_session* s, const mnb_qmoe_problem* node,
     hipError_t e = hipSuccess;
     for (int i = 0; i < 6 && e == hipSuccess; ++i) {
         if (!host[i]) continue;
-        e = hipMalloc(&w->buf[i], size[i]);
+        e = counted_malloc(&w->buf[i], size[i]);
         if (e == hipSuccess)
             e = hipMemcpyAsync(w->buf[i], host[i], size[i], hipMemcpyHostToDevice, s->stream);
     }
@@ -1243,10 +1257,10 @@ int mnb_rmsnorm_weights_upload(mnb_session* s, const mnb_rmsnorm_problem* node,
     if (!w) return fail(MNB_ERR_NOMEM, "weights allocation failed");
     w->s = s;
     w->node = p;
-    hipError_t e = hipMalloc(&w->gamma, want);
+    hipError_t e = counted_malloc(&w->gamma, want);
     if (e == hipSuccess) e = hipMemcpyAsync(w->gamma, gamma, want, hipMemcpyHostToDevice, s->stream);
     if (e == hipSuccess && p.has_bias) {
-        e = hipMalloc(&w->bias, want);
+        e = counted_malloc(&w->bias, want);
         if (e == hipSuccess) e = hipMemcpyAsync(w->bias, bias, want, hipMemcpyHostToDevice, s->stream);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
@@ -1352,8 +1366,8 @@ int mnb_gqa_caches_upload(mnb_session* s, const mnb_gqa_problem* node, const voi
         *out = c;
         return MNB_OK;
     }
-    hipError_t e = hipMalloc(&c->cos, want);
-    if (e == hipSuccess) e = hipMalloc(&c->sin, want);
+    hipError_t e = counted_malloc(&c->cos, want);
+    if (e == hipSuccess) e = counted_malloc(&c->sin, want);
     if (e == hipSuccess) e = hipMemcpyAsync(c->cos, cos_cache, want, hipMemcpyHostToDevice, s->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(c->sin, sin_cache, want, hipMemcpyHostToDevice, s->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(s->stream);

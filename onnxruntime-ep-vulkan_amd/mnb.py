@@ -156,6 +156,7 @@ def load() -> C.CDLL:
         "mnb_device_free": (C.c_int, [C.c_int, vp]),
         "mnb_memcpy": (C.c_int, [C.c_int, vp, vp, sz, C.c_int]),
         "mnb_launch_count": (C.c_uint64, []),
+        "mnb_device_alloc_count": (C.c_uint64, []),
         "mnb_calibrate_mfma": (C.c_int, [i32, i32, vp, vp, vp]),
         "mnb_calibrate_read": (C.c_int, [vp, sz, i32, i32, i32, vp, vp]),
         "mnb_qmoe_check": (C.c_int, [C.POINTER(QmoeProblem)]),
@@ -346,3 +347,8 @@ def gqa(qkv, past_k, past_v, seqlens_k, cos, sin, *, num_heads: int, kv_num_head
 
 def launch_count() -> int:
     return int(load().mnb_launch_count())
+
+
+def device_alloc_count() -> int:
+    """Device allocations the library has made on its own behalf (uploads, staging growth)."""
+    return int(load().mnb_device_alloc_count())

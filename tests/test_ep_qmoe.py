@@ -53,6 +53,18 @@ def test_claimed_forms(host, per_channel, bias, router):
     assert _claim(host, inp, k=2, x_shape=(-1, 256), router_elem=router)[0] == 1
 
 
+def test_gpt_oss_recorded_form_is_claimed(host):
+    """gpt-oss-20b's QMoE as recorded (docs/OP_COVERAGE.md:831-835): 11 declared inputs, 8
+    occupied, swiglu_fusion = 0, per-channel scales.  fc1's 2I channels hold the interleaved
+    gate/linear pairs, so it runs as fusion 1 (ORT's CPU kernel refuses the attribute value,
+    docs/OP_COVERAGE.md:2199-2204, and the reference's census asks for a re-export with 1 over
+    the same weights, tests/ops/test_phi35.py:1445-1453)."""
+    assert host.create_ep(-1) == 0
+    inp = _inputs(per_channel=True)
+    assert _claim(host, inp, k=4, x_shape=(4, 256), extra_inputs=["", "", ""],
+                  attrs_over={"swiglu_fusion": 0}) == (1, ["moe:drop"])
+
+
 def test_concatenated_swiglu_and_no_limit_are_claimed(host):
     assert host.create_ep(-1) == 0
     inp = _inputs()
@@ -65,7 +77,9 @@ def test_concatenated_swiglu_and_no_limit_are_claimed(host):
     ("k_above_experts", dict(k=5, inp={"E": 4})),
     ("relu", dict(attrs_over={"activation_type": "relu"})),
     ("silu", dict(attrs_over={"activation_type": "silu"})),
-    ("unfused_swiglu", dict(attrs_over={"swiglu_fusion": 0})),
+    ("unfused_swiglu_with_fc3", dict(attrs_over={"swiglu_fusion": 0},
+                                     extra_inputs=["moe_fc1", "moe_fc1_scales"])),
+    ("swiglu_fusion_3", dict(attrs_over={"swiglu_fusion": 3})),
     ("sparse_mixer", dict(attrs_over={"use_sparse_mixer": 1})),
     ("eight_bit", dict(attrs_over={"expert_weight_bits": 8})),
     ("fp4", dict(attrs_over={"quant_type": "fp4"})),
@@ -122,6 +136,7 @@ def gpu_host(cuda):
     ((4,), 256, 128, 8, 2, False, 1),
     ((2, 5), 512, 256, 16, 4, True, 2),
     ((64,), 2880, 2880, 32, 4, True, 1),               # gpt-oss-20b expert block
+    ((64,), 2880, 2880, 32, 4, True, 0),               # ... with its recorded swiglu_fusion = 0
 ])
 def test_ep_qmoe_matches_oracle(gpu_host, lead, H, I, E, k, per_channel, fusion):
     print(f"[gpu] ep qmoe lead={lead} H={H} I={I} E={E} k={k} pc={per_channel} f={fusion}",
@@ -130,7 +145,8 @@ def test_ep_qmoe_matches_oracle(gpu_host, lead, H, I, E, k, per_channel, fusion)
     inp = oq.make_qmoe_inputs(T, H, I, E, per_channel=per_channel, seed=T + E)
     gpu_host.reset()
     x_name, r_name, y_name = mh.add_qmoe(gpu_host, "moe", inp, k=k, x_shape=lead + (H,),
-                                         attrs_over={"swiglu_fusion": fusion})
+                                         attrs_over={"swiglu_fusion": fusion},
+                                         extra_inputs=["", "", ""] if fusion == 0 else ())
     assert gpu_host.get_capability() == (1, ["moe:drop"])
     assert gpu_host.compile() == 0, mh.err()
     before = mh.EP_COUNT()
@@ -141,7 +157,7 @@ def test_ep_qmoe_matches_oracle(gpu_host, lead, H, I, E, k, per_channel, fusion)
     y = gpu_host.fetch(y_name, np.float16, T * H)
     assert y.shape == lead + (H,)
     kw = dict(k=k, inter=I, block_size=32, fc1_bias=inp["fc1_bias"], fc2_bias=inp["fc2_bias"],
-              fusion=fusion)
+              fusion=fusion or 1)                 # fusion 0 (gpt-oss) runs interleaved
     args = (inp["x"], inp["logits"], inp["fc1"], inp["fc1_scales"], inp["fc2"], inp["fc2_scales"])
     ref16 = oq.qmoe(*args, f16_points=True, **kw)
     ref = oq.qmoe(*args, **kw)
