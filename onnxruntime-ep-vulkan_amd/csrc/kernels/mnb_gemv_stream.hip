@@ -1,5 +1,7 @@
 // Launch configuration of the streaming decode GEMV (kernel in mnb_gemv_stream.hpp, instantiated
 // per bit width in mnb_gemv_stream_b4.hip / mnb_gemv_stream_b8.hip).
+#include <algorithm>
+
 #include "mnb_gemv_stream.hpp"
 
 namespace mnb {
@@ -18,22 +20,22 @@ constexpr int kNumCUs = 256;
 // workgroup per CU and the launch is left to the row-tiled kernels.
 constexpr int64_t kStreamMaxLds = 96 * 1024;
 
-// Chunks per lane the kernel is instantiated for: 8 for one row and one column per lane group,
-// 4 with two columns or with several rows (two columns only for one row).
-int cpl_cap(int u, int mr) { return u == 1 && mr == 1 ? 8 : 4; }
+// Chunks per lane the kernel is instantiated for: 8 with one column per lane group, 4 with two
+// (two columns only for one row).
+int cpl_cap(int u) { return u == 1 ? 8 : 4; }
 
 // Fills the derived fields (workgroups along N, LDS bytes) of a shape; false when the shape is
 // malformed or exceeds what the kernel is compiled for.
 bool derive(StreamConfig& c, int64_t n, int64_t k, int bits, int bs) {
-    if (c.waves_per_group < 1 || 64 * c.waves_per_group > kStreamMaxThreads) return false;
     if (c.mr < 1 || c.mr > 4 || (c.u != 1 && c.u != 2)) return false;
+    if (c.waves_per_group < 1 || 64 * c.waves_per_group > kStreamMaxThreads) return false;
     if (c.g != 16 && c.g != 32 && c.g != 64) return false;
     if (bits != 4 && bits != 8) return false;
     const int64_t wpc = 128 / bits;
     if (k <= 0 || k % wpc || k % bs || n <= 0) return false;
     const int64_t cpc = k / wpc;
     if (c.mr > 1 && c.u != 1) return false;
-    if (c.cpl < 1 || c.cpl > cpl_cap(c.u, c.mr) || (int64_t)c.g * c.cpl < cpc) return false;
+    if (c.cpl < 1 || c.cpl > cpl_cap(c.u) || (int64_t)c.g * c.cpl < cpc) return false;
     const int64_t cols = (int64_t)c.waves_per_group * (64 / c.g) * c.u;
     const int64_t bpc = k / bs;
     const int64_t zpb = (bpc * bits + 7) / 8;
@@ -47,22 +49,27 @@ bool derive(StreamConfig& c, int64_t n, int64_t k, int bits, int bs) {
 
 StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int bs) {
     StreamConfig c{};
-    c.mr = m <= 1 ? 1 : (int)(m < 4 ? m : 4);
     const int64_t cpc = k / (128 / bits);
+    auto lane_group = [&](int cand) { return (cpc + cand - 1) / cand <= cpl_cap(1); };
+    // One row-tile of all M rows (up to 4): the weights are streamed once.
+    c.mr = m <= 1 ? 1 : (int)(m < 4 ? m : 4);
     // Lane-group width: the best-filled group (G * CPL chunk slots for cpc chunks); among equally
-    // filled ones, the one that puts closest to 16 wavefronts on each CU (one per 64/G columns).
-    // Measured on MI355X for the Phi-3.5 decode shapes: qkv G=32 (18 per CU), gate_up G=16 (16
-    // per CU) rather than G=32 (32 per CU).
+    // filled ones, the one that puts closest to 16 wavefronts on each CU (one per 64/G columns),
+    // 10 with several rows (each wavefront then reads MR rows of activations per chunk, so fewer,
+    // longer wavefronts win).  Measured on MI355X for the Phi-3.5 decode shapes: one row, qkv
+    // G=32 (18 per CU), gate_up G=16 (16 per CU) rather than G=32 (32 per CU); 2-4 rows, qkv and
+    // gate_up G=16, o G=32, down G=64.
     auto waves_per_cu = [&](int cand) {
         return (double)((n + 64 / cand - 1) / (64 / cand)) / kNumCUs;
     };
+    const double target = c.mr == 1 ? 16.0 : 10.0;
     double best_fill = -1.0, best_dist = 0.0;
     int g = 64;
     for (int cand : {64, 32, 16}) {
+        if (!lane_group(cand)) continue;
         const int64_t cpl = (cpc + cand - 1) / cand;
-        if (cpl > cpl_cap(1, c.mr)) continue;
         const double fill = (double)cpc / (double)(cand * cpl);
-        const double dist = __builtin_fabs(waves_per_cu(cand) - 16.0);
+        const double dist = __builtin_fabs(waves_per_cu(cand) - target);
         if (fill > best_fill + 1e-9 || (fill > best_fill - 1e-9 && dist < best_dist)) {
             best_fill = fill;
             best_dist = dist;
@@ -74,29 +81,33 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     // One column per lane group unless that needs more than 32 wavefronts per CU.
     c.u = 1;
     double wpc = waves_per_cu(g);
-    if (wpc > 32.0 && c.mr == 1 && c.cpl <= cpl_cap(2, 1)) {
+    if (wpc > 32.0 && c.mr == 1 && c.cpl <= cpl_cap(2)) {
         c.u = 2;
         wpc /= 2.0;
     }
     // Workgroups: each stages the whole activation vector (2*K bytes per row) before it streams
-    // weights, so more workgroups mean more of that traffic ahead of the weights.  Measured:
-    // about three workgroups per CU for K <= 4096, one for K = 8192; 4..16 wavefronts each.
-    const double groups_per_cu = k <= 4096 ? 3.0 : 1.0;
+    // weights, so more workgroups mean more of that traffic ahead of the weights.  Measured over
+    // every shape of 4..16 wavefronts (MI355X, K=3072: N = 3072, 8192, 9216, 16384, 32064; K=2880,
+    // 4096, 8192): about four workgroups per CU for K <= 4096 (gate_up 8.2 -> 7.3 us, N=32064
+    // 14.8 -> 11.8 us against three per CU), one for K = 8192.  At least K / 1024 wavefronts, so
+    // that the first staging batch (2 * MR 16-byte units per thread) covers all of A.
+    const double groups_per_cu = k <= 4096 ? 4.0 : 1.0;
     int64_t w = (int64_t)(wpc / groups_per_cu + 0.5);
+    const int64_t wmin = std::max<int64_t>(4, (k + 1023) / 1024);
     const int64_t wmax = kStreamMaxThreads / 64;
-    c.waves_per_group = (int)(w < 4 ? 4 : (w > wmax ? wmax : w));
+    c.waves_per_group = (int)std::min(std::max(w, wmin), wmax);
     derive(c, n, k, bits, bs);
     return c;
 }
 
-bool gemv_stream_supported(int64_t m, int64_t k, int bits, int bs) {
+bool gemv_stream_supported(int64_t m, int64_t n, int64_t k, int bits, int bs) {
     if (bits != 4 && bits != 8) return false;
     if (bs != 16 && bs != 32 && bs != 64 && bs != 128) return false;
-    if (m < 1 || m > 4) return false;
+    if (m < 1 || m > 4 || n < 1) return false;
     const int wpc = 128 / bits;
     if (k <= 0 || k % wpc || k % bs) return false;
-    StreamConfig c = gemv_stream_config(m, 1 << 20, k, bits, bs);
-    return derive(c, 1 << 20, k, bits, bs);
+    StreamConfig c = gemv_stream_config(m, n, k, bits, bs);
+    return derive(c, n, k, bits, bs);
 }
 
 hipError_t launch_gemv_stream_cfg(const StreamConfig& cfg, const void* a, const uint8_t* b,
@@ -105,8 +116,9 @@ hipError_t launch_gemv_stream_cfg(const StreamConfig& cfg, const void* a, const 
     if (m == 0) return hipSuccess;
     StreamConfig c = cfg;
     // the shape is checked (the kernel is compiled for kStreamMaxThreads threads per workgroup,
-    // U <= 2, CPL <= 8) and its derived fields recomputed before anything is launched
-    if (m < 0 || c.mr < (m < 4 ? m : 4) || !derive(c, n, k, bits, bs)) return hipErrorInvalidValue;
+    // U <= 2, CPL <= 8) and its derived fields recomputed before anything is launched; row-tiles
+    // of MR rows cover M (grid y)
+    if (m < 0 || !derive(c, n, k, bits, bs)) return hipErrorInvalidValue;
     const int64_t cols = (int64_t)c.waves_per_group * (64 / c.g) * c.u;
     const int64_t bpc = k / bs;
     const int64_t zpb = (bpc * bits + 7) / 8;

@@ -91,7 +91,9 @@ __device__ __forceinline__ u32x4 pair_activations(u32x4 x) {
 template <int BITS>
 __host__ __device__ constexpr int stream_chunk_stride() { return BITS == 4 ? 80 : 48; }
 
-// Units (16 bytes) a thread loads per staging batch: activations, scale bytes, zero-point bytes.
+// Units (16 bytes) a thread loads per staging batch: activations (per row of the row-tile, so
+// that the first batch covers all of A whenever a workgroup has K / 16 threads), scale bytes,
+// zero-point bytes.
 constexpr int kStreamAU = 2;
 constexpr int kStreamSU = 2;
 constexpr int kStreamZU = 1;
@@ -144,9 +146,10 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
     // Every load of this batch is made by every thread (indices past the end are clamped to an
     // in-bounds unit whose value is not used), so the number of loads in flight is the same on
     // every path and waiting for the activations does not wait for the later requests.
-    u32x4 av[kStreamAU];
+    constexpr int AU = kStreamAU * MR;
+    u32x4 av[AU];
 #pragma unroll
-    for (int i = 0; i < kStreamAU; ++i) {
+    for (int i = 0; i < AU; ++i) {
         const int u = min(tid + i * T, a_units - 1);
         const int r = u / upr;
         const int row = min(m0 + r, M - 1);
@@ -200,7 +203,7 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
         }
     };
 #pragma unroll
-    for (int i = 0; i < kStreamAU; ++i) {
+    for (int i = 0; i < AU; ++i) {
         const int u = tid + i * T;
         float t = stage_a(u, av[i]);
         // partner sums over the lane's quad (int4) or pair (int8); out-of-range units add 0
@@ -209,10 +212,10 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
         if (u < a_units) store_sums(u, t);
     }
     // ---- what the first batch did not cover (long K, several rows, unaligned tensors) -------
-    for (int base = tid + kStreamAU * T; base < a_units; base += kStreamAU * T) {
-        u32x4 x[kStreamAU];
+    for (int base = tid + AU * T; base < a_units; base += AU * T) {
+        u32x4 x[AU];
 #pragma unroll
-        for (int i = 0; i < kStreamAU; ++i) {
+        for (int i = 0; i < AU; ++i) {
             const int u = base + i * T;
             const int r = u / upr;
             const int row = min(m0 + min(r, MR - 1), M - 1);
@@ -220,7 +223,7 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
                 x[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)row * K + (int64_t)(u - r * upr) * 8);
         }
 #pragma unroll
-        for (int i = 0; i < kStreamAU; ++i) {
+        for (int i = 0; i < AU; ++i) {
             const int u = base + i * T;
             float t = u < a_units ? stage_a(u, x[i]) : 0.f;
             t += dpp_f<0xB1>(t);
@@ -277,76 +280,173 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
 #pragma unroll
         for (int u = 0; u < U; ++u) acc[r][u] = 0.f;
     const uint16_t* sSr = reinterpret_cast<const uint16_t*>(sS);
+    if constexpr (MR == 1) {
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        // With several rows, keep the scheduler from hoisting every chunk's activation reads
-        // to the top (MR * 16 registers per chunk); one row's are cheap to hold.
-        if constexpr (MR > 1) __builtin_amdgcn_sched_barrier(0);
-        const int c0 = gi + j * G;
-        const bool live = c0 < cpc;
-        const int c = live ? c0 : cpc - 1;
-        f16x2 ap[MR][NP];
-        float asum[MR][SEGS];
+        for (int j = 0; j < CPL; ++j) {
+            const int c0 = gi + j * G;
+            const bool live = c0 < cpc;
+            const int c = live ? c0 : cpc - 1;
+            f16x2 ap[MR][NP];
+            float asum[MR][SEGS];
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            const uint8_t* src = sA + (r * cpc + c) * CST;
+            for (int r = 0; r < MR; ++r) {
+                const uint8_t* src = sA + (r * cpc + c) * CST;
 #pragma unroll
-            for (int q = 0; q < NP / 4; ++q) {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * q);
-                ap[r][4 * q + 0] = as_h2(v.x);
-                ap[r][4 * q + 1] = as_h2(v.y);
-                ap[r][4 * q + 2] = as_h2(v.z);
-                ap[r][4 * q + 3] = as_h2(v.w);
+                for (int q = 0; q < NP / 4; ++q) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * q);
+                    ap[r][4 * q + 0] = as_h2(v.x);
+                    ap[r][4 * q + 1] = as_h2(v.y);
+                    ap[r][4 * q + 2] = as_h2(v.z);
+                    ap[r][4 * q + 3] = as_h2(v.w);
+                }
+#pragma unroll
+                for (int s = 0; s < SEGS; ++s)
+                    asum[r][s] = reinterpret_cast<const float*>(src + 4 * NP)[s];
             }
 #pragma unroll
-            for (int s = 0; s < SEGS; ++s)
-                asum[r][s] = reinterpret_cast<const float*>(src + 4 * NP)[s];
-        }
+            for (int u = 0; u < U; ++u) {
+                const int lc = min(lcol[u], C - 1);
+                const uint32_t w[4] = {bw[u][j].x, bw[u][j].y, bw[u][j].z, bw[u][j].w};
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int lc = min(lcol[u], C - 1);
-            const uint32_t w[4] = {bw[u][j].x, bw[u][j].y, bw[u][j].z, bw[u][j].w};
-#pragma unroll
-            for (int s = 0; s < SEGS; ++s) {
-                const int blk = (c * WPC + s * BS) / BS;
-                float sv1 = (float)__builtin_bit_cast(f16, sSr[lc * bpc + blk]);
-                sv1 = live ? sv1 : 0.f;
-                float zf;
-                if constexpr (!HAS_ZP) {
-                    zf = (float)(1 << (BITS - 1));
-                } else if constexpr (BITS == 4) {
-                    zf = (float)((sZ[lc * zpb + (blk >> 1)] >> ((blk & 1) * 4)) & 0xF);
-                } else {
-                    zf = (float)sZ[lc * zpb + blk];
-                }
-                const float s24 = sv1 * 16777216.0f;
-                const float sz = -sv1 * zf;
-#pragma unroll
-                for (int r = 0; r < MR; ++r) {
-                    float t = 0.f;
-                    float t16 = 0.f;
-#pragma unroll
-                    for (int d = s * DW_PER_SEG; d < (s + 1) * DW_PER_SEG; ++d) {
-                        if constexpr (BITS == 4) {
-                            // Nibble pairs 0 and 2 sit in bits 0-3 of each half (q * 2^-24);
-                            // pairs 1 and 3 are masked in place at bits 4-7 (16q * 2^-24, still
-                            // subnormal) and summed apart, scaled by 1/16 below: one shift per
-                            // dword instead of three.
-                            const uint32_t wh = w[d] >> 8;
-                            t = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x000F000Fu), ap[r][4 * d + 0], t, false);
-                            t = __builtin_amdgcn_fdot2(as_h2(wh & 0x000F000Fu), ap[r][4 * d + 2], t, false);
-                            t16 = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x00F000F0u), ap[r][4 * d + 1], t16, false);
-                            t16 = __builtin_amdgcn_fdot2(as_h2(wh & 0x00F000F0u), ap[r][4 * d + 3], t16, false);
-                        } else {
-                            t = __builtin_amdgcn_fdot2(sub_pair<8, 0>(w[d]), ap[r][2 * d + 0], t, false);
-                            t = __builtin_amdgcn_fdot2(sub_pair<8, 1>(w[d]), ap[r][2 * d + 1], t, false);
-                        }
+                for (int s = 0; s < SEGS; ++s) {
+                    const int blk = (c * WPC + s * BS) / BS;
+                    float sv1 = (float)__builtin_bit_cast(f16, sSr[lc * bpc + blk]);
+                    sv1 = live ? sv1 : 0.f;
+                    float zf;
+                    if constexpr (!HAS_ZP) {
+                        zf = (float)(1 << (BITS - 1));
+                    } else if constexpr (BITS == 4) {
+                        zf = (float)((sZ[lc * zpb + (blk >> 1)] >> ((blk & 1) * 4)) & 0xF);
+                    } else {
+                        zf = (float)sZ[lc * zpb + blk];
                     }
-                    t = __builtin_fmaf(t16, 0.0625f, t);
-                    acc[r][u] = __builtin_fmaf(s24, t, acc[r][u]);
-                    acc[r][u] = __builtin_fmaf(sz, asum[r][s], acc[r][u]);
+                    const float s24 = sv1 * 16777216.0f;
+                    const float sz = -sv1 * zf;
+#pragma unroll
+                    for (int r = 0; r < MR; ++r) {
+                        float t = 0.f;
+                        float t16 = 0.f;
+#pragma unroll
+                        for (int d = s * DW_PER_SEG; d < (s + 1) * DW_PER_SEG; ++d) {
+                            if constexpr (BITS == 4) {
+                                // Nibble pairs 0 and 2 sit in bits 0-3 of each half (q * 2^-24);
+                                // pairs 1 and 3 are masked in place at bits 4-7 (16q * 2^-24, still
+                                // subnormal) and summed apart, scaled by 1/16 below: one shift per
+                                // dword instead of three.
+                                const uint32_t wh = w[d] >> 8;
+                                t = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x000F000Fu), ap[r][4 * d + 0], t, false);
+                                t = __builtin_amdgcn_fdot2(as_h2(wh & 0x000F000Fu), ap[r][4 * d + 2], t, false);
+                                t16 = __builtin_amdgcn_fdot2(as_h2(w[d] & 0x00F000F0u), ap[r][4 * d + 1], t16, false);
+                                t16 = __builtin_amdgcn_fdot2(as_h2(wh & 0x00F000F0u), ap[r][4 * d + 3], t16, false);
+                            } else {
+                                t = __builtin_amdgcn_fdot2(sub_pair<8, 0>(w[d]), ap[r][2 * d + 0], t, false);
+                                t = __builtin_amdgcn_fdot2(sub_pair<8, 1>(w[d]), ap[r][2 * d + 1], t, false);
+                            }
+                        }
+                        t = __builtin_fmaf(t16, 0.0625f, t);
+                        acc[r][u] = __builtin_fmaf(s24, t, acc[r][u]);
+                        acc[r][u] = __builtin_fmaf(sz, asum[r][s], acc[r][u]);
+                    }
                 }
             }
+        }
+    } else {
+        // Several rows: the chunk's weights are unpacked and its scale terms formed once, then
+        // each row's activations are read from LDS and used for all U columns.
+        constexpr int QPD = BITS == 4 ? 4 : 2;           // fp16 pairs per weight dword
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            // keep the scheduler from hoisting every chunk's activation reads to the top
+            __builtin_amdgcn_sched_barrier(0);
+            const int c0 = gi + j * G;
+            const bool live = c0 < cpc;
+            const int c = live ? c0 : cpc - 1;
+            // Per column and block segment: 2^24 * scale and -scale * zp.
+            float s24[U][SEGS], szs[U][SEGS];
+            // The chunk's weights as fp16 subnormal pairs.  int4: for dword d, pairs 0 and 2 sit in
+            // bits 0-3 of each half (q * 2^-24) and pairs 1 and 3 are masked in place at bits 4-7
+            // (16q * 2^-24, still subnormal), summed apart and scaled by 1/16: one shift per dword.
+            uint32_t q[U][4][QPD];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int lc = min(lcol[u], C - 1);
+#pragma unroll
+                for (int s = 0; s < SEGS; ++s) {
+                    const int blk = (c * WPC + s * BS) / BS;
+                    float sv1 = (float)__builtin_bit_cast(f16, sSr[lc * bpc + blk]);
+                    sv1 = live ? sv1 : 0.f;
+                    float zf;
+                    if constexpr (!HAS_ZP) {
+                        zf = (float)(1 << (BITS - 1));
+                    } else if constexpr (BITS == 4) {
+                        zf = (float)((sZ[lc * zpb + (blk >> 1)] >> ((blk & 1) * 4)) & 0xF);
+                    } else {
+                        zf = (float)sZ[lc * zpb + blk];
+                    }
+                    s24[u][s] = sv1 * 16777216.0f;
+                    szs[u][s] = -sv1 * zf;
+                }
+                const uint32_t w[4] = {bw[u][j].x, bw[u][j].y, bw[u][j].z, bw[u][j].w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    if constexpr (BITS == 4) {
+                        const uint32_t wh = w[d] >> 8;
+                        q[u][d][0] = w[d] & 0x000F000Fu;
+                        q[u][d][1] = w[d] & 0x00F000F0u;
+                        q[u][d][2] = wh & 0x000F000Fu;
+                        q[u][d][3] = wh & 0x00F000F0u;
+                    } else {
+                        q[u][d][0] = w[d] & 0x00FF00FFu;
+                        q[u][d][1] = (w[d] >> 8) & 0x00FF00FFu;
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < MR; ++r) {
+                const uint8_t* src = sA + (r * cpc + c) * CST;
+                f16x2 ap[NP];
+#pragma unroll
+                for (int qq = 0; qq < NP / 4; ++qq) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(src + 16 * qq);
+                    ap[4 * qq + 0] = as_h2(v.x);
+                    ap[4 * qq + 1] = as_h2(v.y);
+                    ap[4 * qq + 2] = as_h2(v.z);
+                    ap[4 * qq + 3] = as_h2(v.w);
+                }
+                float asum[SEGS];
+#pragma unroll
+                for (int s = 0; s < SEGS; ++s) asum[s] = reinterpret_cast<const float*>(src + 4 * NP)[s];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+#pragma unroll
+                    for (int s = 0; s < SEGS; ++s) {
+                        float t = 0.f;
+                        float t16 = 0.f;
+#pragma unroll
+                        for (int d = s * DW_PER_SEG; d < (s + 1) * DW_PER_SEG; ++d) {
+                            if constexpr (BITS == 4) {
+                                t = __builtin_amdgcn_fdot2(as_h2(q[u][d][0]), ap[4 * d + 0], t, false);
+                                t = __builtin_amdgcn_fdot2(as_h2(q[u][d][2]), ap[4 * d + 2], t, false);
+                                t16 = __builtin_amdgcn_fdot2(as_h2(q[u][d][1]), ap[4 * d + 1], t16, false);
+                                t16 = __builtin_amdgcn_fdot2(as_h2(q[u][d][3]), ap[4 * d + 3], t16, false);
+                            } else {
+                                t = __builtin_amdgcn_fdot2(as_h2(q[u][d][0]), ap[2 * d + 0], t, false);
+                                t = __builtin_amdgcn_fdot2(as_h2(q[u][d][1]), ap[2 * d + 1], t, false);
+                            }
+                        }
+                        t = __builtin_fmaf(t16, 0.0625f, t);
+                        acc[r][u] = __builtin_fmaf(s24[u][s], t, acc[r][u]);
+                        acc[r][u] = __builtin_fmaf(szs[u][s], asum[s], acc[r][u]);
+                    }
+                }
+            }
+            // The compiler would otherwise sink rows 1.. of every chunk below the last chunk and
+            // hold all of their activations (227 VGPRs at four int4 rows and three chunks: two
+            // wavefronts per SIMD, 3-4x slower): the chunk's sums are finished here.
+#pragma unroll
+            for (int r = 0; r < MR; ++r)
+#pragma unroll
+                for (int u = 0; u < U; ++u) asm volatile("" : "+v"(acc[r][u]));
         }
     }
 #pragma unroll
@@ -389,7 +489,7 @@ hipError_t stream_cpl(const StreamConfig& c, const f16* A, const uint8_t* B, con
     if (c.cpl <= 2) return stream_go<BITS, BS, HAS_ZP, MR, 2, U>(c, A, B, S, Z, Y, m, n, k, st);
     if (c.cpl <= 3) return stream_go<BITS, BS, HAS_ZP, MR, 3, U>(c, A, B, S, Z, Y, m, n, k, st);
     if (c.cpl <= 4) return stream_go<BITS, BS, HAS_ZP, MR, 4, U>(c, A, B, S, Z, Y, m, n, k, st);
-    if constexpr (U == 1 && MR == 1) {
+    if constexpr (U == 1) {
         if (c.cpl <= 6) return stream_go<BITS, BS, HAS_ZP, MR, 6, U>(c, A, B, S, Z, Y, m, n, k, st);
         if (c.cpl <= 8) return stream_go<BITS, BS, HAS_ZP, MR, 8, U>(c, A, B, S, Z, Y, m, n, k, st);
     }

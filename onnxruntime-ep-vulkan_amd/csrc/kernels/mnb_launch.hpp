@@ -36,7 +36,7 @@ struct StreamConfig {
     int64_t lds;         // dynamic LDS bytes (derived)
 };
 
-bool gemv_stream_supported(int64_t m, int64_t k, int bits, int bs);
+bool gemv_stream_supported(int64_t m, int64_t n, int64_t k, int bits, int bs);
 StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int bs);
 hipError_t launch_gemv_stream(const void* a, const uint8_t* b, const void* s, const uint8_t* z,
                               void* y, int64_t m, int64_t n, int64_t k, int bits, int bs,

@@ -184,7 +184,7 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     }
     const bool f16 = p->dtype == MNB_DTYPE_F16;
     const bool fast = f16 && mnb::gemv_supported(p->k, p->bits, p->block_size);
-    const bool stream = f16 && mnb::gemv_stream_supported(p->m, p->k, p->bits, p->block_size);
+    const bool stream = f16 && mnb::gemv_stream_supported(p->m, p->n, p->k, p->bits, p->block_size);
     const bool group = f16 && mnb::group_gemv_supported(p->k, p->bits, p->block_size);
     const bool gemm = f16 && mnb::gemm_supported(p->m, p->n, p->k, p->bits, p->block_size,
                                                   p->has_zero_points != 0);

@@ -142,6 +142,10 @@ SHAPES = [
     (2, 128, 3072, 4, 32, False),
     (3, 48, 2880, 4, 32, True),        # K not a multiple of the 128-weight wave step
     (4, 80, 640, 8, 32, True),
+    (4, 96, 8192, 4, 32, True),        # four int4 rows at K=8192: two row-tiles of two rows
+    (2, 72, 8192, 8, 32, True),        # int8 at K=8192: one-row tiles
+    (3, 40, 8192, 4, 64, False),       # three rows, four chunks per lane
+    (4, 48, 16384, 4, 32, True),       # four one-row tiles
     (5, 64, 512, 8, 16, False),
     (7, 32, 256, 8, 64, True),
     (8, 160, 1024, 8, 128, False),
