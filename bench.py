@@ -12,6 +12,7 @@ into a HIP graph and replayed, so the figure is the device's, not Python's launc
 value = algorithmic bytes of the layer set (65,568,768 B) per step / step time, in GB/s.
 The line also carries, measured in the same run:
   roofline      the dominant decode kernel's algorithmic bytes / its HIP-event launch time vs 8 TB/s
+  batched_decode  the same layer set at M = 4, 8, 16 rows in GB/s of algorithmic bytes
   prefill       MatMulNBits M=2048, K=3072, N=8192 in TFLOP/s vs 2.5 PFLOP/s fp16
   accuracy_level_4  configs[4] (M=16, K=8192, N=3072, bs128, zp, int8 activations) in GB/s
   moe           configs[3] (32 experts, top-4 of 64 tokens, gate_up and down) in GB/s
@@ -441,6 +442,42 @@ def main() -> int:
                 "read_floor_shape": floors[dom][1],
                 "frac_of_read_floor": round(floors[dom][0] / kern_us[dom], 4)}
 
+    # Batched decode: the same layer set at 4, 8 and 16 rows (the north star's M = 1..16 decode
+    # range; not part of `value`).  Per node, HIP events around a graph of `reps` launches with
+    # the weights rotated as in the step; the layer time is the sum over the four nodes.
+    bacts = [torch.randn(16, k, device=dev, generator=gen).to(torch.float16) for _, k, _ in LAYER]
+    bouts = [torch.empty(16, n, dtype=torch.float16, device=dev) for _, _, n in LAYER]
+    batched = []
+    for bm in (4, 8, 16):
+        bprobs = [mnb.problem(bm, n, k, BITS, BS, True) for _, k, n in LAYER]
+
+        def blaunch(i, layer, sp, bprobs=bprobs):
+            B, S, Z = layers[layer][i]
+            rc = lib.mnb_matmul_nbits(C.byref(bprobs[i]), bacts[i].data_ptr(), B.data_ptr(),
+                                      S.data_ptr(), Z.data_ptr(), bouts[i].data_ptr(), None, 0, sp)
+            if rc:
+                mnb.check(rc)
+        node_us = []
+        for i in range(len(LAYER)):
+            g1 = capture(lambda sp, i=i: [blaunch(i, r % copies, sp) for r in range(reps)])
+            g1.replay()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record(stream)
+            g1.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            node_us.append(1e3 * a.elapsed_time(b) / reps)
+            del g1
+        bbytes = sum(node_bytes(bm, k, n) for _, k, n in LAYER)
+        batched.append({"M": bm, "layer_us": round(sum(node_us), 3),
+                        "GB/s": round(bbytes / (sum(node_us) * 1e-6) / 1e9, 1),
+                        "frac_hbm": round(bbytes / (sum(node_us) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        "node_us": {LAYER[i][0]: round(u, 3) for i, u in enumerate(node_us)},
+                        "kernels": sorted({mnb.KERNEL_NAMES.get(mnb.plan(bp).kernel, "?")
+                                           for bp in bprobs})})
+    del bacts, bouts
+
     # Prefill: M in {256, 512, 2048}, K=3072, N=8192, implicit zero point
     # (not part of `value`).  HIP events around a graph of `preps` launches; weights rotate over
     # two copies so consecutive launches do not reuse an L2-resident B.
@@ -782,6 +819,7 @@ def main() -> int:
                    "rotated_bytes": per_layer * copies},
         "roofline": roofline,
         "per_kernel": per_kernel,
+        "batched_decode": batched,
         "prefill": prefill,
         "prefill_8bit": prefill_8bit,
         "mfma_calibration": mfma_cal,

@@ -59,6 +59,8 @@ extern "C" {
                                     registers across a run of 16-column strips */
 #define MNB_KERNEL_ACC4_STREAM 8 /* accuracy_level 4, fp16, <= 16 rows, K % 128 == 0 up to 8192:
                                     int8 MFMA, one 16-column strip per workgroup over all of K */
+#define MNB_KERNEL_BATCH_STREAM 9 /* fp16, int4, block >= 32, 4..16 rows, K % 128 == 0: f16 MFMA,
+                                     1 or 4 16-column strips per workgroup over all of K */
 
 /* One MatMulNBits node: the attributes plus the row count of this call. */
 typedef struct mnb_problem {

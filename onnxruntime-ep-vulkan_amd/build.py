@@ -55,6 +55,7 @@ HIP_SOURCES = [
     CSRC / "kernels" / "mnb_group_gemv.hip",
     CSRC / "kernels" / "mnb_strip_gemv.hip",
     CSRC / "kernels" / "mnb_acc4_stream.hip",
+    CSRC / "kernels" / "mnb_batch_stream.hip",
     CSRC / "kernels" / "mnb_gemv_stream.hip",
     CSRC / "kernels" / "mnb_gemv_stream_b4.hip",
     CSRC / "kernels" / "mnb_gemv_stream_b8.hip",

@@ -1,0 +1,264 @@
+// Batched decode at 4..16 fp16 rows: fp16 activations x int4 weights on gfx950 MFMA, S 16-column
+// strips per workgroup over the whole of K.
+//
+// A workgroup of KW wavefronts owns S consecutive strips of 16 columns; wavefront w owns quads
+// [w R, w R + R) of K (a quad is 128 k; KW R = K / 128) of all S strips.  Every lane first
+// requests the activations it multiplies -- as the v_mfma_f32_16x16x32_f16 A operand, lane (n, g) takes row n
+// (rows past M repeat row M - 1 and are never stored), k = 32 c + 8 g .. + 7 of each 32-k chunk c:
+// 16 bytes, straight into registers, no LDS, used for all S strips -- then its columns' block
+// scales and zero points for the wavefront's quads (one contiguous run per column), then its S R
+// 16-byte weight loads (lane (n, g): chunk 4 q + g of column n of each strip, streamed past the
+// caches).  So nothing waits for another wavefront until the end, and the activations, needed
+// first, are not queued behind the weights.
+// Per quad a 4 x 4 dword transpose across the lane rows leaves lane (n, g) holding, for each chunk
+// c, the eight weights k = 32 c + 8 g .. + 7 of column n -- the B operand -- which become exact
+// fp16 (q - zp) values; the MFMAs of one quant block accumulate its exact-product fp32 partial,
+// scaled by the block's scale into the lane's accumulator (the reference's per-block fp32 partial
+// scaled once, rust/shaders/glsl/templates/q_gemv.comp:571-579).  The KW partial tiles are added
+// in LDS in wavefront order (run-to-run deterministic) and stored as fp16.
+//
+// Each workgroup reads all of A (16 rows x K x 2 bytes, from L2): the price of having no
+// cross-workgroup reduction; S strips per workgroup divide that traffic by S (one strip per
+// workgroup read 96 KB of A per 24 KB of weights at K = 3072 and ran the 16-row gate_up at
+// 19 us, slower than the strip GEMV).
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "mnb_common.hpp"
+#include "mnb_launch.hpp"
+
+namespace mnb {
+
+namespace {
+
+constexpr int kBatchMaxWaves = 16;
+
+template <int BS, bool HAS_ZP, int R, int S>
+__global__ void __launch_bounds__(64 * kBatchMaxWaves)
+batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ Sc,
+             const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K) {
+    constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
+    constexpr int BPQ = 4 / CPB;                         // blocks per quad
+    extern __shared__ f32x4 sRed[];                      // [KW - 1][S][64]
+    const int lane = threadIdx.x & 63;
+    const int kw = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int KW = blockDim.x >> 6;
+    const int nl = lane & 15;
+    const int g = lane >> 4;
+    const int bpc = K / BS;                              // a multiple of 4
+    const int zpb = bpc >> 1;
+    const int strip0 = blockIdx.x * S;
+    const int q0 = kw * R;                               // this wavefront's first quad
+
+    // ---- 1. the activations of the wavefront's quads, as MFMA A operands ---------------------
+    const f16* ar = A + (int64_t)min(nl, M - 1) * K + 128 * q0 + 8 * g;
+    f16x8 av[R][4];
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            av[j][c] = *reinterpret_cast<const f16x8*>(ar + 128 * j + 32 * c);
+
+    // ---- 2. the columns' block scales and zero points for those quads ----------------------
+    constexpr int NS = R * BPQ;                          // blocks of the wavefront's quads
+    constexpr int NZ = (NS + 1) / 2;
+    const int b0 = q0 * BPQ;                             // first block; even unless NS == 1
+    uint16_t sv[S][NS];
+    uint8_t zv[S][NZ];
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        const int col = min(16 * (strip0 + t) + nl, N - 1);
+        const uint16_t* sp = reinterpret_cast<const uint16_t*>(Sc) + (int64_t)col * bpc + b0;
+        const uint8_t* zp = HAS_ZP ? Z + (int64_t)col * zpb + (b0 >> 1) : nullptr;
+        if constexpr (NS % 4 == 0) {
+            // 8-byte and 2-byte aligned: bpc % 4 == 0, b0 % 4 == 0, the launcher checks the bases
+#pragma unroll
+            for (int i = 0; i < NS / 4; ++i) {
+                const u32x2 v = *reinterpret_cast<const u32x2*>(sp + 4 * i);
+                sv[t][4 * i] = (uint16_t)v.x;
+                sv[t][4 * i + 1] = (uint16_t)(v.x >> 16);
+                sv[t][4 * i + 2] = (uint16_t)v.y;
+                sv[t][4 * i + 3] = (uint16_t)(v.y >> 16);
+            }
+            if constexpr (HAS_ZP) {
+#pragma unroll
+                for (int i = 0; i < NZ / 2; ++i) {
+                    const uint16_t v = *reinterpret_cast<const uint16_t*>(zp + 2 * i);
+                    zv[t][2 * i] = (uint8_t)v;
+                    zv[t][2 * i + 1] = (uint8_t)(v >> 8);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NS; ++i) sv[t][i] = sp[i];
+            if constexpr (HAS_ZP) {
+#pragma unroll
+                for (int i = 0; i < NZ; ++i) zv[t][i] = zp[i];
+            }
+        }
+    }
+
+    // ---- 3. the wavefront's weights ----------------------------------------------------------
+    u32x4 bw[S][R];
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        const int col = min(16 * (strip0 + t) + nl, N - 1);
+        const uint8_t* bc = B + (int64_t)col * (K / 2);
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+            bw[t][j] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(bc + 16 * (int64_t)(4 * (q0 + j) + g)));
+    }
+
+    // ---- 4. each strip's partial tile over this wavefront's quads ----------------------------
+    f32x4 acc[S];
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            uint32_t v0 = bw[t][j].x, v1 = bw[t][j].y, v2 = bw[t][j].z, v3 = bw[t][j].w;
+            transpose_rows(v0, v1, v2, v3);
+            const uint32_t wt[4] = {v0, v1, v2, v3};
+            f32x4 dot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int bi = j * BPQ + c / CPB;        // block within the wavefront's range
+                int z = 8;
+                if constexpr (HAS_ZP)
+                    z = (int)((zv[t][(bi + (b0 & 1)) >> 1] >> (((b0 + bi) & 1) * 4)) & 0xFu);
+                const f16x2 zo = zoff4(z);
+                f16x8 bq;
+                bq.s01 = nib_pair<0>(wt[c], zo);
+                bq.s23 = nib_pair<1>(wt[c], zo);
+                bq.s45 = nib_pair<2>(wt[c], zo);
+                bq.s67 = nib_pair<3>(wt[c], zo);
+                dot = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j][c], bq, dot, 0, 0, 0);
+                if ((c + 1) % CPB == 0) {                // block end: scale it
+                    const float sb = (float)__builtin_bit_cast(f16, sv[t][bi]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[t][q] = __builtin_fmaf(dot[q], sb, acc[t][q]);
+                    dot = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+    }
+
+    // ---- 5. the KW partial tiles in wavefront order, stored by wavefront 0 -----------------
+    if (kw > 0) {
+#pragma unroll
+        for (int t = 0; t < S; ++t) sRed[((kw - 1) * S + t) * 64 + lane] = acc[t];
+    }
+    __syncthreads();
+    if (kw > 0) return;
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+        for (int w = 1; w < KW; ++w) acc[t] += sRed[((w - 1) * S + t) * 64 + lane];
+        const int cc = 16 * (strip0 + t) + nl;
+        if (cc >= N) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = 4 * g + q;                     // MFMA output: rows 4g .. 4g + 3
+            if (r < M) Y[(int64_t)r * N + cc] = (f16)acc[t][q];
+        }
+    }
+}
+
+template <int BS, bool HAS_ZP, int S>
+hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b, const void* s,
+                      const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+    const dim3 grid((unsigned)g.gx, 1, 1);
+    const dim3 block((unsigned)(64 * g.waves), 1, 1);
+    const size_t lds = (size_t)(g.waves - 1) * S * 64 * sizeof(f32x4);
+    // instantiated for S R <= 8 only (the geometry's register budget)
+#define MNB_BS(R_)                                                                                \
+    if constexpr (S * R_ <= 8) {                                                                  \
+        hipLaunchKernelGGL((batch_stream<BS, HAS_ZP, R_, S>), grid, block, lds, st,              \
+                           static_cast<const f16*>(a), b, static_cast<const f16*>(s), z,          \
+                           static_cast<f16*>(y), (int)m, (int)n, (int)k);                         \
+    } else {                                                                                      \
+        return hipErrorInvalidValue;                                                              \
+    }
+    switch (g.r) {
+        case 1: MNB_BS(1); break;
+        case 2: MNB_BS(2); break;
+        case 3: MNB_BS(3); break;
+        case 4: MNB_BS(4); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef MNB_BS
+    return hipGetLastError();
+}
+
+template <int BS, bool HAS_ZP>
+hipError_t batch_go(const BatchStreamGeom& g, const void* a, const uint8_t* b, const void* s,
+                    const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+    switch (g.s) {
+        case 1: return batch_go_s<BS, HAS_ZP, 1>(g, a, b, s, z, y, m, n, k, st);
+        case 2: return batch_go_s<BS, HAS_ZP, 2>(g, a, b, s, z, y, m, n, k, st);
+        case 4: return batch_go_s<BS, HAS_ZP, 4>(g, a, b, s, z, y, m, n, k, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamGeom* out) {
+    if (m < 1 || m > 16 || n < 1 || k < 128 || k % 128 || (bs != 32 && bs != 64 && bs != 128))
+        return false;
+    if ((k / bs) % 4) return false;                      // whole 4-block groups of scales
+    const int64_t quads = k / 128;
+    const int64_t strips = (n + 15) / 16;
+    BatchStreamGeom g{};
+    // S strips per workgroup (each wavefront's activation registers serve all S): 4 from 1024
+    // strips, else 1.  Measured at 5..16 rows: 16384 columns (1024 strips) 18.9 -> 14.4 us at
+    // S = 4; 9216 columns (576 strips) slower at S = 2 (fewer workgroups in flight) than at 1.
+    g.s = strips >= 4 * 256 ? 4 : 1;
+    // R quads per wavefront (16 R activation VGPRs, 4 S R weight VGPRs: S R <= 8 keeps the
+    // instantiations within 128): among 1..4 dividing the quads into at most 16 wavefronts, the
+    // one closest to 8 wavefronts (the larger R on a tie).
+    g.r = 0;
+    int64_t best = 0;
+    for (int r : {4, 3, 2, 1}) {
+        if (quads % r || quads / r > kBatchMaxWaves || g.s * r > 8) continue;
+        const int64_t d = std::abs(quads / r - 8);
+        if (g.r == 0 || d < best) {
+            g.r = r;
+            best = d;
+        }
+    }
+    if (g.r == 0) return false;
+    g.waves = (int)(quads / g.r);
+    g.gx = (strips + g.s - 1) / g.s;
+    if (g.gx > 0x7fffffff) return false;
+    *out = g;
+    return true;
+}
+
+bool batch_stream_aligned(const void* a, const uint8_t* b, const void* s, const uint8_t* z) {
+    return reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(s) % 8 == 0 && reinterpret_cast<uintptr_t>(z) % 2 == 0;
+}
+
+hipError_t launch_batch_stream(const BatchStreamGeom& g, const void* a, const uint8_t* b,
+                               const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
+                               int64_t k, int bs, hipStream_t st) {
+    // waves * R == K / 128: every quad of K belongs to exactly one wavefront
+    BatchStreamGeom want{};
+    if (!batch_stream_geometry(m, n, k, bs, &want) || want.r != g.r || want.s != g.s ||
+        want.waves != g.waves || want.gx != g.gx || !batch_stream_aligned(a, b, s, z))
+        return hipErrorInvalidValue;
+#define MNB_BS_ZP(BS_)                                                                            \
+    return z ? batch_go<BS_, true>(g, a, b, s, z, y, m, n, k, st)                                 \
+             : batch_go<BS_, false>(g, a, b, s, z, y, m, n, k, st)
+    switch (bs) {
+        case 32: MNB_BS_ZP(32);
+        case 64: MNB_BS_ZP(64);
+        case 128: MNB_BS_ZP(128);
+        default: return hipErrorInvalidValue;
+    }
+#undef MNB_BS_ZP
+}
+
+}  // namespace mnb

@@ -171,6 +171,21 @@ bool acc4_stream_aligned(const void* qa, const uint8_t* b, const void* s, const 
 hipError_t launch_acc4_stream(const Acc4StreamGeom& g, const int8_t* qa, const float* a_scale,
                               const uint8_t* b, const void* s, const uint8_t* z, void* y,
                               int64_t m, int64_t n, int64_t k, int bs, hipStream_t stream);
+// Batched decode at up to 16 fp16 rows, int4 weights (mnb_batch_stream.hip): s 16-column
+// strips per workgroup over all of K, `waves` wavefronts of r quads each (waves * r == K / 128),
+// activations loaded straight into MFMA registers.  K % 128 == 0, (K / bs) % 4 == 0, bs >= 32.
+struct BatchStreamGeom {
+    int r;               // 128-k quads per wavefront: 1..4
+    int s;               // 16-column strips per workgroup: 1, 2 or 4
+    int waves;           // wavefronts per workgroup, K / (128 r), 1..16
+    int64_t gx;          // workgroups: ceil(strips / s)
+};
+bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamGeom* out);
+// A and B 16-byte, scales 8-byte, zero points 2-byte aligned.
+bool batch_stream_aligned(const void* a, const uint8_t* b, const void* s, const uint8_t* z);
+hipError_t launch_batch_stream(const BatchStreamGeom& g, const void* a, const uint8_t* b,
+                               const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
+                               int64_t k, int bs, hipStream_t stream);
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                        int bs, void* workspace, hipStream_t stream);

@@ -39,8 +39,9 @@ KERNEL_GEMV_STREAM = 5
 KERNEL_GROUP_MFMA = 6
 KERNEL_STRIP_MFMA = 7
 KERNEL_ACC4_STREAM = 8
+KERNEL_BATCH_STREAM = 9
 KERNEL_NAMES = {1: "gemv_mfma", 2: "gemm_mfma", 3: "generic", 4: "acc4_i8", 5: "gemv_stream",
-                6: "group_mfma", 7: "strip_mfma", 8: "acc4_stream"}
+                6: "group_mfma", 7: "strip_mfma", 8: "acc4_stream", 9: "batch_stream"}
 
 
 class Problem(C.Structure):

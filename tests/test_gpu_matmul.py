@@ -35,7 +35,7 @@ def _dev(x, device):
 
 
 # MNB_FORCE_KERNEL values and the planner kernel each one selects.
-FORCED = {"stream": 5, "gemv": 1, "gemm": 2, "generic": 3, "group": 6, "strip": 7}
+FORCED = {"stream": 5, "gemv": 1, "gemm": 2, "generic": 3, "group": 6, "strip": 7, "batch": 9}
 
 
 def _forced_kernel(M, N, K, bits, bs, zp, kernel):
@@ -147,6 +147,12 @@ SHAPES = [
     (3, 40, 8192, 4, 64, False),       # three rows, four chunks per lane
     (4, 48, 16384, 4, 32, True),       # four one-row tiles
     (5, 64, 512, 8, 16, False),
+    (5, 9216, 3072, 4, 32, True),      # qkv at five rows: the batched decode kernel
+    (7, 40, 1024, 4, 64, True),
+    (12, 33, 2048, 4, 128, False),     # partial strip
+    (16, 3072, 8192, 4, 32, True),     # sixteen wavefronts of four quads
+    (6, 8200, 1024, 4, 64, True),      # two strips per workgroup, last strip partial
+    (9, 16400, 512, 4, 32, False),     # four strips per workgroup, last workgroup short
     (7, 32, 256, 8, 64, True),
     (8, 160, 1024, 8, 128, False),
     (9, 64, 4096, 4, 32, True),

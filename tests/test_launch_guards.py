@@ -69,7 +69,7 @@ def test_planner_shapes_stay_within_compiled_bounds():
     bounds = {mnb.KERNEL_GEMV_STREAM: 1024, mnb.KERNEL_GROUP_MFMA: 512,
               mnb.KERNEL_GEMV_MFMA: 1024, mnb.KERNEL_GEMM_MFMA: 512, mnb.KERNEL_ACC4_I8: 1024,
               mnb.KERNEL_STRIP_MFMA: 1024, mnb.KERNEL_GENERIC: 256,
-              mnb.KERNEL_ACC4_STREAM: 1024}
+              mnb.KERNEL_ACC4_STREAM: 1024, mnb.KERNEL_BATCH_STREAM: 1024}
     for m in (1, 2, 3, 4, 5, 8, 16, 17, 33, 64, 65, 256, 2048):
         for k, n in ((3072, 9216), (8192, 3072), (2880, 2880), (128, 48)):
             for bits in (4, 8):
