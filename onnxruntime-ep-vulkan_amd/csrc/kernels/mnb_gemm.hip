@@ -119,7 +119,7 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS bases in SGPRs
     const int wm = wave >> 1;
     const int wn = wave & 1;
 
@@ -144,41 +144,42 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
     const int64_t col_bytes = (int64_t)K * BITS / 8;
     auto gcol = [&](int c) { const int g = n0 + c; return g < N ? g : N - 1; };
 
-    // ---- DMA sources: A (4 instructions per wavefront) ----
-    const f16* a_src[4];
+    // ---- DMA sources: A (4 instructions per wavefront).  Each address is a uniform base (the
+    // step's k offset, in SGPRs) plus this lane's 32-bit byte offset, so a step's requests cost
+    // no 64-bit vector adds (the host keeps A and B below 4 GiB). ----
+    uint32_t a_off[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int row = 32 * wave + 8 * j + (lane >> 3);
         const int kc = (lane & 7) ^ swz(row);
         int gm = m0 + row;
         gm = gm < M ? gm : M - 1;                    // clamped rows are never stored
-        a_src[j] = A + (int64_t)gm * K + 8 * kc;
+        a_off[j] = (uint32_t)(((int64_t)gm * K + 8 * kc) * 2);
     }
     // raw B (wavefronts 0-3; instruction j of lane l: the 16-byte piece that lands at
     // 1 KB * (kRawDma * wave + j) + 16 l, i.e. column (that offset) / bytes-per-column) or the
     // scale and zero-point dwords (wavefronts 4-7)
     constexpr int kColStep = kKS * BITS / 8;         // raw bytes per column and step: 32 or 64
-    const uint8_t* b_src[F::kRawDma];
-    int b_piece[F::kRawDma];
+    uint32_t b_off[F::kRawDma];
 #pragma unroll
     for (int j = 0; j < F::kRawDma; ++j) {
         const int off = 1024 * (F::kRawDma * (wave & 3) + j) + 16 * lane;
-        b_src[j] = B + (int64_t)gcol(off / kColStep) * col_bytes;
-        b_piece[j] = off % kColStep;
+        b_off[j] = (uint32_t)((int64_t)gcol(off / kColStep) * col_bytes + off % kColStep);
     }
 
     auto issue_a = [&](int step, int st) {
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(A) + (int64_t)(s0 + step) * kKS * 2;
         uint8_t* dst = sA + st * kAStage + wave * 4 * 1024;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dma16(a_src[j] + (s0 + step) * kKS, dst + j * 1024);
+        for (int j = 0; j < 4; ++j) dma16(src + a_off[j], dst + j * 1024);
     };
     auto issue_r = [&](int step, int st) {
         uint8_t* base = sR + st * F::kRStage;
         if (wave < 4) {
+            const uint8_t* src = B + (int64_t)(s0 + step) * kColStep;
 #pragma unroll
             for (int j = 0; j < F::kRawDma; ++j)
-                dma16(b_src[j] + (s0 + step) * kColStep + b_piece[j],
-                      base + 1024 * (F::kRawDma * wave + j));
+                dma16(src + b_off[j], base + 1024 * (F::kRawDma * wave + j));
         } else {
             const int blk0 = ((s0 + step) * kKS) / BS;
 #pragma unroll
@@ -284,6 +285,22 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
         asm volatile("" : "+v"(acc[t]));             // keep the adds here, beside the MFMAs
     };
 
+    // Lane parts of the operand addresses, fixed for the whole loop, so that a step adds its
+    // stage base once per address family and every read takes the rest as an immediate offset.
+    // A: row r = 64 wm + 32 i + (lane & 31) holds chunk kc = 2 p + (lane >> 5) (p = 2 sub + h)
+    // at slot kc ^ swz(r); swz depends on bits 0-3 of r only, i.e. on the lane, so the 32-row
+    // half i is + 4096 bytes and p needs one offset each.  (q - z): chunk kc of column
+    // c = 64 wn + 32 j + (lane & 31) at (128 kc + c) * 16 = p * 4096 + j * 512 + lane part.
+    // Scales: 8 bytes per column after the (q - z) values, + 256 bytes per j.
+    int a_lane[4];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+        const int r = wm * 64 + (lane & 31);
+        a_lane[pp] = (r * 8 + ((2 * pp + (lane >> 5)) ^ swz(r))) * 16;
+    }
+    const int b_lane = ((lane >> 5) * 128 + wn * 64 + (lane & 31)) * 16;
+    const int s_lane = kFQ + (wn * 64 + (lane & 31)) * 8;
+
     auto compute = [&](int ast, int fst, auto&& between) {
         const uint8_t* a_base = sA + ast * kAStage;
         const uint8_t* f_base = sF + fst * kFStage;
@@ -291,28 +308,23 @@ gemm_f16_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f1
         auto load_sub = [&](int sub) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int kc = 2 * (2 * sub + h) + (lane >> 5);
+                const int pp = 2 * sub + h;
+                const uint8_t* ap = a_base + a_lane[pp];
+                const uint8_t* bp = f_base + b_lane;
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int row = wm * 64 + 32 * i + (lane & 31);
-                    a[sub][i][h] = *reinterpret_cast<const f16x8*>(
-                        a_base + (row * 8 + (kc ^ swz(row))) * 16);
-                }
+                for (int i = 0; i < 2; ++i)
+                    a[sub][i][h] = *reinterpret_cast<const f16x8*>(ap + 4096 * i);
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int col = wn * 64 + 32 * j + (lane & 31);
-                    b[sub][j][h] = *reinterpret_cast<const f16x8*>(f_base + (kc * 128 + col) * 16);
-                }
+                for (int j = 0; j < 2; ++j)
+                    b[sub][j][h] = *reinterpret_cast<const f16x8*>(bp + 4096 * pp + 512 * j);
             }
         };
         // the step's block scales of the wavefront's two 32-column halves, [j][slot]
         u32x2 sw[2];
         auto load_scales = [&]() {
+            const uint8_t* sp = f_base + s_lane;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int c = wn * 64 + 32 * j + (lane & 31);
-                sw[j] = *reinterpret_cast<const u32x2*>(f_base + kFQ + c * 8);
-            }
+            for (int j = 0; j < 2; ++j) sw[j] = *reinterpret_cast<const u32x2*>(sp + 256 * j);
         };
         auto scale_of = [&](int j, int slot) {
             const uint32_t w = slot < 2 ? sw[j].x : sw[j].y;
@@ -473,6 +485,8 @@ bool gemm_supported(int64_t m, int64_t n, int64_t k, int bits, int bs, bool has_
     if (bs > 32 && (n * bpc) % 2) return false;
     const int64_t zpb = bits == 8 ? bpc : (bpc + 1) / 2;
     if (has_zp && (n * zpb) % 4) return false;
+    // The DMA sources are a uniform base plus a 32-bit byte offset per lane.
+    if (m * k * 2 >= (int64_t)1 << 32 || n * k * bits / 8 >= (int64_t)1 << 32) return false;
     return true;
 }
 
