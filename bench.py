@@ -279,8 +279,13 @@ def main() -> int:
                                            pS.data_ptr(), None, pY.data_ptr(), pws.data_ptr(),
                                            pwsb, sptr))
         torch.cuda.synchronize()
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
         print(f"pmc mode: {args.steps} launches of the prefill GEMM M={pm} K={pk} N={pn} "
-              f"({mnb.KERNEL_NAMES.get(mnb.plan(pprob).kernel)})")
+              f"({mnb.KERNEL_NAMES.get(mnb.plan(pprob).kernel)}), then one copy of "
+              f"{src.numel()} bytes")
         return 0
 
     if args.pmc_launch:

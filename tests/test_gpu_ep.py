@@ -49,6 +49,7 @@ def _check(y, ref, what):
     ((2, 3), 160, 1024, 4, 64, True),          # leading dims fold into M = 6
     ((7,), 48, 256, 8, 16, False),
     ((33,), 96, 512, 4, 128, True),            # MFMA GEMV row tiles
+    ((2, 4), 3072, 3072, 4, 32, True),         # batched decode: 8 rows of o_proj
 ])
 def test_compute_matches_oracle(host, lead, N, K, bits, bs, zp):
     print(f"[gpu] ep lead={lead} N={N} K={K} bits={bits} bs={bs} zp={zp}", flush=True)
