@@ -119,11 +119,15 @@ def test_three_runs_bit_identical_and_row_count_changes(host):
         outs.append(host.fetch(y_name, np.float16, 4 * N).copy())
     assert all(np.array_equal(outs[0].view(np.uint16), o.view(np.uint16)) for o in outs[1:])
     assert not np.array_equal(outs[0][0], outs[0][1])
-    # a different row count through the same compiled node (symbolic batch)
+    # a different row count through the same compiled node (symbolic batch): one row runs the
+    # streaming GEMV, four rows the batched MFMA kernel, which sums in another order -- equal
+    # to the fp16 bar, not bit for bit
     host.feed(a_name, inp["A"][:1])
     assert host.compute(0) == 0, mh.err()
     y1 = host.fetch(y_name, np.float16, N)
-    assert np.array_equal(y1.reshape(-1).view(np.uint16), outs[0][0].view(np.uint16))
+    _check(y1.reshape(1, N), outs[0][0].reshape(1, N).astype(np.float64), "one row vs four")
+    ref = orc.matmul_nbits(inp["A"][:1], inp["B"], inp["scales"], inp["zp"], N, K, 4, 32)
+    _check(y1.reshape(1, N), ref, "one row")
     # zero rows: an empty output, no launch
     host.feed(a_name, inp["A"][:0])
     assert host.compute(0) == 0, mh.err()

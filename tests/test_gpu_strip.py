@@ -36,8 +36,28 @@ def _check(y, ref, what, tol=F16_TOL):
     assert e1 <= tol and e2 <= tol, f"{what}: rel_sig={e1:.3e} rms_norm={e2:.3e}"
 
 
+def _forced(kernel):
+    """Context manager setting MNB_FORCE_KERNEL (read on every plan) for the block."""
+    import contextlib
+    import os
+
+    @contextlib.contextmanager
+    def cm():
+        old = os.environ.get("MNB_FORCE_KERNEL")
+        os.environ["MNB_FORCE_KERNEL"] = kernel
+        try:
+            yield
+        finally:
+            if old is None:
+                os.environ.pop("MNB_FORCE_KERNEL", None)
+            else:
+                os.environ["MNB_FORCE_KERNEL"] = old
+    return cm()
+
+
 STRIP_SHAPES = [
-    # (M, N, K, bs, zp, strip): strip = the planner picks the strip kernel
+    # (M, N, K, bs, zp, strip): strip = the strip kernel takes the shape when asked for
+    # (MNB_FORCE_KERNEL=strip; by default the batched decode kernel takes K % 128 == 0)
     (5, 64, 256, 32, True, True),
     (8, 104, 2880, 32, False, True),     # gpt-oss K: a partial last quad; N ragged (6.5 strips)
     (8, 100, 2880, 32, True, True),      # 45-byte zero-point rows: staged without 16-byte pieces
@@ -56,12 +76,13 @@ def test_strip_gemv_parity(cuda, M, N, K, bs, zp, strip):
     import mnb
     import torch
     print(f"[gpu] strip M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
-    info = mnb.plan(mnb.problem(M, N, K, 4, bs, zp))
-    assert info.kernel == (mnb.KERNEL_STRIP_MFMA if strip else mnb.KERNEL_GROUP_MFMA)
-    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=M + 7 * N)
-    y = mnb.matmul_nbits(_dev(inp["A"], cuda), _dev(inp["B"], cuda), _dev(inp["scales"], cuda),
-                         _dev(inp["zp"], cuda), N, K, 4, bs)
-    torch.cuda.synchronize()
+    with _forced("strip" if strip else "group"):
+        info = mnb.plan(mnb.problem(M, N, K, 4, bs, zp))
+        assert info.kernel == (mnb.KERNEL_STRIP_MFMA if strip else mnb.KERNEL_GROUP_MFMA)
+        inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=M + 7 * N)
+        y = mnb.matmul_nbits(_dev(inp["A"], cuda), _dev(inp["B"], cuda),
+                             _dev(inp["scales"], cuda), _dev(inp["zp"], cuda), N, K, 4, bs)
+        torch.cuda.synchronize()
     ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
     _check(y.cpu().numpy(), ref, f"strip M={M} N={N} K={K}")
 
@@ -69,7 +90,8 @@ def test_strip_gemv_parity(cuda, M, N, K, bs, zp, strip):
 def test_strip_runs_of_several_strips():
     import mnb
     # the planner groups strips into runs when there are many more strips than workgroups
-    info = mnb.plan(mnb.problem(7, 40000, 256, 4, 32, False))
+    with _forced("strip"):
+        info = mnb.plan(mnb.problem(7, 40000, 256, 4, 32, False))
     assert info.kernel == mnb.KERNEL_STRIP_MFMA and info.tile_n >= 32
 
 
