@@ -401,8 +401,8 @@ def main() -> int:
     eager_ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
     # Per-node launch duration: HIP events around a graph of `reps` back-to-back launches of one
-    # node (weights rotated as in the step), divided by `reps`: each launch's device time
-    # including the gap to the next launch on the stream.
+    # node (weights rotated as in the step: "cold", from HBM), divided by `reps`: each launch's
+    # device time including the gap to the next launch on the stream.
     reps = max(20, copies * 4)
     kern_us = []
     for i in range(len(LAYER)):
@@ -415,6 +415,20 @@ def main() -> int:
         b.record(stream)
         torch.cuda.synchronize()
         kern_us.append(1e3 * a.elapsed_time(b) / reps)
+        del g1
+    # The same launches on one weight copy every time ("hot": the 5-29 MB of weights stay in
+    # the 256 MB Infinity Cache), reported beside the rotated ("cold", HBM) times.
+    hot_us = []
+    for i in range(len(LAYER)):
+        g1 = capture(lambda sp, i=i: [launch(i, 0, sp) for _ in range(reps)])
+        g1.replay()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        g1.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        hot_us.append(1e3 * a.elapsed_time(b) / reps)
         del g1
 
     # The read floor of each node's byte count: the least time one launch of a kernel that does
@@ -432,6 +446,7 @@ def main() -> int:
         per_kernel.append({"node": name, "K": k, "N": n, "bytes": nb, "us": round(us, 3),
                            "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
                            "frac_hbm": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                           "hot_us": round(hot_us[i], 3),
                            "read_floor_us": round(floors[i][0], 3),
                            "frac_of_read_floor": round(floors[i][0] / us, 4),
                            "kernel": mnb.KERNEL_NAMES.get(mnb.plan(probs[i]).kernel, "?")})
