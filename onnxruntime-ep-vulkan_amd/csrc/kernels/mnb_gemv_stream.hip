@@ -55,14 +55,15 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     c.mr = m <= 1 ? 1 : (int)(m < 4 ? m : 4);
     // Lane-group width: the best-filled group (G * CPL chunk slots for cpc chunks); among equally
     // filled ones, the one that puts closest to 16 wavefronts on each CU (one per 64/G columns),
-    // 10 with several rows (each wavefront then reads MR rows of activations per chunk, so fewer,
-    // longer wavefronts win).  Measured on MI355X for the Phi-3.5 decode shapes: one row, qkv
-    // G=32 (18 per CU), gate_up G=16 (16 per CU) rather than G=32 (32 per CU); 2-4 rows, qkv and
-    // gate_up G=16, o G=32, down G=64.
+    // 10 with four rows (each wavefront then reads four rows of activations per chunk, so fewer,
+    // longer wavefronts win).  Measured on MI355X for the Phi-3.5 decode shapes: one to three
+    // rows, qkv G=32 (18 per CU; at two rows 6.4 us against 6.9 with G=16), gate_up G=16 (16
+    // per CU) rather than G=32 (32 per CU); four rows, qkv and gate_up G=16; o G=32 and down
+    // G=64 throughout.
     auto waves_per_cu = [&](int cand) {
         return (double)((n + 64 / cand - 1) / (64 / cand)) / kNumCUs;
     };
-    const double target = c.mr == 1 ? 16.0 : 10.0;
+    const double target = c.mr <= 3 ? 16.0 : 10.0;
     double best_fill = -1.0, best_dist = 0.0;
     int g = 64;
     for (int cand : {64, 32, 16}) {

@@ -4,11 +4,15 @@
 // weight loads in flight every memory request -- an L2 hit included -- waits behind that burst
 // (measured on MI355X: a 6 KB L2-resident read takes 0.4 us alone and 1.6-2.7 us while the other
 // workgroups stream).  Whatever a wavefront needs besides its own weights must therefore arrive
-// before the burst starts.  The launch is one to three workgroups per CU (up to 16 wavefronts
-// each); a workgroup first requests what its wavefronts share -- the MR activation rows (an L2 /
-// MALL hit) and its columns' scale and zero-point bytes (cold in HBM) -- stages the activations
-// in LDS as soon as they arrive, and only then issues its weights; the scale and zero-point
-// bytes, requested earlier, reach LDS behind a second barrier while the weights are in flight.
+// before the burst starts.  The launch is one to four workgroups per CU (up to 16 wavefronts
+// each); every thread first requests its share of what the workgroup's wavefronts share -- the
+// MR activation rows (an L2 / MALL hit) and the columns' scale and zero-point bytes (cold in
+// HBM) -- and each wavefront stages its activation share in LDS as soon as it arrives and then
+// issues its weights at once (all activation requests of the launch are out by then); the scale
+// and zero-point bytes reach LDS while the weights are in flight, and one workgroup barrier
+// precedes the compute.  Everything but the pairing and the stores -- the LDS offsets of the
+// staged units, the weight addresses -- is formed before the activations arrive: a wavefront's
+// VALU work between its activations' arrival and its weight requests delays the whole stream.
 // Each wavefront makes exactly one pass: it owns U
 // columns per lane group and issues all of their 16-byte weight loads at once.  The packed weight
 // of column n is K*bits/8 contiguous bytes (B is [N][K/bs][bs*bits/8]); a lane group of G lanes
@@ -147,13 +151,42 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
     // in-bounds unit whose value is not used), so the number of loads in flight is the same on
     // every path and waiting for the activations does not wait for the later requests.
     constexpr int AU = kStreamAU * MR;
+    // Unit u is row r = u / upr (found by comparisons: MR <= 4), chunk c = w / UPC and quarter
+    // (int4) or half (int8) q of that chunk, w = u - r upr.  Its LDS offsets -- the activations
+    // and its chunk's segment-sum slot -- are formed here, from the thread index alone, so that
+    // nothing but the pairing and the stores is left for when the activations arrive.
+    struct Place {
+        const f16* src;                                  // the unit's 8 activations
+        int dst;                                         // LDS offset of its pairs
+        int sum;                                         // LDS offset of its segment's sum
+        bool own;                                        // the unit stores that sum
+    };
+    auto place = [&](int u) {
+        int r = 0;
+#pragma unroll
+        for (int rr = 1; rr < MR; ++rr) r += u >= rr * upr ? 1 : 0;
+        const int w = u - r * upr;
+        const int c = w / UPC;
+        const int q = w - c * UPC;
+        const int cb = (r * cpc + c) * CST;
+        Place p;
+        p.src = A + (int64_t)min(m0 + r, M - 1) * K + (int64_t)w * 8;
+        p.dst = cb + 16 * q;
+        if constexpr (BITS == 4 && SEGS == 2) {          // block 16: two units per segment
+            p.sum = cb + 4 * NP + 4 * (q >> 1);
+            p.own = (q & 1) == 0;
+        } else {
+            p.sum = cb + 4 * NP;
+            p.own = q == 0;
+        }
+        return p;
+    };
     u32x4 av[AU];
+    Place pl[AU];
 #pragma unroll
     for (int i = 0; i < AU; ++i) {
-        const int u = min(tid + i * T, a_units - 1);
-        const int r = u / upr;
-        const int row = min(m0 + r, M - 1);
-        av[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)row * K + (int64_t)(u - r * upr) * 8);
+        pl[i] = place(min(tid + i * T, a_units - 1));
+        av[i] = *reinterpret_cast<const u32x4*>(pl[i].src);
     }
     const int s_units = vec_s ? s_bytes / 16 : 0;
     const int z_units = vec_z ? z_bytes / 16 : 0;
@@ -167,69 +200,57 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
         for (int i = 0; i < kStreamZU; ++i) zv[i] = z4[min(tid + i * T, max(z_units - 1, 0))];
     }
 
+    // The wavefront's weight addresses: lane (group grp, index gi) takes chunks gi, gi + G, ...
+    // of its U columns (clamped to the column's last chunk; a clamped chunk is not summed).
+    int lcol[U];
+    const uint8_t* bcol[U];
+    int boff[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        boff[j] = 16 * min(gi + j * G, cpc - 1);
+        asm volatile("" : "+v"(boff[j]));                // formed here, not after the staging
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int lc = (wave * ng + grp) * U + u;        // column within the workgroup
+        lcol[u] = lc;
+        bcol[u] = B + (int64_t)min(col0 + lc, N - 1) * col_bytes;
+    }
+
     // ---- stage the first batch into LDS ------------------------------------------------------
     const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
-    // Unit u: row r, chunk c, quarter (int4) or half (int8) q of the chunk.  The pairing and the
-    // unit's sum are computed on every lane (a clamped unit past the end included, so that the
-    // loads above are used unconditionally and stay where they are); only real units are stored.
-    auto stage_a = [&](int u, u32x4 x) {
-        const u32x4 p = pair_activations<BITS>(x);
-        if (u < a_units) {
-            const int r = u / upr;
-            const int w = u - r * upr;
-            const int c = w / UPC;
-            const int q = w - c * UPC;
-            *reinterpret_cast<u32x4*>(sA + (r * cpc + c) * CST + 16 * q) = p;
-        }
+    // The pairing and the unit's sum are computed on every lane (a clamped unit past the end
+    // included, so that the loads above are used unconditionally and stay where they are); only
+    // real units are stored.  Segment sums across the units of a chunk: the units of one chunk
+    // sit in UPC consecutive threads (T and the units per row are multiples of UPC), combined in
+    // a fixed order.
+    auto stage_a = [&](bool live, const Place& p, u32x4 x) {
+        const u32x4 pr = pair_activations<BITS>(x);
+        if (live) *reinterpret_cast<u32x4*>(sA + p.dst) = pr;
         float t = 0.f;
-        t = __builtin_amdgcn_fdot2(as_h2(p.x), one2, t, false);
-        t = __builtin_amdgcn_fdot2(as_h2(p.y), one2, t, false);
-        t = __builtin_amdgcn_fdot2(as_h2(p.z), one2, t, false);
-        t = __builtin_amdgcn_fdot2(as_h2(p.w), one2, t, false);
-        return u < a_units ? t : 0.f;
-    };
-    // Segment sums across the units of a chunk: the units of one chunk sit in UPC consecutive
-    // threads (T and the units per row are multiples of UPC), combined in a fixed order.
-    auto store_sums = [&](int u, float t) {
-        const int r = u / upr;
-        const int w = u - r * upr;
-        const int c = w / UPC;
-        const int q = w - c * UPC;
-        float* dst = reinterpret_cast<float*>(sA + (r * cpc + c) * CST + 4 * NP);
-        if constexpr (BITS == 4 && SEGS == 2) {          // block 16: two units per segment
-            if ((q & 1) == 0) dst[q >> 1] = t;
-        } else {
-            if (q == 0) dst[0] = t;
-        }
-    };
-#pragma unroll
-    for (int i = 0; i < AU; ++i) {
-        const int u = tid + i * T;
-        float t = stage_a(u, av[i]);
+        t = __builtin_amdgcn_fdot2(as_h2(pr.x), one2, t, false);
+        t = __builtin_amdgcn_fdot2(as_h2(pr.y), one2, t, false);
+        t = __builtin_amdgcn_fdot2(as_h2(pr.z), one2, t, false);
+        t = __builtin_amdgcn_fdot2(as_h2(pr.w), one2, t, false);
+        t = live ? t : 0.f;
         // partner sums over the lane's quad (int4) or pair (int8); out-of-range units add 0
         t += dpp_f<0xB1>(t);                             // lane ^ 1
         if constexpr (BITS == 4 && SEGS == 1) t += dpp_f<0x4E>(t);   // lane ^ 2
-        if (u < a_units) store_sums(u, t);
-    }
+        if (live && p.own) *reinterpret_cast<float*>(sA + p.sum) = t;
+    };
+#pragma unroll
+    for (int i = 0; i < AU; ++i) stage_a(tid + i * T < a_units, pl[i], av[i]);
     // ---- what the first batch did not cover (long K, several rows, unaligned tensors) -------
     for (int base = tid + AU * T; base < a_units; base += AU * T) {
         u32x4 x[AU];
+        Place px[AU];
 #pragma unroll
         for (int i = 0; i < AU; ++i) {
-            const int u = base + i * T;
-            const int r = u / upr;
-            const int row = min(m0 + min(r, MR - 1), M - 1);
-            if (u < a_units)
-                x[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)row * K + (int64_t)(u - r * upr) * 8);
+            px[i] = place(min(base + i * T, a_units - 1));
+            x[i] = *reinterpret_cast<const u32x4*>(px[i].src);
         }
 #pragma unroll
-        for (int i = 0; i < AU; ++i) {
-            const int u = base + i * T;
-            float t = u < a_units ? stage_a(u, x[i]) : 0.f;
-            t += dpp_f<0xB1>(t);
-            if constexpr (BITS == 4 && SEGS == 1) t += dpp_f<0x4E>(t);
-            if (u < a_units) store_sums(u, t);
-        }
+        for (int i = 0; i < AU; ++i) stage_a(base + i * T < a_units, px[i], x[i]);
     }
     for (int u = tid + kStreamSU * T; u < s_units; u += T)
         reinterpret_cast<u32x4*>(sS)[u] = reinterpret_cast<const u32x4*>(gS)[u];
@@ -240,23 +261,19 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
             reinterpret_cast<u32x4*>(sZ)[u] = reinterpret_cast<const u32x4*>(gZ)[u];
         for (int i = tid + z_units * 16; i < z_bytes; i += T) sZ[i] = gZ[i];
     }
-    __syncthreads();
+    // The weights are issued as soon as this wavefront has staged its activations -- not after
+    // a workgroup barrier -- and are kept below the staging (the activation loads, issued
+    // first, are not queued behind them).
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- the wavefront's weights: every load of the pass, issued at once --------------------
+    // ---- the wavefront's weights: every load of the pass, issued at once (addresses formed
+    // before the activations arrived) --------------------------------------------------------
     u32x4 bw[U][CPL];
-    int lcol[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int lc = (wave * ng + grp) * U + u;        // column within the workgroup
-        lcol[u] = lc;
-        const int cc = min(col0 + lc, N - 1);
-        const uint8_t* bcol = B + (int64_t)cc * col_bytes;
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const int c = min(gi + j * G, cpc - 1);
-            bw[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bcol + (int64_t)c * 16));
-        }
-    }
+        for (int j = 0; j < CPL; ++j)
+            bw[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bcol[u] + boff[j]));
 
     // ---- the scale and zero-point bytes (requested before the weights, from HBM) ------------
 #pragma unroll
