@@ -297,6 +297,57 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
 #pragma unroll
         for (int u = 0; u < U; ++u) acc[r][u] = 0.f;
     const uint16_t* sSr = reinterpret_cast<const uint16_t*>(sS);
+    // Per chunk j, column u and block segment s: the block's scale (0 for a chunk past the
+    // column's end), its zero point, and row r's activation sum over the segment.
+    auto chunk_of = [&](int j) { const int c0 = gi + j * G; return c0 < cpc ? c0 : cpc - 1; };
+    auto scale_of = [&](int j, int u, int s) {
+        const int blk = (chunk_of(j) * WPC + s * BS) / BS;
+        const float sv1 = (float)__builtin_bit_cast(f16, sSr[min(lcol[u], C - 1) * bpc + blk]);
+        return gi + j * G < cpc ? sv1 : 0.f;
+    };
+    auto zp_of = [&](int j, int u, int s) {
+        const int blk = (chunk_of(j) * WPC + s * BS) / BS;
+        const int lc = min(lcol[u], C - 1);
+        if constexpr (!HAS_ZP) return (float)(1 << (BITS - 1));
+        else if constexpr (BITS == 4) return (float)((sZ[lc * zpb + (blk >> 1)] >> ((blk & 1) * 4)) & 0xF);
+        else return (float)sZ[lc * zpb + blk];
+    };
+    auto asum_of = [&](int j, int r, int s) {
+        return reinterpret_cast<const float*>(sA + (r * cpc + chunk_of(j)) * CST + 4 * NP)[s];
+    };
+    // With one column per lane group, what does not depend on the weights is formed first,
+    // while they are still in flight: each chunk's 2^24 * scale, and the zero-point terms
+    // -scale * zp * (activation sum) added into the accumulators; once a chunk's weights arrive
+    // only its unpack, dot products and one scaled add are left.  With two columns these are
+    // formed at their chunk (kept in registers they would not fit beside the 32 weight
+    // registers in the 128 VGPRs of a 1024-thread workgroup).
+    constexpr bool kPre = U == 1;
+    float s24[kPre ? CPL : 1][U][SEGS];
+    if constexpr (kPre) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int s = 0; s < SEGS; ++s) {
+                    const float sv1 = scale_of(j, u, s);
+                    s24[j][u][s] = sv1 * 16777216.0f;
+                    const float sz = -sv1 * zp_of(j, u, s);
+#pragma unroll
+                    for (int r = 0; r < MR; ++r) acc[r][u] = __builtin_fmaf(sz, asum_of(j, r, s), acc[r][u]);
+                }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // chunk j's (column u, segment s) partial t: scaled and, formed here, its zero-point term
+    auto add_partial = [&](int j, int u, int s, int r, float t) {
+        if constexpr (kPre) {
+            acc[r][u] = __builtin_fmaf(s24[kPre ? j : 0][u][s], t, acc[r][u]);
+        } else {
+            const float sv1 = scale_of(j, u, s);
+            acc[r][u] = __builtin_fmaf(sv1 * 16777216.0f, t, acc[r][u]);
+            acc[r][u] = __builtin_fmaf(-sv1 * zp_of(j, u, s), asum_of(j, r, s), acc[r][u]);
+        }
+    };
     if constexpr (MR == 1) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
@@ -304,7 +355,6 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
             const bool live = c0 < cpc;
             const int c = live ? c0 : cpc - 1;
             f16x2 ap[MR][NP];
-            float asum[MR][SEGS];
 #pragma unroll
             for (int r = 0; r < MR; ++r) {
                 const uint8_t* src = sA + (r * cpc + c) * CST;
@@ -316,29 +366,12 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
                     ap[r][4 * q + 2] = as_h2(v.z);
                     ap[r][4 * q + 3] = as_h2(v.w);
                 }
-#pragma unroll
-                for (int s = 0; s < SEGS; ++s)
-                    asum[r][s] = reinterpret_cast<const float*>(src + 4 * NP)[s];
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int lc = min(lcol[u], C - 1);
                 const uint32_t w[4] = {bw[u][j].x, bw[u][j].y, bw[u][j].z, bw[u][j].w};
 #pragma unroll
                 for (int s = 0; s < SEGS; ++s) {
-                    const int blk = (c * WPC + s * BS) / BS;
-                    float sv1 = (float)__builtin_bit_cast(f16, sSr[lc * bpc + blk]);
-                    sv1 = live ? sv1 : 0.f;
-                    float zf;
-                    if constexpr (!HAS_ZP) {
-                        zf = (float)(1 << (BITS - 1));
-                    } else if constexpr (BITS == 4) {
-                        zf = (float)((sZ[lc * zpb + (blk >> 1)] >> ((blk & 1) * 4)) & 0xF);
-                    } else {
-                        zf = (float)sZ[lc * zpb + blk];
-                    }
-                    const float s24 = sv1 * 16777216.0f;
-                    const float sz = -sv1 * zf;
 #pragma unroll
                     for (int r = 0; r < MR; ++r) {
                         float t = 0.f;
@@ -361,8 +394,7 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
                             }
                         }
                         t = __builtin_fmaf(t16, 0.0625f, t);
-                        acc[r][u] = __builtin_fmaf(s24, t, acc[r][u]);
-                        acc[r][u] = __builtin_fmaf(sz, asum[r][s], acc[r][u]);
+                        add_partial(j, u, s, r, t);
                     }
                 }
             }
@@ -378,31 +410,12 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
             const int c0 = gi + j * G;
             const bool live = c0 < cpc;
             const int c = live ? c0 : cpc - 1;
-            // Per column and block segment: 2^24 * scale and -scale * zp.
-            float s24[U][SEGS], szs[U][SEGS];
             // The chunk's weights as fp16 subnormal pairs.  int4: for dword d, pairs 0 and 2 sit in
             // bits 0-3 of each half (q * 2^-24) and pairs 1 and 3 are masked in place at bits 4-7
             // (16q * 2^-24, still subnormal), summed apart and scaled by 1/16: one shift per dword.
             uint32_t q[U][4][QPD];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int lc = min(lcol[u], C - 1);
-#pragma unroll
-                for (int s = 0; s < SEGS; ++s) {
-                    const int blk = (c * WPC + s * BS) / BS;
-                    float sv1 = (float)__builtin_bit_cast(f16, sSr[lc * bpc + blk]);
-                    sv1 = live ? sv1 : 0.f;
-                    float zf;
-                    if constexpr (!HAS_ZP) {
-                        zf = (float)(1 << (BITS - 1));
-                    } else if constexpr (BITS == 4) {
-                        zf = (float)((sZ[lc * zpb + (blk >> 1)] >> ((blk & 1) * 4)) & 0xF);
-                    } else {
-                        zf = (float)sZ[lc * zpb + blk];
-                    }
-                    s24[u][s] = sv1 * 16777216.0f;
-                    szs[u][s] = -sv1 * zf;
-                }
                 const uint32_t w[4] = {bw[u][j].x, bw[u][j].y, bw[u][j].z, bw[u][j].w};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
@@ -430,9 +443,6 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
                     ap[4 * qq + 2] = as_h2(v.z);
                     ap[4 * qq + 3] = as_h2(v.w);
                 }
-                float asum[SEGS];
-#pragma unroll
-                for (int s = 0; s < SEGS; ++s) asum[s] = reinterpret_cast<const float*>(src + 4 * NP)[s];
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
 #pragma unroll
@@ -452,8 +462,7 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
                             }
                         }
                         t = __builtin_fmaf(t16, 0.0625f, t);
-                        acc[r][u] = __builtin_fmaf(s24[u][s], t, acc[r][u]);
-                        acc[r][u] = __builtin_fmaf(szs[u][s], asum[s], acc[r][u]);
+                        add_partial(j, u, s, r, t);
                     }
                 }
             }
