@@ -55,10 +55,13 @@ int hip_fail(hipError_t e, const char* what) {
 
 // Rows above which the prefill GEMM replaces the 16-row MFMA GEMV.
 constexpr int64_t kGemmMinRows = 64;
-// Fewest rows the batched decode kernel is planned for (below: the streaming GEMV).  Measured on
-// the Phi-3.5 decode shapes: at 4 rows the batched kernel is ahead on every node (qkv 9.9 vs 10.7
-// us, down 9.6 vs 10.7 us), at 2-3 rows the streaming GEMV on most.
-constexpr int64_t kBatchMinRows = 4;
+// Rows from which the batched decode kernel is planned (below: the streaming GEMV), and at four
+// rows the weight bytes under which it still is.  Measured on the Phi-3.5 decode shapes at four
+// rows: the streaming GEMV ahead on qkv (9.5 vs 10.1 us), gate_up (12.0 vs 12.7) and down (8.4
+// vs 9.6), the batched kernel on o (4.7 MB of weights: 5.1 vs 6.0 us); at 2-3 rows the
+// streaming GEMV on every node, at 5 and more it cannot stream the weights once.
+constexpr int64_t kBatchMinRows = 5;
+constexpr int64_t kBatchFourRowsBelow = 8 << 20;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -205,8 +208,10 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     mnb::BatchStreamGeom bg{};
     const bool batch = f16 && p->bits == 4 &&
                        mnb::batch_stream_geometry(p->m, p->n, p->k, p->block_size, &bg);
-    if (batch && p->m >= kBatchMinRows) kern = MNB_KERNEL_BATCH_STREAM;
-    if (stream && p->m < kBatchMinRows) kern = MNB_KERNEL_GEMV_STREAM;
+    const bool batch_rows = p->m >= kBatchMinRows ||
+                            (p->m == 4 && b_bytes_of(p) < kBatchFourRowsBelow) || !stream;
+    if (batch && p->m >= 4 && batch_rows) kern = MNB_KERNEL_BATCH_STREAM;
+    if (stream && !(batch && batch_rows)) kern = MNB_KERNEL_GEMV_STREAM;
     const int forced = forced_kernel();
     if (forced == MNB_KERNEL_GENERIC) kern = MNB_KERNEL_GENERIC;
     if (forced == MNB_KERNEL_GEMV_MFMA && fast) kern = MNB_KERNEL_GEMV_MFMA;
