@@ -40,8 +40,13 @@ bool derive(StreamConfig& c, int64_t n, int64_t k, int bits, int bs) {
     const int64_t bpc = k / bs;
     const int64_t zpb = (bpc * bits + 7) / 8;
     c.groups = (n + cols - 1) / cols;
+    // the activations, and unless each lane loads its own, the columns' scale and zero-point bytes
+    // (c.cpl and the instantiated chunk count agree on that: both are at most 4 where it holds)
+    const int segs = (128 / bits) > bs ? (128 / bits) / bs : 1;
     c.lds = c.mr * cpc * (bits == 4 ? stream_chunk_stride<4>() : stream_chunk_stride<8>()) +
-            ((cols * bpc * 2 + 15) & ~15) + ((cols * zpb + 15) & ~15);
+            (stream_lane_scales(c.cpl, c.u, segs)
+                 ? 0
+                 : ((cols * bpc * 2 + 15) & ~15) + ((cols * zpb + 15) & ~15));
     return c.groups <= 0x7fffffff && c.lds <= kStreamMaxLds;
 }
 

@@ -7,10 +7,11 @@
 // before the burst starts.  The launch is one to four workgroups per CU (up to 16 wavefronts
 // each); every thread first requests its share of what the workgroup's wavefronts share -- the
 // MR activation rows (an L2 / MALL hit) and the columns' scale and zero-point bytes (cold in
-// HBM) -- and each wavefront stages its activation share in LDS as soon as it arrives and then
-// issues its weights at once (all activation requests of the launch are out by then); the scale
-// and zero-point bytes reach LDS while the weights are in flight, and one workgroup barrier
-// precedes the compute.  Everything but the pairing and the stores -- the LDS offsets of the
+// HBM; with at most four chunks per lane each lane instead loads its own chunks' scales and
+// zero points into registers) -- and each wavefront stages its activation share in LDS as soon
+// as it arrives and then issues its weights at once (all activation requests of the launch are
+// out by then); the scale and zero-point bytes reach LDS while the weights are in flight, and
+// one workgroup barrier precedes the compute.  Everything but the pairing and the stores -- the LDS offsets of the
 // staged units, the weight addresses -- is formed before the activations arrive: a wavefront's
 // VALU work between its activations' arrival and its weight requests delays the whole stream.
 // Each wavefront makes exactly one pass: it owns U
@@ -102,6 +103,16 @@ constexpr int kStreamAU = 2;
 constexpr int kStreamSU = 2;
 constexpr int kStreamZU = 1;
 
+// Whether a lane loads its chunks' block scales and zero points itself, straight into registers
+// (at most four (chunk, column, segment) triples: one 2-byte and one 1-byte load each), rather
+// than the workgroup staging its columns' scale and zero-point bytes in LDS.  The lane's own
+// loads keep the workgroup barrier from waiting for those HBM reads, but every load instruction
+// costs address-unit time whatever its width; measured on MI355X: qkv (three chunks per lane)
+// 5.25 -> 5.00 us, o (three) 3.61 -> 3.48 us, gate_up (six) 6.64 -> 6.72 us.
+__host__ __device__ constexpr bool stream_lane_scales(int cpl, int u, int segs) {
+    return cpl * u * segs <= 4;
+}
+
 // One workgroup = `waves` wavefronts (blockDim.x / 64) = C = waves * (64/G) * U consecutive
 // columns, col0 = blockIdx.x * C; MR rows of A (m0 = blockIdx.y * MR).  vec_s / vec_z: the
 // workgroup's scale / zero-point byte ranges may be copied with 16-byte loads (the host checked
@@ -117,6 +128,7 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
     constexpr int DW_PER_SEG = 4 / SEGS;                 // dwords of a chunk per block segment
     constexpr int UPC = WPC / 8;                         // 16-byte activation units per chunk
     constexpr int CST = stream_chunk_stride<BITS>();
+    constexpr bool REG = stream_lane_scales(CPL, U, SEGS);
     extern __shared__ __align__(16) uint8_t smem[];
 
     const int T = (int)blockDim.x;
@@ -188,16 +200,18 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
         pl[i] = place(min(tid + i * T, a_units - 1));
         av[i] = *reinterpret_cast<const u32x4*>(pl[i].src);
     }
-    const int s_units = vec_s ? s_bytes / 16 : 0;
-    const int z_units = vec_z ? z_bytes / 16 : 0;
+    const int s_units = vec_s && !REG ? s_bytes / 16 : 0;
+    const int z_units = vec_z && !REG ? z_bytes / 16 : 0;
     const u32x4* s4 = reinterpret_cast<const u32x4*>(s_units > 0 ? gS : reinterpret_cast<const uint8_t*>(A));
     const u32x4* z4 = reinterpret_cast<const u32x4*>(z_units > 0 ? gZ : reinterpret_cast<const uint8_t*>(A));
     u32x4 sv[kStreamSU], zv[kStreamZU];
+    if constexpr (!REG) {
 #pragma unroll
-    for (int i = 0; i < kStreamSU; ++i) sv[i] = s4[min(tid + i * T, max(s_units - 1, 0))];
-    if constexpr (HAS_ZP) {
+        for (int i = 0; i < kStreamSU; ++i) sv[i] = s4[min(tid + i * T, max(s_units - 1, 0))];
+        if constexpr (HAS_ZP) {
 #pragma unroll
-        for (int i = 0; i < kStreamZU; ++i) zv[i] = z4[min(tid + i * T, max(z_units - 1, 0))];
+            for (int i = 0; i < kStreamZU; ++i) zv[i] = z4[min(tid + i * T, max(z_units - 1, 0))];
+        }
     }
 
     // The wavefront's weight addresses: lane (group grp, index gi) takes chunks gi, gi + G, ...
@@ -215,6 +229,25 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
         const int lc = (wave * ng + grp) * U + u;        // column within the workgroup
         lcol[u] = lc;
         bcol[u] = B + (int64_t)min(col0 + lc, N - 1) * col_bytes;
+    }
+    auto chunk_of = [&](int j) { return min(gi + j * G, cpc - 1); };
+    // With few chunks per lane, the lane's own block scales and zero points: for fixed (chunk,
+    // column, segment) the G lanes of a group read consecutive scale bytes of one column.
+    uint16_t sraw[REG ? CPL : 1][U][SEGS];
+    uint8_t zraw[REG ? CPL : 1][U][SEGS];
+    if constexpr (REG) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int s = 0; s < SEGS; ++s) {
+                    const int64_t cc = min(col0 + lcol[u], N - 1);
+                    const int blk = (chunk_of(j) * WPC + s * BS) / BS;
+                    sraw[REG ? j : 0][u][s] = reinterpret_cast<const uint16_t*>(S)[cc * bpc + blk];
+                    if constexpr (HAS_ZP)
+                        zraw[REG ? j : 0][u][s] = Z[cc * zpb + (BITS == 4 ? blk >> 1 : blk)];
+                }
     }
 
     // ---- stage the first batch into LDS ------------------------------------------------------
@@ -252,14 +285,16 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
 #pragma unroll
         for (int i = 0; i < AU; ++i) stage_a(base + i * T < a_units, px[i], x[i]);
     }
-    for (int u = tid + kStreamSU * T; u < s_units; u += T)
-        reinterpret_cast<u32x4*>(sS)[u] = reinterpret_cast<const u32x4*>(gS)[u];
-    for (int i = 2 * (tid + s_units * 8); i < s_bytes; i += 2 * T)   // 2-byte remainder / path
-        *reinterpret_cast<uint16_t*>(sS + i) = *reinterpret_cast<const uint16_t*>(gS + i);
-    if constexpr (HAS_ZP) {
-        for (int u = tid + kStreamZU * T; u < z_units; u += T)
-            reinterpret_cast<u32x4*>(sZ)[u] = reinterpret_cast<const u32x4*>(gZ)[u];
-        for (int i = tid + z_units * 16; i < z_bytes; i += T) sZ[i] = gZ[i];
+    if constexpr (!REG) {
+        for (int u = tid + kStreamSU * T; u < s_units; u += T)
+            reinterpret_cast<u32x4*>(sS)[u] = reinterpret_cast<const u32x4*>(gS)[u];
+        for (int i = 2 * (tid + s_units * 8); i < s_bytes; i += 2 * T)   // 2-byte remainder / path
+            *reinterpret_cast<uint16_t*>(sS + i) = *reinterpret_cast<const uint16_t*>(gS + i);
+        if constexpr (HAS_ZP) {
+            for (int u = tid + kStreamZU * T; u < z_units; u += T)
+                reinterpret_cast<u32x4*>(sZ)[u] = reinterpret_cast<const u32x4*>(gZ)[u];
+            for (int i = tid + z_units * 16; i < z_bytes; i += T) sZ[i] = gZ[i];
+        }
     }
     // The weights are issued as soon as this wavefront has staged its activations -- not after
     // a workgroup barrier -- and are kept below the staging (the activation loads, issued
@@ -276,16 +311,18 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
             bw[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bcol[u] + boff[j]));
 
     // ---- the scale and zero-point bytes (requested before the weights, from HBM) ------------
+    if constexpr (!REG) {
 #pragma unroll
-    for (int i = 0; i < kStreamSU; ++i) {
-        const int u = tid + i * T;
-        if (u < s_units) reinterpret_cast<u32x4*>(sS)[u] = sv[i];
-    }
-    if constexpr (HAS_ZP) {
-#pragma unroll
-        for (int i = 0; i < kStreamZU; ++i) {
+        for (int i = 0; i < kStreamSU; ++i) {
             const int u = tid + i * T;
-            if (u < z_units) reinterpret_cast<u32x4*>(sZ)[u] = zv[i];
+            if (u < s_units) reinterpret_cast<u32x4*>(sS)[u] = sv[i];
+        }
+        if constexpr (HAS_ZP) {
+#pragma unroll
+            for (int i = 0; i < kStreamZU; ++i) {
+                const int u = tid + i * T;
+                if (u < z_units) reinterpret_cast<u32x4*>(sZ)[u] = zv[i];
+            }
         }
     }
     __syncthreads();
@@ -299,18 +336,18 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
     const uint16_t* sSr = reinterpret_cast<const uint16_t*>(sS);
     // Per chunk j, column u and block segment s: the block's scale (0 for a chunk past the
     // column's end), its zero point, and row r's activation sum over the segment.
-    auto chunk_of = [&](int j) { const int c0 = gi + j * G; return c0 < cpc ? c0 : cpc - 1; };
     auto scale_of = [&](int j, int u, int s) {
         const int blk = (chunk_of(j) * WPC + s * BS) / BS;
-        const float sv1 = (float)__builtin_bit_cast(f16, sSr[min(lcol[u], C - 1) * bpc + blk]);
-        return gi + j * G < cpc ? sv1 : 0.f;
+        const uint16_t raw = REG ? sraw[REG ? j : 0][u][s] : sSr[min(lcol[u], C - 1) * bpc + blk];
+        return gi + j * G < cpc ? (float)__builtin_bit_cast(f16, raw) : 0.f;
     };
     auto zp_of = [&](int j, int u, int s) {
         const int blk = (chunk_of(j) * WPC + s * BS) / BS;
         const int lc = min(lcol[u], C - 1);
+        const int zb = REG ? zraw[REG ? j : 0][u][s] : sZ[lc * zpb + (BITS == 4 ? blk >> 1 : blk)];
         if constexpr (!HAS_ZP) return (float)(1 << (BITS - 1));
-        else if constexpr (BITS == 4) return (float)((sZ[lc * zpb + (blk >> 1)] >> ((blk & 1) * 4)) & 0xF);
-        else return (float)sZ[lc * zpb + blk];
+        else if constexpr (BITS == 4) return (float)((zb >> ((blk & 1) * 4)) & 0xF);
+        else return (float)zb;
     };
     auto asum_of = [&](int j, int r, int s) {
         return reinterpret_cast<const float*>(sA + (r * cpc + chunk_of(j)) * CST + 4 * NP)[s];
