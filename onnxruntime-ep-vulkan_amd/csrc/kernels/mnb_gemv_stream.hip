@@ -1,6 +1,7 @@
 // Launch configuration of the streaming decode GEMV (kernel in mnb_gemv_stream.hpp, instantiated
 // per bit width in mnb_gemv_stream_b4.hip / mnb_gemv_stream_b8.hip).
 #include <algorithm>
+#include <cmath>
 
 #include "mnb_gemv_stream.hpp"
 
@@ -94,14 +95,30 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     // Workgroups: each stages the whole activation vector (2*K bytes per row) before it streams
     // weights, so more workgroups mean more of that traffic ahead of the weights.  Measured over
     // every shape of 4..16 wavefronts (MI355X, K=3072: N = 3072, 8192, 9216, 16384, 32064; K=2880,
-    // 4096, 8192): about four workgroups per CU for K <= 4096 (gate_up 8.2 -> 7.3 us, N=32064
-    // 14.8 -> 11.8 us against three per CU), one for K = 8192.  At least K / 1024 wavefronts, so
+    // 4096, 8192): three to five workgroups per CU for K <= 4096, the count that fills the CUs
+    // evenly (the busiest CU's workgroups against the mean) taken among them, then the one closest
+    // to four per CU (gate_up 1024 x 4 7.3 us against 820 x 5 8.2 us; qkv 768 x 6 4.84 us
+    // against 922 x 5 4.87-4.95 us); one per CU for K = 8192.  At least K / 1024 wavefronts, so
     // that the first staging batch (2 * MR 16-byte units per thread) covers all of A.
-    const double groups_per_cu = k <= 4096 ? 4.0 : 1.0;
-    int64_t w = (int64_t)(wpc / groups_per_cu + 0.5);
     const int64_t wmin = std::max<int64_t>(4, (k + 1023) / 1024);
     const int64_t wmax = kStreamMaxThreads / 64;
-    c.waves_per_group = (int)std::min(std::max(w, wmin), wmax);
+    auto clampw = [&](int64_t w) { return std::min(std::max(w, wmin), wmax); };
+    const double waves_total = wpc * kNumCUs;
+    int64_t w = clampw((int64_t)(wpc / (k <= 4096 ? 4.0 : 1.0) + 0.5));
+    if (k <= 4096) {
+        double best_imb = 0.0, best_d = 0.0;
+        for (int64_t cand = clampw((int64_t)(wpc / 5.0 + 0.5)); cand <= clampw((int64_t)(wpc / 3.0 + 0.5)); ++cand) {
+            const double groups = std::ceil(waves_total / (double)cand);
+            const double imb = std::ceil(groups / kNumCUs) * kNumCUs / groups;
+            const double d = __builtin_fabs(groups / kNumCUs - 4.0);
+            if (best_imb == 0.0 || imb < best_imb - 1e-9 || (imb < best_imb + 1e-9 && d < best_d)) {
+                best_imb = imb;
+                best_d = d;
+                w = cand;
+            }
+        }
+    }
+    c.waves_per_group = (int)w;
     derive(c, n, k, bits, bs);
     return c;
 }

@@ -250,6 +250,19 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
                 }
     }
 
+    // With the lane's own scales, its first weight chunk is requested here, ahead of the
+    // activation staging: the stream starts earlier, while the activation requests, made first,
+    // stay ahead of it (measured: qkv 5.01 -> 4.89 us, o 3.48 -> 3.34, down 4.67 -> 4.48; two
+    // early chunks, or one with the workgroup-staged scales, measured slower).
+    constexpr int EW = REG ? (CPL < 1 ? CPL : 1) : 0;
+    u32x4 bw[U][CPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < EW; ++j)
+            bw[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bcol[u] + boff[j]));
+    __builtin_amdgcn_sched_barrier(0);
+
     // ---- stage the first batch into LDS ------------------------------------------------------
     const f16x2 one2 = {(f16)1.0f, (f16)1.0f};
     // The pairing and the unit's sum are computed on every lane (a clamped unit past the end
@@ -303,11 +316,10 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
 
     // ---- the wavefront's weights: every load of the pass, issued at once (addresses formed
     // before the activations arrived) --------------------------------------------------------
-    u32x4 bw[U][CPL];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int j = 0; j < CPL; ++j)
+        for (int j = EW; j < CPL; ++j)
             bw[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bcol[u] + boff[j]));
 
     // ---- the scale and zero-point bytes (requested before the weights, from HBM) ------------
