@@ -60,38 +60,43 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     // One row-tile of all M rows (up to 4): the weights are streamed once.
     c.mr = m <= 1 ? 1 : (int)(m < 4 ? m : 4);
     // Lane-group width: the best-filled group (G * CPL chunk slots for cpc chunks); among equally
-    // filled ones, the one that puts closest to 16 wavefronts on each CU (one per 64/G columns),
+    // filled ones, at one row the one whose lanes load their own scales (at most four chunks per
+    // lane), then the one that puts closest to 16 wavefronts on each CU (one per 64/G columns),
     // 10 with four rows (each wavefront then reads four rows of activations per chunk, so fewer,
-    // longer wavefronts win).  Measured on MI355X for the Phi-3.5 decode shapes: one to three
-    // rows, qkv G=32 (18 per CU; at two rows 6.4 us against 6.9 with G=16), gate_up G=16 (16
-    // per CU) rather than G=32 (32 per CU); four rows, qkv and gate_up G=16; o G=32 and down
-    // G=64 throughout.
+    // longer wavefronts win).  Measured on MI355X: one row, G=32 for gate_up (6.46 us against
+    // 6.71 with G=16), N=32064 (10.4 against 11.4), K=4096 N=14336 (7.3 against 8.3); two to four
+    // rows, gate_up G=16 (at four rows 11.3 against 12.8 with G=32), qkv G=32 up to three rows
+    // and G=16 at four, o G=32 and down G=64 throughout.
     auto waves_per_cu = [&](int cand) {
         return (double)((n + 64 / cand - 1) / (64 / cand)) / kNumCUs;
     };
+    const int segs = (128 / bits) > bs ? (128 / bits) / bs : 1;
     const double target = c.mr <= 3 ? 16.0 : 10.0;
     double best_fill = -1.0, best_dist = 0.0;
+    bool best_lane = false;
     int g = 64;
     for (int cand : {64, 32, 16}) {
         if (!lane_group(cand)) continue;
         const int64_t cpl = (cpc + cand - 1) / cand;
         const double fill = (double)cpc / (double)(cand * cpl);
+        const bool lane = c.mr == 1 && stream_lane_scales((int)cpl, 1, segs);
         const double dist = __builtin_fabs(waves_per_cu(cand) - target);
-        if (fill > best_fill + 1e-9 || (fill > best_fill - 1e-9 && dist < best_dist)) {
+        const bool better =
+            fill > best_fill + 1e-9 ||
+            (fill > best_fill - 1e-9 && (lane > best_lane || (lane == best_lane && dist < best_dist)));
+        if (better) {
             best_fill = fill;
+            best_lane = lane;
             best_dist = dist;
             g = cand;
         }
     }
     c.g = g;
     c.cpl = (int)((cpc + g - 1) / g);
-    // One column per lane group unless that needs more than 32 wavefronts per CU.
+    // One column per lane group (two measured slower once lanes load their own scales: gate_up
+    // 6.89 against 6.46 us, N=32064 11.5 against 10.4; the launcher still takes U = 2).
     c.u = 1;
-    double wpc = waves_per_cu(g);
-    if (wpc > 32.0 && c.mr == 1 && c.cpl <= cpl_cap(2)) {
-        c.u = 2;
-        wpc /= 2.0;
-    }
+    const double wpc = waves_per_cu(g);
     // Workgroups: each stages the whole activation vector (2*K bytes per row) before it streams
     // weights, so more workgroups mean more of that traffic ahead of the weights.  Measured over
     // every shape of 4..16 wavefronts (MI355X, K=3072: N = 3072, 8192, 9216, 16384, 32064; K=2880,
@@ -105,7 +110,11 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     auto clampw = [&](int64_t w) { return std::min(std::max(w, wmin), wmax); };
     const double waves_total = wpc * kNumCUs;
     int64_t w = clampw((int64_t)(wpc / (k <= 4096 ? 4.0 : 1.0) + 0.5));
-    if (k <= 4096) {
+    if (k <= 4096 && wpc > 32.0) {
+        // more wavefronts than a CU holds at once: the smallest workgroups, which the CUs take up
+        // as they finish others (N=32064: 4008 x 4 10.4 us against 1002 x 16 11.6 us)
+        w = wmin;
+    } else if (k <= 4096) {
         double best_imb = 0.0, best_d = 0.0;
         for (int64_t cand = clampw((int64_t)(wpc / 5.0 + 0.5)); cand <= clampw((int64_t)(wpc / 3.0 + 0.5)); ++cand) {
             const double groups = std::ceil(waves_total / (double)cand);
