@@ -21,22 +21,20 @@ constexpr int kNumCUs = 256;
 // workgroup per CU and the launch is left to the row-tiled kernels.
 constexpr int64_t kStreamMaxLds = 96 * 1024;
 
-// Chunks per lane the kernel is instantiated for: 8 with one column per lane group, 4 with two
-// (two columns only for one row).
-int cpl_cap(int u) { return u == 1 ? 8 : 4; }
+// Chunks per lane the kernel is instantiated for (one column per lane group).
+constexpr int kStreamMaxCpl = 8;
 
 // Fills the derived fields (workgroups along N, LDS bytes) of a shape; false when the shape is
 // malformed or exceeds what the kernel is compiled for.
 bool derive(StreamConfig& c, int64_t n, int64_t k, int bits, int bs) {
-    if (c.mr < 1 || c.mr > 4 || (c.u != 1 && c.u != 2)) return false;
+    if (c.mr < 1 || c.mr > 4 || c.u != 1) return false;
     if (c.waves_per_group < 1 || 64 * c.waves_per_group > kStreamMaxThreads) return false;
     if (c.g != 16 && c.g != 32 && c.g != 64) return false;
     if (bits != 4 && bits != 8) return false;
     const int64_t wpc = 128 / bits;
     if (k <= 0 || k % wpc || k % bs || n <= 0) return false;
     const int64_t cpc = k / wpc;
-    if (c.mr > 1 && c.u != 1) return false;
-    if (c.cpl < 1 || c.cpl > cpl_cap(c.u) || (int64_t)c.g * c.cpl < cpc) return false;
+    if (c.cpl < 1 || c.cpl > kStreamMaxCpl || (int64_t)c.g * c.cpl < cpc) return false;
     const int64_t cols = (int64_t)c.waves_per_group * (64 / c.g) * c.u;
     const int64_t bpc = k / bs;
     const int64_t zpb = (bpc * bits + 7) / 8;
@@ -56,7 +54,7 @@ bool derive(StreamConfig& c, int64_t n, int64_t k, int bits, int bs) {
 StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int bs) {
     StreamConfig c{};
     const int64_t cpc = k / (128 / bits);
-    auto lane_group = [&](int cand) { return (cpc + cand - 1) / cand <= cpl_cap(1); };
+    auto lane_group = [&](int cand) { return (cpc + cand - 1) / cand <= kStreamMaxCpl; };
     // One row-tile of all M rows (up to 4): the weights are streamed once.
     c.mr = m <= 1 ? 1 : (int)(m < 4 ? m : 4);
     // Lane-group width: the best-filled group (G * CPL chunk slots for cpc chunks); among equally
@@ -94,7 +92,7 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     c.g = g;
     c.cpl = (int)((cpc + g - 1) / g);
     // One column per lane group (two measured slower once lanes load their own scales: gate_up
-    // 6.89 against 6.46 us, N=32064 11.5 against 10.4; the launcher still takes U = 2).
+    // 6.89 against 6.46 us, N=32064 11.5 against 10.4).
     c.u = 1;
     const double wpc = waves_per_cu(g);
     // Workgroups: each stages the whole activation vector (2*K bytes per row) before it streams
@@ -148,7 +146,7 @@ hipError_t launch_gemv_stream_cfg(const StreamConfig& cfg, const void* a, const 
     if (m == 0) return hipSuccess;
     StreamConfig c = cfg;
     // the shape is checked (the kernel is compiled for kStreamMaxThreads threads per workgroup,
-    // U <= 2, CPL <= 8) and its derived fields recomputed before anything is launched; row-tiles
+    // U == 1, CPL <= 8) and its derived fields recomputed before anything is launched; row-tiles
     // of MR rows cover M (grid y)
     if (m < 0 || !derive(c, n, k, bits, bs)) return hipErrorInvalidValue;
     const int64_t cols = (int64_t)c.waves_per_group * (64 / c.g) * c.u;

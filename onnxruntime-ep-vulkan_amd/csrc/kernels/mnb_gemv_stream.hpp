@@ -15,7 +15,8 @@
 // staged units, the weight addresses -- is formed before the activations arrive: a wavefront's
 // VALU work between its activations' arrival and its weight requests delays the whole stream.
 // Each wavefront makes exactly one pass: it owns U
-// columns per lane group and issues all of their 16-byte weight loads at once.  The packed weight
+// columns per lane group (written for U, launched with U = 1) and issues all of their 16-byte
+// weight loads at once.  The packed weight
 // of column n is K*bits/8 contiguous bytes (B is [N][K/bs][bs*bits/8]); a lane group of G lanes
 // (G = 16, 32 or 64) owns a column and lane i of the group takes chunks i, i+G, i+2G, ... (a
 // "chunk" is 16 bytes: 32 int4 or 16 int8 weights), so one load instruction covers 64/G runs of
@@ -364,38 +365,27 @@ gemv_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16*
     auto asum_of = [&](int j, int r, int s) {
         return reinterpret_cast<const float*>(sA + (r * cpc + chunk_of(j)) * CST + 4 * NP)[s];
     };
-    // With one column per lane group, what does not depend on the weights is formed first,
-    // while they are still in flight: each chunk's 2^24 * scale, and the zero-point terms
-    // -scale * zp * (activation sum) added into the accumulators; once a chunk's weights arrive
-    // only its unpack, dot products and one scaled add are left.  With two columns these are
-    // formed at their chunk (kept in registers they would not fit beside the 32 weight
-    // registers in the 128 VGPRs of a 1024-thread workgroup).
-    constexpr bool kPre = U == 1;
-    float s24[kPre ? CPL : 1][U][SEGS];
-    if constexpr (kPre) {
+    // What does not depend on the weights is formed first, while they are still in flight:
+    // each chunk's 2^24 * scale, and the zero-point terms -scale * zp * (activation sum) added
+    // into the accumulators; once a chunk's weights arrive only its unpack, dot products and
+    // one scaled add are left.
+    float s24[CPL][U][SEGS];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j)
+    for (int j = 0; j < CPL; ++j)
 #pragma unroll
-            for (int u = 0; u < U; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-                for (int s = 0; s < SEGS; ++s) {
-                    const float sv1 = scale_of(j, u, s);
-                    s24[j][u][s] = sv1 * 16777216.0f;
-                    const float sz = -sv1 * zp_of(j, u, s);
+            for (int s = 0; s < SEGS; ++s) {
+                const float sv1 = scale_of(j, u, s);
+                s24[j][u][s] = sv1 * 16777216.0f;
+                const float sz = -sv1 * zp_of(j, u, s);
 #pragma unroll
-                    for (int r = 0; r < MR; ++r) acc[r][u] = __builtin_fmaf(sz, asum_of(j, r, s), acc[r][u]);
-                }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    // chunk j's (column u, segment s) partial t: scaled and, formed here, its zero-point term
+                for (int r = 0; r < MR; ++r) acc[r][u] = __builtin_fmaf(sz, asum_of(j, r, s), acc[r][u]);
+            }
+    __builtin_amdgcn_sched_barrier(0);
+    // chunk j's (column u, segment s) partial t, scaled
     auto add_partial = [&](int j, int u, int s, int r, float t) {
-        if constexpr (kPre) {
-            acc[r][u] = __builtin_fmaf(s24[kPre ? j : 0][u][s], t, acc[r][u]);
-        } else {
-            const float sv1 = scale_of(j, u, s);
-            acc[r][u] = __builtin_fmaf(sv1 * 16777216.0f, t, acc[r][u]);
-            acc[r][u] = __builtin_fmaf(-sv1 * zp_of(j, u, s), asum_of(j, r, s), acc[r][u]);
-        }
+        acc[r][u] = __builtin_fmaf(s24[j][u][s], t, acc[r][u]);
     };
     if constexpr (MR == 1) {
 #pragma unroll
@@ -564,21 +554,18 @@ hipError_t stream_cpl(const StreamConfig& c, const f16* A, const uint8_t* B, con
     if (c.cpl <= 2) return stream_go<BITS, BS, HAS_ZP, MR, 2, U>(c, A, B, S, Z, Y, m, n, k, st);
     if (c.cpl <= 3) return stream_go<BITS, BS, HAS_ZP, MR, 3, U>(c, A, B, S, Z, Y, m, n, k, st);
     if (c.cpl <= 4) return stream_go<BITS, BS, HAS_ZP, MR, 4, U>(c, A, B, S, Z, Y, m, n, k, st);
-    if constexpr (U == 1) {
-        if (c.cpl <= 6) return stream_go<BITS, BS, HAS_ZP, MR, 6, U>(c, A, B, S, Z, Y, m, n, k, st);
-        if (c.cpl <= 8) return stream_go<BITS, BS, HAS_ZP, MR, 8, U>(c, A, B, S, Z, Y, m, n, k, st);
-    }
+    if (c.cpl <= 6) return stream_go<BITS, BS, HAS_ZP, MR, 6, U>(c, A, B, S, Z, Y, m, n, k, st);
+    if (c.cpl <= 8) return stream_go<BITS, BS, HAS_ZP, MR, 8, U>(c, A, B, S, Z, Y, m, n, k, st);
     return hipErrorInvalidValue;
 }
 
 template <int BITS, int BS, bool HAS_ZP>
 hipError_t stream_rows(const StreamConfig& c, const f16* A, const uint8_t* B, const f16* S,
                        const uint8_t* Z, f16* Y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
-    // two columns per lane group only for one row (with more rows the registers would not fit)
+    // one column per lane group (derive() refuses others): two per group measured slower once
+    // lanes load their own scales, and would not fit the registers with several rows
     switch (c.mr) {
-        case 1:
-            if (c.u == 2) return stream_cpl<BITS, BS, HAS_ZP, 1, 2>(c, A, B, S, Z, Y, m, n, k, st);
-            return stream_cpl<BITS, BS, HAS_ZP, 1, 1>(c, A, B, S, Z, Y, m, n, k, st);
+        case 1: return stream_cpl<BITS, BS, HAS_ZP, 1, 1>(c, A, B, S, Z, Y, m, n, k, st);
         case 2: return stream_cpl<BITS, BS, HAS_ZP, 2, 1>(c, A, B, S, Z, Y, m, n, k, st);
         case 3: return stream_cpl<BITS, BS, HAS_ZP, 3, 1>(c, A, B, S, Z, Y, m, n, k, st);
         case 4: return stream_cpl<BITS, BS, HAS_ZP, 4, 1>(c, A, B, S, Z, Y, m, n, k, st);

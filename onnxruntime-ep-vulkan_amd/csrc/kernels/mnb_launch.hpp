@@ -29,7 +29,7 @@ struct StreamConfig {
     int mr;              // rows of A per workgroup row-tile (1..4)
     int g;               // lanes per column (16, 32, 64)
     int cpl;             // 16-byte chunks per lane (ceil(chunks per column / g))
-    int u;               // columns per lane group (1 or 2)
+    int u;               // columns per lane group (1; the launcher refuses others)
     int waves_per_group; // wavefronts per workgroup (1..16)
     int vec_s, vec_z;    // scale / zero-point bytes staged with 16-byte loads (set at launch)
     int64_t groups;      // workgroups along N (derived)

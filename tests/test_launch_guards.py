@@ -57,8 +57,8 @@ def test_stream_launch_refuses_malformed_shapes():
     assert _call(_cfg(mr=5)) == HIP_ERROR_INVALID_VALUE
     assert _call(_cfg(u=3)) == HIP_ERROR_INVALID_VALUE
     assert _call(_cfg(cpl=9)) == HIP_ERROR_INVALID_VALUE          # above the instantiated 8
-    assert _call(_cfg(u=2, cpl=6)) == HIP_ERROR_INVALID_VALUE     # two columns: at most 4
-    assert _call(_cfg(mr=2, u=2)) == HIP_ERROR_INVALID_VALUE      # two columns: one row only
+    assert _call(_cfg(u=2)) == HIP_ERROR_INVALID_VALUE            # one column per lane group
+    assert _call(_cfg(mr=2, u=2)) == HIP_ERROR_INVALID_VALUE
 
 
 def test_planner_shapes_stay_within_compiled_bounds():
