@@ -136,6 +136,9 @@ SHAPES = [
     (3, 50, 2048, 4, 16, True),
     (4, 64, 4096, 4, 128, False),
     (1, 33, 256, 4, 32, True),         # odd N, partial column tile
+    (1, 200, 2048, 8, 32, True),       # int8, two chunks per lane: lanes load their own scales
+    (1, 96, 2048, 4, 16, True),        # block 16: two segments per chunk, lane-loaded scales
+    (1, 32064, 3072, 4, 32, True),     # more wavefronts than the CUs hold: smallest workgroups
     (1, 47, 512, 4, 16, False),
     (1, 65, 1024, 4, 64, True),
     (1, 96, 2048, 4, 128, True),
