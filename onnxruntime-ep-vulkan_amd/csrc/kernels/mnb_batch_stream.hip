@@ -197,6 +197,7 @@ hipError_t batch_go(const BatchStreamGeom& g, const void* a, const uint8_t* b, c
     switch (g.s) {
         case 1: return batch_go_s<BS, HAS_ZP, 1>(g, a, b, s, z, y, m, n, k, st);
         case 2: return batch_go_s<BS, HAS_ZP, 2>(g, a, b, s, z, y, m, n, k, st);
+        case 3: return batch_go_s<BS, HAS_ZP, 3>(g, a, b, s, z, y, m, n, k, st);
         case 4: return batch_go_s<BS, HAS_ZP, 4>(g, a, b, s, z, y, m, n, k, st);
         default: return hipErrorInvalidValue;
     }
@@ -211,22 +212,23 @@ bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamG
     const int64_t quads = k / 128;
     const int64_t strips = (n + 15) / 16;
     BatchStreamGeom g{};
-    // S strips per workgroup (each wavefront's activation registers serve all S): 4 from 1024
-    // strips, else 1.  Measured at 5..16 rows: 16384 columns (1024 strips) 18.9 -> 14.4 us at
-    // S = 4; 9216 columns (576 strips) slower at S = 2 (fewer workgroups in flight) than at 1.
-    g.s = strips >= 4 * 256 ? 4 : 1;
-    // R quads per wavefront (16 R activation VGPRs, 4 S R weight VGPRs: S R <= 8 keeps the
-    // instantiations within 128): among 1..4 dividing the quads into at most 16 wavefronts, the
-    // one closest to 8 wavefronts (the larger R on a tie).
+    // S strips per workgroup (each wavefront's activation registers serve all S, so the
+    // activation rows are read once per S strips): the fewest that keep the launch within one
+    // workgroup per CU, at most 4.  R quads per wavefront (16 R activation VGPRs, 4 S R weight
+    // VGPRs: S R <= 8 keeps the instantiations within 128): the largest of 4..1 that divides the
+    // quads into at most 16 wavefronts.  Measured on MI355X (same-run sweep of S 1-4 x R 1-4):
+    // qkv (576 strips) S = 3, R = 2 at 8 / 16 rows 9.7 / 11.5 us against 11.5 / 14.8 at S = 1,
+    // R = 3; o (192 strips) R = 4 5.4 / 6.4 us against 5.7 / 6.8 at R = 3; gate_up (1024
+    // strips) S = 4, R = 2 14.3 us at 16 rows against 15.2 at S = 2.
+    // (Fewer strips where no R fits: long K needs R = 4 to stay within 16 wavefronts.)
     g.r = 0;
-    int64_t best = 0;
-    for (int r : {4, 3, 2, 1}) {
-        if (quads % r || quads / r > kBatchMaxWaves || g.s * r > 8) continue;
-        const int64_t d = std::abs(quads / r - 8);
-        if (g.r == 0 || d < best) {
+    for (g.s = (int)std::min<int64_t>(4, (strips + 255) / 256); g.s >= 1 && g.r == 0; --g.s) {
+        for (int r : {4, 3, 2, 1}) {
+            if (quads % r || quads / r > kBatchMaxWaves || g.s * r > 8) continue;
             g.r = r;
-            best = d;
+            break;
         }
+        if (g.r) break;
     }
     if (g.r == 0) return false;
     g.waves = (int)(quads / g.r);

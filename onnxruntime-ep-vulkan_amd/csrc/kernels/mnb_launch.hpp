@@ -176,7 +176,7 @@ hipError_t launch_acc4_stream(const Acc4StreamGeom& g, const int8_t* qa, const f
 // activations loaded straight into MFMA registers.  K % 128 == 0, (K / bs) % 4 == 0, bs >= 32.
 struct BatchStreamGeom {
     int r;               // 128-k quads per wavefront: 1..4
-    int s;               // 16-column strips per workgroup: 1, 2 or 4
+    int s;               // 16-column strips per workgroup: 1 to 4
     int waves;           // wavefronts per workgroup, K / (128 r), 1..16
     int64_t gx;          // workgroups: ceil(strips / s)
 };

@@ -156,6 +156,7 @@ SHAPES = [
     (16, 3072, 8192, 4, 32, True),     # sixteen wavefronts of four quads
     (6, 8200, 1024, 4, 64, True),      # two strips per workgroup, last strip partial
     (9, 16400, 512, 4, 32, False),     # four strips per workgroup, last workgroup short
+    (7, 8320, 1024, 4, 64, False),     # three strips per workgroup, last workgroup one strip
     (7, 32, 256, 8, 64, True),
     (8, 160, 1024, 8, 128, False),
     (9, 64, 4096, 4, 32, True),
