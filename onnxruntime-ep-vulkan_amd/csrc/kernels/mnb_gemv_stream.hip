@@ -97,27 +97,29 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     const double wpc = waves_per_cu(g);
     // Workgroups: each stages the whole activation vector (2*K bytes per row) before it streams
     // weights, so more workgroups mean more of that traffic ahead of the weights.  Measured over
-    // every shape of 4..16 wavefronts (MI355X, K=3072: N = 3072, 8192, 9216, 16384, 32064; K=2880,
-    // 4096, 8192): three to five workgroups per CU for K <= 4096, the count that fills the CUs
-    // evenly (the busiest CU's workgroups against the mean) taken among them, then the one closest
-    // to four per CU (gate_up 1024 x 4 7.3 us against 820 x 5 8.2 us; qkv 768 x 6 4.84 us
-    // against 922 x 5 4.87-4.95 us); one per CU for K = 8192.  At least K / 1024 wavefronts, so
-    // that the first staging batch (2 * MR 16-byte units per thread) covers all of A.
+    // every shape of 4..16 wavefronts (MI355X, K=3072: N = 3072, 8192, 9216, 16384, 32064; K=2048,
+    // 2880, 4096, 8192, 14336): for K <= 4096 the wavefront count that fills the CUs most evenly
+    // (the busiest CU's workgroups against the mean), then the one closest to four workgroups per
+    // CU -- one per CU below 16 wavefronts per CU (gate_up 1024 x 8 6.46 us, qkv 768 x 6 4.84 us
+    // against 922 x 5 4.9 us, o 256 x 6 3.30 us against 384 x 4 3.36, K=2880 N=5120 256 x 10
+    // 3.74 us against 640 x 4 3.89); one workgroup per CU for K > 4096.  At least K / 1024
+    // wavefronts, so that the first staging batch (2 * MR 16-byte units per thread) covers all of A.
     const int64_t wmin = std::max<int64_t>(4, (k + 1023) / 1024);
     const int64_t wmax = kStreamMaxThreads / 64;
     auto clampw = [&](int64_t w) { return std::min(std::max(w, wmin), wmax); };
     const double waves_total = wpc * kNumCUs;
-    int64_t w = clampw((int64_t)(wpc / (k <= 4096 ? 4.0 : 1.0) + 0.5));
+    int64_t w = clampw((int64_t)(wpc + 0.5));
     if (k <= 4096 && wpc > 32.0) {
         // more wavefronts than a CU holds at once: the smallest workgroups, which the CUs take up
         // as they finish others (N=32064: 4008 x 4 10.4 us against 1002 x 16 11.6 us)
         w = wmin;
     } else if (k <= 4096) {
+        const double want = wpc >= 16.0 ? 4.0 : 1.0;
         double best_imb = 0.0, best_d = 0.0;
-        for (int64_t cand = clampw((int64_t)(wpc / 5.0 + 0.5)); cand <= clampw((int64_t)(wpc / 3.0 + 0.5)); ++cand) {
+        for (int64_t cand = wmin; cand <= wmax; ++cand) {
             const double groups = std::ceil(waves_total / (double)cand);
             const double imb = std::ceil(groups / kNumCUs) * kNumCUs / groups;
-            const double d = __builtin_fabs(groups / kNumCUs - 4.0);
+            const double d = __builtin_fabs(groups / kNumCUs - want);
             if (best_imb == 0.0 || imb < best_imb - 1e-9 || (imb < best_imb + 1e-9 && d < best_d)) {
                 best_imb = imb;
                 best_d = d;
