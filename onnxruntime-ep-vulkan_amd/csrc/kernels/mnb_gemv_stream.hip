@@ -98,35 +98,36 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     // Workgroups: each stages the whole activation vector (2*K bytes per row) before it streams
     // weights, so more workgroups mean more of that traffic ahead of the weights.  Measured over
     // every shape of 4..16 wavefronts (MI355X, K=3072: N = 3072, 8192, 9216, 16384, 32064; K=2048,
-    // 2880, 4096, 8192, 14336): for K <= 4096 the wavefront count that fills the CUs most evenly
-    // (the busiest CU's workgroups against the mean), then the one closest to four workgroups per
-    // CU -- one per CU below 16 wavefronts per CU (gate_up 1024 x 8 6.46 us, qkv 768 x 6 4.84 us
-    // against 922 x 5 4.9 us, o 256 x 6 3.30 us against 384 x 4 3.36, K=2880 N=5120 256 x 10
-    // 3.74 us against 640 x 4 3.89); one workgroup per CU for K > 4096.  At least K / 1024
-    // wavefronts, so that the first staging batch (2 * MR 16-byte units per thread) covers all of A.
+    // 2880, 4096, 8192, 14336): the wavefront count that fills the CUs most evenly (the busiest
+    // CU's workgroups against the mean), then the one closest to about eight wavefronts per
+    // workgroup (wavefronts per CU / 8 workgroups per CU, 1 to 4), then the larger (gate_up
+    // 1024 x 8 6.46 us; qkv 512 x 9 4.89 us against 922 x 5 4.98; o 256 x 6 3.30 against 384 x 4
+    // 3.34; K=2880 N=5120 256 x 10 3.71 against 640 x 4 3.74; K=4096 N=4096 512 x 8 3.71 against
+    // 1024 x 4 3.90; down 256 x 12 4.43 against 512 x 6 4.83).  At least K / 1024 wavefronts, so
+    // that the first staging batch (2 * MR 16-byte units per thread) covers all of A.
     const int64_t wmin = std::max<int64_t>(4, (k + 1023) / 1024);
     const int64_t wmax = kStreamMaxThreads / 64;
-    auto clampw = [&](int64_t w) { return std::min(std::max(w, wmin), wmax); };
     const double waves_total = wpc * kNumCUs;
-    int64_t w = clampw((int64_t)(wpc + 0.5));
-    if (k <= 4096 && wpc > 32.0) {
-        // more wavefronts than a CU holds at once: the smallest workgroups, which the CUs take up
-        // as they finish others (N=32064: 4008 x 4 10.4 us against 1002 x 16 11.6 us)
-        w = wmin;
-    } else if (k <= 4096) {
-        const double want = wpc >= 16.0 ? 4.0 : 1.0;
+    int64_t w = wmin;
+    if (wpc <= 32.0) {
+        // (with several rows, four workgroups per CU: qkv at two rows 768 x 6 6.2 us against
+        // 512 x 9 6.5 us)
+        const double want = c.mr == 1 ? std::min(4.0, std::max(1.0, wpc / 8.0)) : 4.0;
         double best_imb = 0.0, best_d = 0.0;
         for (int64_t cand = wmin; cand <= wmax; ++cand) {
             const double groups = std::ceil(waves_total / (double)cand);
             const double imb = std::ceil(groups / kNumCUs) * kNumCUs / groups;
             const double d = __builtin_fabs(groups / kNumCUs - want);
-            if (best_imb == 0.0 || imb < best_imb - 1e-9 || (imb < best_imb + 1e-9 && d < best_d)) {
+            if (best_imb == 0.0 || imb < best_imb - 1e-9 ||
+                (imb < best_imb + 1e-9 && d < best_d + 1e-9)) {
                 best_imb = imb;
                 best_d = d;
                 w = cand;
             }
         }
     }
+    // (above 32 wavefronts per CU, more than a CU holds at once: the smallest workgroups, which
+    // the CUs take up as they finish others; N=32064: 4008 x 4 10.4 us against 1002 x 16 11.6 us)
     c.waves_per_group = (int)w;
     derive(c, n, k, bits, bs);
     return c;
