@@ -5,12 +5,14 @@
 // layout -- within every 128-k quad a lane row's chunks 0,1 and 2,3 are two 16-byte pieces --
 // and their fp32 scales block-major over 16 rows).  A workgroup of KW wavefronts owns one strip
 // of 16 columns; wavefront w owns quads [w R, w R + R) of K (KW R = K / 128):
-//   * every thread first requests its share of the 16 rows' codes and scales (2R 16-byte pieces
-//     and R * blocks-per-quad / 4 scales), then its wavefront's block scales and zero points,
-//     then its R quads of weights (lane (n, g): 16 bytes of column n, chunk 4q + g, streamed
-//     past the caches) -- so the activations, needed first, are not queued behind the weights;
-//   * the codes go to LDS (rows padded by 16 bytes: the 16 rows' reads start in distinct bank
-//     groups), one barrier, and each wavefront computes: a 4 x 4 dword transpose across the lane
+//   * every wavefront first requests its own quads' codes of the 16 rows (2R 16-byte pieces
+//     per lane) and their activation scales; one barrier that waits for no load puts all of
+//     these requests ahead of any weight request in the CU (whose vector memory returns data in
+//     request order); then the wavefront's block scales and zero points, then its R quads of
+//     weights (lane (n, g): 16 bytes of column n, chunk 4q + g, streamed past the caches);
+//   * each wavefront stages its own codes in LDS (rows padded by 16 bytes: the 16 rows' reads
+//     start in distinct bank groups; no workgroup barrier, no other wavefront reads them) and
+//     computes quad by quad as its weights arrive: a 4 x 4 dword transpose across the lane
 //     rows gives the B operands, weights become exact int8 (q - zp), v_mfma_i32_16x16x64_i8
 //     (16x16x32 for block 32) gives exact int32 block dots, scaled by a_scale * b_scale in fp32;
 //   * the KW partial tiles are added in LDS in wavefront order (run-to-run deterministic) and
@@ -30,11 +32,14 @@ namespace mnb {
 
 namespace {
 
-constexpr int kAcc4sMaxWaves = 16;
+// Wavefronts per workgroup the kernel is compiled for: 8 at R = 8 quads per wavefront (K = 8192;
+// its 2R code pieces and R weight chunks per lane need more than the 128 VGPRs of 16 wavefronts),
+// 16 below.
+constexpr int acc4s_max_waves(int r) { return r == 8 ? 8 : 16; }
 constexpr size_t kAcc4sMaxLds = 160 * 1024;
 
 template <int BS, bool HAS_ZP, int R>
-__global__ void __launch_bounds__(64 * kAcc4sMaxWaves)
+__global__ void __launch_bounds__(64 * acc4s_max_waves(R))
 acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
             const uint8_t* __restrict__ B, const f16* __restrict__ Sc,
             const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K) {
@@ -46,7 +51,6 @@ acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
     const int lane = threadIdx.x & 63;
     const int kw = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int KW = blockDim.x >> 6;
-    const int T = blockDim.x;
     const int nl = lane & 15;
     const int g = lane >> 4;
     const int quads = K >> 7;                            // = KW * R
@@ -59,25 +63,33 @@ acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
     float* const sSa = reinterpret_cast<float*>(smem + 16 * RB);          // [bpc][16] + 4
     f32x4* const sRed = reinterpret_cast<f32x4*>(smem + 16 * RB + bpc * 64 + 16);
 
-    // ---- 1. this thread's share of the codes and activation scales -------------------------
-    // 16 rows x quads x 8 pieces = T * PA exactly.  The workgroup's T = 64 KW threads cover 8 / R
-    // whole rows of ppr = 8 quads pieces, so piece i of thread t is piece p0 of row
-    // row0 + i * 8 / R; rows past M repeat row M - 1 (never stored).
-    const int t = threadIdx.x;
-    const int ppr = 8 * quads;                           // pieces per row
-    const int row0 = t / ppr;
-    const int p0 = t - row0 * ppr;
-    constexpr int kRowStep = 8 / R;
+    // ---- 1. this wavefront's own codes and activation scales -------------------------------
+    // The wavefront's quads of the 16 rows are 16 x 8R pieces: one load instruction covers 8 / R
+    // whole rows of them (8R lanes per row), 2R instructions all 16 rows; rows past M repeat row
+    // M - 1 (never stored).  Its activation scales are one contiguous run of 16 R BPQ floats.
+    constexpr int LPR = 8 * R;
+    constexpr int RPI = 8 / R;
+    constexpr int NSA = 16 * R * BPQ;
+    constexpr int PSW = (NSA + 63) / 64;
+    const int prow = lane / LPR;
+    const int ppc = lane % LPR;
     u32x4 va[PA];
 #pragma unroll
     for (int i = 0; i < PA; ++i) {
-        const int row = min(row0 + i * kRowStep, M - 1);
-        va[i] = *reinterpret_cast<const u32x4*>(qa + (int64_t)row * K + 16 * p0);
+        const int row = min(i * RPI + prow, M - 1);
+        va[i] = *reinterpret_cast<const u32x4*>(qa + (int64_t)row * K + 128 * q0 + 16 * ppc);
     }
     const int nsc = bpc * 16;
-    float vs[PS];
+    const int sbase = 16 * q0 * BPQ;
+    float vs[PSW];
 #pragma unroll
-    for (int i = 0; i < PS; ++i) vs[i] = a_scale[min(t + i * T, nsc - 1)];
+    for (int i = 0; i < PSW; ++i) vs[i] = a_scale[sbase + min(lane + 64 * i, NSA - 1)];
+    // every wavefront's activation requests go out before any wavefront's weight requests (the
+    // CU's vector memory returns data in request order, so codes requested behind another
+    // wavefront's weights would wait for those); the barrier waits for no load
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. the wavefront's block scales and zero points (contiguous per column) -----------
     const int col = min(16 * strip + nl, N - 1);
@@ -123,19 +135,22 @@ acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
         bw[j] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4*>(bc + 16 * (int64_t)(4 * (q0 + j) + g)));
 
-    // ---- 4. stage the codes and scales; unpredicated stores (a dummy slot for the scales
-    // past the end), so that only the activation loads are waited for here --------------------
+    // all of the loads above are issued before the staging below waits for the first of them
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 4. stage the wavefront's own codes and scales: no other wavefront reads them, and a
+    // wavefront's LDS accesses complete in program order, so no workgroup barrier ------------
 #pragma unroll
     for (int i = 0; i < PA; ++i)
-        *reinterpret_cast<u32x4*>(sA + (row0 + i * kRowStep) * RB + 16 * p0) = va[i];
+        *reinterpret_cast<u32x4*>(sA + (i * RPI + prow) * RB + 128 * q0 + 16 * ppc) = va[i];
 #pragma unroll
-    for (int i = 0; i < PS; ++i) {
-        const int u = t + i * T;
-        sSa[u < nsc ? u : nsc + (u & 3)] = vs[i];
+    for (int i = 0; i < PSW; ++i) {
+        const int u = lane + 64 * i;
+        sSa[u < NSA ? sbase + u : nsc + (u & 3)] = vs[i];    // a dummy slot past the end
     }
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---- 5. the strip's partial tile over this wavefront's quads -----------------------------
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -236,10 +251,11 @@ bool acc4_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, Acc4StreamGeo
     const int64_t quads = k / 128;
     Acc4StreamGeom g{};
     // R quads per wavefront: the largest of 8, 4, 2, 1 that divides K into at least 8
-    // wavefronts (into all of its quads when there are fewer than 8), at most 16 wavefronts.
+    // wavefronts (into all of its quads when there are fewer than 8), at most 16 wavefronts (8
+    // at R = 8: K = 9216 with block 128 now goes to the strip GEMV).
     g.r = 0;
     for (int r : {8, 4, 2, 1}) {
-        if (quads % r == 0 && (quads / r >= 8 || r == 1) && quads / r <= kAcc4sMaxWaves) {
+        if (quads % r == 0 && (quads / r >= 8 || r == 1) && quads / r <= acc4s_max_waves(r)) {
             g.r = r;
             break;
         }
