@@ -56,10 +56,12 @@ int hip_fail(hipError_t e, const char* what) {
 // Rows above which the prefill GEMM replaces the 16-row MFMA GEMV.
 constexpr int64_t kGemmMinRows = 64;
 // Rows from which the batched decode kernel is planned (below: the streaming GEMV), and at four
-// rows the weight bytes under which it still is.  Measured on the Phi-3.5 decode shapes at four
-// rows: the streaming GEMV ahead on qkv (9.5 vs 10.1 us), gate_up (12.0 vs 12.7) and down (8.4
-// vs 9.6), the batched kernel on o (4.7 MB of weights: 5.1 vs 6.0 us); at 2-3 rows the
-// streaming GEMV on every node, at 5 and more it cannot stream the weights once.
+// rows where it still is: with several strips per workgroup, or under this many weight bytes.
+// Measured on the Phi-3.5 decode shapes at four rows (cold weights): the batched kernel ahead on
+// qkv (3 strips per workgroup: 9.3 vs 10.0 us), gate_up (4: 11.7 vs 12.6) and o (4.7 MB of
+// weights: 5.1 vs 6.0 us), the streaming GEMV on down (one strip per workgroup, 12.6 MB: 8.7 vs
+// 9.5); at 2-3 rows the streaming GEMV on every node, at 5 and more it cannot stream the weights
+// once.
 constexpr int64_t kBatchMinRows = 5;
 constexpr int64_t kBatchFourRowsBelow = 8 << 20;
 
@@ -209,7 +211,8 @@ int mnb_plan(const mnb_problem* p, mnb_plan_info* out) {
     const bool batch = f16 && p->bits == 4 &&
                        mnb::batch_stream_geometry(p->m, p->n, p->k, p->block_size, &bg);
     const bool batch_rows = p->m >= kBatchMinRows ||
-                            (p->m == 4 && b_bytes_of(p) < kBatchFourRowsBelow) || !stream;
+                            (p->m == 4 && (bg.s >= 2 || b_bytes_of(p) < kBatchFourRowsBelow)) ||
+                            !stream;
     if (batch && p->m >= 4 && batch_rows) kern = MNB_KERNEL_BATCH_STREAM;
     if (stream && !(batch && batch_rows)) kern = MNB_KERNEL_GEMV_STREAM;
     const int forced = forced_kernel();
