@@ -616,7 +616,10 @@ hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* 
     if (m == 0) return hipSuccess;
     if (k % bs || (bs != 16 && bs != 32 && bs != 64 && bs != 128)) return hipErrorInvalidValue;
     const int64_t groups = m * (k / 8);
-    const dim3 grid((unsigned)((groups + 255) / 256));
+    // one thread per 8 values; small activations (decode: at most 256 workgroups of 256) in
+    // workgroups of one wavefront, so that every CU takes a share of the loads
+    const int tpb = groups <= 256 * 256 ? 64 : 256;
+    const dim3 grid((unsigned)((groups + tpb - 1) / tpb));
     // scales [m][k/bs], or block-major [k/bs][scale_rows] when scale_rows > 0
     const int s_row = scale_rows > 0 ? 1 : (int)(k / bs);
     const int s_blk = scale_rows > 0 ? (int)scale_rows : 1;
@@ -625,27 +628,27 @@ hipError_t launch_quantize_a_int8(const void* a, bool a_f16, int8_t* qa, float* 
 #define MNB_Q(T_, BS_)                                                                            \
     do {                                                                                          \
         if (quads && vec)                                                                         \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 2, true>), grid, dim3(256), 0, st,       \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 2, true>), grid, dim3(tpb), 0, st,       \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
                                (int)ncnt, s_row, s_blk);                                          \
         else if (quads)                                                                           \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 2, false>), grid, dim3(256), 0, st,      \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 2, false>), grid, dim3(tpb), 0, st,      \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
                                (int)ncnt, s_row, s_blk);                                          \
         else if (permuted && vec)                                                                 \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 1, true>), grid, dim3(256), 0, st,       \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 1, true>), grid, dim3(tpb), 0, st,       \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
                                (int)ncnt, s_row, s_blk);                                          \
         else if (vec)                                                                             \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 0, true>), grid, dim3(256), 0, st,       \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 0, true>), grid, dim3(tpb), 0, st,       \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
                                (int)ncnt, s_row, s_blk);                                          \
         else if (permuted)                                                                        \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 1, false>), grid, dim3(256), 0, st,      \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 1, false>), grid, dim3(tpb), 0, st,      \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
                                (int)ncnt, s_row, s_blk);                                          \
         else                                                                                      \
-            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 0, false>), grid, dim3(256), 0, st,      \
+            hipLaunchKernelGGL((quantize_a_int8<T_, BS_, 0, false>), grid, dim3(tpb), 0, st,      \
                                static_cast<const T_*>(a), qa, scale, qsum, (int)m, (int)k, cnt,   \
                                (int)ncnt, s_row, s_blk);                                          \
     } while (0)

@@ -71,7 +71,7 @@ def test_planner_shapes_stay_within_compiled_bounds():
               mnb.KERNEL_STRIP_MFMA: 1024, mnb.KERNEL_GENERIC: 256,
               mnb.KERNEL_ACC4_STREAM: 1024, mnb.KERNEL_BATCH_STREAM: 1024}
     for m in (1, 2, 3, 4, 5, 8, 16, 17, 33, 64, 65, 256, 2048):
-        for k, n in ((3072, 9216), (8192, 3072), (2880, 2880), (128, 48)):
+        for k, n in ((3072, 9216), (8192, 3072), (9216, 3072), (2880, 2880), (128, 48)):
             for bits in (4, 8):
                 for bs in (16, 32, 64, 128):
                     for level in (0, 4):
@@ -80,7 +80,10 @@ def test_planner_shapes_stay_within_compiled_bounds():
                             info = mnb.plan(p)
                         except mnb.MnbError:
                             continue
-                        assert 64 * info.waves_per_group <= bounds[info.kernel], (m, k, n, bits, bs, level, info.kernel, info.waves_per_group)
+                        bound = bounds[info.kernel]
+                        if info.kernel == mnb.KERNEL_ACC4_STREAM and (k // 128) // info.waves_per_group == 8:
+                            bound = 512                  # 8 quads per wavefront: compiled for 8 wavefronts
+                        assert 64 * info.waves_per_group <= bound, (m, k, n, bits, bs, level, info.kernel, info.waves_per_group)
 
 
 def test_noalloc_refuses_level_4_beyond_its_scratch():
