@@ -116,3 +116,35 @@ def test_rmsnorm_refuses_wide_fp32_rows():
             assert b"hidden" in lib.mnb_last_error()
         rc = lib.mnb_skip_rmsnorm(C.byref(p), None, None, None, None, None, None, None)
         assert (rc == mnb.MNB_ERR_INVALID) if ok else (rc == mnb.MNB_ERR_UNSUPPORTED)
+
+
+def test_decode_routing_by_rows_and_strips():
+    """Host planning of the Phi-3.5 decode nodes (int4, block 32, zero points): up to three rows
+    stream the weights once per row-tile on gemv_stream; at four rows the batched kernel takes
+    the nodes it packs several strips into per workgroup (qkv, gate_up) or with under 8 MiB of
+    weights (o), gemv_stream keeps down (one strip per workgroup, 12 MiB); from five rows on the
+    batched kernel takes every node."""
+    import mnb
+
+    nodes = {"qkv": (3072, 9216), "o": (3072, 3072), "gate_up": (3072, 16384), "down": (8192, 3072)}
+    want4 = {"qkv": mnb.KERNEL_BATCH_STREAM, "o": mnb.KERNEL_BATCH_STREAM,
+             "gate_up": mnb.KERNEL_BATCH_STREAM, "down": mnb.KERNEL_GEMV_STREAM}
+    for name, (k, n) in nodes.items():
+        for m in (1, 2, 3):
+            assert mnb.plan(mnb.problem(m, n, k, 4, 32, True)).kernel == mnb.KERNEL_GEMV_STREAM, (name, m)
+        assert mnb.plan(mnb.problem(4, n, k, 4, 32, True)).kernel == want4[name], name
+        for m in (5, 8, 16):
+            assert mnb.plan(mnb.problem(m, n, k, 4, 32, True)).kernel == mnb.KERNEL_BATCH_STREAM, (name, m)
+
+
+def test_level4_stream_kernel_k_limit():
+    """accuracy_level 4 at 16 fp16 rows: K = 8192 takes the strip-per-workgroup int8 kernel with
+    8 quads per wavefront (8 wavefronts, the most it is compiled for at that depth); K = 9216 with
+    block 128 would need 9 such wavefronts and goes to the int8 strip GEMV instead."""
+    import mnb
+
+    p = mnb.problem(16, 3072, 8192, 4, 128, True, mnb.DTYPE_F16, 4)
+    info = mnb.plan(p)
+    assert info.kernel == mnb.KERNEL_ACC4_STREAM and info.waves_per_group == 8
+    p = mnb.problem(16, 3072, 9216, 4, 128, True, mnb.DTYPE_F16, 4)
+    assert mnb.plan(p).kernel == mnb.KERNEL_ACC4_I8
