@@ -151,6 +151,8 @@ SHAPES = [
     (4, 48, 16384, 4, 32, True),       # four one-row tiles
     (5, 64, 512, 8, 16, False),
     (5, 9216, 3072, 4, 32, True),      # qkv at five rows: the batched decode kernel
+    (4, 9216, 3072, 4, 32, True),      # qkv at four rows: batched, three strips per workgroup
+    (4, 16400, 1024, 4, 32, False),    # four rows, four strips per workgroup, last workgroup one strip
     (7, 40, 1024, 4, 64, True),
     (12, 33, 2048, 4, 128, False),     # partial strip
     (16, 3072, 8192, 4, 32, True),     # sixteen wavefronts of four quads
