@@ -3,13 +3,14 @@
 //
 // A workgroup of KW wavefronts owns S consecutive strips of 16 columns; wavefront w owns quads
 // [w R, w R + R) of K (a quad is 128 k; KW R = K / 128) of all S strips.  Every lane first
-// requests the activations it multiplies -- as the v_mfma_f32_16x16x32_f16 A operand, lane (n, g) takes row n
-// (rows past M repeat row M - 1 and are never stored), k = 32 c + 8 g .. + 7 of each 32-k chunk c:
-// 16 bytes, straight into registers, no LDS, used for all S strips -- then its columns' block
-// scales and zero points for the wavefront's quads (one contiguous run per column), then its S R
-// 16-byte weight loads (lane (n, g): chunk 4 q + g of column n of each strip, streamed past the
-// caches).  So nothing waits for another wavefront until the end, and the activations, needed
-// first, are not queued behind the weights.
+// requests the activations of the wavefront's quads -- one load per 4 rows x 256 bytes of a quad
+// (rows past M repeat row M - 1 and are never stored) -- then its columns' block scales and zero
+// points for those quads (one contiguous run per column), then its S R 16-byte weight loads
+// (lane (n, g): chunk 4 q + g of column n of each strip, streamed past the caches), so the
+// activations, needed first, are not queued behind the weights.  Quad by quad the activations
+// pass through the wavefront's own LDS slot into the v_mfma_f32_16x16x32_f16 A operand layout
+// (lane (n, g): row n, k = 32 c + 8 g .. + 7 of each 32-k chunk c), kept in registers for all S
+// strips; nothing waits for another wavefront until the end.
 // Per quad a 4 x 4 dword transpose across the lane rows leaves lane (n, g) holding, for each chunk
 // c, the eight weights k = 32 c + 8 g .. + 7 of column n -- the B operand -- which become exact
 // fp16 (q - zp) values; the MFMAs of one quant block accumulate its exact-product fp32 partial,
@@ -33,6 +34,9 @@ namespace mnb {
 namespace {
 
 constexpr int kBatchMaxWaves = 16;
+// Bytes per row of a wavefront's LDS slot: one quad of fp16 activations (256 bytes) padded by 16
+// so that the 16 rows' operand reads start in distinct bank groups.
+constexpr int kBatchSlotRow = 256 + 16;
 
 template <int BS, bool HAS_ZP, int R, int S>
 __global__ void __launch_bounds__(64 * kBatchMaxWaves)
@@ -40,7 +44,7 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
              const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K) {
     constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
     constexpr int BPQ = 4 / CPB;                         // blocks per quad
-    extern __shared__ f32x4 sRed[];                      // [KW - 1][S][64]
+    extern __shared__ f32x4 sRed[];                      // [KW - 1][S][64], then KW slots
     const int lane = threadIdx.x & 63;
     const int kw = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int KW = blockDim.x >> 6;
@@ -51,15 +55,17 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
     const int strip0 = blockIdx.x * S;
     const int q0 = kw * R;                               // this wavefront's first quad
 
-    // ---- 1. the activations of the wavefront's quads, as MFMA A operands ---------------------
-    const f16* ar = A + (int64_t)min(nl, M - 1) * K + 128 * q0 + 8 * g;
-    f16x8 av[R][4];
+    // ---- 1. the activations of the wavefront's quads: each load covers 4 rows x 256 bytes of
+    // one quad (whole lines; loading the MFMA operands directly touched 16 half lines per load)
+    const int lrow = lane >> 4;
+    const int lpc = lane & 15;
+    f16x8 raw[R][4];
 #pragma unroll
     for (int j = 0; j < R; ++j)
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            av[j][c] = *reinterpret_cast<const f16x8*>(ar + 128 * j + 32 * c);
-
+            raw[j][c] = *reinterpret_cast<const f16x8*>(
+                A + (int64_t)min(4 * c + lrow, M - 1) * K + 128 * (q0 + j) + 8 * lpc);
     // ---- 2. the columns' block scales and zero points for those quads ----------------------
     constexpr int NS = R * BPQ;                          // blocks of the wavefront's quads
     constexpr int NZ = (NS + 1) / 2;
@@ -116,6 +122,28 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
     // stream waits on its own arrivals: 16 rows, gate_up 14.4 -> 12.7 us, qkv 11.3 -> 10.5 us);
     // with one strip the compiler's interleaving measured faster (o 6.2 against 6.6 us).
     if constexpr (S > 1) __builtin_amdgcn_sched_barrier(0);
+
+    // ---- the activations into the MFMA operand layout (lane (n, g): row n, k = 32 c + 8 g ..
+    // + 7 of each chunk c), quad by quad through the wavefront's own LDS slot: no other
+    // wavefront touches it and a wavefront's LDS accesses complete in program order ----------
+    uint8_t* const slot = reinterpret_cast<uint8_t*>(sRed) + (size_t)(KW - 1) * S * 64 * 16 +
+                          (size_t)kw * 16 * kBatchSlotRow;
+    f16x8 av[R][4];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            *reinterpret_cast<f16x8*>(slot + (4 * c + lrow) * kBatchSlotRow + 16 * lpc) = raw[j][c];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            av[j][c] = *reinterpret_cast<const f16x8*>(slot + nl * kBatchSlotRow + 64 * c + 16 * g);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
 
     // ---- 4. each strip's partial tile over this wavefront's quads ----------------------------
     f32x4 acc[S];
@@ -176,10 +204,17 @@ hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b,
                       const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
     const dim3 grid((unsigned)g.gx, 1, 1);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
-    const size_t lds = (size_t)(g.waves - 1) * S * 64 * sizeof(f32x4);
+    const size_t lds = (size_t)(g.waves - 1) * S * 64 * sizeof(f32x4) +
+                       (size_t)g.waves * 16 * kBatchSlotRow;
     // instantiated for S R <= 8 only (the geometry's register budget)
 #define MNB_BS(R_)                                                                                \
     if constexpr (S * R_ <= 8) {                                                                  \
+        if (lds > 64 * 1024) {                                                                    \
+            const hipError_t ea = hipFuncSetAttribute(                                           \
+                reinterpret_cast<const void*>(batch_stream<BS, HAS_ZP, R_, S>),                  \
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                            \
+            if (ea != hipSuccess) return ea;                                                      \
+        }                                                                                         \
         hipLaunchKernelGGL((batch_stream<BS, HAS_ZP, R_, S>), grid, block, lds, st,              \
                            static_cast<const f16*>(a), b, static_cast<const f16*>(s), z,          \
                            static_cast<f16*>(y), (int)m, (int)n, (int)k);                         \
