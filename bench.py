@@ -2,14 +2,15 @@
 
 Workload: the Phi-3.5-mini decode layer set at M=1, int4,
 block_size 32, packed uint8 zero points — qkv (K=3072, N=9216), o (3072 -> 3072), gate_up
-(3072 -> 16384), down (8192 -> 3072).  One step = those four MatMulNBits launches over one
-layer's weights.  The weights of L layer copies (>= 2 x the 256 MB Infinity Cache) are rotated
-step by step so every step streams its weights from HBM, as a real decode does.  Inputs are
-synthetic (seeded), resident in HBM before the timed region.  The timed steps are recorded once
-into a HIP graph and replayed, so the figure is the device's, not Python's launch overhead
-(the same steps launched one by one from Python are reported as eager_ms_per_step).
+(3072 -> 16384), down (8192 -> 3072).  One step = one token's MatMulNBits work: those four
+launches over each of the model's 32 layers (128 launches, 2,098,200,576 bytes), every layer with
+weights of its own, so a step streams 2.1 GB from HBM (8x the 256 MB Infinity Cache) as a real
+decode does.  Inputs are synthetic (seeded), resident in HBM before the timed region.  The timed
+steps are recorded once into a HIP graph and replayed, so the figure is the device's, not
+Python's launch overhead (the same steps launched one by one from Python are reported as
+eager_ms_per_step).
 
-value = algorithmic bytes of the layer set (65,568,768 B) per step / step time, in GB/s.
+value = algorithmic bytes of one token (32 x 65,568,768 B) per step / step time, in GB/s.
 The line also carries, measured in the same run:
   roofline      the dominant decode kernel's algorithmic bytes / its HIP-event launch time vs 8 TB/s
   batched_decode  the same layer set at M = 4, 8, 16 rows in GB/s of algorithmic bytes
@@ -44,6 +45,7 @@ for _p in (str(ROOT), str(PKG)):
 HBM_PEAK_GBS = 8000.0
 F16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 * 1024 * 1024
+LAYERS_PER_TOKEN = 32  # Phi-3.5-mini's decoder layers: one bench step is one token
 
 LAYER = [  # (name, K, N)
     ("qkv_proj", 3072, 9216),
@@ -193,8 +195,8 @@ def stock_ort_probe() -> str:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--pmc-node", default=None,
@@ -232,7 +234,8 @@ def main() -> int:
     gen.manual_seed(20260801)
 
     per_layer = sum(node_bytes(1, k, n) for _, k, n in LAYER)
-    copies = max(2, -(-2 * MALL_BYTES // per_layer))
+    per_token = LAYERS_PER_TOKEN * per_layer
+    copies = LAYERS_PER_TOKEN            # one weight set per layer
     layers = [[make_weights(torch, dev, k, n, gen) for _, k, n in LAYER] for _ in range(copies)]
     acts = [torch.randn(1, k, device=dev, generator=gen).to(torch.float16) for _, k, _ in LAYER]
     outs = [torch.empty(1, n, dtype=torch.float16, device=dev) for _, _, n in LAYER]
@@ -248,8 +251,9 @@ def main() -> int:
             mnb.check(rc)
 
     def step(s, sp=sptr):
-        for i in range(len(LAYER)):
-            launch(i, s % copies, sp)
+        for layer in range(LAYERS_PER_TOKEN):
+            for i in range(len(LAYER)):
+                launch(i, layer, sp)
 
     if args.read_floor:
         region = torch.empty(1536 << 20, dtype=torch.uint8, device=dev)
@@ -365,7 +369,7 @@ def main() -> int:
     graph = capture(lambda sp: [step(s, sp) for s in range(args.steps)])
     graph.replay()
     torch.cuda.synchronize()
-    # the graph's last step used the same weight copy as eager step (steps-1) % copies
+    # every step launches the same 128 nodes: one eager step must reproduce the graph's outputs
     for s in range(args.steps - 1, args.steps):
         step(s)
     torch.cuda.synchronize()
@@ -390,7 +394,7 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms_step = wall * 1e3 / args.steps
     dev_ms_step = ev0.elapsed_time(ev1) / args.steps
-    value = per_layer / (ms_step * 1e-3) / 1e9
+    value = per_token / (ms_step * 1e-3) / 1e9
 
     # The same steps launched one by one from Python (reported, not the value).
     torch.cuda.synchronize()
@@ -450,6 +454,8 @@ def main() -> int:
                            "read_floor_us": round(floors[i][0], 3),
                            "frac_of_read_floor": round(floors[i][0] / us, 4),
                            "kernel": mnb.KERNEL_NAMES.get(mnb.plan(probs[i]).kernel, "?")})
+    # the token's time as the sum of its launches, each timed on its own (32 x the four nodes)
+    node_sum_ms = LAYERS_PER_TOKEN * sum(kern_us) * 1e-3
     dom = max(range(len(LAYER)), key=lambda i: kern_us[i])
     dom_bytes = node_bytes(1, LAYER[dom][1], LAYER[dom][2])
     achieved = dom_bytes / (kern_us[dom] * 1e-6) / 1e9
@@ -832,11 +838,14 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f16 activations x int4 weights, fp32 accumulate",
         "data": "synthetic (seeded): A ~ N(0,1), uniform nibbles and zero points, scales |N(0,1)|*0.02",
-        "config": {"workload": "Phi-3.5-mini decode layer set, M=1, int4 block_size=32 with "
-                               "zero_points (qkv 3072->9216, o 3072->3072, gate_up 3072->16384, "
-                               "down 8192->3072)",
-                   "bytes_per_step": per_layer, "weight_copies_rotated": copies,
-                   "rotated_bytes": per_layer * copies},
+        "config": {"workload": "Phi-3.5-mini decode, one token's MatMulNBits work per step: "
+                               "32 layers x (qkv 3072->9216, o 3072->3072, gate_up "
+                               "3072->16384, down 8192->3072), M=1, int4 block_size=32 with "
+                               "zero_points, every layer its own weights",
+                   "layers": LAYERS_PER_TOKEN, "launches_per_step": LAYERS_PER_TOKEN * len(LAYER),
+                   "bytes_per_step": per_token, "bytes_per_layer": per_layer},
+        "node_sum_ms_per_step": round(node_sum_ms, 5),
+        "step_over_node_sum": round(ms_step / node_sum_ms, 4),
         "roofline": roofline,
         "per_kernel": per_kernel,
         "batched_decode": batched,

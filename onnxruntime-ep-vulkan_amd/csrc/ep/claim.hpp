@@ -156,6 +156,10 @@ struct QmoeFacts {
     float activation_beta = 0.0f;
     bool has_swiglu_limit = false;
     float swiglu_limit = 0.0f;
+    // Session option ep.qmoe_unfused_as_interleaved: claim swiglu_fusion = 0 without fc3 (the
+    // gpt-oss export as recorded) and run it as the interleaved layout.  That reading is inferred
+    // from the reference's census, not pinned by any fixture, so it is off unless asked for.
+    bool unfused_as_interleaved = false;
 };
 
 // Extents read off the weight shapes when the claim succeeds.
@@ -202,6 +206,9 @@ inline ClaimDecision claim_qmoe(const QmoeFacts& f, QmoeShape* shape = nullptr) 
         if (f.inputs[i].present)
             return decline("input " + std::to_string(i) +
                            " (fc3 / zero points / FP4-FP8 scales) is not implemented");
+    if (f.swiglu_fusion == 0 && !f.unfused_as_interleaved)
+        return decline("swiglu_fusion = 0 without fc3: its layout is not specified by ORT; set "
+                       "ep.qmoe_unfused_as_interleaved=1 to run it as the interleaved layout");
     const InputFacts& x = f.inputs[0];
     const InputFacts& r = f.inputs[1];
     if (!x.present || x.elem_type != kElemFloat16) return decline("input is not float16");

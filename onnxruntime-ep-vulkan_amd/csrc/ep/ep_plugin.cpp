@@ -440,6 +440,7 @@ struct Ep {
     mnb_session* session = nullptr;
     bool keep_constant_initializers = false;
     bool claim_enabled = true;
+    bool qmoe_unfused_as_interleaved = false;   // ep.qmoe_unfused_as_interleaved
     // Device-memory mode: the HBM memory device ORT places this EP's tensors on (owned by the
     // factory's memory info), else null.
     const OrtMemoryDevice* memory_device = nullptr;
@@ -946,7 +947,9 @@ void get_capability(Ep* ep, const OrtGraph* graph, OrtEpGraphSupportInfo* suppor
         }
         if (is_qmoe(op, dom)) {
             const std::string name = node_string(api, node, api->Node_GetName);
-            const ClaimDecision d = claim_qmoe(qmoe_facts(api, node));
+            QmoeFacts qf = qmoe_facts(api, node);
+            qf.unfused_as_interleaved = ep->qmoe_unfused_as_interleaved;
+            const ClaimDecision d = claim_qmoe(qf);
             if (!d.claim) {
                 claim_log("decline %s: %s", name.c_str(), d.reason.c_str());
                 continue;
@@ -1018,7 +1021,8 @@ std::vector<size_t> fused_input_map(const OrtApi* api, const OrtNode* node, cons
 
 std::unique_ptr<NodeKernel> compile_qmoe(Ep* ep, const OrtNode* node, const OrtNode* fused) {
     const OrtApi* api = ep->api;
-    const QmoeFacts f = qmoe_facts(api, node);
+    QmoeFacts f = qmoe_facts(api, node);
+    f.unfused_as_interleaved = ep->qmoe_unfused_as_interleaved;
     QmoeShape shape;
     const ClaimDecision d = claim_qmoe(f, &shape);
     if (!d.claim) fail(ORT_EP_FAIL, "compiled node fails the QMoE claim predicate: %s", d.reason.c_str());
@@ -1421,6 +1425,8 @@ OrtStatus* ORT_API_CALL f_create_ep(OrtEpFactory* self, const OrtHardwareDevice*
         }
         if (session_option(api, so, "ep.keep_constant_initializers", &opt))
             ep->keep_constant_initializers = opt == "1" || opt == "true";
+        if (session_option(api, so, "ep.qmoe_unfused_as_interleaved", &opt))
+            ep->qmoe_unfused_as_interleaved = opt == "1" || opt == "true";
         // ep.max_claim_ops: comma-separated allowlist (reference: rust/src/ep.rs:39-160);
         // claiming is on only when MatMulNBits is listed.
         if (session_option(api, so, "ep.max_claim_ops", &opt))

@@ -223,11 +223,8 @@ hipError_t acc4s_go(const Acc4StreamGeom& g, const int8_t* qa, const float* sa, 
 #define MNB_A4S(R_)                                                                               \
     do {                                                                                          \
         auto kern = acc4_stream<BS, HAS_ZP, R_>;                                                  \
-        if (g.lds > 64 * 1024) {                                                                  \
-            const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),      \
-                hipFuncAttributeMaxDynamicSharedMemorySize, (int)g.lds);                          \
-            if (ea != hipSuccess) return ea;                                                      \
-        }                                                                                         \
+        const hipError_t ea = allow_dynamic_lds(reinterpret_cast<const void*>(kern), g.lds);     \
+        if (ea != hipSuccess) return ea;                                                          \
         hipLaunchKernelGGL(kern, grid, block, g.lds, st, qa, sa, b, static_cast<const f16*>(s),   \
                            z, static_cast<f16*>(y), (int)m, (int)n, (int)k);                      \
     } while (0)

@@ -59,13 +59,17 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
     // one quad (whole lines; loading the MFMA operands directly touched 16 half lines per load)
     const int lrow = lane >> 4;
     const int lpc = lane & 15;
+    // A load whose four rows all lie past M (4 c >= M: uniform over the wavefront) is not made;
+    // those rows take zeros and their MFMA output rows are never stored.
     f16x8 raw[R][4];
 #pragma unroll
     for (int j = 0; j < R; ++j)
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-            raw[j][c] = *reinterpret_cast<const f16x8*>(
-                A + (int64_t)min(4 * c + lrow, M - 1) * K + 128 * (q0 + j) + 8 * lpc);
+            raw[j][c] = 4 * c < M ? *reinterpret_cast<const f16x8*>(
+                                        A + (int64_t)min(4 * c + lrow, M - 1) * K +
+                                        128 * (q0 + j) + 8 * lpc)
+                                  : f16x8{};
     // ---- 2. the columns' block scales and zero points for those quads ----------------------
     constexpr int NS = R * BPQ;                          // blocks of the wavefront's quads
     constexpr int NZ = (NS + 1) / 2;
@@ -209,12 +213,9 @@ hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b,
     // instantiated for S R <= 8 only (the geometry's register budget)
 #define MNB_BS(R_)                                                                                \
     if constexpr (S * R_ <= 8) {                                                                  \
-        if (lds > 64 * 1024) {                                                                    \
-            const hipError_t ea = hipFuncSetAttribute(                                           \
-                reinterpret_cast<const void*>(batch_stream<BS, HAS_ZP, R_, S>),                  \
-                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                            \
-            if (ea != hipSuccess) return ea;                                                      \
-        }                                                                                         \
+        const hipError_t ea = allow_dynamic_lds(                                                  \
+            reinterpret_cast<const void*>(batch_stream<BS, HAS_ZP, R_, S>), lds);                \
+        if (ea != hipSuccess) return ea;                                                          \
         hipLaunchKernelGGL((batch_stream<BS, HAS_ZP, R_, S>), grid, block, lds, st,              \
                            static_cast<const f16*>(a), b, static_cast<const f16*>(s), z,          \
                            static_cast<f16*>(y), (int)m, (int)n, (int)k);                         \

@@ -519,8 +519,7 @@ static hipError_t gemm_go(const GemmConfig& c, const void* a, const uint8_t* b, 
     auto kern = gemm_f16_mfma<BITS, BS, HAS_ZP>;
     constexpr int lds = GemmForm<BITS, BS>::kLds;
     // More than 64 KB of dynamic LDS must be allowed explicitly (for the current device).
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    const hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
     if (e != hipSuccess) return e;
     const int ks = part ? c.ksplit : 1;
     const int64_t items = c.tiles_m * c.tiles_n * ks;

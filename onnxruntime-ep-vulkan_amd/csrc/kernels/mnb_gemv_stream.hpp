@@ -537,11 +537,8 @@ template <int BITS, int BS, bool HAS_ZP, int MR, int CPL, int U>
 hipError_t stream_go(const StreamConfig& c, const f16* A, const uint8_t* B, const f16* S,
                      const uint8_t* Z, f16* Y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
     auto kern = gemv_stream<BITS, BS, HAS_ZP, MR, CPL, U>;
-    if (c.lds > 64 * 1024) {                             // above the default dynamic LDS limit
-        const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)c.lds);
-        if (ea != hipSuccess) return ea;
-    }
+    const hipError_t ea = allow_dynamic_lds(reinterpret_cast<const void*>(kern), (size_t)c.lds);
+    if (ea != hipSuccess) return ea;
     const dim3 grid((unsigned)c.groups, (unsigned)((m + MR - 1) / MR), 1);
     const dim3 block((unsigned)(64 * c.waves_per_group), 1, 1);
     hipLaunchKernelGGL(kern, grid, block, (size_t)c.lds, st, A, B, S, Z, Y, (int)m, (int)n, (int)k,

@@ -527,11 +527,8 @@ static hipError_t group_mt(const GroupGeom& g, const void* a, const float* a_sca
 #define MNB_GROUP_GO(MT_)                                                                          \
     do {                                                                                          \
         auto kern = group_gemv<T, I8, BS, HAS_ZP, MT_>;                                           \
-        if (g.lds > 64 * 1024) {                                                                  \
-            const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),      \
-                hipFuncAttributeMaxDynamicSharedMemorySize, (int)g.lds);                          \
-            if (ea != hipSuccess) return ea;                                                      \
-        }                                                                                         \
+        const hipError_t ea = allow_dynamic_lds(reinterpret_cast<const void*>(kern), g.lds);     \
+        if (ea != hipSuccess) return ea;                                                          \
         hipLaunchKernelGGL(kern, grid, block, g.lds, st, a, a_scale, row_index, offsets, b, S, z, \
                            Y, (int)m, (int)n, (int)k, g.ksplit, g.runs_per_split, part, cnt);     \
     } while (0)

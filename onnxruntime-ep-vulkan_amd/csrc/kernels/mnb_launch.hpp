@@ -4,7 +4,30 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 namespace mnb {
+
+// Dynamic LDS above 64 KiB must be allowed per kernel (hipFuncAttributeMaxDynamicSharedMemorySize).
+// The attribute is set once per kernel and device, to the largest size that kernel has been
+// launched with there, so repeated launches (an EP's decode loop, a graph capture) make no
+// further runtime call beyond a table lookup.
+inline hipError_t allow_dynamic_lds(const void* kern, size_t bytes) {
+    if (bytes <= 64 * 1024) return hipSuccess;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, size_t> allowed;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& have = allowed[{kern, dev}];
+    if (have >= bytes) return hipSuccess;
+    const hipError_t e =
+        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) have = bytes;
+    return e;
+}
 
 // Threads per workgroup each kernel family is compiled for (its __launch_bounds__).  A launcher
 // refuses a launch shape above its kernel's limit before anything reaches the device: a

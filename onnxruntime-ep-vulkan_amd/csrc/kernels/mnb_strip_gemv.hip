@@ -511,11 +511,8 @@ hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
     auto kern = strip_gemv<I8, BS, HAS_ZP, QW, SWIGLU>;
     if (g.lds > 80 * 1024 || 64 * g.waves > strip_max_threads(I8, BS, QW))
         return hipErrorInvalidValue;
-    if (g.lds > 64 * 1024) {                             // above the default dynamic LDS limit
-        const hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-            hipFuncAttributeMaxDynamicSharedMemorySize, (int)g.lds);
-        if (ea != hipSuccess) return ea;
-    }
+    const hipError_t ea = allow_dynamic_lds(reinterpret_cast<const void*>(kern), g.lds);
+    if (ea != hipSuccess) return ea;
     const dim3 grid((unsigned)g.gx, (unsigned)g.gy, (unsigned)g.gz);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     hipLaunchKernelGGL(kern, grid, block, g.lds, st, a, a_scale, row_index,

@@ -53,16 +53,24 @@ def test_claimed_forms(host, per_channel, bias, router):
     assert _claim(host, inp, k=2, x_shape=(-1, 256), router_elem=router)[0] == 1
 
 
-def test_gpt_oss_recorded_form_is_claimed(host):
+def test_gpt_oss_recorded_form_is_claimed_when_asked(host):
     """gpt-oss-20b's QMoE as recorded (docs/OP_COVERAGE.md:831-835): 11 declared inputs, 8
-    occupied, swiglu_fusion = 0, per-channel scales.  fc1's 2I channels hold the interleaved
-    gate/linear pairs, so it runs as fusion 1 (ORT's CPU kernel refuses the attribute value,
-    docs/OP_COVERAGE.md:2199-2204, and the reference's census asks for a re-export with 1 over
-    the same weights, tests/ops/test_phi35.py:1445-1453)."""
+    occupied, swiglu_fusion = 0, per-channel scales.  Read as fc1's 2I channels holding the
+    interleaved gate/linear pairs, it runs as fusion 1 (ORT's CPU kernel refuses the attribute
+    value, docs/OP_COVERAGE.md:2199-2204, and the reference's census asks for a re-export with 1
+    over the same weights, tests/ops/test_phi35.py:1445-1453).  That reading is an inference with
+    parity unpinned, so it is claimed only under ep.qmoe_unfused_as_interleaved=1 and declined
+    by default."""
+    host.option("ep.qmoe_unfused_as_interleaved", "1")
     assert host.create_ep(-1) == 0
-    inp = _inputs(per_channel=True)
-    assert _claim(host, inp, k=4, x_shape=(4, 256), extra_inputs=["", "", ""],
-                  attrs_over={"swiglu_fusion": 0}) == (1, ["moe:drop"])
+    assert _claim(host, _inputs(per_channel=True), k=4, x_shape=(4, 256),
+                  extra_inputs=["", "", ""], attrs_over={"swiglu_fusion": 0}) == (1, ["moe:drop"])
+
+
+def test_gpt_oss_recorded_form_is_declined_by_default(host):
+    assert host.create_ep(-1) == 0
+    assert _claim(host, _inputs(per_channel=True), k=4, x_shape=(4, 256),
+                  extra_inputs=["", "", ""], attrs_over={"swiglu_fusion": 0}) == (0, [])
 
 
 def test_concatenated_swiglu_and_no_limit_are_claimed(host):
@@ -143,6 +151,11 @@ def test_ep_qmoe_matches_oracle(gpu_host, lead, H, I, E, k, per_channel, fusion)
           flush=True)
     T = int(np.prod(lead))
     inp = oq.make_qmoe_inputs(T, H, I, E, per_channel=per_channel, seed=T + E)
+    if fusion == 0:
+        # the inferred interleaved reading of the recorded form is opt-in: a second EP on the
+        # same host, created after the option is set
+        gpu_host.option("ep.qmoe_unfused_as_interleaved", "1")
+        assert gpu_host.create_ep(0) == 0, mh.err()
     gpu_host.reset()
     x_name, r_name, y_name = mh.add_qmoe(gpu_host, "moe", inp, k=k, x_shape=lead + (H,),
                                          attrs_over={"swiglu_fusion": fusion},

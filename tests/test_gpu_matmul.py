@@ -159,6 +159,10 @@ SHAPES = [
     (6, 8200, 1024, 4, 64, True),      # two strips per workgroup, last strip partial
     (9, 16400, 512, 4, 32, False),     # four strips per workgroup, last workgroup short
     (7, 8320, 1024, 4, 64, False),     # three strips per workgroup, last workgroup one strip
+    (8, 768, 768, 4, 32, True),        # batched: three quads per wavefront (R = 3)
+    (16, 3072, 2304, 4, 32, True),     # batched R = 3 at Gemma-2's hidden size
+    (8, 2000, 768, 4, 64, True),       # batched R = 3, block 64: six scales, three zp bytes
+    (8, 20000, 1920, 4, 32, False),    # batched R = 1 with four strips, 15 wavefronts
     (7, 32, 256, 8, 64, True),
     (8, 160, 1024, 8, 128, False),
     (9, 64, 4096, 4, 32, True),

@@ -137,6 +137,31 @@ def test_decode_routing_by_rows_and_strips():
             assert mnb.plan(mnb.problem(m, n, k, 4, 32, True)).kernel == mnb.KERNEL_BATCH_STREAM, (name, m)
 
 
+# (M, N, K, bs, zp) -> (quads per wavefront R, wavefronts per workgroup) of the batched decode
+# kernel; the GPU parity shapes of tests/test_gpu_matmul.py run these same plans, so every
+# instantiation family (R = 1..4, the unaligned scale/zero-point loads of R = 3) stays covered.
+BATCH_PLANS = {
+    (8, 768, 768, 32, True): (3, 2),
+    (16, 3072, 2304, 32, True): (3, 6),
+    (8, 2000, 768, 64, True): (3, 2),
+    (8, 20000, 1920, 32, False): (1, 15),
+    (16, 3072, 8192, 32, True): (4, 16),
+    (5, 9216, 3072, 32, True): (2, 12),
+}
+
+
+def test_batched_decode_geometry_of_parity_shapes():
+    """The planner's batched-decode geometry for the parity shapes that cover each quads-per-
+    wavefront instantiation: R = (K / 128) / waves_per_group."""
+    import mnb
+
+    for (m, n, k, bs, zp), (r, waves) in BATCH_PLANS.items():
+        info = mnb.plan(mnb.problem(m, n, k, 4, bs, zp))
+        assert info.kernel == mnb.KERNEL_BATCH_STREAM, (m, n, k)
+        assert info.waves_per_group == waves, (m, n, k, info.waves_per_group)
+        assert (k // 128) // info.waves_per_group == r, (m, n, k)
+
+
 def test_level4_stream_kernel_k_limit():
     """accuracy_level 4 at 16 fp16 rows: K = 8192 takes the strip-per-workgroup int8 kernel with
     8 quads per wavefront (8 wavefronts, the most it is compiled for at that depth); K = 9216 with

@@ -5,7 +5,10 @@ array in place of the workspace, so its outputs must be bit-identical to the wor
 point's on the same inputs.  Two calls in a row, the second with a smaller problem, show that the
 scratch is reused correctly (the int8 path's split-K counters are cleared by the call); a prefill
 GEMM whose K-split partials fit uses the scratch, one that does not runs unsplit; accuracy_level 4
-beyond the scratch is refused before anything is launched.
+beyond the scratch is refused before anything is launched.  No call of the allocation-free entry
+point changes the library's device-allocation counter, and a call recorded in a HIP graph
+(accuracy_level 4 and the batched decode kernel) replays bit-identically to its eager run, with
+other calls on the same scratch between the replays.
 """
 
 from __future__ import annotations
@@ -46,9 +49,12 @@ def _both(cuda, M, N, K, bs, zp, level, seed, a_dtype=np.float16):
     mnb.check(lib.mnb_matmul_nbits(C.byref(p), t["A"].data_ptr(), t["B"].data_ptr(),
                                    t["scales"].data_ptr(), zptr, y_ws.data_ptr(), ws.data_ptr(),
                                    ws_bytes, st))
+    torch.cuda.synchronize()
+    allocs = mnb.device_alloc_count()
     mnb.check(lib.mnb_matmul_nbits_noalloc(C.byref(p), t["A"].data_ptr(), t["B"].data_ptr(),
                                            t["scales"].data_ptr(), zptr, y_na.data_ptr(), st))
     torch.cuda.synchronize()
+    assert mnb.device_alloc_count() == allocs, "the allocation-free entry point allocated"
     return inp, y_ws.cpu().numpy(), y_na.cpu().numpy(), ws_bytes
 
 
@@ -121,3 +127,63 @@ def test_level_4_beyond_scratch_is_refused(cuda):
     rc = mnb.load().mnb_matmul_nbits_noalloc(C.byref(p), None, None, None, None, None, None)
     assert rc == mnb.MNB_ERR_UNSUPPORTED
     assert b"scratch" in mnb.load().mnb_last_error()
+
+
+@pytest.mark.parametrize("M,N,K,bs,zp,level,kernel", [
+    (16, 3072, 8192, 128, True, 4, "ACC4_STREAM"),      # quantiser + GEMV
+    (8, 3072, 3072, 32, True, 0, "BATCH_STREAM"),       # batched decode (no scratch needed)
+    (256, 8192, 3072, 32, False, 0, "GEMM_MFMA"),       # prefill K split: partials in scratch
+])
+def test_graph_replays_match_eager(cuda, M, N, K, bs, zp, level, kernel):
+    """The allocation-free call recorded into a HIP graph (torch.cuda.CUDAGraph stream capture),
+    replayed three times with an eager allocation-free call of another shape between replays (it
+    overwrites the shared scratch): every replay equals the eager output bit for bit, and neither
+    the capture nor the replays allocate."""
+    import mnb
+    import torch
+
+    print(f"[gpu] noalloc graph {kernel} M={M} N={N} K={K} bs{bs} level {level}", flush=True)
+    p = mnb.problem(M, N, K, 4, bs, zp, mnb.DTYPE_F16, level)
+    assert mnb.plan(p).kernel == getattr(mnb, "KERNEL_" + kernel)
+    lib = mnb.load()
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=M + K)
+    t = {k: _dev(v, cuda) for k, v in inp.items()}
+    zptr = t["zp"].data_ptr() if zp else None
+    y = torch.full((M, N), float("nan"), dtype=torch.float16, device=cuda)
+
+    def call(stream_ptr):
+        mnb.check(lib.mnb_matmul_nbits_noalloc(C.byref(p), t["A"].data_ptr(), t["B"].data_ptr(),
+                                               t["scales"].data_ptr(), zptr, y.data_ptr(),
+                                               stream_ptr))
+
+    # another shape on the same scratch (level 4 at 16 rows: codes and scales of other values)
+    o_inp = orc.make_inputs(16, 512, 4096, bits=4, block_size=64, with_zp=True, seed=5)
+    o_t = {k: _dev(v, cuda) for k, v in o_inp.items()}
+    o_p = mnb.problem(16, 512, 4096, 4, 64, True, mnb.DTYPE_F16, 4)
+    o_y = torch.empty(16, 512, dtype=torch.float16, device=cuda)
+
+    def other():
+        mnb.check(lib.mnb_matmul_nbits_noalloc(
+            C.byref(o_p), o_t["A"].data_ptr(), o_t["B"].data_ptr(), o_t["scales"].data_ptr(),
+            o_t["zp"].data_ptr(), o_y.data_ptr(), int(torch.cuda.current_stream().cuda_stream)))
+
+    call(int(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    eager = y.cpu().numpy().copy()
+    assert np.isfinite(eager).all()
+    allocs = mnb.device_alloc_count()
+    g = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g, stream=cs):
+        call(int(cs.cuda_stream))
+    torch.cuda.synchronize()
+    for rep in range(3):
+        y.fill_(float("nan"))
+        other()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert _same(y.cpu().numpy(), eager), f"replay {rep} differs from the eager call"
+    assert mnb.device_alloc_count() == allocs
+    del g
