@@ -476,6 +476,13 @@ gemm_splitk_sum(const float* __restrict__ part, f16* __restrict__ Y, int64_t mn,
 // Host side
 // ------------------------------------------------------------------------------------------
 
+hipError_t launch_splitk_sum(const float* part, void* y, int64_t mn, int ksplit, hipStream_t st) {
+    const unsigned blocks = (unsigned)std::min<int64_t>((mn / 4 + 255) / 256, 4096);
+    hipLaunchKernelGGL(gemm_splitk_sum, dim3(blocks), dim3(256), 0, st, part,
+                       static_cast<f16*>(y), mn, ksplit);
+    return hipGetLastError();
+}
+
 bool gemm_supported(int64_t m, int64_t n, int64_t k, int bits, int bs, bool has_zp) {
     if (m <= 0 || n <= 0 || (bits != 4 && bits != 8) || k <= 0 || k % kKS) return false;
     if (bs != 16 && bs != 32 && bs != 64 && bs != 128) return false;
@@ -527,12 +534,7 @@ static hipError_t gemm_go(const GemmConfig& c, const void* a, const uint8_t* b, 
     hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, static_cast<const f16*>(a), b,
                        static_cast<const f16*>(s), z, static_cast<f16*>(y), (int)m, (int)n,
                        (int)k, (int)c.tiles_m, (int)c.tiles_n, ks, ks > 1 ? part : nullptr);
-    if (ks > 1) {
-        const int64_t mn = m * n;
-        const unsigned blocks = (unsigned)std::min<int64_t>((mn / 4 + 255) / 256, 4096);
-        hipLaunchKernelGGL(gemm_splitk_sum, dim3(blocks), dim3(256), 0, st, part,
-                           static_cast<f16*>(y), mn, ks);
-    }
+    if (ks > 1) return launch_splitk_sum(part, y, m * n, ks, st);
     return hipGetLastError();
 }
 

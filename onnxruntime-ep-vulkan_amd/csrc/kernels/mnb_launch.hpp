@@ -87,6 +87,9 @@ hipError_t launch_gemm_cfg(const GemmConfig& c, const void* a, const uint8_t* b,
                            const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                            int bs, hipStream_t stream, void* workspace = nullptr,
                            size_t workspace_bytes = 0);
+// Y = the sum of `ksplit` fp32 partial planes of m*n elements, in split order.
+hipError_t launch_splitk_sum(const float* part, void* y, int64_t mn, int ksplit,
+                             hipStream_t stream);
 
 // Launch shape of the row-tiled MFMA GEMV (mnb_group_gemv.hip).
 struct GroupGeom {

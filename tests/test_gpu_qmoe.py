@@ -61,6 +61,7 @@ def _check(y, ref16, ref):
     e_sig16 = orc.max_rel_err_significant(y, ref16)
     e_rms = orc.max_err_rms_normalised(y, ref)
     errs = (e_rms16, e_sig16, e_rms)
+    print(f"[gpu] qmoe errors: rms16={e_rms16:.3e} sig16={e_sig16:.3e} rms={e_rms:.3e}", flush=True)
     assert e_rms16 <= TOL_RMS, errs
     assert e_sig16 <= TOL_SIGNIFICANT, errs
     assert e_rms <= TOL_EXACT_RMS, errs
