@@ -63,6 +63,7 @@ HIP_SOURCES = [
     CSRC / "kernels" / "mnb_qmoe.hip",
     CSRC / "kernels" / "mnb_rmsnorm.hip",
     CSRC / "kernels" / "mnb_gqa.hip",
+    CSRC / "kernels" / "mnb_stage.hip",
     CSRC / "shim" / "mnb_shim.hip",
 ]
 EP_SOURCES: list[Path] = sorted((CSRC / "ep").glob("*.cpp"))

@@ -267,6 +267,20 @@ hipError_t launch_gqa(const GqaArgs& a, const void* qkv, const void* past_k, con
                       const int32_t* seqlens, const void* cos_cache, const void* sin_cache,
                       void* out, void* pres_k, void* pres_v, void* workspace, hipStream_t stream);
 
+// Byte copies between pinned host memory and device memory, up to kMaxStageSegs segments in
+// one launch (mnb_stage.hip).  Host pointers must be device-accessible (hipHostMalloc).
+constexpr int kMaxStageSegs = 8;
+struct StageSeg {
+    const void* src;
+    void* dst;
+    uint64_t bytes;
+};
+struct StageList {
+    StageSeg seg[kMaxStageSegs];
+    int n;
+};
+hipError_t launch_stage_copy(const StageList& l, hipStream_t stream);
+
 // Roofline calibration (mnb_calibrate.hip): workgroups x 4 wavefronts x iters x 16 MFMAs.
 hipError_t launch_mfma_calibrate(const void* operands, float* out, int workgroups, int iters,
                                  hipStream_t stream);

@@ -39,6 +39,13 @@ hipError_t counted_malloc(T** p, size_t bytes) {
     return e;
 }
 
+// The pinned host staging of a session's host-I/O calls, counted with the device allocations.
+hipError_t counted_host_malloc(void** p, size_t bytes) {
+    const hipError_t e = hipHostMalloc(p, bytes, hipHostMallocDefault);
+    if (e == hipSuccess) g_device_allocs.fetch_add(1);
+    return e;
+}
+
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -775,6 +782,10 @@ struct mnb_session {
     size_t y_cap = 0;
     void* ws = nullptr;
     size_t ws_cap = 0;
+    // Pinned host staging of host tensors (HostIo), and its device-side address
+    void* pin = nullptr;
+    void* pin_dev = nullptr;
+    size_t pin_cap = 0;
 };
 
 struct mnb_weights {
@@ -875,6 +886,7 @@ int mnb_session_destroy(mnb_session* s) {
     if (s->a_dev) (void)hipFree(s->a_dev);
     if (s->y_dev) (void)hipFree(s->y_dev);
     if (s->ws) (void)hipFree(s->ws);
+    if (s->pin) (void)hipHostFree(s->pin);
     if (s->stream) (void)hipStreamDestroy(s->stream);
     delete s;
     return MNB_OK;
@@ -990,13 +1002,100 @@ static int sgrow(mnb_session* s, void** p, size_t* cap, size_t need) {
     return grow(p, cap, need);
 }
 
-// The end of a session call: host synchronisation, except for async sessions whose call read
-// and wrote device memory only (host tensors must be complete when the call returns).
-static int finish(mnb_session* s, bool host_io) {
-    if (s->async && !host_io) return MNB_OK;
-    const hipError_t e = hipStreamSynchronize(s->stream);
-    return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+// The session's pinned staging buffer, at least `need` bytes.  The stream is drained before an
+// old buffer is freed: a copy enqueued from it may still run.
+static int pin_grow(mnb_session* s, size_t need) {
+    if (need <= s->pin_cap) return MNB_OK;
+    if (s->pin) {
+        const hipError_t e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        (void)hipHostFree(s->pin);
+    }
+    s->pin = s->pin_dev = nullptr;
+    s->pin_cap = 0;
+    hipError_t e = counted_host_malloc(&s->pin, need);
+    if (e != hipSuccess) {
+        s->pin = nullptr;
+        return fail(MNB_ERR_NOMEM, "hipHostMalloc(%zu): %s", need, hipGetErrorString(e));
+    }
+    e = hipHostGetDevicePointer(&s->pin_dev, s->pin, 0);
+    if (e != hipSuccess) {
+        (void)hipHostFree(s->pin);
+        s->pin = s->pin_dev = nullptr;
+        return hip_fail(e, "hipHostGetDevicePointer");
+    }
+    s->pin_cap = need;
+    return MNB_OK;
 }
+
+// The host tensors of one session call.  Inputs are copied on the CPU into the session's pinned
+// buffer and moved to their device staging by one copy launch; outputs are moved into the pinned
+// buffer by one launch after the node's kernels and copied out on the CPU once the stream has
+// drained.  So a call is upload launch -> kernels -> download launch -> one synchronisation,
+// instead of a runtime copy per tensor.  Use: in() / out() for every host tensor, upload(), the
+// kernels, download(), end().
+struct HostIo {
+    mnb_session* s;
+    mnb::StageList up{}, down{};
+    const void* in_host[mnb::kMaxStageSegs] = {};
+    void* out_host[mnb::kMaxStageSegs] = {};
+    size_t in_off[mnb::kMaxStageSegs] = {}, out_off[mnb::kMaxStageSegs] = {};
+    size_t total = 0;
+    bool enqueued = false;
+
+    explicit HostIo(mnb_session* sess) : s(sess) {}
+    bool any() const { return up.n + down.n > 0; }
+    static size_t slot(size_t b) { return (b + 255) & ~(size_t)255; }
+    void in(const void* host, void* dev, size_t bytes) {
+        in_off[up.n] = total;
+        in_host[up.n] = host;
+        up.seg[up.n++] = {nullptr, dev, bytes};
+        total += slot(bytes);
+    }
+    void out(void* host, const void* dev, size_t bytes) {
+        out_off[down.n] = total;
+        out_host[down.n] = host;
+        down.seg[down.n++] = {dev, nullptr, bytes};
+        total += slot(bytes);
+    }
+    int upload() {
+        if (!any()) return MNB_OK;
+        int rc = pin_grow(s, total);
+        if (rc) return rc;
+        uint8_t* ph = static_cast<uint8_t*>(s->pin);
+        uint8_t* pd = static_cast<uint8_t*>(s->pin_dev);
+        for (int i = 0; i < up.n; ++i) {
+            std::memcpy(ph + in_off[i], in_host[i], up.seg[i].bytes);
+            up.seg[i].src = pd + in_off[i];
+        }
+        for (int i = 0; i < down.n; ++i) down.seg[i].dst = pd + out_off[i];
+        enqueued = true;
+        const hipError_t e = mnb::launch_stage_copy(up, s->stream);
+        return e == hipSuccess ? MNB_OK : hip_fail(e, "host input upload");
+    }
+    int download() {
+        const hipError_t e = mnb::launch_stage_copy(down, s->stream);
+        return e == hipSuccess ? MNB_OK : hip_fail(e, "host output download");
+    }
+    // The call's end: `rc` is its status so far.  Host tensors are complete when this returns;
+    // after a failure the stream is still drained, so no copy reads the pinned buffer later.
+    int end(int rc) {
+        if (rc) {
+            if (enqueued) (void)hipStreamSynchronize(s->stream);
+            return rc;
+        }
+        if (!any()) {
+            if (s->async) return MNB_OK;
+            const hipError_t e = hipStreamSynchronize(s->stream);
+            return e == hipSuccess ? MNB_OK : hip_fail(e, "hipStreamSynchronize");
+        }
+        const hipError_t e = hipStreamSynchronize(s->stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        const uint8_t* ph = static_cast<const uint8_t*>(s->pin);
+        for (int i = 0; i < down.n; ++i) std::memcpy(out_host[i], ph + out_off[i], down.seg[i].bytes);
+        return MNB_OK;
+    }
+};
 
 int mnb_weights_upload(mnb_session* s, const mnb_problem* node, const void* b_host,
                        size_t b_bytes, const void* scales_host, size_t scales_bytes,
@@ -1092,25 +1191,23 @@ int mnb_session_run(mnb_session* s, const mnb_weights* w, int64_t m, const void*
     const void* a_dev = a;
     void* y_dev = y;
     int rc;
-    if (!a_on_device) {                                  // stage A into HBM
+    HostIo io(s);
+    if (!a_on_device) {
         rc = sgrow(s, &s->a_dev, &s->a_cap, a_bytes);
         if (rc) return rc;
-        hipError_t e = hipMemcpyAsync(s->a_dev, a, a_bytes, hipMemcpyHostToDevice, s->stream);
-        if (e != hipSuccess) return hip_fail(e, "A upload");
+        io.in(a, s->a_dev, a_bytes);
         a_dev = s->a_dev;
     }
     if (!y_on_device) {
         rc = sgrow(s, &s->y_dev, &s->y_cap, y_bytes);
         if (rc) return rc;
+        io.out(y, s->y_dev, y_bytes);
         y_dev = s->y_dev;
     }
-    rc = run_locked(s, w, m, a_dev, y_dev);
-    if (rc) return rc;
-    if (!y_on_device) {
-        hipError_t e = hipMemcpyAsync(y, s->y_dev, y_bytes, hipMemcpyDeviceToHost, s->stream);
-        if (e != hipSuccess) return hip_fail(e, "Y download");
-    }
-    return finish(s, !a_on_device || !y_on_device);
+    rc = io.upload();
+    if (!rc) rc = run_locked(s, w, m, a_dev, y_dev);
+    if (!rc) rc = io.download();
+    return io.end(rc);
 }
 
 struct mnb_qmoe_weights {
@@ -1238,25 +1335,23 @@ int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows
     const void* xd = x;
     const void* ld = router_logits;
     void* yd = y_on_device ? y : s->y_dev;
-    hipError_t e = hipSuccess;
+    HostIo io(s);
     if (!x_on_device) {
-        e = hipMemcpyAsync(st + x_off, x, x_bytes, hipMemcpyHostToDevice, s->stream);
+        io.in(x, st + x_off, x_bytes);
         xd = st + x_off;
     }
-    if (e == hipSuccess && !logits_on_device) {
-        e = hipMemcpyAsync(st + l_off, router_logits, l_bytes, hipMemcpyHostToDevice, s->stream);
+    if (!logits_on_device) {
+        io.in(router_logits, st + l_off, l_bytes);
         ld = st + l_off;
     }
-    if (e != hipSuccess) return hip_fail(e, "QMoE input upload");
-    rc = mnb_qmoe(&p, xd, ld, static_cast<const uint8_t*>(w->buf[0]), w->buf[1], w->buf[2],
-                  static_cast<const uint8_t*>(w->buf[3]), w->buf[4], w->buf[5], yd, s->ws,
-                  s->ws_cap, s->stream);
-    if (rc) return rc;
-    if (!y_on_device) {
-        e = hipMemcpyAsync(y, s->y_dev, x_bytes, hipMemcpyDeviceToHost, s->stream);
-        if (e != hipSuccess) return hip_fail(e, "QMoE output download");
-    }
-    return finish(s, !x_on_device || !logits_on_device || !y_on_device);
+    if (!y_on_device) io.out(y, s->y_dev, x_bytes);
+    rc = io.upload();
+    if (!rc)
+        rc = mnb_qmoe(&p, xd, ld, static_cast<const uint8_t*>(w->buf[0]), w->buf[1], w->buf[2],
+                      static_cast<const uint8_t*>(w->buf[3]), w->buf[4], w->buf[5], yd, s->ws,
+                      s->ws_cap, s->stream);
+    if (!rc) rc = io.download();
+    return io.end(rc);
 }
 
 struct mnb_rmsnorm_weights {
@@ -1341,24 +1436,21 @@ int mnb_session_run_rmsnorm(mnb_session* s, const mnb_rmsnorm_weights* w, int64_
     const void* kd = p.has_skip ? skip : nullptr;
     void* yd = y_on_device ? y : outb;
     void* qd = sum_out ? (sum_on_device ? sum_out : outb + slot) : nullptr;
-    hipError_t e = hipSuccess;
+    HostIo io(s);
     if (!x_on_device) {
-        e = hipMemcpyAsync(in, x, bytes, hipMemcpyHostToDevice, s->stream);
+        io.in(x, in, bytes);
         xd = in;
     }
-    if (e == hipSuccess && p.has_skip && !skip_on_device) {
-        e = hipMemcpyAsync(in + slot, skip, bytes, hipMemcpyHostToDevice, s->stream);
+    if (p.has_skip && !skip_on_device) {
+        io.in(skip, in + slot, bytes);
         kd = in + slot;
     }
-    if (e != hipSuccess) return hip_fail(e, "RMSNorm input upload");
-    rc = mnb_skip_rmsnorm(&p, xd, kd, w->gamma, w->bias, yd, qd, s->stream);
-    if (rc) return rc;
-    if (!y_on_device) e = hipMemcpyAsync(y, yd, bytes, hipMemcpyDeviceToHost, s->stream);
-    if (e == hipSuccess && sum_out && !sum_on_device)
-        e = hipMemcpyAsync(sum_out, qd, bytes, hipMemcpyDeviceToHost, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "RMSNorm output download");
-    return finish(s, !x_on_device || (p.has_skip && !skip_on_device) || !y_on_device ||
-                         (sum_out && !sum_on_device));
+    if (!y_on_device) io.out(y, yd, bytes);
+    if (sum_out && !sum_on_device) io.out(sum_out, qd, bytes);
+    rc = io.upload();
+    if (!rc) rc = mnb_skip_rmsnorm(&p, xd, kd, w->gamma, w->bias, yd, qd, s->stream);
+    if (!rc) rc = io.download();
+    return io.end(rc);
 }
 
 struct mnb_gqa_caches {
@@ -1489,13 +1581,9 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
     void* od = out_dev ? attn_out : ob + o_out;
     void* rkd = present_key;
     void* rvd = present_value;
-    hipError_t e = hipSuccess;
-    // any host tensor: the call returns only after the stream has finished
-    const bool host_io = !qkv_dev || (p.past_len_max && !past_dev) || !seq_dev || !out_dev ||
-                         (p.present_len && !pres_dev) || (own_caches && !cache_dev);
+    HostIo io(s);
     auto up = [&](const void* src, size_t off, size_t bytes) -> const void* {
-        if (e == hipSuccess && bytes)
-            e = hipMemcpyAsync(in + off, src, bytes, hipMemcpyHostToDevice, s->stream);
+        if (bytes) io.in(src, in + off, bytes);
         return in + off;
     };
     if (!qkv_dev) qd = up(packed_qkv, o_qkv, qkv_b);
@@ -1510,7 +1598,6 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
         cd = up(cos_cache, o_cos, cache_b);
         snd = up(sin_cache, o_sin, cache_b);
     }
-    if (e != hipSuccess) return hip_fail(e, "GroupQueryAttention input upload");
     if (in_place) {
         rkd = const_cast<void*>(pkd);
         rvd = const_cast<void*>(pvd);
@@ -1518,16 +1605,15 @@ int mnb_session_run_gqa(mnb_session* s, const mnb_gqa_caches* c, const mnb_gqa_p
         rkd = ob + o_rk;
         rvd = ob + o_rv;
     }
-    rc = mnb_gqa(&p, qd, pkd, pvd, sd, cd, snd, od, rkd, rvd, s->ws, s->ws_cap, s->stream);
-    if (rc) return rc;
-    if (!out_dev) e = hipMemcpyAsync(attn_out, od, out_b, hipMemcpyDeviceToHost, s->stream);
-    if (e == hipSuccess && !pres_dev && p.present_len) {
-        e = hipMemcpyAsync(present_key, rkd, pres_b, hipMemcpyDeviceToHost, s->stream);
-        if (e == hipSuccess)
-            e = hipMemcpyAsync(present_value, rvd, pres_b, hipMemcpyDeviceToHost, s->stream);
+    if (!out_dev) io.out(attn_out, od, out_b);
+    if (!pres_dev && p.present_len) {
+        io.out(present_key, rkd, pres_b);
+        io.out(present_value, rvd, pres_b);
     }
-    if (e != hipSuccess) return hip_fail(e, "GroupQueryAttention output download");
-    return finish(s, host_io);
+    rc = io.upload();
+    if (!rc) rc = mnb_gqa(&p, qd, pkd, pvd, sd, cd, snd, od, rkd, rvd, s->ws, s->ws_cap, s->stream);
+    if (!rc) rc = io.download();
+    return io.end(rc);
 }
 
 int mnb_session_run_host(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_host,
