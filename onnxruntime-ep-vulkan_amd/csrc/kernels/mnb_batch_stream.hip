@@ -44,7 +44,7 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
              const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K) {
     constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
     constexpr int BPQ = 4 / CPB;                         // blocks per quad
-    extern __shared__ f32x4 sRed[];                      // [KW - 1][S][64], then KW slots
+    extern __shared__ f32x4 sRed[];                      // [KW][S][64], then KW slots
     const int lane = threadIdx.x & 63;
     const int kw = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int KW = blockDim.x >> 6;
@@ -130,7 +130,7 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
     // ---- the activations into the MFMA operand layout (lane (n, g): row n, k = 32 c + 8 g ..
     // + 7 of each chunk c), quad by quad through the wavefront's own LDS slot: no other
     // wavefront touches it and a wavefront's LDS accesses complete in program order ----------
-    uint8_t* const slot = reinterpret_cast<uint8_t*>(sRed) + (size_t)(KW - 1) * S * 64 * 16 +
+    uint8_t* const slot = reinterpret_cast<uint8_t*>(sRed) + (size_t)KW * S * 64 * 16 +
                           (size_t)kw * 16 * kBatchSlotRow;
     f16x8 av[R][4];
 #pragma unroll
@@ -183,23 +183,22 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
         }
     }
 
-    // ---- 5. the KW partial tiles in wavefront order, stored by wavefront 0 -----------------
-    if (kw > 0) {
+    // ---- 5. the KW partial tiles added in wavefront order (run-to-run deterministic): every
+    // wavefront stores its tiles, then each thread sums its outputs over the KW tiles, so the
+    // sum is one short chain per thread instead of (KW - 1) S dependent reads in wavefront 0 -----
+    float* const red = reinterpret_cast<float*>(sRed);   // [KW][S][64 lanes][4]
 #pragma unroll
-        for (int t = 0; t < S; ++t) sRed[((kw - 1) * S + t) * 64 + lane] = acc[t];
-    }
+    for (int t = 0; t < S; ++t) sRed[(kw * S + t) * 64 + lane] = acc[t];
     __syncthreads();
-    if (kw > 0) return;
-#pragma unroll
-    for (int t = 0; t < S; ++t) {
-        for (int w = 1; w < KW; ++w) acc[t] += sRed[((w - 1) * S + t) * 64 + lane];
-        const int cc = 16 * (strip0 + t) + nl;
-        if (cc >= N) continue;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = 4 * g + q;                     // MFMA output: rows 4g .. 4g + 3
-            if (r < M) Y[(int64_t)r * N + cc] = (f16)acc[t][q];
-        }
+    for (int o = threadIdx.x; o < S * 256; o += blockDim.x) {
+        // output o: strip ot, row orow, column on (fastest, so consecutive threads store along
+        // a row); lane (on + 16 (orow / 4)) of every wavefront holds it in element orow % 4
+        const int on = o & 15, orow = (o >> 4) & 15, ot = o >> 8;
+        const int src = ((ot * 64 + (orow >> 2) * 16 + on) << 2) + (orow & 3);
+        float v = red[src];
+        for (int w = 1; w < KW; ++w) v += red[w * S * 256 + src];
+        const int cc = 16 * (strip0 + ot) + on;
+        if (cc < N && orow < M) Y[(int64_t)orow * N + cc] = (f16)v;
     }
 }
 
@@ -208,7 +207,7 @@ hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b,
                       const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
     const dim3 grid((unsigned)g.gx, 1, 1);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
-    const size_t lds = (size_t)(g.waves - 1) * S * 64 * sizeof(f32x4) +
+    const size_t lds = (size_t)g.waves * S * 64 * sizeof(f32x4) +
                        (size_t)g.waves * 16 * kBatchSlotRow;
     // instantiated for S R <= 8 only (the geometry's register budget)
 #define MNB_BS(R_)                                                                                \

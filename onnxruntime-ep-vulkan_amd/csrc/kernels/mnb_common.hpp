@@ -46,10 +46,9 @@ __device__ __forceinline__ uint32_t dup_byte(uint32_t w) {
 
 // The constant pair (1024 + z, 64 + z) that turns 4-bit magic halves into q - z.
 __device__ __forceinline__ f16x2 zoff4(int z) {
-    f16x2 r;
-    r.x = (f16)(-(1024 + z));
-    r.y = (f16)(-(64 + z));
-    return r;
+    // z in 0..15: -(1024 + z) is 0xE400 | z and -(64 + z) is 0xD400 | (z << 4) in fp16 (the
+    // exponent fields of 1024 and 64, z in the mantissa), formed without a conversion
+    return as_h2(0xD400E400u | (uint32_t)z | ((uint32_t)z << 20));
 }
 
 // Four exact (q - z) pairs from one dword of eight 4-bit weights, natural element order:

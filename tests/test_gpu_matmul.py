@@ -295,6 +295,41 @@ def test_gemm_k_split_plan():
         assert info.workspace_bytes == (ks * m * 8192 * 4 if ks > 1 else 0)
 
 
+def test_gemm_k_split_graph_replays(cuda):
+    """A K-split GEMM (the split launch and the partial sum) recorded in a graph: each replay
+    (eager work and a synchronisation between them) is bit-identical to the eager call."""
+    import mnb
+    import torch
+
+    M, N, K = 512, 4096, 3072                          # 64 tiles, four K splits each
+    p = mnb.problem(M, N, K, 4, 32, True)
+    assert mnb.plan(p).grid_x == 4 * 64
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=32, with_zp=True, seed=4096)
+    t = {k: _dev(inp[k], cuda) for k in ("A", "B", "scales", "zp")}
+    ws = torch.empty(mnb.workspace_bytes(p), dtype=torch.uint8, device=cuda)
+    y = torch.empty(M, N, dtype=torch.float16, device=cuda)
+    print("[gpu] gemm K split in a graph, 3 replays", flush=True)
+    eager = mnb.matmul_nbits(t["A"], t["B"], t["scales"], t["zp"], N, K, 4, 32).cpu().numpy()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mnb.matmul_nbits(t["A"], t["B"], t["scales"], t["zp"], N, K, 4, 32, out=y, workspace=ws,
+                         stream=s.cuda_stream)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        mnb.matmul_nbits(t["A"], t["B"], t["scales"], t["zp"], N, K, 4, 32, out=y, workspace=ws,
+                         stream=s.cuda_stream)
+    for r in range(3):
+        y.fill_(0)
+        mnb.matmul_nbits(t["A"][:1], t["B"], t["scales"], t["zp"], N, K, 4, 32)   # eager work
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint16), eager.view(np.uint16)), f"replay {r}"
+
+
 @pytest.mark.parametrize("M,N,K,bs,zp", [(256, 8192, 3072, 32, False), (300, 130, 2048, 128, True),
                                          (129, 300, 1024, 64, False)])
 def test_gemm_k_split_and_unsplit_runs(cuda, M, N, K, bs, zp):
