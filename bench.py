@@ -13,7 +13,9 @@ eager_ms_per_step).
 value = algorithmic bytes of one token (32 x 65,568,768 B) per step / step time, in GB/s.
 The line also carries, measured in the same run:
   roofline      the dominant decode kernel's algorithmic bytes / its HIP-event launch time vs 8 TB/s
-  batched_decode  the same layer set at M = 4, 8, 16 rows in GB/s of algorithmic bytes
+  batched_decode  the same layer set at M = 4, 8, 16 rows in GB/s of algorithmic bytes (raw
+                device pointers, ORT layout), and batched_decode_session: the same through the
+                session layer with the strip-major weight copy (ep.strip_major_weights)
   prefill       MatMulNBits M=2048, K=3072, N=8192 in TFLOP/s vs 2.5 PFLOP/s fp16
   accuracy_level_4  configs[4] (M=16, K=8192, N=3072, bs128, zp, int8 activations) in GB/s
   moe           configs[3] (32 experts, top-4 of 64 tokens, gate_up and down) in GB/s
@@ -502,6 +504,68 @@ def main() -> int:
                         "node_us": {LAYER[i][0]: round(u, 3) for i, u in enumerate(node_us)},
                         "kernels": sorted({mnb.KERNEL_NAMES.get(mnb.plan(bp).kernel, "?")
                                            for bp in bprobs})})
+
+    # The same batched decode through the session layer, as the EP runs it with
+    # ep.strip_major_weights=1: each node's weights uploaded once (mnb_weights_upload) with their
+    # strip-major copy (mnb_weights_prepack), then mnb_session_run_device on the session's own
+    # stream; a graph of launches per node on that stream, weights rotated over the same 32
+    # layer copies as the raw launches above.
+    sess = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(sess)))
+    sstream = torch.cuda.ExternalStream(int(lib.mnb_session_stream(sess)))
+    scopies = copies
+    sw = []
+    for c in range(scopies):
+        row = []
+        for i, (_, k, n) in enumerate(LAYER):
+            B, S, Z = (t.cpu().numpy() for t in layers[c][i])
+            w = C.c_void_p()
+            p0 = mnb.problem(0, n, k, BITS, BS, True)
+            mnb.check(lib.mnb_weights_upload(sess, C.byref(p0), B.ctypes.data, B.nbytes,
+                                             S.ctypes.data, S.nbytes, Z.ctypes.data, Z.nbytes,
+                                             C.byref(w)))
+            mnb.check(lib.mnb_weights_prepack(w, None))
+            row.append(w)
+        sw.append(row)
+    batched_session = []
+    for bm in (4, 8, 16):
+        node_us = []
+        for i in range(len(LAYER)):
+            def slaunch(r, i=i, bm=bm):
+                rc = lib.mnb_session_run_device(sess, sw[r % scopies][i], bm, bacts[i].data_ptr(),
+                                                bouts[i].data_ptr())
+                if rc:
+                    mnb.check(rc)
+            for r in range(2):
+                slaunch(r)
+            torch.cuda.synchronize()
+            g1 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g1, stream=sstream):
+                for r in range(reps):
+                    slaunch(r)
+            # a replay runs on the stream current at the call (here `stream`): time it there
+            g1.replay()
+            best = float("inf")
+            for _ in range(3):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                a.record(stream)
+                g1.replay()
+                b.record(stream)
+                torch.cuda.synchronize()
+                best = min(best, 1e3 * a.elapsed_time(b) / reps)
+            node_us.append(best)
+            del g1
+        bbytes = sum(node_bytes(bm, k, n) for _, k, n in LAYER)
+        batched_session.append({
+            "M": bm, "layer_us": round(sum(node_us), 3),
+            "GB/s": round(bbytes / (sum(node_us) * 1e-6) / 1e9, 1),
+            "frac_hbm": round(bbytes / (sum(node_us) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "node_us": {LAYER[i][0]: round(u, 3) for i, u in enumerate(node_us)}})
+    for row in sw:
+        for w in row:
+            lib.mnb_weights_release(w)
+    lib.mnb_session_destroy(sess)
     del bacts, bouts
 
     # Prefill: M in {256, 512, 2048}, K=3072, N=8192, implicit zero point
@@ -849,6 +913,11 @@ def main() -> int:
         "roofline": roofline,
         "per_kernel": per_kernel,
         "batched_decode": batched,
+        "batched_decode_session": {
+            "path": "EP session layer with ep.strip_major_weights=1: mnb_weights_upload + "
+                    "mnb_weights_prepack (strip-major copy), mnb_session_run_device; M = 4 rows "
+                    "plan the streaming GEMV (ORT's layout) on down_proj",
+            "rows": batched_session},
         "prefill": prefill,
         "prefill_8bit": prefill_8bit,
         "mfma_calibration": mfma_cal,

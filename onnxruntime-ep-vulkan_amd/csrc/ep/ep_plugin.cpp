@@ -96,6 +96,13 @@ void mnb_ok(int rc, const char* what) {
     throw EpError(code, std::string(what) + ": " + mnb_last_error());
 }
 
+// The strip-major copy of a node's weights (ep.strip_major_weights).  Nodes the batched decode
+// kernel never runs keep ORT's layout only; any other failure fails the upload.
+void prepack_weights(mnb_weights* w) {
+    const int rc = mnb_weights_prepack(w, nullptr);
+    if (rc != MNB_ERR_UNSUPPORTED) mnb_ok(rc, "strip-major copy of MatMulNBits weights");
+}
+
 OrtStatus* to_status(const OrtApi* api, OrtErrorCode code, const std::string& msg) {
     if (!api) return nullptr;
     return api->CreateStatus(code, msg.c_str());
@@ -441,6 +448,7 @@ struct Ep {
     bool keep_constant_initializers = false;
     bool claim_enabled = true;
     bool qmoe_unfused_as_interleaved = false;   // ep.qmoe_unfused_as_interleaved
+    bool strip_major_weights = false;           // ep.strip_major_weights: mnb_weights_prepack
     // Device-memory mode: the HBM memory device ORT places this EP's tensors on (owned by the
     // factory's memory info), else null.
     const OrtMemoryDevice* memory_device = nullptr;
@@ -852,6 +860,7 @@ void compute_node(Ep* ep, NodeKernel& k, OrtKernelContext* ctx) {
         mnb_ok(mnb_weights_upload(ep->session, &k.prob, host[0], bytes[0], host[1], bytes[1],
                                   host[2], bytes[2], &k.weights),
                "uploading MatMulNBits weights");
+        if (ep->strip_major_weights) prepack_weights(k.weights);
     }
     mnb_ok(mnb_session_run(sess, k.weights, m, adata, a_dev ? 1 : 0, ydata, y_dev ? 1 : 0),
            "MatMulNBits kernel");
@@ -1259,6 +1268,7 @@ std::unique_ptr<NodeKernel> compile_one(Ep* ep, const OrtGraph* graph, const Ort
         mnb_ok(mnb_weights_upload(sess, &k->prob, host[0], bytes[0], host[1], bytes[1],
                                   host[2], bytes[2], &k->weights),
                "uploading MatMulNBits weights at Compile");
+        if (ep->strip_major_weights) prepack_weights(k->weights);
         k->resident = true;
     } else {
         for (int r = 0; r < 3; ++r) {
@@ -1427,6 +1437,10 @@ OrtStatus* ORT_API_CALL f_create_ep(OrtEpFactory* self, const OrtHardwareDevice*
             ep->keep_constant_initializers = opt == "1" || opt == "true";
         if (session_option(api, so, "ep.qmoe_unfused_as_interleaved", &opt))
             ep->qmoe_unfused_as_interleaved = opt == "1" || opt == "true";
+        // ep.strip_major_weights: each MatMulNBits node the batched decode kernel can run also
+        // keeps a strip-major copy of its weights (twice the node's weight memory)
+        if (session_option(api, so, "ep.strip_major_weights", &opt))
+            ep->strip_major_weights = opt == "1" || opt == "true";
         // ep.max_claim_ops: comma-separated allowlist (reference: rust/src/ep.rs:39-160);
         // claiming is on only when MatMulNBits is listed.
         if (session_option(api, so, "ep.max_claim_ops", &opt))

@@ -41,7 +41,8 @@ constexpr int kBatchSlotRow = 256 + 16;
 template <int BS, bool HAS_ZP, int R, int S>
 __global__ void __launch_bounds__(64 * kBatchMaxWaves)
 batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ Sc,
-             const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K) {
+             const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K,
+             const uint8_t* __restrict__ Bs) {
     constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
     constexpr int BPQ = 4 / CPB;                         // blocks per quad
     extern __shared__ f32x4 sRed[];                      // [KW][S][64], then KW slots
@@ -109,16 +110,25 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
         }
     }
 
-    // ---- 3. the wavefront's weights ----------------------------------------------------------
+    // ---- 3. the wavefront's weights: lane (n, g) takes chunk 4 q + g of column n, either from
+    // ORT's layout (16 columns x 64 bytes per load instruction) or from the strip-major copy made
+    // at upload (mnb_weights_prepack: the same 16 x 64 bytes stored as one 1 KB run per strip
+    // and quad, in this lane order) ----------------------------------------------------------------
     u32x4 bw[S][R];
 #pragma unroll
     for (int t = 0; t < S; ++t) {
-        const int col = min(16 * (strip0 + t) + nl, N - 1);
-        const uint8_t* bc = B + (int64_t)col * (K / 2);
+        const uint8_t* bc;
+        if (Bs) {
+            const int st = min(strip0 + t, (N + 15) / 16 - 1);
+            bc = Bs + (int64_t)st * (K / 128) * 1024 + 64 * nl + 16 * g;
+        } else {
+            const int col = min(16 * (strip0 + t) + nl, N - 1);
+            bc = B + (int64_t)col * (K / 2) + 16 * g;
+        }
 #pragma unroll
         for (int j = 0; j < R; ++j)
             bw[t][j] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4*>(bc + 16 * (int64_t)(4 * (q0 + j) + g)));
+                reinterpret_cast<const u32x4*>(bc + (Bs ? 1024 : 64) * (int64_t)(q0 + j)));
     }
 
     // With several strips, every weight request goes out before the first wait (left to itself
@@ -204,7 +214,8 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
 
 template <int BS, bool HAS_ZP, int S>
 hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b, const void* s,
-                      const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+                      const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st,
+                      const uint8_t* bs_) {
     const dim3 grid((unsigned)g.gx, 1, 1);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     const size_t lds = (size_t)g.waves * S * 64 * sizeof(f32x4) +
@@ -217,7 +228,7 @@ hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b,
         if (ea != hipSuccess) return ea;                                                          \
         hipLaunchKernelGGL((batch_stream<BS, HAS_ZP, R_, S>), grid, block, lds, st,              \
                            static_cast<const f16*>(a), b, static_cast<const f16*>(s), z,          \
-                           static_cast<f16*>(y), (int)m, (int)n, (int)k);                         \
+                           static_cast<f16*>(y), (int)m, (int)n, (int)k, bs_);                    \
     } else {                                                                                      \
         return hipErrorInvalidValue;                                                              \
     }
@@ -234,12 +245,13 @@ hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b,
 
 template <int BS, bool HAS_ZP>
 hipError_t batch_go(const BatchStreamGeom& g, const void* a, const uint8_t* b, const void* s,
-                    const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+                    const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, hipStream_t st,
+                    const uint8_t* bs_) {
     switch (g.s) {
-        case 1: return batch_go_s<BS, HAS_ZP, 1>(g, a, b, s, z, y, m, n, k, st);
-        case 2: return batch_go_s<BS, HAS_ZP, 2>(g, a, b, s, z, y, m, n, k, st);
-        case 3: return batch_go_s<BS, HAS_ZP, 3>(g, a, b, s, z, y, m, n, k, st);
-        case 4: return batch_go_s<BS, HAS_ZP, 4>(g, a, b, s, z, y, m, n, k, st);
+        case 1: return batch_go_s<BS, HAS_ZP, 1>(g, a, b, s, z, y, m, n, k, st, bs_);
+        case 2: return batch_go_s<BS, HAS_ZP, 2>(g, a, b, s, z, y, m, n, k, st, bs_);
+        case 3: return batch_go_s<BS, HAS_ZP, 3>(g, a, b, s, z, y, m, n, k, st, bs_);
+        case 4: return batch_go_s<BS, HAS_ZP, 4>(g, a, b, s, z, y, m, n, k, st, bs_);
         default: return hipErrorInvalidValue;
     }
 }
@@ -279,6 +291,37 @@ bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamG
     return true;
 }
 
+// ORT's int4 B [N][K / 2] -> the strip-major copy [ceil(N / 16)][K / 128][16 columns][4] x 16
+// bytes that batch_stream reads one 1 KB run per load instruction from; columns past N are zero.
+// One thread per 16-byte piece.
+__global__ void __launch_bounds__(256)
+strip_pack(const u32x4* __restrict__ B, u32x4* __restrict__ dst, int64_t N, int64_t K,
+           int64_t pieces) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= pieces) return;
+    const int64_t kq = K / 128;
+    const int g = (int)(i & 3), n = (int)((i >> 2) & 15);
+    const int64_t q = (i >> 6) % kq, st = (i >> 6) / kq;
+    const int64_t col = 16 * st + n;
+    dst[i] = col < N ? B[(col * (K / 2) + 16 * (4 * q + g)) / 16] : u32x4{0u, 0u, 0u, 0u};
+}
+
+int64_t strip_pack_bytes(int64_t n, int64_t k) { return (n + 15) / 16 * (k / 128) * 1024; }
+
+hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
+                             hipStream_t st) {
+    if (n < 1 || k < 128 || k % 128 || reinterpret_cast<uintptr_t>(b) % 16 ||
+        reinterpret_cast<uintptr_t>(dst) % 16)
+        return hipErrorInvalidValue;
+    const int64_t pieces = strip_pack_bytes(n, k) / 16;
+    const int64_t blocks = (pieces + 255) / 256;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(strip_pack, dim3((unsigned)blocks), dim3(256), 0, st,
+                       reinterpret_cast<const u32x4*>(b), reinterpret_cast<u32x4*>(dst), n, k,
+                       pieces);
+    return hipGetLastError();
+}
+
 bool batch_stream_aligned(const void* a, const uint8_t* b, const void* s, const uint8_t* z) {
     return reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(s) % 8 == 0 && reinterpret_cast<uintptr_t>(z) % 2 == 0;
@@ -286,15 +329,16 @@ bool batch_stream_aligned(const void* a, const uint8_t* b, const void* s, const 
 
 hipError_t launch_batch_stream(const BatchStreamGeom& g, const void* a, const uint8_t* b,
                                const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
-                               int64_t k, int bs, hipStream_t st) {
+                               int64_t k, int bs, hipStream_t st, const uint8_t* b_strips) {
     // waves * R == K / 128: every quad of K belongs to exactly one wavefront
     BatchStreamGeom want{};
     if (!batch_stream_geometry(m, n, k, bs, &want) || want.r != g.r || want.s != g.s ||
-        want.waves != g.waves || want.gx != g.gx || !batch_stream_aligned(a, b, s, z))
+        want.waves != g.waves || want.gx != g.gx || !batch_stream_aligned(a, b, s, z) ||
+        reinterpret_cast<uintptr_t>(b_strips) % 16)
         return hipErrorInvalidValue;
 #define MNB_BS_ZP(BS_)                                                                            \
-    return z ? batch_go<BS_, true>(g, a, b, s, z, y, m, n, k, st)                                 \
-             : batch_go<BS_, false>(g, a, b, s, z, y, m, n, k, st)
+    return z ? batch_go<BS_, true>(g, a, b, s, z, y, m, n, k, st, b_strips)                       \
+             : batch_go<BS_, false>(g, a, b, s, z, y, m, n, k, st, b_strips)
     switch (bs) {
         case 32: MNB_BS_ZP(32);
         case 64: MNB_BS_ZP(64);

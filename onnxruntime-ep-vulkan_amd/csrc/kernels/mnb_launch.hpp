@@ -209,9 +209,16 @@ struct BatchStreamGeom {
 bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamGeom* out);
 // A and B 16-byte, scales 8-byte, zero points 2-byte aligned.
 bool batch_stream_aligned(const void* a, const uint8_t* b, const void* s, const uint8_t* z);
+// b_strips: the strip-major copy of B (launch_strip_pack), read in place of b when not null.
 hipError_t launch_batch_stream(const BatchStreamGeom& g, const void* a, const uint8_t* b,
                                const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
-                               int64_t k, int bs, hipStream_t stream);
+                               int64_t k, int bs, hipStream_t stream,
+                               const uint8_t* b_strips = nullptr);
+// The strip-major copy of an int4 B (K % 128 == 0): strip_pack_bytes(n, k) bytes, 16-byte
+// aligned, columns past N zero.
+int64_t strip_pack_bytes(int64_t n, int64_t k);
+hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
+                             hipStream_t stream);
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                        int bs, void* workspace, hipStream_t stream);

@@ -295,9 +295,13 @@ int mnb_workspace_bytes(const mnb_problem* p, size_t* bytes) {
     return MNB_OK;
 }
 
-int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, const void* scales,
-                     const uint8_t* zero_points, void* y, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// mnb_matmul_nbits with, from the session layer, the node's strip-major copy of B
+// (mnb_weights_prepack), which the batched decode kernel reads in place of B when it runs.
+static int matmul_impl(const mnb_problem* p, const void* a, const uint8_t* b,
+                       const uint8_t* b_strips, const void* scales, const uint8_t* zero_points,
+                       void* y, void* workspace, size_t workspace_bytes, void* stream) {
     mnb_plan_info info;
     int rc = mnb_plan(p, &info);
     if (rc) return rc;
@@ -358,7 +362,7 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
         if (!mnb::batch_stream_geometry(p->m, p->n, p->k, p->block_size, &bg))
             return fail(MNB_ERR_UNSUPPORTED, "batched decode geometry");
         e = mnb::launch_batch_stream(bg, a, b, scales, zero_points, y, p->m, p->n, p->k,
-                                     p->block_size, st);
+                                     p->block_size, st, b_strips);
     } else if (kern == MNB_KERNEL_STRIP_MFMA) {
         mnb::StripGeom sg{};
         if (!mnb::strip_geometry(p->n, p->k, 1, p->m, false, p->block_size,
@@ -386,6 +390,15 @@ int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, cons
     if (e != hipSuccess) return hip_fail(e, "MatMulNBits kernel launch");
     g_launches.fetch_add(1);
     return MNB_OK;
+}
+
+extern "C" {
+
+int mnb_matmul_nbits(const mnb_problem* p, const void* a, const uint8_t* b, const void* scales,
+                     const uint8_t* zero_points, void* y, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+    return matmul_impl(p, a, b, nullptr, scales, zero_points, y, workspace, workspace_bytes,
+                       stream);
 }
 
 }  // extern "C"
@@ -794,6 +807,7 @@ struct mnb_weights {
     uint8_t* b = nullptr;
     void* scales = nullptr;
     uint8_t* zp = nullptr;
+    uint8_t* strips = nullptr;   // strip-major copy of B (mnb_weights_prepack), or null
 };
 
 int mnb_device_count(int* count) {
@@ -1150,7 +1164,41 @@ int mnb_weights_release(mnb_weights* w) {
     if (w->b) (void)hipFree(w->b);
     if (w->scales) (void)hipFree(w->scales);
     if (w->zp) (void)hipFree(w->zp);
+    if (w->strips) (void)hipFree(w->strips);
     delete w;
+    return MNB_OK;
+}
+
+int mnb_weights_prepack(mnb_weights* w, int64_t* bytes) {
+    if (bytes) *bytes = 0;
+    if (!w) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    const mnb_problem& p = w->node;
+    mnb::BatchStreamGeom bg{};
+    if (p.dtype != MNB_DTYPE_F16 || p.bits != 4 || p.accuracy_level == 4 ||
+        !mnb::batch_stream_geometry(16, p.n, p.k, p.block_size, &bg))
+        return fail(MNB_ERR_UNSUPPORTED,
+                    "no strip-major layout for this node: the batched decode kernel takes fp16 "
+                    "A, 4-bit B, K %% 128 == 0 and blocks of 32, 64 or 128 with whole groups of "
+                    "four (N=%lld K=%lld bits=%d block_size=%d)",
+                    (long long)p.n, (long long)p.k, p.bits, p.block_size);
+    const int64_t nb = mnb::strip_pack_bytes(p.n, p.k);
+    std::lock_guard<std::mutex> lk(w->s->mu);
+    (void)hipSetDevice(w->s->device);
+    if (!w->strips) {
+        uint8_t* d = nullptr;
+        hipError_t e = counted_malloc(&d, (size_t)nb);
+        if (e != hipSuccess)
+            return fail(MNB_ERR_NOMEM, "hipMalloc(%lld) for the strip-major copy: %s",
+                        (long long)nb, hipGetErrorString(e));
+        e = mnb::launch_strip_pack(w->b, d, p.n, p.k, w->s->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(w->s->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return hip_fail(e, "strip-major copy");
+        }
+        w->strips = d;
+    }
+    if (bytes) *bytes = nb;
     return MNB_OK;
 }
 
@@ -1165,8 +1213,8 @@ static int run_locked(mnb_session* s, const mnb_weights* w, int64_t m, const voi
         rc = sgrow(s, &s->ws, &s->ws_cap, ws);
         if (rc) return rc;
     }
-    return mnb_matmul_nbits(&p, a_dev, w->b, w->scales, w->zp, y_dev, s->ws, s->ws_cap,
-                            s->stream);
+    return matmul_impl(&p, a_dev, w->b, w->strips, w->scales, w->zp, y_dev, s->ws, s->ws_cap,
+                       s->stream);
 }
 
 int mnb_session_run_device(mnb_session* s, const mnb_weights* w, int64_t m, const void* a_dev,

@@ -150,6 +150,7 @@ def load() -> C.CDLL:
         "mnb_weights_upload": (C.c_int, [vp, C.POINTER(Problem), vp, sz, vp, sz, vp, sz,
                                          C.POINTER(vp)]),
         "mnb_weights_release": (C.c_int, [vp]),
+        "mnb_weights_prepack": (C.c_int, [vp, C.POINTER(i64)]),
         "mnb_session_run_device": (C.c_int, [vp, vp, i64, vp, vp]),
         "mnb_session_run_host": (C.c_int, [vp, vp, i64, vp, vp]),
         "mnb_session_run": (C.c_int, [vp, vp, i64, vp, C.c_int, vp, C.c_int]),

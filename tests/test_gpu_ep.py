@@ -283,3 +283,28 @@ def test_stream_aware_chain_matches_oracle(dm_host):
     assert np.array_equal(outs[0].view(np.uint16), outs[2].view(np.uint16))
     assert dm_host.notification_roundtrip() == 0, mh.err()
 
+
+
+@pytest.mark.parametrize("M,N,K,bs,zp", [(16, 3072, 3072, 32, True), (8, 3000, 8192, 128, False),
+                                         (1, 3072, 3072, 32, True)])
+def test_strip_major_weights_option(host, M, N, K, bs, zp):
+    """ep.strip_major_weights=1: Compile also keeps each node's strip-major copy of B
+    (mnb_weights_prepack), which Compute reads when the plan is the batched decode kernel; the
+    output is bit-identical to the same node on an EP without the option, and within the bar of
+    the oracle."""
+    print(f"[gpu] ep strip-major M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=7 * M + N)
+    ys = []
+    for opt in ("0", "1"):
+        host.option("ep.strip_major_weights", opt)
+        assert host.create_ep(0) == 0, mh.err()
+        host.reset()
+        a_name, y_name = mh.add_matmul_nbits(host, "mm", inp, N, K, 4, bs, (M, K))
+        assert host.get_capability() == (1, ["mm:drop"])
+        assert host.compile() == 0, mh.err()
+        host.feed(a_name, inp["A"])
+        assert host.compute(0) == 0, mh.err()
+        ys.append(host.fetch(y_name, np.float16, M * N).reshape(M, N))
+    assert np.array_equal(ys[0].view(np.uint16), ys[1].view(np.uint16))
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
+    _check(ys[1], ref, "ep strip-major")

@@ -1,0 +1,101 @@
+"""GPU parity of the upload-time strip-major weight layout (mnb_weights_prepack).
+
+A prepacked node's session calls that plan the batched decode kernel (4 to 16 fp16 rows) read
+the strip-major copy of B; every other plan reads ORT's layout.  The copy holds the same bytes in
+another order and the kernel does the same arithmetic on them, so the bar is bit-identical
+output against the same node uploaded without the copy, plus the fp16 bar of the rest of the
+suite against the oracle (max relative error 2e-3 over significant elements, |y_ref| >= 0.1 RMS).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import matmul_nbits as orc
+
+pytestmark = pytest.mark.gpu
+
+F16_TOL = 2e-3
+
+
+def _upload(lib, mnb, s, inp, N, K, bs, zp):
+    p = mnb.problem(0, N, K, 4, bs, zp)
+    w = C.c_void_p()
+    B, S, Z = inp["B"], inp["scales"], inp["zp"]
+    mnb.check(lib.mnb_weights_upload(s, C.byref(p), B.ctypes.data, B.nbytes, S.ctypes.data,
+                                     S.nbytes, Z.ctypes.data if zp else None,
+                                     Z.nbytes if zp else 0, C.byref(w)))
+    return w
+
+
+@pytest.mark.parametrize("M,N,K,bs,zp", [
+    (16, 3072, 3072, 32, True),     # Phi-3.5 o_proj: one strip per workgroup
+    (16, 9216, 3072, 32, True),     # qkv_proj: three strips per workgroup
+    (8, 3000, 8192, 128, True),     # N past the last whole strip, K = 8192 (16 wavefronts)
+    (4, 1000, 2048, 64, False),     # implied zero point, partial last strip
+    (12, 768, 768, 32, False),      # three quads per wavefront
+    (1, 3072, 3072, 32, True),      # one row: the streaming GEMV, ORT's layout
+])
+def test_prepacked_matches_ort_layout(cuda, M, N, K, bs, zp):
+    import mnb
+    import torch
+
+    lib = mnb.load()
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=31 * M + N)
+    plan = mnb.plan(mnb.problem(M, N, K, 4, bs, zp)).kernel
+    if M >= 4:
+        assert plan == mnb.KERNEL_BATCH_STREAM, f"plan {plan}: the test would not read the copy"
+    print(f"[gpu] prepack M={M} N={N} K={K} bs={bs} zp={zp} (plan {plan})", flush=True)
+    s = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(s)))
+    try:
+        w_ort = _upload(lib, mnb, s, inp, N, K, bs, zp)
+        w_pk = _upload(lib, mnb, s, inp, N, K, bs, zp)
+        nb = C.c_int64(0)
+        mnb.check(lib.mnb_weights_prepack(w_pk, C.byref(nb)))
+        assert nb.value == -(-N // 16) * (K // 128) * 1024
+        mnb.check(lib.mnb_weights_prepack(w_pk, None))          # a second call: nothing to do
+        A = torch.from_numpy(np.ascontiguousarray(inp["A"])).to(cuda)
+        ys = []
+        for w in (w_ort, w_pk, w_pk):
+            y = torch.empty(M, N, dtype=torch.float16, device=cuda)
+            mnb.check(lib.mnb_session_run(s, w, M, A.data_ptr(), 1, y.data_ptr(), 1))
+            ys.append(y.cpu().numpy())
+        assert np.array_equal(ys[0].view(np.uint16), ys[1].view(np.uint16))
+        assert np.array_equal(ys[1].view(np.uint16), ys[2].view(np.uint16))
+        ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
+        assert np.isfinite(ys[1]).all()
+        assert orc.max_rel_err_significant(ys[1], ref) <= F16_TOL
+        assert orc.max_err_rms_normalised(ys[1], ref) <= F16_TOL
+        mnb.check(lib.mnb_weights_release(w_ort))
+        mnb.check(lib.mnb_weights_release(w_pk))
+    finally:
+        lib.mnb_session_destroy(s)
+
+
+@pytest.mark.parametrize("bits,bs,K,level", [(8, 32, 3072, 0), (4, 16, 3072, 0),
+                                              (4, 32, 3040, 0), (4, 128, 8192, 4)])
+def test_prepack_refuses_nodes_the_batched_kernel_never_runs(cuda, bits, bs, K, level):
+    import mnb
+
+    lib = mnb.load()
+    N = 256
+    inp = orc.make_inputs(1, N, K, bits=bits, block_size=bs, with_zp=True, seed=5)
+    s = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(s)))
+    try:
+        p = mnb.problem(0, N, K, bits, bs, True, mnb.DTYPE_F16, level)
+        w = C.c_void_p()
+        B, S, Z = inp["B"], inp["scales"], inp["zp"]
+        mnb.check(lib.mnb_weights_upload(s, C.byref(p), B.ctypes.data, B.nbytes, S.ctypes.data,
+                                         S.nbytes, Z.ctypes.data, Z.nbytes, C.byref(w)))
+        nb = C.c_int64(-1)
+        assert lib.mnb_weights_prepack(w, C.byref(nb)) == mnb.MNB_ERR_UNSUPPORTED
+        assert nb.value == 0
+        assert b"strip-major" in lib.mnb_last_error()
+        mnb.check(lib.mnb_weights_release(w))
+    finally:
+        lib.mnb_session_destroy(s)
