@@ -303,15 +303,16 @@ int mnb_weights_upload(mnb_session* s, const mnb_problem* node, const void* b_ho
                        const void* zp_host, size_t zp_bytes, mnb_weights** out);
 int mnb_weights_release(mnb_weights* w);
 
-/* Upload-time weight layout for the batched decode kernel (4 to 16 fp16 rows): adds a copy of B
- * in which each 16-column strip's weights for each 128-k quad are one contiguous 1 KB run in the
- * kernel's lane order (ORT's layout spreads the same bytes over 16 columns x 64 bytes), made on
- * the device from the uploaded B.  Session calls whose plan is the batched kernel then read the
- * copy; every other kernel (the streaming GEMV at 1 to 3 rows, the prefill GEMM, ...) keeps
- * reading B in ORT's layout, which stays resident, so the node holds its weights twice.  Once per
- * node (a second call does nothing); *bytes (may be NULL) receives the copy's size.
- * MNB_ERR_UNSUPPORTED for nodes the batched kernel never runs (not fp16 x int4, K % 128 != 0,
- * blocks other than 32/64/128, accuracy_level 4).  Replaces the reference's prepack seam, where
+/* Upload-time weight layout for the batched decode kernels (4 to 16 fp16 rows, and the int8
+ * GEMV of accuracy_level 4 at up to 16 rows): adds a copy of B in which each 16-column strip's
+ * weights for each 128-k quad are one contiguous 1 KB run in the kernels' lane order (ORT's
+ * layout spreads the same bytes over 16 columns x 64 bytes), made on the device from the
+ * uploaded B.  Session calls whose plan is one of those kernels then read the copy; every other
+ * kernel (the streaming GEMV at 1 to 3 rows, the prefill GEMM, ...) keeps reading B in ORT's
+ * layout, which stays resident, so the node holds its weights twice.  Once per node (a second
+ * call does nothing); *bytes (may be NULL) receives the copy's size.  MNB_ERR_UNSUPPORTED for
+ * nodes those kernels never run (not fp16 x int4, K % 128 != 0, blocks other than 32/64/128,
+ * K > 8192 at accuracy_level 4).  Replaces the reference's prepack seam, where
  * a kernel may re-lay a node's weights once at upload (rust/src/engine.rs:372-468; its
  * MatMulNBits prepack is the identity, rust/src/ops/quant.rs:676-682). */
 int mnb_weights_prepack(mnb_weights* w, int64_t* bytes);

@@ -42,7 +42,8 @@ template <int BS, bool HAS_ZP, int R>
 __global__ void __launch_bounds__(64 * acc4s_max_waves(R))
 acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
             const uint8_t* __restrict__ B, const f16* __restrict__ Sc,
-            const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K) {
+            const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K,
+            const uint8_t* __restrict__ Bs) {
     constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
     constexpr int BPQ = 4 / CPB;                         // blocks per quad
     constexpr int PA = 2 * R;                            // 16-byte code pieces per thread
@@ -127,13 +128,15 @@ acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
         }
     }
 
-    // ---- 3. the wavefront's weights ----------------------------------------------------------
-    const uint8_t* bc = B + (int64_t)col * (K / 2);
+    // ---- 3. the wavefront's weights: lane (n, g) takes chunk 4 q + g of column n, from ORT's
+    // layout or from the strip-major copy (one 1 KB run per strip and quad, launch_strip_pack) -
+    const uint8_t* const bc = Bs ? Bs + (int64_t)strip * (K / 128) * 1024 + 64 * nl + 16 * g
+                                 : B + (int64_t)col * (K / 2) + 16 * g;
     u32x4 bw[R];
 #pragma unroll
     for (int j = 0; j < R; ++j)
         bw[j] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(bc + 16 * (int64_t)(4 * (q0 + j) + g)));
+            reinterpret_cast<const u32x4*>(bc + (Bs ? 1024 : 64) * (int64_t)(q0 + j)));
 
     // all of the loads above are issued before the staging below waits for the first of them
     __builtin_amdgcn_sched_barrier(0);
@@ -200,24 +203,27 @@ acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
         }
     }
 
-    // ---- 6. the KW partial tiles in wavefront order, stored by wavefront 0 -----------------
-    if (kw > 0) sRed[kw * 64 + lane] = acc;
+    // ---- 6. the KW partial tiles added in wavefront order (run-to-run deterministic): every
+    // wavefront stores its tile, then each thread sums its outputs over them ------------------
+    sRed[kw * 64 + lane] = acc;
     __syncthreads();
-    if (kw > 0) return;
-    for (int w = 1; w < KW; ++w) acc += sRed[w * 64 + lane];
-    const int cc = 16 * strip + nl;
-    if (cc >= N) return;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = 4 * g + q;                         // MFMA output: rows 4g .. 4g + 3
-        if (r < M) Y[(int64_t)r * N + cc] = (f16)acc[q];
+    const float* const red = reinterpret_cast<const float*>(sRed);
+    for (int o = threadIdx.x; o < 256; o += blockDim.x) {
+        // output o: row orow, column on (fastest, so consecutive threads store along a row);
+        // lane (on + 16 (orow / 4)) of every wavefront holds it in element orow % 4
+        const int on = o & 15, orow = o >> 4;
+        const int src = (((orow >> 2) * 16 + on) << 2) + (orow & 3);
+        float v = red[src];
+        for (int w = 1; w < KW; ++w) v += red[w * 256 + src];
+        const int cc = 16 * strip + on;
+        if (cc < N && orow < M) Y[(int64_t)orow * N + cc] = (f16)v;
     }
 }
 
 template <int BS, bool HAS_ZP>
 hipError_t acc4s_go(const Acc4StreamGeom& g, const int8_t* qa, const float* sa, const uint8_t* b,
                     const void* s, const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k,
-                    hipStream_t st) {
+                    hipStream_t st, const uint8_t* bs_) {
     const dim3 grid((unsigned)g.gx, 1, 1);
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
 #define MNB_A4S(R_)                                                                               \
@@ -226,7 +232,7 @@ hipError_t acc4s_go(const Acc4StreamGeom& g, const int8_t* qa, const float* sa, 
         const hipError_t ea = allow_dynamic_lds(reinterpret_cast<const void*>(kern), g.lds);     \
         if (ea != hipSuccess) return ea;                                                          \
         hipLaunchKernelGGL(kern, grid, block, g.lds, st, qa, sa, b, static_cast<const f16*>(s),   \
-                           z, static_cast<f16*>(y), (int)m, (int)n, (int)k);                      \
+                           z, static_cast<f16*>(y), (int)m, (int)n, (int)k, bs_);                 \
     } while (0)
     switch (g.r) {
         case 1: MNB_A4S(1); break;
@@ -281,15 +287,17 @@ bool acc4_stream_aligned(const void* qa, const uint8_t* b, const void* s, const 
 
 hipError_t launch_acc4_stream(const Acc4StreamGeom& g, const int8_t* qa, const float* sa,
                               const uint8_t* b, const void* s, const uint8_t* z, void* y,
-                              int64_t m, int64_t n, int64_t k, int bs, hipStream_t st) {
+                              int64_t m, int64_t n, int64_t k, int bs, hipStream_t st,
+                              const uint8_t* b_strips) {
     // the staging covers 16 rows x K exactly with 2R pieces per thread: waves * R == K / 128
     Acc4StreamGeom want{};
     if (!acc4_stream_geometry(m, n, k, bs, &want) || want.r != g.r || want.waves != g.waves ||
-        want.gx != g.gx || want.lds != g.lds || !acc4_stream_aligned(qa, b, s, z))
+        want.gx != g.gx || want.lds != g.lds || !acc4_stream_aligned(qa, b, s, z) ||
+        reinterpret_cast<uintptr_t>(b_strips) % 16)
         return hipErrorInvalidValue;
 #define MNB_A4S_ZP(BS_)                                                                           \
-    return z ? acc4s_go<BS_, true>(g, qa, sa, b, s, z, y, m, n, k, st)                           \
-             : acc4s_go<BS_, false>(g, qa, sa, b, s, z, y, m, n, k, st)
+    return z ? acc4s_go<BS_, true>(g, qa, sa, b, s, z, y, m, n, k, st, b_strips)                 \
+             : acc4s_go<BS_, false>(g, qa, sa, b, s, z, y, m, n, k, st, b_strips)
     switch (bs) {
         case 32: MNB_A4S_ZP(32);
         case 64: MNB_A4S_ZP(64);

@@ -708,7 +708,7 @@ size_t acc4_workspace_bytes(int64_t m, int64_t n, int64_t k, int bs, bool a_f16)
 
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
-                       int bs, void* workspace, hipStream_t st) {
+                       int bs, void* workspace, hipStream_t st, const uint8_t* b_strips) {
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     GroupGeom g{};
@@ -726,7 +726,7 @@ hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* 
         hipError_t e = launch_quantize_a_int8(a, true, qa, sa, nullptr, true, m, k, bs, st,
                                               nullptr, 0, 16, true);
         if (e != hipSuccess) return e;
-        return launch_acc4_stream(ag, qa, sa, b, s, z, y, m, n, k, bs, st);
+        return launch_acc4_stream(ag, qa, sa, b, s, z, y, m, n, k, bs, st, b_strips);
     }
     if (stream || strip) {
         // (the planned kernel, or the fallback of the strip-per-workgroup one for sub-aligned

@@ -194,9 +194,11 @@ bool acc4_stream_planned(bool a_f16, int64_t m, int64_t n, int64_t k, int bs,
                          Acc4StreamGeom* out);
 // Codes and B 16-byte, scales 8-byte, zero points 2-byte aligned.
 bool acc4_stream_aligned(const void* qa, const uint8_t* b, const void* s, const uint8_t* z);
+// b_strips: the strip-major copy of B (launch_strip_pack), read in place of b when not null.
 hipError_t launch_acc4_stream(const Acc4StreamGeom& g, const int8_t* qa, const float* a_scale,
                               const uint8_t* b, const void* s, const uint8_t* z, void* y,
-                              int64_t m, int64_t n, int64_t k, int bs, hipStream_t stream);
+                              int64_t m, int64_t n, int64_t k, int bs, hipStream_t stream,
+                              const uint8_t* b_strips = nullptr);
 // Batched decode at up to 16 fp16 rows, int4 weights (mnb_batch_stream.hip): s 16-column
 // strips per workgroup over all of K, `waves` wavefronts of r quads each (waves * r == K / 128),
 // activations loaded straight into MFMA registers.  K % 128 == 0, (K / bs) % 4 == 0, bs >= 32.
@@ -221,7 +223,8 @@ hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t 
                              hipStream_t stream);
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
-                       int bs, void* workspace, hipStream_t stream);
+                       int bs, void* workspace, hipStream_t stream,
+                       const uint8_t* b_strips = nullptr);
 
 GemvGeom gemv_geometry(int64_t m, int64_t n, int64_t k, int bits, int bs);
 bool gemv_supported(int64_t k, int bits, int block_size);

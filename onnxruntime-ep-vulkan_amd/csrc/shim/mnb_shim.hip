@@ -356,7 +356,7 @@ static int matmul_impl(const mnb_problem* p, const void* a, const uint8_t* b,
             return fail(MNB_ERR_INVALID, "accuracy_level 4 needs B 16-byte and the workspace "
                                          "256-byte aligned");
         e = mnb::launch_acc4(a, p->dtype == MNB_DTYPE_F16, b, scales, zero_points, y, p->m,
-                             p->n, p->k, p->bits, p->block_size, workspace, st);
+                             p->n, p->k, p->bits, p->block_size, workspace, st, b_strips);
     } else if (kern == MNB_KERNEL_BATCH_STREAM) {
         mnb::BatchStreamGeom bg{};
         if (!mnb::batch_stream_geometry(p->m, p->n, p->k, p->block_size, &bg))
@@ -1173,14 +1173,21 @@ int mnb_weights_prepack(mnb_weights* w, int64_t* bytes) {
     if (bytes) *bytes = 0;
     if (!w) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
     const mnb_problem& p = w->node;
+    // the kernels that read the copy: the batched decode kernel, and at accuracy_level 4 the
+    // strip-per-workgroup int8 GEMV
     mnb::BatchStreamGeom bg{};
-    if (p.dtype != MNB_DTYPE_F16 || p.bits != 4 || p.accuracy_level == 4 ||
-        !mnb::batch_stream_geometry(16, p.n, p.k, p.block_size, &bg))
+    mnb::Acc4StreamGeom ag{};
+    const bool reader =
+        p.dtype == MNB_DTYPE_F16 && p.bits == 4 &&
+        (p.accuracy_level == 4 ? mnb::acc4_stream_geometry(16, p.n, p.k, p.block_size, &ag)
+                               : mnb::batch_stream_geometry(16, p.n, p.k, p.block_size, &bg));
+    if (!reader)
         return fail(MNB_ERR_UNSUPPORTED,
-                    "no strip-major layout for this node: the batched decode kernel takes fp16 "
+                    "no strip-major layout for this node: the kernels that read it take fp16 "
                     "A, 4-bit B, K %% 128 == 0 and blocks of 32, 64 or 128 with whole groups of "
-                    "four (N=%lld K=%lld bits=%d block_size=%d)",
-                    (long long)p.n, (long long)p.k, p.bits, p.block_size);
+                    "four (and K <= 8192 at accuracy_level 4) (N=%lld K=%lld bits=%d "
+                    "block_size=%d level=%d)",
+                    (long long)p.n, (long long)p.k, p.bits, p.block_size, p.accuracy_level);
     const int64_t nb = mnb::strip_pack_bytes(p.n, p.k);
     std::lock_guard<std::mutex> lk(w->s->mu);
     (void)hipSetDevice(w->s->device);

@@ -1,7 +1,8 @@
 """GPU parity of the upload-time strip-major weight layout (mnb_weights_prepack).
 
-A prepacked node's session calls that plan the batched decode kernel (4 to 16 fp16 rows) read
-the strip-major copy of B; every other plan reads ORT's layout.  The copy holds the same bytes in
+A prepacked node's session calls that plan the batched decode kernel (4 to 16 fp16 rows) or, at
+accuracy_level 4, the strip-per-workgroup int8 GEMV read the strip-major copy of B; every other
+plan reads ORT's layout.  The copy holds the same bytes in
 another order and the kernel does the same arithmetic on them, so the bar is bit-identical
 output against the same node uploaded without the copy, plus the fp16 bar of the rest of the
 suite against the oracle (max relative error 2e-3 over significant elements, |y_ref| >= 0.1 RMS).
@@ -77,7 +78,7 @@ def test_prepacked_matches_ort_layout(cuda, M, N, K, bs, zp):
 
 
 @pytest.mark.parametrize("bits,bs,K,level", [(8, 32, 3072, 0), (4, 16, 3072, 0),
-                                              (4, 32, 3040, 0), (4, 128, 8192, 4)])
+                                              (4, 32, 3040, 0), (4, 128, 16384, 4)])
 def test_prepack_refuses_nodes_the_batched_kernel_never_runs(cuda, bits, bs, K, level):
     import mnb
 
@@ -97,5 +98,49 @@ def test_prepack_refuses_nodes_the_batched_kernel_never_runs(cuda, bits, bs, K, 
         assert nb.value == 0
         assert b"strip-major" in lib.mnb_last_error()
         mnb.check(lib.mnb_weights_release(w))
+    finally:
+        lib.mnb_session_destroy(s)
+
+
+@pytest.mark.parametrize("M,N,K,bs,zp", [(16, 3072, 8192, 128, True),
+                                         (5, 500, 1024, 32, False),
+                                         (9, 1040, 2048, 64, True)])
+def test_prepacked_accuracy_level_4(cuda, M, N, K, bs, zp):
+    """accuracy_level 4 at up to 16 fp16 rows: the int8 GEMV reads the strip-major copy;
+    bit-identical to the node without it, and the level-4 oracle at the fp16 bar."""
+    import mnb
+    import torch
+
+    lib = mnb.load()
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=3 * M + N)
+    p4 = mnb.problem(M, N, K, 4, bs, zp, mnb.DTYPE_F16, 4)
+    assert mnb.plan(p4).kernel == mnb.KERNEL_ACC4_STREAM
+    print(f"[gpu] prepack acc4 M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
+    s = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(s)))
+    try:
+        ws = []
+        for pack in (False, True):
+            p = mnb.problem(0, N, K, 4, bs, zp, mnb.DTYPE_F16, 4)
+            w = C.c_void_p()
+            B, S, Z = inp["B"], inp["scales"], inp["zp"]
+            mnb.check(lib.mnb_weights_upload(s, C.byref(p), B.ctypes.data, B.nbytes,
+                                             S.ctypes.data, S.nbytes,
+                                             Z.ctypes.data if zp else None,
+                                             Z.nbytes if zp else 0, C.byref(w)))
+            if pack:
+                mnb.check(lib.mnb_weights_prepack(w, None))
+            ws.append(w)
+        A = torch.from_numpy(np.ascontiguousarray(inp["A"])).to(cuda)
+        ys = []
+        for w in ws:
+            y = torch.empty(M, N, dtype=torch.float16, device=cuda)
+            mnb.check(lib.mnb_session_run(s, w, M, A.data_ptr(), 1, y.data_ptr(), 1))
+            ys.append(y.cpu().numpy())
+        assert np.array_equal(ys[0].view(np.uint16), ys[1].view(np.uint16))
+        ref = orc.matmul_nbits_acc4(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, bs)
+        assert orc.max_rel_err_significant(ys[1], ref) <= F16_TOL
+        for w in ws:
+            mnb.check(lib.mnb_weights_release(w))
     finally:
         lib.mnb_session_destroy(s)
