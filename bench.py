@@ -865,6 +865,59 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": round(q_bytes / (q_us * 1e-6) / 1e9, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(q_bytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
+
+    # The same layer through the session layer as the EP runs it with ep.strip_major_weights=1:
+    # both weight copies uploaded (mnb_qmoe_weights_upload) with their strip-major expert
+    # weights (mnb_qmoe_weights_prepack); an async session, so device-resident calls return
+    # once enqueued and can be recorded into a graph on the session's stream.
+    qsess = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(qsess)))
+    mnb.check(lib.mnb_session_set_async(qsess, 1))
+    qstream = torch.cuda.ExternalStream(int(lib.mnb_session_stream(qsess)))
+    qsw = []
+    for tens in q_w:
+        host = [t.cpu().numpy() for t in tens]
+        w = C.c_void_p()
+        p0 = mnb.qmoe_problem(0, MK, q_I, E, TOPK, BS, 1, True, 1.702, 1.0, 7.0)
+        mnb.check(lib.mnb_qmoe_weights_upload(qsess, C.byref(p0), 0,
+                                              *[v for h in host for v in (h.ctypes.data, h.nbytes)],
+                                              C.byref(w)))
+        mnb.check(lib.mnb_qmoe_weights_prepack(w, None))
+        qsw.append(w)
+        del host
+
+    def qslaunch(r):
+        rc = lib.mnb_session_run_qmoe(qsess, qsw[r % 2], T, q_x.data_ptr(), 1, q_lg.data_ptr(), 1,
+                                      q_y.data_ptr(), 1)
+        if rc:
+            mnb.check(rc)
+    for r in range(2):
+        qslaunch(r)
+    torch.cuda.synchronize()
+    lib.mnb_session_synchronize(qsess)
+    qg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(qg, stream=qstream):
+        for r in range(10):
+            qslaunch(r)
+    qg.replay()
+    qs_us = float("inf")
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        qg.replay()                      # a replay runs on the current stream: timed there
+        b.record(stream)
+        torch.cuda.synchronize()
+        qs_us = min(qs_us, 1e3 * a.elapsed_time(b) / 10)
+    del qg
+    for w in qsw:
+        lib.mnb_qmoe_weights_release(w)
+    lib.mnb_session_destroy(qsess)
+    qmoe["session_strip_major"] = {
+        "path": "mnb_qmoe_weights_upload + mnb_qmoe_weights_prepack, mnb_session_run_qmoe "
+                "(async session, device tensors)",
+        "us": round(qs_us, 2), "GB/s": round(q_bytes / (qs_us * 1e-6) / 1e9, 1),
+        "frac_hbm": round(q_bytes / (qs_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     del q_w
 
     # The EP's Compute call (mnb_session_run, synchronous) for qkv at M=1: host I/O (A and Y in

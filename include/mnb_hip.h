@@ -358,6 +358,13 @@ int mnb_qmoe_weights_upload(mnb_session* s, const mnb_qmoe_problem* node,
                             const void* fc2_scales, size_t fc2_scales_bytes, const void* fc2_bias,
                             size_t fc2_bias_bytes, mnb_qmoe_weights** out);
 int mnb_qmoe_weights_release(mnb_qmoe_weights* w);
+/* mnb_weights_prepack for a QMoE node: strip-major copies of the fc1 and fc2 expert weights
+ * ([E][ceil(N/16)][ceil(K/128)] 1 KB runs, chunks past K zero), read by the expert-grouped strip
+ * GEMV (up to 16 expected rows per expert) in place of ORT's layout, which stays resident for
+ * the row-tiled GEMV of larger batches; the node then holds its expert weights twice.  Once per
+ * node; *bytes (may be NULL) receives the copies' size.  Same seam as mnb_weights_prepack
+ * (rust/src/engine.rs:372-468); the reference has no QMoE kernel (rust/src/ops/moe.rs:92-94). */
+int mnb_qmoe_weights_prepack(mnb_qmoe_weights* w, int64_t* bytes);
 /* One QMoE Compute with x, the router logits and y each in host memory or in the session
  * device's memory; host tensors are staged through HBM; returns after the stream finished. */
 int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows, const void* x,

@@ -1076,6 +1076,9 @@ std::unique_ptr<NodeKernel> compile_qmoe(Ep* ep, const OrtNode* node, const OrtN
                                    bytes[0], host[1], bytes[1], host[2], bytes[2], host[3],
                                    bytes[3], host[4], bytes[4], host[5], bytes[5], &k->qweights),
            "uploading QMoE expert weights at Compile");
+    if (ep->strip_major_weights)
+        mnb_ok(mnb_qmoe_weights_prepack(k->qweights, nullptr),
+               "strip-major copy of the QMoE expert weights");
     k->resident = true;
     return k;
 }
@@ -1437,8 +1440,9 @@ OrtStatus* ORT_API_CALL f_create_ep(OrtEpFactory* self, const OrtHardwareDevice*
             ep->keep_constant_initializers = opt == "1" || opt == "true";
         if (session_option(api, so, "ep.qmoe_unfused_as_interleaved", &opt))
             ep->qmoe_unfused_as_interleaved = opt == "1" || opt == "true";
-        // ep.strip_major_weights: each MatMulNBits node the batched decode kernel can run also
-        // keeps a strip-major copy of its weights (twice the node's weight memory)
+        // ep.strip_major_weights: each MatMulNBits node the batched decode kernels can run, and
+        // each QMoE node, also keeps a strip-major copy of its weights (twice the node's weight
+        // memory)
         if (session_option(api, so, "ep.strip_major_weights", &opt))
             ep->strip_major_weights = opt == "1" || opt == "true";
         // ep.max_claim_ops: comma-separated allowlist (reference: rust/src/ep.rs:39-160);

@@ -291,29 +291,33 @@ bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamG
     return true;
 }
 
-// ORT's int4 B [N][K / 2] -> the strip-major copy [ceil(N / 16)][K / 128][16 columns][4] x 16
-// bytes that batch_stream reads one 1 KB run per load instruction from; columns past N are zero.
-// One thread per 16-byte piece.
+// ORT's int4 B [groups][N][K / 2] -> the strip-major copy
+// [groups][ceil(N / 16)][ceil(K / 128)][16 columns][4 chunks] x 16 bytes that the batched and
+// strip kernels read one 1 KB run per load instruction from; columns past N and chunks past K
+// (a partial last quad) are zero.  One thread per 16-byte piece.
 __global__ void __launch_bounds__(256)
 strip_pack(const u32x4* __restrict__ B, u32x4* __restrict__ dst, int64_t N, int64_t K,
            int64_t pieces) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= pieces) return;
-    const int64_t kq = K / 128;
+    const int64_t kq = (K + 127) / 128, ns = (N + 15) / 16, chunks = K / 32;
     const int g = (int)(i & 3), n = (int)((i >> 2) & 15);
-    const int64_t q = (i >> 6) % kq, st = (i >> 6) / kq;
-    const int64_t col = 16 * st + n;
-    dst[i] = col < N ? B[(col * (K / 2) + 16 * (4 * q + g)) / 16] : u32x4{0u, 0u, 0u, 0u};
+    const int64_t q = (i >> 6) % kq, st = (i >> 6) / kq % ns, grp = (i >> 6) / kq / ns;
+    const int64_t col = 16 * st + n, c = 4 * q + g;
+    dst[i] = col < N && c < chunks ? B[((grp * N + col) * (K / 2) + 16 * c) / 16]
+                                   : u32x4{0u, 0u, 0u, 0u};
 }
 
-int64_t strip_pack_bytes(int64_t n, int64_t k) { return (n + 15) / 16 * (k / 128) * 1024; }
+int64_t strip_pack_bytes(int64_t n, int64_t k, int64_t groups) {
+    return groups * ((n + 15) / 16) * ((k + 127) / 128) * 1024;
+}
 
 hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
-                             hipStream_t st) {
-    if (n < 1 || k < 128 || k % 128 || reinterpret_cast<uintptr_t>(b) % 16 ||
+                             hipStream_t st, int64_t groups) {
+    if (n < 1 || k < 32 || k % 32 || groups < 1 || reinterpret_cast<uintptr_t>(b) % 16 ||
         reinterpret_cast<uintptr_t>(dst) % 16)
         return hipErrorInvalidValue;
-    const int64_t pieces = strip_pack_bytes(n, k) / 16;
+    const int64_t pieces = strip_pack_bytes(n, k, groups) / 16;
     const int64_t blocks = (pieces + 255) / 256;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL(strip_pack, dim3((unsigned)blocks), dim3(256), 0, st,

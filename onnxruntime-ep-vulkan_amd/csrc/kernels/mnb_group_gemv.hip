@@ -589,14 +589,15 @@ hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index
                                          const int32_t* offsets, int64_t groups,
                                          int64_t rows_bound, int64_t rows_hint, const uint8_t* b,
                                          const void* s, const uint8_t* z, void* y, int64_t m,
-                                         int64_t n, int64_t k, int bits, int bs, hipStream_t st) {
+                                         int64_t n, int64_t k, int bits, int bs, hipStream_t st,
+                                         const uint8_t* b_strips) {
     if (!group_gemv_supported(k, bits, bs)) return hipErrorInvalidValue;
     if (m == 0 || groups == 0) return hipSuccess;
     StripGeom sg;
     if (rows_hint <= 16 && !strip_gemv_forced_off() && strip_gemv_aligned(a, b, s, z, false) &&
         strip_geometry(n, k, groups, rows_bound, false, bs, z != nullptr, &sg))
         return launch_strip_gemv(sg, false, a, nullptr, row_index, offsets, b, s, z, y, m, n, k,
-                                 bs, st);
+                                 bs, st, nullptr, b_strips);
     // Tile height from the expected rows per group; enough row tiles for the bound (tiles past
     // a group's last row leave at once).
     GroupGeom g = group_geometry(std::max<int64_t>(1, std::min(rows_hint, rows_bound)), n, k,

@@ -125,7 +125,7 @@ hipError_t launch_group_gemv_f16_bounded(const void* a, const int32_t* row_index
                                          int64_t rows_bound, int64_t rows_hint, const uint8_t* b,
                                          const void* s, const uint8_t* z, void* y, int64_t m,
                                          int64_t n, int64_t k, int bits, int bs,
-                                         hipStream_t stream);
+                                         hipStream_t stream, const uint8_t* b_strips = nullptr);
 // Launch shape of the strip GEMV (mnb_strip_gemv.hip): at most 16 rows per group, the
 // activations of a wavefront's K share held in registers across a run of column strips.
 struct StripGeom {
@@ -167,7 +167,8 @@ hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const f
                              const int32_t* row_index,
                              const int32_t* offsets, const uint8_t* b, const void* s,
                              const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bs,
-                             hipStream_t stream, const StripSwiglu* swiglu = nullptr);
+                             hipStream_t stream, const StripSwiglu* swiglu = nullptr,
+                             const uint8_t* b_strips = nullptr);
 
 // cnt / ncnt: split-K counters of a following int8 GEMV, cleared by the quantiser (may be null).
 // scale_rows > 0 writes the scales block-major, [k/bs][scale_rows] (rows >= m untouched).
@@ -216,11 +217,12 @@ hipError_t launch_batch_stream(const BatchStreamGeom& g, const void* a, const ui
                                const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
                                int64_t k, int bs, hipStream_t stream,
                                const uint8_t* b_strips = nullptr);
-// The strip-major copy of an int4 B (K % 128 == 0): strip_pack_bytes(n, k) bytes, 16-byte
-// aligned, columns past N zero.
-int64_t strip_pack_bytes(int64_t n, int64_t k);
+// The strip-major copy of an int4 B [groups][N][K / 2] (K % 32 == 0):
+// [groups][ceil(N / 16)][ceil(K / 128)][16 columns][4 chunks] x 16 bytes, strip_pack_bytes
+// bytes, 16-byte aligned; columns past N and chunks past K zero.
+int64_t strip_pack_bytes(int64_t n, int64_t k, int64_t groups = 1);
 hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
-                             hipStream_t stream);
+                             hipStream_t stream, int64_t groups = 1);
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                        int bs, void* workspace, hipStream_t stream,
@@ -247,9 +249,12 @@ struct QmoeArgs {
     float alpha, beta, limit;
 };
 size_t qmoe_workspace_bytes(const QmoeArgs& q);
+// fc1_strips / fc2_strips: strip-major copies of the expert weights (launch_strip_pack over the
+// experts), read by the strip GEMV in place of fc1 / fc2 when not null.
 hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, const uint8_t* fc1,
                        const void* fc1_s, const void* fc1_b, const uint8_t* fc2, const void* fc2_s,
-                       const void* fc2_b, void* y, void* workspace, hipStream_t stream);
+                       const void* fc2_b, void* y, void* workspace, hipStream_t stream,
+                       const uint8_t* fc1_strips = nullptr, const uint8_t* fc2_strips = nullptr);
 
 // RMSNorm with optional fused residual add (mnb_rmsnorm.hip).
 bool rmsnorm_supported(int64_t hidden, bool f16);

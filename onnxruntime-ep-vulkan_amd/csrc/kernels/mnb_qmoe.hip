@@ -422,7 +422,8 @@ size_t qmoe_workspace_bytes(const QmoeArgs& q) { return qmoe_layout(q).total; }
 
 hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, const uint8_t* fc1,
                        const void* fc1_s, const void* fc1_b, const uint8_t* fc2, const void* fc2_s,
-                       const void* fc2_b, void* y, void* workspace, hipStream_t st) {
+                       const void* fc2_b, void* y, void* workspace, hipStream_t st,
+                       const uint8_t* fc1_strips, const uint8_t* fc2_strips) {
     if (q.rows == 0) return hipSuccess;
     const QmoeLayout l = qmoe_layout(q);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -477,7 +478,7 @@ hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, con
             sw.k = q.k;
         }
         e = launch_strip_gemv(sg, false, x, nullptr, row_token, offsets, fc1, fc1_s, nullptr, act,
-                              R, 2 * q.inter, q.hidden, q.block_size, st, &sw);
+                              R, 2 * q.inter, q.hidden, q.block_size, st, &sw, fc1_strips);
         if (e != hipSuccess) return e;
     } else {
         e = launch_group_gemv_f16_bounded(x, row_token, offsets, q.experts, q.rows, hint, fc1,
@@ -491,7 +492,8 @@ hipError_t launch_qmoe(const QmoeArgs& q, const void* x, const void* logits, con
         if (e != hipSuccess) return e;
     }
     e = launch_group_gemv_f16_bounded(act, nullptr, offsets, q.experts, q.rows, hint, fc2, fc2_s,
-                                      nullptr, o, R, q.hidden, q.inter, 4, q.block_size, st);
+                                      nullptr, o, R, q.hidden, q.inter, 4, q.block_size, st,
+                                      fc2_strips);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(qmoe_combine, dim3(grid_for(q.rows * (q.hidden / 8))), dim3(256), 0, st, o,
                        static_cast<const f16*>(fc2_b), expert_of, weight_of, pos_of,

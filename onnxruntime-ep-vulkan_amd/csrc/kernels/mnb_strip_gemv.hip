@@ -94,7 +94,8 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
            const int32_t* __restrict__ row_index,
            const int32_t* __restrict__ offsets, const uint8_t* __restrict__ B,
            const f16* __restrict__ Sc, const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M,
-           int N, int K, int S, int vec_s, int vec_z, StripSwiglu sw) {
+           int N, int K, int S, int vec_s, int vec_z, StripSwiglu sw,
+           const uint8_t* __restrict__ Bs) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int CPB = BS / 32;                         // 32-k chunks per block: 1, 2 or 4
     constexpr int BPQ = 4 / CPB;                         // blocks per quad
@@ -121,15 +122,30 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
     const int q_n = ((wave + 1) * Q) / W - q_lo;         // quads of this wavefront, <= QW
     const uint8_t* __restrict__ Bg = B + wb;
 
+    // Lane (n, g) takes chunk 4 q + g of column n: from ORT's layout, or from the strip-major
+    // copy (launch_strip_pack: per group, strip and quad one 1 KB run in this lane order, the
+    // chunks past K zero; chunks past K are never used either way).
+    const int nst = (N + 15) >> 4;
     auto fetch = [&](int s, u32x4(&buf)[QW]) {
-        const int col = min(n0 + 16 * s + nl, N - 1);
-        const uint8_t* bc = Bg + (int64_t)col * (K / 2);
+        const uint8_t* bc;
+        int64_t step;
+        if (Bs) {
+            const int st = min((n0 >> 4) + s, nst - 1);
+            bc = Bs + (((int64_t)e * nst + st) * Q + q_lo) * 1024 + 64 * nl + 16 * g;
+            step = 1024;
+        } else {
+            const int col = min(n0 + 16 * s + nl, N - 1);
+            bc = Bg + (int64_t)col * (K / 2) + 16 * (4 * q_lo + g);
+            step = 64;
+        }
 #pragma unroll
         for (int j = 0; j < QW; ++j) {
             if (j < q_n) {                               // wave-uniform
-                const int c = min(4 * (q_lo + j) + g, chunks - 1);
-                buf[j] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4*>(bc + 16 * (int64_t)c));
+                // ORT's layout: the last quad's chunks past K are clamped onto the last chunk
+                const int64_t off = Bs || 4 * (q_lo + j) + g < chunks
+                                        ? step * j
+                                        : 16 * (int64_t)(chunks - 1 - (4 * q_lo + g));
+                buf[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bc + off));
             }
         }
     };
@@ -504,7 +520,7 @@ hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
                     const int32_t* row_index,
                     const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
                     void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
-                    const StripSwiglu& sw, hipStream_t st) {
+                    const StripSwiglu& sw, hipStream_t st, const uint8_t* bs_) {
     if constexpr (strip_max_threads(I8, BS, QW) == 0 || (SWIGLU && (I8 || HAS_ZP))) {
         return hipErrorInvalidValue;                     // not instantiated (see above)
     } else {
@@ -517,7 +533,7 @@ hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
     hipLaunchKernelGGL(kern, grid, block, g.lds, st, a, a_scale, row_index,
                        offsets, b, static_cast<const f16*>(s), z, static_cast<f16*>(y), (int)m,
-                       (int)n, (int)k, g.strips, vec_s, vec_z, sw);
+                       (int)n, (int)k, g.strips, vec_s, vec_z, sw, bs_);
     return hipGetLastError();
     }
 }
@@ -527,11 +543,11 @@ hipError_t strip_qw(const StripGeom& g, const void* a, const float* a_scale,
                     const int32_t* row_index,
                     const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
                     void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
-                    const StripSwiglu& sw, hipStream_t st) {
+                    const StripSwiglu& sw, hipStream_t st, const uint8_t* bs_) {
 #define MNB_STRIP_GO(QW_)                                                                          \
     case QW_:                                                                                      \
         return strip_go<I8, BS, HAS_ZP, QW_, SWIGLU>(g, a, a_scale, row_index, offsets, b, s, z, y, \
-                                                     m, n, k, vec_s, vec_z, sw, st)
+                                                     m, n, k, vec_s, vec_z, sw, st, bs_)
     switch (g.qw) {
         MNB_STRIP_GO(1);
         MNB_STRIP_GO(2);
@@ -549,15 +565,15 @@ hipError_t strip_bs(int bs, const StripGeom& g, const void* a, const float* a_sc
                     const int32_t* row_index,
                     const int32_t* offsets, const uint8_t* b, const void* s, const uint8_t* z,
                     void* y, int64_t m, int64_t n, int64_t k, int vec_s, int vec_z,
-                    const StripSwiglu* sw, hipStream_t st) {
+                    const StripSwiglu* sw, hipStream_t st, const uint8_t* bs_) {
     const StripSwiglu none{};
 #define MNB_STRIP_ZP(BS_)                                                                          \
     if (sw) return strip_qw<I8, BS_, false, true>(g, a, a_scale, row_index, offsets, b, s, z, y,   \
-                                                  m, n, k, vec_s, vec_z, *sw, st);                 \
+                                                  m, n, k, vec_s, vec_z, *sw, st, bs_);            \
     return z ? strip_qw<I8, BS_, true, false>(g, a, a_scale, row_index, offsets, b, s, z, y, m, n, \
-                                              k, vec_s, vec_z, none, st)                           \
+                                              k, vec_s, vec_z, none, st, bs_)                      \
              : strip_qw<I8, BS_, false, false>(g, a, a_scale, row_index, offsets, b, s, z, y, m,   \
-                                               n, k, vec_s, vec_z, none, st)
+                                               n, k, vec_s, vec_z, none, st, bs_)
     switch (bs) {
         case 32: MNB_STRIP_ZP(32);
         case 64: MNB_STRIP_ZP(64);
@@ -580,10 +596,11 @@ hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const f
                              const int32_t* row_index,
                              const int32_t* offsets, const uint8_t* b, const void* s,
                              const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bs,
-                             hipStream_t st, const StripSwiglu* swiglu) {
+                             hipStream_t st, const StripSwiglu* swiglu, const uint8_t* b_strips) {
     if (m == 0) return hipSuccess;
     if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(b) % 16 ||
-        (i8 && !a_scale) || (swiglu && (i8 || z || n % 2)))
+        reinterpret_cast<uintptr_t>(b_strips) % 16 || (i8 && !a_scale) ||
+        (swiglu && (i8 || z || n % 2)))
         return hipErrorInvalidValue;
     const int64_t bpc = k / bs;
     const int64_t zpb = (bpc + 1) / 2;
@@ -592,8 +609,8 @@ hipError_t launch_strip_gemv(const StripGeom& g, bool i8, const void* a, const f
     const bool multi = offsets != nullptr && g.gy > 1;
     const int vec_s = reinterpret_cast<uintptr_t>(s) % 16 == 0 && (!multi || (n * bpc * 2) % 16 == 0);
     const int vec_z = z && reinterpret_cast<uintptr_t>(z) % 16 == 0 && (!multi || (n * zpb) % 16 == 0);
-    if (i8) return strip_bs<true>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, nullptr, st);
-    return strip_bs<false>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, swiglu, st);
+    if (i8) return strip_bs<true>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, nullptr, st, b_strips);
+    return strip_bs<false>(bs, g, a, a_scale, row_index, offsets, b, s, z, y, m, n, k, vec_s, vec_z, swiglu, st, b_strips);
 }
 
 }  // namespace mnb

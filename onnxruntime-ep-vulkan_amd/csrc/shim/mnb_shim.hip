@@ -620,10 +620,15 @@ int mnb_qmoe_workspace_bytes(const mnb_qmoe_problem* p, size_t* bytes) {
     return MNB_OK;
 }
 
-int mnb_qmoe(const mnb_qmoe_problem* p, const void* x, const void* router_logits,
-             const uint8_t* fc1_weights, const void* fc1_scales, const void* fc1_bias,
-             const uint8_t* fc2_weights, const void* fc2_scales, const void* fc2_bias, void* y,
-             void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// mnb_qmoe with, from the session layer, strip-major copies of the expert weights
+// (mnb_qmoe_weights_prepack), which the strip GEMV reads in place of fc1 / fc2 when it runs.
+static int qmoe_impl(const mnb_qmoe_problem* p, const void* x, const void* router_logits,
+                     const uint8_t* fc1_weights, const void* fc1_scales, const void* fc1_bias,
+                     const uint8_t* fc2_weights, const void* fc2_scales, const void* fc2_bias,
+                     void* y, void* workspace, size_t workspace_bytes, void* stream,
+                     const uint8_t* fc1_strips, const uint8_t* fc2_strips) {
     int rc = mnb_qmoe_check(p);
     if (rc) return rc;
     if (p->rows == 0) return MNB_OK;
@@ -641,10 +646,21 @@ int mnb_qmoe(const mnb_qmoe_problem* p, const void* x, const void* router_logits
         return fail(MNB_ERR_INVALID, "x, y, the weights and the biases must be 16-byte aligned");
     hipError_t e = mnb::launch_qmoe(q, x, router_logits, fc1_weights, fc1_scales, fc1_bias,
                                     fc2_weights, fc2_scales, fc2_bias, y, workspace,
-                                    static_cast<hipStream_t>(stream));
+                                    static_cast<hipStream_t>(stream), fc1_strips, fc2_strips);
     if (e != hipSuccess) return hip_fail(e, "QMoE launch");
     g_launches.fetch_add(1);
     return MNB_OK;
+}
+
+extern "C" {
+
+int mnb_qmoe(const mnb_qmoe_problem* p, const void* x, const void* router_logits,
+             const uint8_t* fc1_weights, const void* fc1_scales, const void* fc1_bias,
+             const uint8_t* fc2_weights, const void* fc2_scales, const void* fc2_bias, void* y,
+             void* workspace, size_t workspace_bytes, void* stream) {
+    return qmoe_impl(p, x, router_logits, fc1_weights, fc1_scales, fc1_bias, fc2_weights,
+                     fc2_scales, fc2_bias, y, workspace, workspace_bytes, stream, nullptr,
+                     nullptr);
 }
 
 // ---- RMSNorm --------------------------------------------------------------------------------
@@ -1269,6 +1285,7 @@ struct mnb_qmoe_weights {
     mnb_session* s = nullptr;
     mnb_qmoe_problem node{};
     void* buf[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};  // w1 s1 b1 w2 s2 b2
+    uint8_t* strips[2] = {nullptr, nullptr};   // strip-major fc1 / fc2 (mnb_qmoe_weights_prepack)
 };
 
 int mnb_qmoe_weights_release(mnb_qmoe_weights* w) {
@@ -1277,7 +1294,40 @@ int mnb_qmoe_weights_release(mnb_qmoe_weights* w) {
     (void)hipStreamSynchronize(w->s->stream);
     for (void* b : w->buf)
         if (b) (void)hipFree(b);
+    for (uint8_t* b : w->strips)
+        if (b) (void)hipFree(b);
     delete w;
+    return MNB_OK;
+}
+
+int mnb_qmoe_weights_prepack(mnb_qmoe_weights* w, int64_t* bytes) {
+    if (bytes) *bytes = 0;
+    if (!w) return fail(MNB_ERR_INVALID, "a NULL argument was passed");
+    const mnb_qmoe_problem& p = w->node;
+    // fc1 is [E][2 I][H / 2], fc2 [E][H][I / 2]: N and K of each expert GEMV
+    const int64_t n[2] = {2 * p.inter, p.hidden}, kk[2] = {p.hidden, p.inter};
+    int64_t total = 0;
+    std::lock_guard<std::mutex> lk(w->s->mu);
+    (void)hipSetDevice(w->s->device);
+    for (int f = 0; f < 2; ++f) {
+        const int64_t nb = mnb::strip_pack_bytes(n[f], kk[f], p.num_experts);
+        total += nb;
+        if (w->strips[f]) continue;
+        uint8_t* d = nullptr;
+        hipError_t e = counted_malloc(&d, (size_t)nb);
+        if (e != hipSuccess)
+            return fail(MNB_ERR_NOMEM, "hipMalloc(%lld) for the strip-major fc%d: %s",
+                        (long long)nb, f + 1, hipGetErrorString(e));
+        e = mnb::launch_strip_pack(static_cast<const uint8_t*>(w->buf[3 * f]), d, n[f], kk[f],
+                                   w->s->stream, p.num_experts);
+        if (e == hipSuccess) e = hipStreamSynchronize(w->s->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return hip_fail(e, "strip-major copy of the QMoE weights");
+        }
+        w->strips[f] = d;
+    }
+    if (bytes) *bytes = total;
     return MNB_OK;
 }
 
@@ -1402,9 +1452,9 @@ int mnb_session_run_qmoe(mnb_session* s, const mnb_qmoe_weights* w, int64_t rows
     if (!y_on_device) io.out(y, s->y_dev, x_bytes);
     rc = io.upload();
     if (!rc)
-        rc = mnb_qmoe(&p, xd, ld, static_cast<const uint8_t*>(w->buf[0]), w->buf[1], w->buf[2],
-                      static_cast<const uint8_t*>(w->buf[3]), w->buf[4], w->buf[5], yd, s->ws,
-                      s->ws_cap, s->stream);
+        rc = qmoe_impl(&p, xd, ld, static_cast<const uint8_t*>(w->buf[0]), w->buf[1], w->buf[2],
+                       static_cast<const uint8_t*>(w->buf[3]), w->buf[4], w->buf[5], yd, s->ws,
+                       s->ws_cap, s->stream, w->strips[0], w->strips[1]);
     if (!rc) rc = io.download();
     return io.end(rc);
 }

@@ -168,6 +168,7 @@ def load() -> C.CDLL:
         "mnb_qmoe_weights_upload": (C.c_int, [vp, C.POINTER(QmoeProblem), i32, vp, sz, vp, sz,
                                               vp, sz, vp, sz, vp, sz, vp, sz, C.POINTER(vp)]),
         "mnb_qmoe_weights_release": (C.c_int, [vp]),
+        "mnb_qmoe_weights_prepack": (C.c_int, [vp, C.POINTER(i64)]),
         "mnb_session_run_qmoe": (C.c_int, [vp, vp, i64, vp, C.c_int, vp, C.c_int, vp, C.c_int]),
         "mnb_rmsnorm_check": (C.c_int, [C.POINTER(RmsNormProblem)]),
         "mnb_skip_rmsnorm": (C.c_int, [C.POINTER(RmsNormProblem), vp, vp, vp, vp, vp, vp, vp]),

@@ -178,3 +178,26 @@ def test_ep_qmoe_matches_oracle(gpu_host, lead, H, I, E, k, per_channel, fusion)
     assert orc.max_err_rms_normalised(y, ref16) <= 2e-3
     assert orc.max_rel_err_significant(y, ref16) <= 1e-2
     assert orc.max_err_rms_normalised(y, ref) <= 5e-3
+
+
+@pytest.mark.gpu
+def test_ep_qmoe_strip_major_weights_option(gpu_host):
+    """ep.strip_major_weights=1: Compile also keeps strip-major copies of the expert weights
+    (mnb_qmoe_weights_prepack); Compute's output is bit-identical to an EP without the option."""
+    print("[gpu] ep qmoe strip-major option T=64 H=I=2880 E=32 k=4", flush=True)
+    T, H, I, E, k = 64, 2880, 2880, 32, 4
+    inp = oq.make_qmoe_inputs(T, H, I, E, per_channel=True, seed=4321)
+    ys = []
+    for opt in ("0", "1"):
+        gpu_host.option("ep.strip_major_weights", opt)
+        assert gpu_host.create_ep(0) == 0, mh.err()
+        gpu_host.reset()
+        x_name, r_name, y_name = mh.add_qmoe(gpu_host, "moe", inp, k=k, x_shape=(T, H))
+        assert gpu_host.get_capability() == (1, ["moe:drop"])
+        assert gpu_host.compile() == 0, mh.err()
+        gpu_host.feed(x_name, inp["x"])
+        gpu_host.feed(r_name, inp["logits"])
+        assert gpu_host.compute(0) == 0, mh.err()
+        ys.append(gpu_host.fetch(y_name, np.float16, T * H))
+    assert np.array_equal(ys[0].view(np.uint16), ys[1].view(np.uint16))
+    assert np.isfinite(ys[1].astype(np.float32)).all()

@@ -191,3 +191,54 @@ def test_session_qmoe_per_channel_scales_host_io(cuda):
         if w.value:
             lib.mnb_qmoe_weights_release(w)
         lib.mnb_session_destroy(sess)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,H,I,E,k,bs,fusion", [
+    (64, 2880, 2880, 32, 4, 32, 1),      # K = 2880 ends in a partial quad
+    (8, 512, 256, 32, 4, 32, 1),
+    (5, 256, 128, 8, 4, 64, 2),
+    (20, 256, 128, 96, 4, 32, 1),        # E > 64
+    (300, 256, 128, 16, 4, 32, 1),       # row-tiled GEMVs: the copy is not read
+])
+def test_session_qmoe_strip_major(cuda, T, H, I, E, k, bs, fusion):
+    """mnb_qmoe_weights_prepack: the expert-grouped strip GEMV reads strip-major copies of fc1
+    and fc2 (chunks past K zero); the output is bit-identical to the same node without them,
+    and within the bars above of the oracle."""
+    import mnb
+    import torch
+
+    print(f"[gpu] qmoe strip-major T={T} H={H} I={I} E={E} k={k} bs={bs} f={fusion}", flush=True)
+    inp = oq.make_qmoe_inputs(T, H, I, E, seed=T + 3 * E, block_size=bs)
+    ref16, ref = _refs(inp, k, I, bs, fusion, 7.0, True)
+    lib = mnb.load()
+    sess = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(sess)))
+    arrs = [np.ascontiguousarray(inp[n]) for n in ("fc1", "fc1_scales", "fc1_bias", "fc2",
+                                                    "fc2_scales", "fc2_bias")]
+    ws, ys = [], []
+    try:
+        for pack in (False, True):
+            w = C.c_void_p()
+            p = mnb.qmoe_problem(0, H, I, E, k, bs, fusion, True)
+            mnb.check(lib.mnb_qmoe_weights_upload(
+                sess, C.byref(p), 0, *[v for a in arrs for v in (a.ctypes.data, a.nbytes)],
+                C.byref(w)))
+            ws.append(w)
+            if pack:
+                nb = C.c_int64(0)
+                mnb.check(lib.mnb_qmoe_weights_prepack(w, C.byref(nb)))
+                assert nb.value == E * 1024 * (-(-2 * I // 16) * -(-H // 128) +
+                                               -(-H // 16) * -(-I // 128))
+            x, lg = _t(inp["x"], cuda), _t(inp["logits"], cuda)
+            y = torch.empty(T, H, dtype=torch.float16, device=cuda)
+            mnb.check(lib.mnb_session_run_qmoe(sess, w, T, x.data_ptr(), 1, lg.data_ptr(), 1,
+                                               y.data_ptr(), 1))
+            torch.cuda.synchronize()
+            ys.append(y.cpu().numpy())
+        assert np.array_equal(ys[0].view(np.uint16), ys[1].view(np.uint16))
+        _check(ys[1].astype(np.float32), ref16, ref)
+    finally:
+        for w in ws:
+            lib.mnb_qmoe_weights_release(w)
+        lib.mnb_session_destroy(sess)
