@@ -77,6 +77,66 @@ def test_prepacked_matches_ort_layout(cuda, M, N, K, bs, zp):
         lib.mnb_session_destroy(s)
 
 
+def _strip_plan(mnb, M, N, K, bs, zp):
+    """The kernel a session call of a prepacked node runs: the planner's, except that a
+    streaming-GEMV plan at 3 rows (when the batched kernel would take several strips per
+    workgroup) or at 4 rows moves to the batched kernel, which then reads the copy."""
+    import os
+    plan = mnb.plan(mnb.problem(M, N, K, 4, bs, zp)).kernel
+    if plan == mnb.KERNEL_GEMV_STREAM and M >= 3:
+        os.environ["MNB_FORCE_KERNEL"] = "batch"
+        try:
+            forced = mnb.plan(mnb.problem(M, N, K, 4, bs, zp))
+        finally:
+            os.environ.pop("MNB_FORCE_KERNEL", None)
+        if forced.kernel == mnb.KERNEL_BATCH_STREAM and (M >= 4 or forced.tile_n >= 32):
+            return mnb.KERNEL_BATCH_STREAM
+    return plan
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 9216, 3072), (4, 3072, 8192), (3, 3072, 3072),
+                                   (2, 9216, 3072)])
+def test_prepacked_small_row_routing(cuda, M, N, K):
+    """A prepacked node's 3- and 4-row calls take the batched kernel on the copy where the
+    streaming GEMV is slower (qkv at 3 rows, down at 4 rows), and keep the streaming GEMV
+    elsewhere (o at 3 rows, 2 rows): bit-identical to the ORT-layout node run on the same kernel
+    (MNB_FORCE_KERNEL), and within the bar of the oracle."""
+    import os
+    import mnb
+    import torch
+
+    lib = mnb.load()
+    inp = orc.make_inputs(M, N, K, bits=4, block_size=32, with_zp=True, seed=11 * M + N)
+    want = _strip_plan(mnb, M, N, K, 32, True)
+    assert want == (mnb.KERNEL_BATCH_STREAM if (M, N) in ((3, 9216), (4, 3072))
+                    else mnb.KERNEL_GEMV_STREAM)
+    print(f"[gpu] prepack routing M={M} N={N} K={K} -> kernel {want}", flush=True)
+    s = C.c_void_p()
+    mnb.check(lib.mnb_session_create(0, C.byref(s)))
+    try:
+        w_ort = _upload(lib, mnb, s, inp, N, K, 32, True)
+        w_pk = _upload(lib, mnb, s, inp, N, K, 32, True)
+        mnb.check(lib.mnb_weights_prepack(w_pk, None))
+        A = torch.from_numpy(np.ascontiguousarray(inp["A"])).to(cuda)
+        ys = []
+        for w, force in ((w_pk, None), (w_ort, "batch" if want == mnb.KERNEL_BATCH_STREAM else None)):
+            if force:
+                os.environ["MNB_FORCE_KERNEL"] = force
+            try:
+                y = torch.empty(M, N, dtype=torch.float16, device=cuda)
+                mnb.check(lib.mnb_session_run(s, w, M, A.data_ptr(), 1, y.data_ptr(), 1))
+                ys.append(y.cpu().numpy())
+            finally:
+                os.environ.pop("MNB_FORCE_KERNEL", None)
+        assert np.array_equal(ys[0].view(np.uint16), ys[1].view(np.uint16))
+        ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, 32)
+        assert orc.max_rel_err_significant(ys[0], ref) <= F16_TOL
+        mnb.check(lib.mnb_weights_release(w_ort))
+        mnb.check(lib.mnb_weights_release(w_pk))
+    finally:
+        lib.mnb_session_destroy(s)
+
+
 @pytest.mark.parametrize("bits,bs,K,level", [(8, 32, 3072, 0), (4, 16, 3072, 0),
                                               (4, 32, 3040, 0), (4, 128, 16384, 4)])
 def test_prepack_refuses_nodes_the_batched_kernel_never_runs(cuda, bits, bs, K, level):
