@@ -51,7 +51,7 @@ bool derive(StreamConfig& c, int64_t n, int64_t k, int bits, int bs) {
 
 }  // namespace
 
-StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int bs) {
+static StreamConfig stream_config_search(int64_t m, int64_t n, int64_t k, int bits, int bs) {
     StreamConfig c{};
     const int64_t cpc = k / (128 / bits);
     auto lane_group = [&](int cand) { return (cpc + cand - 1) / cand <= kStreamMaxCpl; };
@@ -130,6 +130,24 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
     // the CUs take up as they finish others; N=32064: 4008 x 4 10.4 us against 1002 x 16 11.6 us)
     c.waves_per_group = (int)w;
     derive(c, n, k, bits, bs);
+    return c;
+}
+
+// The search above runs for the planner's support check, its plan and the launch of every call;
+// a shape repeats from one token to the next, so each thread keeps its last eight answers.
+StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int bs) {
+    struct Memo {
+        int64_t m, n, k;
+        int bits, bs;
+        StreamConfig c;
+        bool used;
+    };
+    thread_local Memo memo[8];
+    thread_local unsigned next = 0;
+    for (const Memo& e : memo)
+        if (e.used && e.m == m && e.n == n && e.k == k && e.bits == bits && e.bs == bs) return e.c;
+    const StreamConfig c = stream_config_search(m, n, k, bits, bs);
+    memo[next++ & 7] = Memo{m, n, k, bits, bs, c, true};
     return c;
 }
 
