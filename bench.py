@@ -18,6 +18,8 @@ The line also carries, measured in the same run:
                 session layer with the strip-major weight copy (ep.strip_major_weights)
   prefill       MatMulNBits M=2048, K=3072, N=8192 in TFLOP/s vs 2.5 PFLOP/s fp16
   accuracy_level_4  configs[4] (M=16, K=8192, N=3072, bs128, zp, int8 activations) in GB/s
+  decode_f32    the layer set at M=1 with fp32 activations, scales and output in GB/s, and qkv
+                on the generic kernel beside it
   moe           configs[3] (32 experts, top-4 of 64 tokens, gate_up and down) in GB/s
   qmoe          configs[3] as one fused QMoE op (routing, both expert GEMVs, SwiGLU, combine)
   mfma_calibration  the fp16 MFMA rate the chip sustains on random and on constant operands
@@ -783,6 +785,53 @@ def main() -> int:
         "frac_hbm": round(a_bytes / (as_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     del a_w
 
+    # fp32 activations, scales and output (the form of ORT's CPU-exported int4 models): the
+    # Phi-3.5 layer set at M=1 through mnb_matmul_nbits, the same packed weights and zero points
+    # with fp32 scales, rotated over the 32 layer copies; qkv also on the generic kernel, which
+    # every fp32 call ran before the fp32 streaming GEMV.
+    f_scales = [[S.float() for (_, S, _) in layer] for layer in layers]
+    f_acts = [torch.randn(1, k, device=dev, generator=gen) for _, k, _ in LAYER]
+    f_outs = [torch.empty(1, n, dtype=torch.float32, device=dev) for _, _, n in LAYER]
+    f_probs = [mnb.problem(1, n, k, BITS, BS, True, mnb.DTYPE_F32) for _, k, n in LAYER]
+
+    def f32_bytes(k, n):
+        bpc = k // BS
+        return n * k // 2 + 4 * n * bpc + n * ((bpc * 4 + 7) // 8) + 4 * k + 4 * n
+
+    def flaunch(i, r, sp):
+        B, _, Z = layers[r % copies][i]
+        rc = lib.mnb_matmul_nbits(C.byref(f_probs[i]), f_acts[i].data_ptr(), B.data_ptr(),
+                                  f_scales[r % copies][i].data_ptr(), Z.data_ptr(),
+                                  f_outs[i].data_ptr(), None, 0, sp)
+        if rc:
+            mnb.check(rc)
+
+    f32_nodes = []
+    for i, (name, k, n) in enumerate(LAYER):
+        us = graph_time_us(lambda r, sp, i=i: flaunch(i, r, sp), reps)
+        nb = f32_bytes(k, n)
+        f32_nodes.append({"node": name, "bytes": nb, "us": round(us, 3),
+                          "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
+                          "frac_hbm": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                          "kernel": mnb.KERNEL_NAMES.get(mnb.plan(f_probs[i]).kernel, "?")})
+    f_layer_us = sum(x["us"] for x in f32_nodes)
+    f_layer_bytes = sum(x["bytes"] for x in f32_nodes)
+    old_force = os.environ.get("MNB_FORCE_KERNEL")
+    os.environ["MNB_FORCE_KERNEL"] = "generic"
+    try:
+        f_generic_us = graph_time_us(lambda r, sp: flaunch(0, r, sp), 8)
+    finally:
+        if old_force is None:
+            os.environ.pop("MNB_FORCE_KERNEL", None)
+        else:
+            os.environ["MNB_FORCE_KERNEL"] = old_force
+    decode_f32 = {"config": "Phi-3.5 decode layer set, M=1, fp32 A / scales / Y, int4 bs32 zp",
+                  "nodes": f32_nodes, "layer_us": round(f_layer_us, 3),
+                  "GB/s": round(f_layer_bytes / (f_layer_us * 1e-6) / 1e9, 1),
+                  "frac_hbm": round(f_layer_bytes / (f_layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                  "qkv_generic_us": round(f_generic_us, 3)}
+    del f_scales
+
     # gpt-oss-shaped MoE: 32 experts, 64 tokens, softmax top-4 routing of
     # N(0,1) logits (seeded), per-expert int4 bs32 gate_up (2880 -> 5760) and down (2880 -> 2880).
     E, T, TOPK, MK = 32, 64, 4, 2880
@@ -1016,13 +1065,14 @@ def main() -> int:
         "batched_decode": batched,
         "batched_decode_session": {
             "path": "EP session layer with ep.strip_major_weights=1: mnb_weights_upload + "
-                    "mnb_weights_prepack (strip-major copy), mnb_session_run_device; M = 4 rows "
-                    "plan the streaming GEMV (ORT's layout) on down_proj",
+                    "mnb_weights_prepack (strip-major copy), mnb_session_run_device; every "
+                    "node at 4-16 rows runs the batched kernel on the strip-major copy",
             "rows": batched_session},
         "prefill": prefill,
         "prefill_8bit": prefill_8bit,
         "mfma_calibration": mfma_cal,
         "accuracy_level_4": acc4,
+        "decode_f32": decode_f32,
         "moe": moe,
         "qmoe": qmoe,
         "session_io": session_io,

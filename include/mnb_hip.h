@@ -53,7 +53,7 @@ extern "C" {
 #define MNB_KERNEL_GEMM_MFMA 2   /* fp16, M > 64: dequantise-into-LDS f16 MFMA GEMM */
 #define MNB_KERNEL_GENERIC 3     /* any dtype/bits/block: per-block fp32 partial, scaled once */
 #define MNB_KERNEL_ACC4_I8 4     /* accuracy_level 4: int8 A, int8 MFMA, int32 block dots */
-#define MNB_KERNEL_GEMV_STREAM 5 /* fp16, M <= 4: coalesced 16-byte-chunk streaming GEMV */
+#define MNB_KERNEL_GEMV_STREAM 5 /* M <= 4: coalesced 16-byte-chunk streaming GEMV (fp16 or fp32) */
 #define MNB_KERNEL_GROUP_MFMA 6  /* fp16, int4, block >= 32: row-tiled 16x16x32 MFMA GEMV */
 #define MNB_KERNEL_STRIP_MFMA 7  /* fp16, int4, block >= 32, 5..16 rows: activations held in
                                     registers across a run of 16-column strips */

@@ -222,10 +222,15 @@ static int plan_search(const mnb_problem* p, mnb_plan_info* out) {
                             !stream;
     if (batch && p->m >= 4 && batch_rows) kern = MNB_KERNEL_BATCH_STREAM;
     if (stream && !(batch && batch_rows)) kern = MNB_KERNEL_GEMV_STREAM;
+    // fp32 activations, M <= 4: the fp32 streaming GEMV (same launch shape as the fp16 one)
+    mnb::StreamConfig c32{};
+    const bool stream32 = !f16 && mnb::gemv_stream_f32_config(p->m, p->n, p->k, p->bits,
+                                                              p->block_size, &c32);
+    if (stream32) kern = MNB_KERNEL_GEMV_STREAM;
     const int forced = forced_kernel();
     if (forced == MNB_KERNEL_GENERIC) kern = MNB_KERNEL_GENERIC;
     if (forced == MNB_KERNEL_GEMV_MFMA && fast) kern = MNB_KERNEL_GEMV_MFMA;
-    if (forced == MNB_KERNEL_GEMV_STREAM && stream) kern = MNB_KERNEL_GEMV_STREAM;
+    if (forced == MNB_KERNEL_GEMV_STREAM && (stream || stream32)) kern = MNB_KERNEL_GEMV_STREAM;
     if (forced == MNB_KERNEL_GEMM_MFMA && gemm) kern = MNB_KERNEL_GEMM_MFMA;
     if (forced == MNB_KERNEL_GROUP_MFMA && group) kern = MNB_KERNEL_GROUP_MFMA;
     if (forced == MNB_KERNEL_STRIP_MFMA && strip) kern = MNB_KERNEL_STRIP_MFMA;
@@ -242,7 +247,7 @@ static int plan_search(const mnb_problem* p, mnb_plan_info* out) {
         return MNB_OK;
     } else if (kern == MNB_KERNEL_GEMV_STREAM) {
         const mnb::StreamConfig c =
-            mnb::gemv_stream_config(p->m, p->n, p->k, p->bits, p->block_size);
+            f16 ? mnb::gemv_stream_config(p->m, p->n, p->k, p->bits, p->block_size) : c32;
         out->waves_per_group = c.waves_per_group;
         out->tile_n = c.waves_per_group * (64 / c.g) * c.u;
         out->tile_m = c.mr;
@@ -412,8 +417,11 @@ static int matmul_impl(const mnb_problem* p, const void* a, const uint8_t* b,
         e = mnb::launch_gemm(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
                              p->block_size, st, workspace, workspace_bytes);
     } else if (kern == MNB_KERNEL_GEMV_STREAM) {
-        e = mnb::launch_gemv_stream(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
-                                    p->block_size, st);
+        e = p->dtype == MNB_DTYPE_F16
+                ? mnb::launch_gemv_stream(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
+                                          p->block_size, st)
+                : mnb::launch_gemv_stream_f32(a, b, scales, zero_points, y, p->m, p->n, p->k,
+                                              p->bits, p->block_size, st);
     } else if (kern == MNB_KERNEL_GEMV_MFMA) {
         e = mnb::launch_gemv_f16(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
                                  p->block_size, st);

@@ -184,11 +184,24 @@ def test_random_parity_f16(cuda, M, N, K, bits, bs, zp, kernel):
     _check_f16(y, ref, f"{kernel} M={M} N={N} K={K} b{bits} bs{bs} zp={zp}")
 
 
-@pytest.mark.parametrize("M,N,K,bits,bs,zp", [(1, 40, 256, 4, 32, True), (6, 24, 512, 8, 64, False),
-                                              (3, 17, 128, 4, 16, True), (9, 50, 1024, 4, 128, False)])
+# The first four run the generic kernel's forms (and the fp32 streaming GEMV at M <= 4); the rest
+# are fp32 decode shapes of the streaming GEMV: the Phi-3.5 nodes at one to four rows, int8,
+# blocks 16-128, a column count that leaves the last workgroup partial.
+F32_SHAPES = [(1, 40, 256, 4, 32, True), (6, 24, 512, 8, 64, False), (3, 17, 128, 4, 16, True),
+              (9, 50, 1024, 4, 128, False),
+              (1, 9216, 3072, 4, 32, True), (1, 3072, 8192, 4, 32, True), (2, 3072, 8192, 4, 32, True),
+              (4, 1000, 3072, 4, 32, False), (3, 16384, 3072, 4, 32, True), (1, 640, 2048, 8, 64, True),
+              (2, 500, 1024, 8, 16, False), (4, 300, 4096, 4, 128, True), (1, 2880, 2880, 4, 16, False)]
+
+
+@pytest.mark.parametrize("M,N,K,bits,bs,zp", F32_SHAPES)
 def test_random_parity_f32(cuda, M, N, K, bits, bs, zp):
+    import mnb
     inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=7 + M, a_dtype=np.float32)
-    print(f"[gpu] parity f32 M={M} N={N} K={K}", flush=True)
+    kern = mnb.plan(mnb.problem(M, N, K, bits, bs, zp, mnb.DTYPE_F32)).kernel
+    print(f"[gpu] parity f32 M={M} N={N} K={K} bits={bits} bs={bs} zp={zp} kernel {kern}", flush=True)
+    if M <= 3:
+        assert kern == mnb.KERNEL_GEMV_STREAM
     y = _run(inp, N, K, bits, bs, cuda)
     ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
     assert orc.max_rel_err_significant(y, ref) <= F32_TOL

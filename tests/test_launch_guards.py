@@ -137,6 +137,32 @@ def test_decode_routing_by_rows_and_strips():
             assert mnb.plan(mnb.problem(m, n, k, 4, 32, True)).kernel == mnb.KERNEL_BATCH_STREAM, (name, m)
 
 
+def test_fp32_decode_routing():
+    """fp32 activations at one to four rows take the fp32 streaming GEMV (reported as the
+    streaming kernel, with the fp16 launch shape) wherever its staged rows fit in LDS; more rows,
+    or four rows of K = 8192 (147 KB of fp32 staging), stay on the generic kernel."""
+    import mnb
+
+    f32 = mnb.DTYPE_F32
+    for k, n in ((3072, 9216), (3072, 3072), (3072, 16384), (8192, 3072)):
+        for m in (1, 2, 3):
+            for bits in (4, 8):
+                for bs in (16, 32, 64, 128):
+                    info = mnb.plan(mnb.problem(m, n, k, bits, bs, True, f32))
+                    wpc = 128 // bits                    # weights per staged 16-byte chunk
+                    if m * (k // wpc) * (4 * wpc + 16) > 96 * 1024:
+                        assert info.kernel == mnb.KERNEL_GENERIC, (m, n, k, bits, bs)
+                        continue
+                    assert info.kernel == mnb.KERNEL_GEMV_STREAM, (m, n, k, bits, bs)
+                    assert 64 * info.waves_per_group <= 1024
+                    f16 = mnb.plan(mnb.problem(m, n, k, bits, bs, True))
+                    assert (info.waves_per_group, info.tile_n, info.grid_x) == \
+                        (f16.waves_per_group, f16.tile_n, f16.grid_x), (m, n, k, bits, bs)
+    assert mnb.plan(mnb.problem(4, 9216, 3072, 4, 32, True, f32)).kernel == mnb.KERNEL_GEMV_STREAM
+    assert mnb.plan(mnb.problem(4, 3072, 8192, 4, 32, True, f32)).kernel == mnb.KERNEL_GENERIC
+    assert mnb.plan(mnb.problem(5, 3072, 3072, 4, 32, True, f32)).kernel == mnb.KERNEL_GENERIC
+
+
 # (M, N, K, bs, zp) -> (quads per wavefront R, wavefronts per workgroup) of the batched decode
 # kernel; the GPU parity shapes of tests/test_gpu_matmul.py run these same plans, so every
 # instantiation family (R = 1..4, the unaligned scale/zero-point loads of R = 3) stays covered.
