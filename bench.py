@@ -20,6 +20,8 @@ The line also carries, measured in the same run:
   accuracy_level_4  configs[4] (M=16, K=8192, N=3072, bs128, zp, int8 activations) in GB/s
   decode_f32    the layer set at M=1 with fp32 activations, scales and output in GB/s, and qkv
                 on the generic kernel beside it
+  prefill_f32   configs[2]'s GEMM (M = 256, 2048) with fp32 activations in TFLOP/s vs the
+                157.3 TFLOP/s fp32 matrix peak
   moe           configs[3] (32 experts, top-4 of 64 tokens, gate_up and down) in GB/s
   qmoe          configs[3] as one fused QMoE op (routing, both expert GEMVs, SwiGLU, combine)
   mfma_calibration  the fp16 MFMA rate the chip sustains on random and on constant operands
@@ -832,6 +834,33 @@ def main() -> int:
                   "qkv_generic_us": round(f_generic_us, 3)}
     del f_scales
 
+    # fp32 prefill: configs[2]'s GEMM shape with fp32 activations, scales and output, on the
+    # fp32 MFMA GEMM (weights dequantised exactly to fp32 in LDS), against the fp32 matrix peak.
+    F32_MFMA_PEAK_TFLOPS = 157.3
+    prefill_f32 = []
+    for pm in (256, 2048):
+        pk, pn = 3072, 8192
+        pw = [make_weights(torch, dev, pk, pn, gen, zp=False) for _ in range(2)]
+        pS = [S.float() for (_, S, _) in pw]
+        pA = torch.randn(pm, pk, device=dev, generator=gen)
+        pY = torch.empty(pm, pn, dtype=torch.float32, device=dev)
+        pprob = mnb.problem(pm, pn, pk, BITS, BS, False, mnb.DTYPE_F32)
+
+        def plaunch(r, sp):
+            rc = lib.mnb_matmul_nbits(C.byref(pprob), pA.data_ptr(), pw[r % 2][0].data_ptr(),
+                                      pS[r % 2].data_ptr(), None, pY.data_ptr(), None, 0, sp)
+            if rc:
+                mnb.check(rc)
+
+        us = graph_time_us(plaunch, 10)
+        tf = 2.0 * pm * pn * pk / (us * 1e-6) / 1e12
+        prefill_f32.append({"M": pm, "K": pk, "N": pn, "us": round(us, 2), "TFLOP/s": round(tf, 1),
+                            "kernel": mnb.KERNEL_NAMES.get(mnb.plan(pprob).kernel, "?") + " (fp32)",
+                            "roofline": {"bound": "mfma", "achieved": round(tf, 1),
+                                         "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                         "frac": round(tf / F32_MFMA_PEAK_TFLOPS, 4)}})
+        del pw, pS, pA, pY
+
     # gpt-oss-shaped MoE: 32 experts, 64 tokens, softmax top-4 routing of
     # N(0,1) logits (seeded), per-expert int4 bs32 gate_up (2880 -> 5760) and down (2880 -> 2880).
     E, T, TOPK, MK = 32, 64, 4, 2880
@@ -1073,6 +1102,7 @@ def main() -> int:
         "mfma_calibration": mfma_cal,
         "accuracy_level_4": acc4,
         "decode_f32": decode_f32,
+        "prefill_f32": prefill_f32,
         "moe": moe,
         "qmoe": qmoe,
         "session_io": session_io,

@@ -50,7 +50,7 @@ extern "C" {
 
 /* Kernel families the planner can select (reported by mnb_plan, forced by MNB_FORCE_KERNEL). */
 #define MNB_KERNEL_GEMV_MFMA 1   /* fp16, M <= 64: streaming GEMV on 16x16x32 f16 MFMA */
-#define MNB_KERNEL_GEMM_MFMA 2   /* fp16, M > 64: dequantise-into-LDS f16 MFMA GEMM */
+#define MNB_KERNEL_GEMM_MFMA 2   /* M > 64: dequantise-into-LDS MFMA GEMM (fp16, or fp32 M > 64) */
 #define MNB_KERNEL_GENERIC 3     /* any dtype/bits/block: per-block fp32 partial, scaled once */
 #define MNB_KERNEL_ACC4_I8 4     /* accuracy_level 4: int8 A, int8 MFMA, int32 block dots */
 #define MNB_KERNEL_GEMV_STREAM 5 /* M <= 4: coalesced 16-byte-chunk streaming GEMV (fp16 or fp32) */

@@ -60,6 +60,7 @@ HIP_SOURCES = [
     CSRC / "kernels" / "mnb_gemv_stream_b4.hip",
     CSRC / "kernels" / "mnb_gemv_stream_b8.hip",
     CSRC / "kernels" / "mnb_gemv_f32.hip",
+    CSRC / "kernels" / "mnb_gemm_f32.hip",
     CSRC / "kernels" / "mnb_calibrate.hip",
     CSRC / "kernels" / "mnb_qmoe.hip",
     CSRC / "kernels" / "mnb_rmsnorm.hip",

@@ -38,6 +38,7 @@ template <int BITS>
 __host__ __device__ constexpr int f32_chunk_stride() { return 4 * (128 / BITS) + 16; }
 
 constexpr int kF32MaxCpl = 8;
+constexpr int64_t kF32MaxRows = 64;                    // row-tiles of up to four rows above that
 constexpr int64_t kF32MaxLds = 96 * 1024;
 constexpr int kF32AU = 2;                               // 16-byte activation units per thread and batch
 
@@ -277,19 +278,28 @@ hipError_t f32_bs(const StreamConfig& c, int bs, const float* A, const uint8_t* 
 }  // namespace
 
 // The fp16 streaming GEMV's launch shape (lane-group width, chunks per lane, wavefronts per
-// workgroup, row-tile) with this kernel's LDS: the staged fp32 chunks of the row-tile.
+// workgroup) for a row-tile of up to four rows -- the largest whose staged fp32 chunks fit the
+// LDS cap -- and this kernel's LDS.  Above one tile the grid's y dimension walks the row-tiles,
+// each streaming the weights again: up to 64 rows, still far fewer weight reads than the
+// generic kernel's (one pass per four rows, every activation element loaded per weight).
 bool gemv_stream_f32_config(int64_t m, int64_t n, int64_t k, int bits, int bs, StreamConfig* out) {
-    if (!gemv_stream_supported(m, n, k, bits, bs)) return false;
-    StreamConfig c = gemv_stream_config(m, n, k, bits, bs);
+    if (m < 1 || m > kF32MaxRows) return false;
     const int64_t wpc = 128 / bits;
-    const int64_t cpc = k / wpc;
-    if (c.u != 1 || c.cpl < 1 || c.cpl > kF32MaxCpl || (int64_t)c.g * c.cpl < cpc) return false;
-    const int64_t cols = (int64_t)c.waves_per_group * (64 / c.g);
-    c.groups = (n + cols - 1) / cols;
-    c.lds = c.mr * cpc * (bits == 4 ? f32_chunk_stride<4>() : f32_chunk_stride<8>());
-    if (c.lds > kF32MaxLds || c.groups > 0x7fffffff) return false;
-    if (out) *out = c;
-    return true;
+    for (int64_t mr = std::min<int64_t>(m, 4); mr >= 1; --mr) {
+        if (!gemv_stream_supported(mr, n, k, bits, bs)) continue;
+        StreamConfig c = gemv_stream_config(mr, n, k, bits, bs);
+        const int64_t cpc = k / wpc;
+        if (c.u != 1 || c.cpl < 1 || c.cpl > kF32MaxCpl || (int64_t)c.g * c.cpl < cpc) return false;
+        const int64_t cols = (int64_t)c.waves_per_group * (64 / c.g);
+        c.groups = (n + cols - 1) / cols;
+        c.lds = c.mr * cpc * (bits == 4 ? f32_chunk_stride<4>() : f32_chunk_stride<8>());
+        if (c.groups > 0x7fffffff) return false;
+        if (c.lds > kF32MaxLds) continue;
+        if ((m + c.mr - 1) / c.mr > 65535) return false;
+        if (out) *out = c;
+        return true;
+    }
+    return false;
 }
 
 hipError_t launch_gemv_stream_f32(const void* a, const uint8_t* b, const void* s, const uint8_t* z,

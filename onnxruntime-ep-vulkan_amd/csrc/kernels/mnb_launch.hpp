@@ -64,6 +64,12 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
 hipError_t launch_gemv_stream(const void* a, const uint8_t* b, const void* s, const uint8_t* z,
                               void* y, int64_t m, int64_t n, int64_t k, int bits, int bs,
                               hipStream_t stream);
+// fp32 prefill (mnb_gemm_f32.hip): fp32 MFMA GEMM, 128 x 128 tiles of 4 wavefronts, K % 32 == 0.
+bool gemm_f32_supported(int64_t m, int64_t n, int64_t k, int bits, int bs);
+size_t gemm_f32_lds();
+hipError_t launch_gemm_f32(const void* a, const uint8_t* b, const void* s, const uint8_t* z,
+                           void* y, int64_t m, int64_t n, int64_t k, int bits, int bs,
+                           hipStream_t stream);
 // fp32 activations, scales and output (mnb_gemv_f32.hip): the fp16 launch shape with fp32 staging;
 // false when the shape is outside what the kernel is compiled for.
 bool gemv_stream_f32_config(int64_t m, int64_t n, int64_t k, int bits, int bs, StreamConfig* out);

@@ -226,16 +226,28 @@ static int plan_search(const mnb_problem* p, mnb_plan_info* out) {
     mnb::StreamConfig c32{};
     const bool stream32 = !f16 && mnb::gemv_stream_f32_config(p->m, p->n, p->k, p->bits,
                                                               p->block_size, &c32);
+    // fp32 activations above that: the fp32 MFMA GEMM over weights dequantised into LDS
+    const bool gemm32 = !f16 && mnb::gemm_f32_supported(p->m, p->n, p->k, p->bits, p->block_size);
     if (stream32) kern = MNB_KERNEL_GEMV_STREAM;
+    else if (gemm32) kern = MNB_KERNEL_GEMM_MFMA;
     const int forced = forced_kernel();
     if (forced == MNB_KERNEL_GENERIC) kern = MNB_KERNEL_GENERIC;
     if (forced == MNB_KERNEL_GEMV_MFMA && fast) kern = MNB_KERNEL_GEMV_MFMA;
     if (forced == MNB_KERNEL_GEMV_STREAM && (stream || stream32)) kern = MNB_KERNEL_GEMV_STREAM;
-    if (forced == MNB_KERNEL_GEMM_MFMA && gemm) kern = MNB_KERNEL_GEMM_MFMA;
+    if (forced == MNB_KERNEL_GEMM_MFMA && (gemm || gemm32)) kern = MNB_KERNEL_GEMM_MFMA;
     if (forced == MNB_KERNEL_GROUP_MFMA && group) kern = MNB_KERNEL_GROUP_MFMA;
     if (forced == MNB_KERNEL_STRIP_MFMA && strip) kern = MNB_KERNEL_STRIP_MFMA;
     if (forced == MNB_KERNEL_BATCH_STREAM && batch) kern = MNB_KERNEL_BATCH_STREAM;
     out->kernel = kern;
+    if (kern == MNB_KERNEL_GEMM_MFMA && !f16) {
+        out->waves_per_group = 4;                        // 128 x 128 tiles, no K split
+        out->tile_n = 128;
+        out->tile_m = 128;
+        out->grid_x = ((p->m + 127) / 128) * ((p->n + 127) / 128);
+        out->grid_y = 1;
+        out->workspace_bytes = 0;
+        return MNB_OK;
+    }
     if (kern == MNB_KERNEL_GEMM_MFMA) {
         const mnb::GemmConfig c = mnb::gemm_config(p->m, p->n, p->k);
         out->waves_per_group = 8;
@@ -380,7 +392,7 @@ static int matmul_impl(const mnb_problem* p, const void* a, const uint8_t* b,
     // case of the same form.
     if (kern == MNB_KERNEL_STRIP_MFMA && !mnb::strip_gemv_aligned(a, b, scales, zero_points, false))
         kern = MNB_KERNEL_GROUP_MFMA;
-    if (kern == MNB_KERNEL_GEMM_MFMA &&
+    if (kern == MNB_KERNEL_GEMM_MFMA && p->dtype == MNB_DTYPE_F16 &&
         (!aligned(scales, 4) || !aligned(zero_points, 4) ||
          !mnb::gemm_supported(p->m, p->n, p->k, p->bits, p->block_size, zero_points != nullptr))) {
         if (mnb::group_gemv_supported(p->k, p->bits, p->block_size))
@@ -414,8 +426,11 @@ static int matmul_impl(const mnb_problem* p, const void* a, const uint8_t* b,
         e = mnb::launch_group_gemv_f16(a, nullptr, nullptr, 1, p->m, b, scales, zero_points, y,
                                        p->m, p->n, p->k, p->bits, p->block_size, st);
     } else if (kern == MNB_KERNEL_GEMM_MFMA) {
-        e = mnb::launch_gemm(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
-                             p->block_size, st, workspace, workspace_bytes);
+        e = p->dtype == MNB_DTYPE_F16
+                ? mnb::launch_gemm(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
+                                   p->block_size, st, workspace, workspace_bytes)
+                : mnb::launch_gemm_f32(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,
+                                       p->block_size, st);
     } else if (kern == MNB_KERNEL_GEMV_STREAM) {
         e = p->dtype == MNB_DTYPE_F16
                 ? mnb::launch_gemv_stream(a, b, scales, zero_points, y, p->m, p->n, p->k, p->bits,

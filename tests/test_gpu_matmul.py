@@ -191,7 +191,11 @@ F32_SHAPES = [(1, 40, 256, 4, 32, True), (6, 24, 512, 8, 64, False), (3, 17, 128
               (9, 50, 1024, 4, 128, False),
               (1, 9216, 3072, 4, 32, True), (1, 3072, 8192, 4, 32, True), (2, 3072, 8192, 4, 32, True),
               (4, 1000, 3072, 4, 32, False), (3, 16384, 3072, 4, 32, True), (1, 640, 2048, 8, 64, True),
-              (2, 500, 1024, 8, 16, False), (4, 300, 4096, 4, 128, True), (1, 2880, 2880, 4, 16, False)]
+              (2, 500, 1024, 8, 16, False), (4, 300, 4096, 4, 128, True), (1, 2880, 2880, 4, 16, False),
+              (4, 3072, 8192, 4, 32, True), (16, 3072, 3072, 4, 32, True), (37, 700, 2048, 8, 32, True),
+              (64, 256, 8192, 4, 64, False), (70, 48, 512, 4, 32, True),
+              (256, 3072, 3072, 4, 32, True), (130, 1000, 2048, 8, 64, False), (300, 257, 1024, 4, 16, True),
+              (2048, 384, 3072, 4, 32, False), (97, 8192, 512, 8, 128, True)]
 
 
 @pytest.mark.parametrize("M,N,K,bits,bs,zp", F32_SHAPES)
@@ -200,9 +204,21 @@ def test_random_parity_f32(cuda, M, N, K, bits, bs, zp):
     inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=7 + M, a_dtype=np.float32)
     kern = mnb.plan(mnb.problem(M, N, K, bits, bs, zp, mnb.DTYPE_F32)).kernel
     print(f"[gpu] parity f32 M={M} N={N} K={K} bits={bits} bs={bs} zp={zp} kernel {kern}", flush=True)
-    if M <= 3:
-        assert kern == mnb.KERNEL_GEMV_STREAM
+    assert kern == (mnb.KERNEL_GEMV_STREAM if M <= 64 else mnb.KERNEL_GEMM_MFMA)
     y = _run(inp, N, K, bits, bs, cuda)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
+    assert orc.max_rel_err_significant(y, ref) <= F32_TOL
+    assert orc.max_err_rms_normalised(y, ref) <= F32_TOL
+
+
+@pytest.mark.parametrize("M,N,K,bits,bs,zp", [(6, 24, 512, 8, 64, False), (9, 50, 1024, 4, 128, False),
+                                              (2, 40, 256, 4, 16, True)])
+def test_generic_parity_f32(cuda, M, N, K, bits, bs, zp):
+    """The generic kernel's fp32 form (forced: the planner sends these shapes to the streaming
+    GEMV), against the same oracle and bar."""
+    inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=17 + M, a_dtype=np.float32)
+    print(f"[gpu] parity f32 generic M={M} N={N} K={K}", flush=True)
+    y = _run(inp, N, K, bits, bs, cuda, "generic")
     ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
     assert orc.max_rel_err_significant(y, ref) <= F32_TOL
     assert orc.max_err_rms_normalised(y, ref) <= F32_TOL

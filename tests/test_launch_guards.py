@@ -138,29 +138,35 @@ def test_decode_routing_by_rows_and_strips():
 
 
 def test_fp32_decode_routing():
-    """fp32 activations at one to four rows take the fp32 streaming GEMV (reported as the
-    streaming kernel, with the fp16 launch shape) wherever its staged rows fit in LDS; more rows,
-    or four rows of K = 8192 (147 KB of fp32 staging), stay on the generic kernel."""
+    """fp32 activations at 1-64 rows take the fp32 streaming GEMV (reported as the streaming
+    kernel): row-tiles of the most rows, up to four, whose staged fp32 chunks fit in 96 KB of
+    LDS, each tile with the fp16 kernel's launch shape for that row count; above 64 rows the fp32
+    MFMA GEMM."""
     import mnb
 
     f32 = mnb.DTYPE_F32
     for k, n in ((3072, 9216), (3072, 3072), (3072, 16384), (8192, 3072)):
-        for m in (1, 2, 3):
+        for m in (1, 2, 3, 4, 5, 8, 16, 33, 64):
             for bits in (4, 8):
                 for bs in (16, 32, 64, 128):
                     info = mnb.plan(mnb.problem(m, n, k, bits, bs, True, f32))
                     wpc = 128 // bits                    # weights per staged 16-byte chunk
-                    if m * (k // wpc) * (4 * wpc + 16) > 96 * 1024:
-                        assert info.kernel == mnb.KERNEL_GENERIC, (m, n, k, bits, bs)
-                        continue
+                    mr = max(r for r in range(1, min(m, 4) + 1)
+                             if r * (k // wpc) * (4 * wpc + 16) <= 96 * 1024)
                     assert info.kernel == mnb.KERNEL_GEMV_STREAM, (m, n, k, bits, bs)
+                    assert (info.tile_m, info.grid_y) == (mr, -(-m // mr)), (m, n, k, bits, bs)
                     assert 64 * info.waves_per_group <= 1024
-                    f16 = mnb.plan(mnb.problem(m, n, k, bits, bs, True))
-                    assert (info.waves_per_group, info.tile_n, info.grid_x) == \
-                        (f16.waves_per_group, f16.tile_n, f16.grid_x), (m, n, k, bits, bs)
-    assert mnb.plan(mnb.problem(4, 9216, 3072, 4, 32, True, f32)).kernel == mnb.KERNEL_GEMV_STREAM
-    assert mnb.plan(mnb.problem(4, 3072, 8192, 4, 32, True, f32)).kernel == mnb.KERNEL_GENERIC
-    assert mnb.plan(mnb.problem(5, 3072, 3072, 4, 32, True, f32)).kernel == mnb.KERNEL_GENERIC
+                    f16 = mnb.plan(mnb.problem(mr, n, k, bits, bs, True))
+                    if f16.kernel == mnb.KERNEL_GEMV_STREAM:   # (at four rows fp16 may batch)
+                        assert (info.waves_per_group, info.tile_n, info.grid_x) == \
+                            (f16.waves_per_group, f16.tile_n, f16.grid_x), (m, n, k, bits, bs)
+    # above 64 rows the fp32 MFMA GEMM: 128 x 128 tiles of four wavefronts, no workspace
+    for m in (65, 256, 2048):
+        info = mnb.plan(mnb.problem(m, 8192, 3072, 4, 32, True, f32))
+        assert info.kernel == mnb.KERNEL_GEMM_MFMA and info.waves_per_group == 4
+        assert info.grid_x == -(-m // 128) * 64 and info.workspace_bytes == 0
+    # K not a multiple of the GEMM's 32-k step: the generic kernel
+    assert mnb.plan(mnb.problem(65, 64, 48, 4, 16, True, f32)).kernel == mnb.KERNEL_GENERIC
 
 
 # (M, N, K, bs, zp) -> (quads per wavefront R, wavefronts per workgroup) of the batched decode
