@@ -64,9 +64,10 @@ StreamConfig gemv_stream_config(int64_t m, int64_t n, int64_t k, int bits, int b
 hipError_t launch_gemv_stream(const void* a, const uint8_t* b, const void* s, const uint8_t* z,
                               void* y, int64_t m, int64_t n, int64_t k, int bits, int bs,
                               hipStream_t stream);
-// fp32 prefill (mnb_gemm_f32.hip): fp32 MFMA GEMM, 128 x 128 tiles of 4 wavefronts, K % 32 == 0.
+// fp32 prefill (mnb_gemm_f32.hip): fp32 MFMA GEMM, 128 (or 64) x 128 tiles of 4 wavefronts,
+// K % 32 == 0.
 bool gemm_f32_supported(int64_t m, int64_t n, int64_t k, int bits, int bs);
-size_t gemm_f32_lds();
+int gemm_f32_tile_rows(int64_t m, int64_t n);       // 128, or 64 when 128-row tiles under-fill
 hipError_t launch_gemm_f32(const void* a, const uint8_t* b, const void* s, const uint8_t* z,
                            void* y, int64_t m, int64_t n, int64_t k, int bits, int bs,
                            hipStream_t stream);

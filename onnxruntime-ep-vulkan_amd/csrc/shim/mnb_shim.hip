@@ -240,10 +240,11 @@ static int plan_search(const mnb_problem* p, mnb_plan_info* out) {
     if (forced == MNB_KERNEL_BATCH_STREAM && batch) kern = MNB_KERNEL_BATCH_STREAM;
     out->kernel = kern;
     if (kern == MNB_KERNEL_GEMM_MFMA && !f16) {
-        out->waves_per_group = 4;                        // 128 x 128 tiles, no K split
+        const int bm = mnb::gemm_f32_tile_rows(p->m, p->n);
+        out->waves_per_group = 4;                        // bm x 128 tiles, no K split
         out->tile_n = 128;
-        out->tile_m = 128;
-        out->grid_x = ((p->m + 127) / 128) * ((p->n + 127) / 128);
+        out->tile_m = bm;
+        out->grid_x = ((p->m + bm - 1) / bm) * ((p->n + 127) / 128);
         out->grid_y = 1;
         out->workspace_bytes = 0;
         return MNB_OK;

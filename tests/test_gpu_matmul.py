@@ -195,7 +195,8 @@ F32_SHAPES = [(1, 40, 256, 4, 32, True), (6, 24, 512, 8, 64, False), (3, 17, 128
               (4, 3072, 8192, 4, 32, True), (16, 3072, 3072, 4, 32, True), (37, 700, 2048, 8, 32, True),
               (64, 256, 8192, 4, 64, False), (70, 48, 512, 4, 32, True),
               (256, 3072, 3072, 4, 32, True), (130, 1000, 2048, 8, 64, False), (300, 257, 1024, 4, 16, True),
-              (2048, 384, 3072, 4, 32, False), (97, 8192, 512, 8, 128, True)]
+              (2048, 384, 3072, 4, 32, False), (97, 8192, 512, 8, 128, True),
+              (512, 8192, 512, 4, 32, True), (1024, 4096, 1024, 8, 64, False)]   # 128-row tiles
 
 
 @pytest.mark.parametrize("M,N,K,bits,bs,zp", F32_SHAPES)

@@ -160,11 +160,12 @@ def test_fp32_decode_routing():
                     if f16.kernel == mnb.KERNEL_GEMV_STREAM:   # (at four rows fp16 may batch)
                         assert (info.waves_per_group, info.tile_n, info.grid_x) == \
                             (f16.waves_per_group, f16.tile_n, f16.grid_x), (m, n, k, bits, bs)
-    # above 64 rows the fp32 MFMA GEMM: 128 x 128 tiles of four wavefronts, no workspace
-    for m in (65, 256, 2048):
+    # above 64 rows the fp32 MFMA GEMM: 128 x 128 tiles of four wavefronts (64 x 128 where the
+    # 128-row tiles would number fewer than the 256 CUs), no workspace
+    for m, bm in ((65, 64), (256, 64), (512, 128), (2048, 128)):
         info = mnb.plan(mnb.problem(m, 8192, 3072, 4, 32, True, f32))
         assert info.kernel == mnb.KERNEL_GEMM_MFMA and info.waves_per_group == 4
-        assert info.grid_x == -(-m // 128) * 64 and info.workspace_bytes == 0
+        assert info.tile_m == bm and info.grid_x == -(-m // bm) * 64 and info.workspace_bytes == 0
     # K not a multiple of the GEMM's 32-k step: the generic kernel
     assert mnb.plan(mnb.problem(65, 64, 48, 4, 16, True, f32)).kernel == mnb.KERNEL_GENERIC
 
