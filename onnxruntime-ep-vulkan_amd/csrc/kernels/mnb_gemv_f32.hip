@@ -16,11 +16,12 @@
 // distinct multiples of 4 for i = 0..15).
 //
 // Arithmetic.  The reference forms, per (column, quant block), the fp32 sum of a * (q - zp) and
-// scales it once (q_gemv.comp:571-579).  Here a chunk's weights become fp32 by a byte-to-float
-// conversion (exact), each product is one fp32 FMA, and the chunk's partial over a block segment
-// is recovered as  sum a*q - zp * sum a  (the activation sum from the staging) and scaled by the
-// block's scale in fp32: one conversion and one FMA per weight.  The G lane accumulators of a
-// column are summed by a fixed butterfly (run-to-run deterministic).
+// scales it once (q_gemv.comp:571-579).  Here the weights enter fp32 FMAs as fp16 subnormals
+// q * 2^-24 (one AND per pair), which v_fma_mix_f32 reads as exact fp32 operands: one mixed FMA
+// per weight, no conversion.  The chunk's partial over a block segment is recovered as
+// sum a*q - zp * sum a  (the activation sum from the staging) and scaled by the block's scale in
+// fp32.  The G lane accumulators of a column are summed by a fixed butterfly (run-to-run
+// deterministic).
 #include <algorithm>
 
 #include "mnb_common.hpp"
@@ -41,31 +42,6 @@ constexpr int kF32MaxCpl = 8;
 constexpr int64_t kF32MaxRows = 64;                    // row-tiles of up to four rows above that
 constexpr int64_t kF32MaxLds = 96 * 1024;
 constexpr int kF32AU = 2;                               // 16-byte activation units per thread and batch
-
-// Weight k of a chunk (natural order) as fp32, from its four dwords: int4 weight 8d + 2b + h is
-// nibble h of byte b of dword d; int8 weight 4d + b is byte b.
-template <int BITS>
-__device__ __forceinline__ void chunk_to_f32(const u32x4 w, float* q) {
-    const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if constexpr (BITS == 4) {
-            // the masks stay whole dwords (opaque to the compiler), so each weight is one
-            // v_cvt_f32_ubyteN instead of a bit-field extract plus a conversion
-            uint32_t lo = d[i] & 0x0F0F0F0Fu;
-            uint32_t hi = (d[i] >> 4) & 0x0F0F0F0Fu;
-            asm volatile("" : "+v"(lo), "+v"(hi));
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                q[8 * i + 2 * b] = (float)((lo >> (8 * b)) & 0xFFu);
-                q[8 * i + 2 * b + 1] = (float)((hi >> (8 * b)) & 0xFFu);
-            }
-        } else {
-#pragma unroll
-            for (int b = 0; b < 4; ++b) q[4 * i + b] = (float)((d[i] >> (8 * b)) & 0xFFu);
-        }
-    }
-}
 
 template <int BITS, int BS, bool HAS_ZP, int MR, int CPL>
 __global__ void __launch_bounds__(kStreamMaxThreads)
@@ -182,8 +158,11 @@ gemv_stream_f32(const float* __restrict__ A, const uint8_t* __restrict__ B,
     for (int j = 0; j < CPL; ++j) {
         const bool live = gi + j * G < cpc;
         const int c = chunk_of(j);
-        float q[WPC];
-        chunk_to_f32<BITS>(bw[j], q);
+        // The chunk's weights as fp16 subnormal pairs q * 2^-24 (one AND each), read by
+        // v_fma_mix_f32 as exact fp32 operands: int4 dword d gives (w[8d], w[8d+4]) and, masked in
+        // place at 16 q * 2^-24, (w[8d+1], w[8d+5]); w >> 8 the same for 8d+2 / 8d+6 and
+        // 8d+3 / 8d+7.  int8: bytes (0, 2) and, after a shift, (1, 3).
+        const uint32_t wd[4] = {bw[j].x, bw[j].y, bw[j].z, bw[j].w};
 #pragma unroll
         for (int r = 0; r < MR; ++r) {
             const uint8_t* src = smem + (r * cpc + c) * CST;
@@ -199,9 +178,32 @@ gemv_stream_f32(const float* __restrict__ A, const uint8_t* __restrict__ B,
             const float* asum = reinterpret_cast<const float*>(src + 4 * WPC);
 #pragma unroll
             for (int s = 0; s < SEGS; ++s) {
-                float p = 0.f;
+                float t = 0.f, t16 = 0.f;
 #pragma unroll
-                for (int e = s * WPS; e < (s + 1) * WPS; ++e) p = __builtin_fmaf(a[e], q[e], p);
+                for (int d = 4 * s / SEGS; d < 4 * (s + 1) / SEGS; ++d) {
+                    if constexpr (BITS == 4) {
+                        const uint32_t wh = wd[d] >> 8;
+                        const f16x2 p0 = as_h2(wd[d] & 0x000F000Fu), p1 = as_h2(wd[d] & 0x00F000F0u);
+                        const f16x2 p2 = as_h2(wh & 0x000F000Fu), p3 = as_h2(wh & 0x00F000F0u);
+                        t = __builtin_fmaf(a[8 * d + 0], (float)p0.x, t);
+                        t = __builtin_fmaf(a[8 * d + 4], (float)p0.y, t);
+                        t16 = __builtin_fmaf(a[8 * d + 1], (float)p1.x, t16);
+                        t16 = __builtin_fmaf(a[8 * d + 5], (float)p1.y, t16);
+                        t = __builtin_fmaf(a[8 * d + 2], (float)p2.x, t);
+                        t = __builtin_fmaf(a[8 * d + 6], (float)p2.y, t);
+                        t16 = __builtin_fmaf(a[8 * d + 3], (float)p3.x, t16);
+                        t16 = __builtin_fmaf(a[8 * d + 7], (float)p3.y, t16);
+                    } else {
+                        const f16x2 p0 = as_h2(wd[d] & 0x00FF00FFu);
+                        const f16x2 p1 = as_h2((wd[d] >> 8) & 0x00FF00FFu);
+                        t = __builtin_fmaf(a[4 * d + 0], (float)p0.x, t);
+                        t = __builtin_fmaf(a[4 * d + 2], (float)p0.y, t);
+                        t = __builtin_fmaf(a[4 * d + 1], (float)p1.x, t);
+                        t = __builtin_fmaf(a[4 * d + 3], (float)p1.y, t);
+                    }
+                }
+                // sum a*q over the segment: 2^24 t + 2^20 t16 (exact power-of-two scalings)
+                float p = __builtin_fmaf(t16, 0.0625f, t) * 16777216.0f;
                 p = __builtin_fmaf(-zf[j][s], asum[s], p);
                 acc[r] = __builtin_fmaf(live ? sc[j][s] : 0.f, p, acc[r]);
             }
