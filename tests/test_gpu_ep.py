@@ -151,17 +151,29 @@ def test_weights_as_graph_inputs_are_read_every_call(host):
         _check(y, orc.matmul_nbits(inp["A"], d["B"], d["scales"], d["zp"], N, K, 4, 32), "inputs")
 
 
-def test_fp32_node(host):
-    N, K = 40, 512
-    inp = orc.make_inputs(3, N, K, with_zp=True, seed=11, a_dtype=np.float32)
+@pytest.mark.parametrize("M,N,K,bits,bs,zp", [
+    (3, 40, 512, 4, 32, True),        # fp32 streaming GEMV, one row-tile
+    (1, 3072, 3072, 4, 32, False),    # BASELINE configs[0]'s shape with fp32 activations
+    (24, 300, 1024, 8, 64, True),     # row-tiled fp32 streaming GEMV
+    (200, 512, 2048, 4, 32, True),    # fp32 MFMA GEMM
+])
+def test_fp32_node(host, M, N, K, bits, bs, zp):
+    """fp32 activations through the plugin's Compute: the fp32 kernels the planner takes at each
+    row count, against the oracle at the fp32 bar."""
+    import mnb
+    kern = mnb.plan(mnb.problem(M, N, K, bits, bs, zp, mnb.DTYPE_F32)).kernel
+    print(f"[gpu] ep fp32 M={M} N={N} K={K} bits={bits} bs={bs} zp={zp} kernel {kern}", flush=True)
+    assert kern == (mnb.KERNEL_GEMV_STREAM if M <= 64 else mnb.KERNEL_GEMM_MFMA)
+    inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=11 + M,
+                          a_dtype=np.float32)
     host.reset()
-    a_name, y_name = mh.add_matmul_nbits(host, "mm", inp, N, K, 4, 32, (3, K), a_dtype=np.float32)
+    a_name, y_name = mh.add_matmul_nbits(host, "mm", inp, N, K, bits, bs, (M, K), a_dtype=np.float32)
     host.get_capability()
     assert host.compile() == 0, mh.err()
     host.feed(a_name, inp["A"])
     assert host.compute(0) == 0, mh.err()
-    y = host.fetch(y_name, np.float32, 3 * N)
-    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, 4, 32)
+    y = host.fetch(y_name, np.float32, M * N)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
     assert orc.max_rel_err_significant(y, ref) <= 1e-5
 
 
