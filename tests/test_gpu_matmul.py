@@ -212,6 +212,20 @@ def test_random_parity_f32(cuda, M, N, K, bits, bs, zp):
     assert orc.max_err_rms_normalised(y, ref) <= F32_TOL
 
 
+@pytest.mark.parametrize("M,N,K,bits,bs,zp", [(1, 64, 32768, 4, 32, True), (2, 100, 16384, 8, 32, False)])
+def test_wide_k_parity_f32(cuda, M, N, K, bits, bs, zp):
+    """A few fp32 rows whose staged activations exceed the streaming GEMV's LDS (K = 16-32 K):
+    the planner takes the fp32 GEMM (one 64-row tile) instead."""
+    import mnb
+    assert mnb.plan(mnb.problem(M, N, K, bits, bs, zp, mnb.DTYPE_F32)).kernel == mnb.KERNEL_GEMM_MFMA
+    inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=23 + M, a_dtype=np.float32)
+    print(f"[gpu] parity f32 wide K M={M} N={N} K={K}", flush=True)
+    y = _run(inp, N, K, bits, bs, cuda)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
+    assert orc.max_rel_err_significant(y, ref) <= F32_TOL
+    assert orc.max_err_rms_normalised(y, ref) <= F32_TOL
+
+
 @pytest.mark.parametrize("M,N,K,bits,bs,zp", [(6, 24, 512, 8, 64, False), (9, 50, 1024, 4, 128, False),
                                               (2, 40, 256, 4, 16, True)])
 def test_generic_parity_f32(cuda, M, N, K, bits, bs, zp):
