@@ -38,7 +38,24 @@ constexpr int kBatchMaxWaves = 16;
 // so that the 16 rows' operand reads start in distinct bank groups.
 constexpr int kBatchSlotRow = 256 + 16;
 
-template <int BS, bool HAS_ZP, int R, int S>
+// Eight exact fp16 (q - z) from one dword of the MFMA-native copy (strip_pack with native set):
+// its nibbles hold k0 k2 k4 k6 in bits 0-15 and k1 k3 k5 k7 in bits 16-31, so each pair (k_2p,
+// k_2p+1) sits at one nibble position of the two halves -- (k0, k1), (k4, k5) at bits 0-3 of w
+// and of w >> 8, giving 1024 + q less (1024 + z); (k2, k3), (k6, k7) at bits 4-7, giving
+// 1024 + 16 q, times 1/16, less (64 + z).  One shift, four and-ors and four packed fp16 ops per
+// dword (the ORT layout needs a byte duplicate per pair besides).
+__device__ __forceinline__ f16x8 native_pairs(uint32_t w, f16x2 zlo, f16x2 zhi) {
+    const uint32_t wh = w >> 8;
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    f16x8 r;
+    r.s01 = as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) + zlo;
+    r.s23 = __builtin_elementwise_fma(as_h2(and_or(w, 0x00F000F0u, 0x64006400u)), sixteenth, zhi);
+    r.s45 = as_h2(and_or(wh, 0x000F000Fu, 0x64006400u)) + zlo;
+    r.s67 = __builtin_elementwise_fma(as_h2(and_or(wh, 0x00F000F0u, 0x64006400u)), sixteenth, zhi);
+    return r;
+}
+
+template <int BS, bool HAS_ZP, int R, int S, bool NATIVE>
 __global__ void __launch_bounds__(64 * kBatchMaxWaves)
 batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ Sc,
              const uint8_t* __restrict__ Z, f16* __restrict__ Y, int M, int N, int K,
@@ -118,7 +135,7 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
 #pragma unroll
     for (int t = 0; t < S; ++t) {
         const uint8_t* bc;
-        if (Bs) {
+        if constexpr (NATIVE) {
             const int st = min(strip0 + t, (N + 15) / 16 - 1);
             bc = Bs + (int64_t)st * (K / 128) * 1024 + 64 * nl + 16 * g;
         } else {
@@ -128,7 +145,7 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
 #pragma unroll
         for (int j = 0; j < R; ++j)
             bw[t][j] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4*>(bc + (Bs ? 1024 : 64) * (int64_t)(q0 + j)));
+                reinterpret_cast<const u32x4*>(bc + (NATIVE ? 1024 : 64) * (int64_t)(q0 + j)));
     }
 
     // With several strips, every weight request goes out before the first wait (left to itself
@@ -166,8 +183,10 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
         acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < R; ++j) {
+            // ORT's layout: lane (n, g) holds chunk g of its column, the 4 x 4 dword transpose
+            // gives it dword g of every chunk c; the native copy stores it that way already
             uint32_t v0 = bw[t][j].x, v1 = bw[t][j].y, v2 = bw[t][j].z, v3 = bw[t][j].w;
-            transpose_rows(v0, v1, v2, v3);
+            if constexpr (!NATIVE) transpose_rows(v0, v1, v2, v3);
             const uint32_t wt[4] = {v0, v1, v2, v3};
             f32x4 dot = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -176,12 +195,18 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
                 int z = 8;
                 if constexpr (HAS_ZP)
                     z = (int)((zv[t][(bi + (b0 & 1)) >> 1] >> (((b0 + bi) & 1) * 4)) & 0xFu);
-                const f16x2 zo = zoff4(z);
                 f16x8 bq;
-                bq.s01 = nib_pair<0>(wt[c], zo);
-                bq.s23 = nib_pair<1>(wt[c], zo);
-                bq.s45 = nib_pair<2>(wt[c], zo);
-                bq.s67 = nib_pair<3>(wt[c], zo);
+                if constexpr (NATIVE) {
+                    // (-(1024 + z), -(1024 + z)) and (-(64 + z), -(64 + z)), z in the mantissas
+                    bq = native_pairs(wt[c], as_h2(0xE400E400u + (uint32_t)z * 0x10001u),
+                                      as_h2(0xD400D400u + (uint32_t)z * 0x100010u));
+                } else {
+                    const f16x2 zo = zoff4(z);
+                    bq.s01 = nib_pair<0>(wt[c], zo);
+                    bq.s23 = nib_pair<1>(wt[c], zo);
+                    bq.s45 = nib_pair<2>(wt[c], zo);
+                    bq.s67 = nib_pair<3>(wt[c], zo);
+                }
                 dot = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j][c], bq, dot, 0, 0, 0);
                 if ((c + 1) % CPB == 0) {                // block end: scale it
                     const float sb = (float)__builtin_bit_cast(f16, sv[t][bi]);
@@ -221,14 +246,18 @@ hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b,
     const size_t lds = (size_t)g.waves * S * 64 * sizeof(f32x4) +
                        (size_t)g.waves * 16 * kBatchSlotRow;
     // instantiated for S R <= 8 only (the geometry's register budget)
-#define MNB_BS(R_)                                                                                \
-    if constexpr (S * R_ <= 8) {                                                                  \
+#define MNB_BS_GO(R_, NAT_)                                                                       \
+    {                                                                                             \
         const hipError_t ea = allow_dynamic_lds(                                                  \
-            reinterpret_cast<const void*>(batch_stream<BS, HAS_ZP, R_, S>), lds);                \
+            reinterpret_cast<const void*>(batch_stream<BS, HAS_ZP, R_, S, NAT_>), lds);          \
         if (ea != hipSuccess) return ea;                                                          \
-        hipLaunchKernelGGL((batch_stream<BS, HAS_ZP, R_, S>), grid, block, lds, st,              \
+        hipLaunchKernelGGL((batch_stream<BS, HAS_ZP, R_, S, NAT_>), grid, block, lds, st,        \
                            static_cast<const f16*>(a), b, static_cast<const f16*>(s), z,          \
                            static_cast<f16*>(y), (int)m, (int)n, (int)k, bs_);                    \
+    }
+#define MNB_BS(R_)                                                                                \
+    if constexpr (S * R_ <= 8) {                                                                  \
+        if (bs_) MNB_BS_GO(R_, true) else MNB_BS_GO(R_, false)                                    \
     } else {                                                                                      \
         return hipErrorInvalidValue;                                                              \
     }
@@ -240,6 +269,7 @@ hipError_t batch_go_s(const BatchStreamGeom& g, const void* a, const uint8_t* b,
         default: return hipErrorInvalidValue;
     }
 #undef MNB_BS
+#undef MNB_BS_GO
     return hipGetLastError();
 }
 
@@ -297,15 +327,36 @@ bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamG
 // (a partial last quad) are zero.  One thread per 16-byte piece.
 __global__ void __launch_bounds__(256)
 strip_pack(const u32x4* __restrict__ B, u32x4* __restrict__ dst, int64_t N, int64_t K,
-           int64_t pieces) {
+           int64_t pieces, int native) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= pieces) return;
     const int64_t kq = (K + 127) / 128, ns = (N + 15) / 16, chunks = K / 32;
     const int g = (int)(i & 3), n = (int)((i >> 2) & 15);
     const int64_t q = (i >> 6) % kq, st = (i >> 6) / kq % ns, grp = (i >> 6) / kq / ns;
-    const int64_t col = 16 * st + n, c = 4 * q + g;
-    dst[i] = col < N && c < chunks ? B[((grp * N + col) * (K / 2) + 16 * c) / 16]
-                                   : u32x4{0u, 0u, 0u, 0u};
+    const int64_t col = 16 * st + n;
+    auto chunk = [&](int64_t c) {
+        return col < N && c < chunks ? B[((grp * N + col) * (K / 2) + 16 * c) / 16]
+                                     : u32x4{0u, 0u, 0u, 0u};
+    };
+    if (!native) {
+        dst[i] = chunk(4 * q + g);
+        return;
+    }
+    // MFMA-native: dword c of the piece is dword g of chunk 4 q + c (what the ORT layout's
+    // 4 x 4 transpose across the quad's lanes yields), its nibbles reordered from k0..k7 to
+    // k0 k2 k4 k6 (bits 0-15) and k1 k3 k5 k7 (bits 16-31)
+    u32x4 out;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const u32x4 v = chunk(4 * q + c);
+        const uint32_t d = g == 0 ? v.x : g == 1 ? v.y : g == 2 ? v.z : v.w;
+        uint32_t r = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            r |= ((d >> (4 * k)) & 0xFu) << ((k & 1) ? 16 + 4 * (k >> 1) : 4 * (k >> 1));
+        out[c] = r;
+    }
+    dst[i] = out;
 }
 
 int64_t strip_pack_bytes(int64_t n, int64_t k, int64_t groups) {
@@ -313,7 +364,7 @@ int64_t strip_pack_bytes(int64_t n, int64_t k, int64_t groups) {
 }
 
 hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
-                             hipStream_t st, int64_t groups) {
+                             hipStream_t st, int64_t groups, bool native) {
     if (n < 1 || k < 32 || k % 32 || groups < 1 || reinterpret_cast<uintptr_t>(b) % 16 ||
         reinterpret_cast<uintptr_t>(dst) % 16)
         return hipErrorInvalidValue;
@@ -322,7 +373,7 @@ hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t 
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL(strip_pack, dim3((unsigned)blocks), dim3(256), 0, st,
                        reinterpret_cast<const u32x4*>(b), reinterpret_cast<u32x4*>(dst), n, k,
-                       pieces);
+                       pieces, native ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -225,17 +225,21 @@ struct BatchStreamGeom {
 bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamGeom* out);
 // A and B 16-byte, scales 8-byte, zero points 2-byte aligned.
 bool batch_stream_aligned(const void* a, const uint8_t* b, const void* s, const uint8_t* z);
-// b_strips: the strip-major copy of B (launch_strip_pack), read in place of b when not null.
+// b_strips: the MFMA-native strip-major copy of B (launch_strip_pack with native set), read in
+// place of b when not null.
 hipError_t launch_batch_stream(const BatchStreamGeom& g, const void* a, const uint8_t* b,
                                const void* s, const uint8_t* z, void* y, int64_t m, int64_t n,
                                int64_t k, int bs, hipStream_t stream,
                                const uint8_t* b_strips = nullptr);
 // The strip-major copy of an int4 B [groups][N][K / 2] (K % 32 == 0):
 // [groups][ceil(N / 16)][ceil(K / 128)][16 columns][4 chunks] x 16 bytes, strip_pack_bytes
-// bytes, 16-byte aligned; columns past N and chunks past K zero.
+// bytes, 16-byte aligned; columns past N and chunks past K zero.  native: each 16-byte piece
+// (lane (n, g)) instead holds dword g of the quad's four chunks, nibbles reordered to
+// k0 k2 k4 k6 k1 k3 k5 k7 -- the batched decode kernel's operands without a transpose (read by
+// launch_batch_stream only; the level-4 and MoE copies keep the plain order).
 int64_t strip_pack_bytes(int64_t n, int64_t k, int64_t groups = 1);
 hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
-                             hipStream_t stream, int64_t groups = 1);
+                             hipStream_t stream, int64_t groups = 1, bool native = false);
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                        int bs, void* workspace, hipStream_t stream,

@@ -1272,7 +1272,9 @@ int mnb_weights_prepack(mnb_weights* w, int64_t* bytes) {
         if (e != hipSuccess)
             return fail(MNB_ERR_NOMEM, "hipMalloc(%lld) for the strip-major copy: %s",
                         (long long)nb, hipGetErrorString(e));
-        e = mnb::launch_strip_pack(w->b, d, p.n, p.k, w->s->stream);
+        // level 0: the batched kernel's MFMA-native order; level 4: the plain strip order the
+        // int8 kernel reads
+        e = mnb::launch_strip_pack(w->b, d, p.n, p.k, w->s->stream, 1, p.accuracy_level != 4);
         if (e == hipSuccess) e = hipStreamSynchronize(w->s->stream);
         if (e != hipSuccess) {
             (void)hipFree(d);
