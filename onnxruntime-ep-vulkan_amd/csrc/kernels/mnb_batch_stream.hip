@@ -38,23 +38,6 @@ constexpr int kBatchMaxWaves = 16;
 // so that the 16 rows' operand reads start in distinct bank groups.
 constexpr int kBatchSlotRow = 256 + 16;
 
-// Eight exact fp16 (q - z) from one dword of the MFMA-native copy (strip_pack with native set):
-// its nibbles hold k0 k2 k4 k6 in bits 0-15 and k1 k3 k5 k7 in bits 16-31, so each pair (k_2p,
-// k_2p+1) sits at one nibble position of the two halves -- (k0, k1), (k4, k5) at bits 0-3 of w
-// and of w >> 8, giving 1024 + q less (1024 + z); (k2, k3), (k6, k7) at bits 4-7, giving
-// 1024 + 16 q, times 1/16, less (64 + z).  One shift, four and-ors and four packed fp16 ops per
-// dword (the ORT layout needs a byte duplicate per pair besides).
-__device__ __forceinline__ f16x8 native_pairs(uint32_t w, f16x2 zlo, f16x2 zhi) {
-    const uint32_t wh = w >> 8;
-    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
-    f16x8 r;
-    r.s01 = as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) + zlo;
-    r.s23 = __builtin_elementwise_fma(as_h2(and_or(w, 0x00F000F0u, 0x64006400u)), sixteenth, zhi);
-    r.s45 = as_h2(and_or(wh, 0x000F000Fu, 0x64006400u)) + zlo;
-    r.s67 = __builtin_elementwise_fma(as_h2(and_or(wh, 0x00F000F0u, 0x64006400u)), sixteenth, zhi);
-    return r;
-}
-
 template <int BS, bool HAS_ZP, int R, int S, bool NATIVE>
 __global__ void __launch_bounds__(64 * kBatchMaxWaves)
 batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16* __restrict__ Sc,

@@ -60,6 +60,23 @@ __device__ __forceinline__ f16x2 nib_pair(uint32_t w, f16x2 zo) {
     return __builtin_elementwise_fma(as_h2(t), mul, zo);
 }
 
+// Eight exact fp16 (q - z) from one dword of the MFMA-native strip copy (launch_strip_pack with native set):
+// its nibbles hold k0 k2 k4 k6 in bits 0-15 and k1 k3 k5 k7 in bits 16-31, so each pair (k_2p,
+// k_2p+1) sits at one nibble position of the two halves -- (k0, k1), (k4, k5) at bits 0-3 of w
+// and of w >> 8, giving 1024 + q less (1024 + z); (k2, k3), (k6, k7) at bits 4-7, giving
+// 1024 + 16 q, times 1/16, less (64 + z).  One shift, four and-ors and four packed fp16 ops per
+// dword (the ORT layout needs a byte duplicate per pair besides).
+__device__ __forceinline__ f16x8 native_pairs(uint32_t w, f16x2 zlo, f16x2 zhi) {
+    const uint32_t wh = w >> 8;
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    f16x8 r;
+    r.s01 = as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) + zlo;
+    r.s23 = __builtin_elementwise_fma(as_h2(and_or(w, 0x00F000F0u, 0x64006400u)), sixteenth, zhi);
+    r.s45 = as_h2(and_or(wh, 0x000F000Fu, 0x64006400u)) + zlo;
+    r.s67 = __builtin_elementwise_fma(as_h2(and_or(wh, 0x00F000F0u, 0x64006400u)), sixteenth, zhi);
+    return r;
+}
+
 // Eight fp16 dequantised weights (natural order) from one dword of 4-bit weights.
 __device__ __forceinline__ f16x8 dequant8_4b(uint32_t w, f16x2 zo, f16x2 s2) {
     const f16x2 p0 = nib_pair<0>(w, zo) * s2;

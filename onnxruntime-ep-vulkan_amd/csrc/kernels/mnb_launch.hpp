@@ -235,8 +235,9 @@ hipError_t launch_batch_stream(const BatchStreamGeom& g, const void* a, const ui
 // [groups][ceil(N / 16)][ceil(K / 128)][16 columns][4 chunks] x 16 bytes, strip_pack_bytes
 // bytes, 16-byte aligned; columns past N and chunks past K zero.  native: each 16-byte piece
 // (lane (n, g)) instead holds dword g of the quad's four chunks, nibbles reordered to
-// k0 k2 k4 k6 k1 k3 k5 k7 -- the batched decode kernel's operands without a transpose (read by
-// launch_batch_stream only; the level-4 and MoE copies keep the plain order).
+// k0 k2 k4 k6 k1 k3 k5 k7 -- the fp16 MFMA operands without a transpose (the level-0 copies
+// read by launch_batch_stream and the QMoE expert copies read by the fp16 strip GEMV; the
+// level-4 copies read by the int8 kernel keep the plain order).
 int64_t strip_pack_bytes(int64_t n, int64_t k, int64_t groups = 1);
 hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
                              hipStream_t stream, int64_t groups = 1, bool native = false);

@@ -88,7 +88,8 @@ struct LdsCopy {
 }  // namespace
 
 // SWIGLU: the stored tile is SwiGLU of its interleaved (gate, linear) column pairs (StripSwiglu).
-template <bool I8, int BS, bool HAS_ZP, int QW, bool SWIGLU>
+// NATIVE (fp16 only): Bs is the MFMA-native strip copy (no lane transpose, reordered nibbles).
+template <bool I8, int BS, bool HAS_ZP, int QW, bool SWIGLU, bool NATIVE>
 __global__ void __launch_bounds__(strip_max_threads(I8, BS, QW) ? strip_max_threads(I8, BS, QW) : 256)
 strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
            const int32_t* __restrict__ row_index,
@@ -311,7 +312,7 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
         for (int j = 0; j < QW; ++j) {
             if (j >= q_n) break;                         // wave-uniform
             uint32_t v0 = buf[j].x, v1 = buf[j].y, v2 = buf[j].z, v3 = buf[j].w;
-            transpose_rows(v0, v1, v2, v3);
+            if constexpr (!NATIVE) transpose_rows(v0, v1, v2, v3);
             const uint32_t wt[4] = {v0, v1, v2, v3};
             if constexpr (!I8) {
                 f32x4 d = {0.f, 0.f, 0.f, 0.f};
@@ -321,12 +322,17 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
                     const int blk = min((32 * c) / BS, bpc - 1);
                     int z = 8;
                     if constexpr (HAS_ZP) z = (int)((lz[blk >> 1] >> ((blk & 1) * 4)) & 0xFu);
-                    const f16x2 zo = zoff4(z);
                     f16x8 bop;
-                    bop.s01 = nib_pair<0>(wt[t], zo);
-                    bop.s23 = nib_pair<1>(wt[t], zo);
-                    bop.s45 = nib_pair<2>(wt[t], zo);
-                    bop.s67 = nib_pair<3>(wt[t], zo);
+                    if constexpr (NATIVE) {
+                        bop = native_pairs(wt[t], as_h2(0xE400E400u + (uint32_t)z * 0x10001u),
+                                           as_h2(0xD400D400u + (uint32_t)z * 0x100010u));
+                    } else {
+                        const f16x2 zo = zoff4(z);
+                        bop.s01 = nib_pair<0>(wt[t], zo);
+                        bop.s23 = nib_pair<1>(wt[t], zo);
+                        bop.s45 = nib_pair<2>(wt[t], zo);
+                        bop.s67 = nib_pair<3>(wt[t], zo);
+                    }
                     d = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[j][t], bop, d, 0, 0, 0);
                     if ((t + 1) % CPB == 0) {            // block end: scale its partial once
                         const float sc = (float)ls[blk];
@@ -524,7 +530,10 @@ hipError_t strip_go(const StripGeom& g, const void* a, const float* a_scale,
     if constexpr (strip_max_threads(I8, BS, QW) == 0 || (SWIGLU && (I8 || HAS_ZP))) {
         return hipErrorInvalidValue;                     // not instantiated (see above)
     } else {
-    auto kern = strip_gemv<I8, BS, HAS_ZP, QW, SWIGLU>;
+    // the fp16 path reads a strip copy in the MFMA-native order (the only copies passed to it
+    // are the QMoE experts', packed that way); the int8 path is never given one
+    auto kern = !I8 && bs_ ? strip_gemv<I8, BS, HAS_ZP, QW, SWIGLU, !I8>
+                           : strip_gemv<I8, BS, HAS_ZP, QW, SWIGLU, false>;
     if (g.lds > 80 * 1024 || 64 * g.waves > strip_max_threads(I8, BS, QW))
         return hipErrorInvalidValue;
     const hipError_t ea = allow_dynamic_lds(reinterpret_cast<const void*>(kern), g.lds);

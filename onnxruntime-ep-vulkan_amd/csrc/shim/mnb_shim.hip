@@ -1379,8 +1379,9 @@ int mnb_qmoe_weights_prepack(mnb_qmoe_weights* w, int64_t* bytes) {
         if (e != hipSuccess)
             return fail(MNB_ERR_NOMEM, "hipMalloc(%lld) for the strip-major fc%d: %s",
                         (long long)nb, f + 1, hipGetErrorString(e));
+        // the MFMA-native order the fused QMoE's fp16 strip GEMV reads
         e = mnb::launch_strip_pack(static_cast<const uint8_t*>(w->buf[3 * f]), d, n[f], kk[f],
-                                   w->s->stream, p.num_experts);
+                                   w->s->stream, p.num_experts, true);
         if (e == hipSuccess) e = hipStreamSynchronize(w->s->stream);
         if (e != hipSuccess) {
             (void)hipFree(d);
