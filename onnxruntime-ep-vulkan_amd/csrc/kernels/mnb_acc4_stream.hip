@@ -38,7 +38,9 @@ namespace {
 constexpr int acc4s_max_waves(int r) { return r == 8 ? 8 : 16; }
 constexpr size_t kAcc4sMaxLds = 160 * 1024;
 
-template <int BS, bool HAS_ZP, int R>
+// MFMA: Bs is the strip copy in the int8 MFMA order (launch_strip_pack kStripMfmaI8: each lane's
+// 16 bytes are its operand dwords of the quad's four chunks, no lane transpose).
+template <int BS, bool HAS_ZP, int R, bool MFMA>
 __global__ void __launch_bounds__(64 * acc4s_max_waves(R))
 acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
             const uint8_t* __restrict__ B, const f16* __restrict__ Sc,
@@ -165,7 +167,7 @@ acc4_stream(const int8_t* __restrict__ qa, const float* __restrict__ a_scale,
         const i32x2 aq[4] = {i32x2{(int32_t)a01.x, (int32_t)a01.y}, i32x2{(int32_t)a01.z, (int32_t)a01.w},
                              i32x2{(int32_t)a23.x, (int32_t)a23.y}, i32x2{(int32_t)a23.z, (int32_t)a23.w}};
         uint32_t v0 = bw[j].x, v1 = bw[j].y, v2 = bw[j].z, v3 = bw[j].w;
-        transpose_rows(v0, v1, v2, v3);
+        if constexpr (!MFMA) transpose_rows(v0, v1, v2, v3);
         const uint32_t wt[4] = {v0, v1, v2, v3};
         i32x2 bq[4];
 #pragma unroll
@@ -228,7 +230,7 @@ hipError_t acc4s_go(const Acc4StreamGeom& g, const int8_t* qa, const float* sa, 
     const dim3 block((unsigned)(64 * g.waves), 1, 1);
 #define MNB_A4S(R_)                                                                               \
     do {                                                                                          \
-        auto kern = acc4_stream<BS, HAS_ZP, R_>;                                                  \
+        auto kern = bs_ ? acc4_stream<BS, HAS_ZP, R_, true> : acc4_stream<BS, HAS_ZP, R_, false>;\
         const hipError_t ea = allow_dynamic_lds(reinterpret_cast<const void*>(kern), g.lds);     \
         if (ea != hipSuccess) return ea;                                                          \
         hipLaunchKernelGGL(kern, grid, block, g.lds, st, qa, sa, b, static_cast<const f16*>(s),   \

@@ -310,7 +310,7 @@ bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamG
 // (a partial last quad) are zero.  One thread per 16-byte piece.
 __global__ void __launch_bounds__(256)
 strip_pack(const u32x4* __restrict__ B, u32x4* __restrict__ dst, int64_t N, int64_t K,
-           int64_t pieces, int native) {
+           int64_t pieces, int order) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= pieces) return;
     const int64_t kq = (K + 127) / 128, ns = (N + 15) / 16, chunks = K / 32;
@@ -321,22 +321,25 @@ strip_pack(const u32x4* __restrict__ B, u32x4* __restrict__ dst, int64_t N, int6
         return col < N && c < chunks ? B[((grp * N + col) * (K / 2) + 16 * c) / 16]
                                      : u32x4{0u, 0u, 0u, 0u};
     };
-    if (!native) {
+    if (order == kStripPlain) {
         dst[i] = chunk(4 * q + g);
         return;
     }
-    // MFMA-native: dword c of the piece is dword g of chunk 4 q + c (what the ORT layout's
-    // 4 x 4 transpose across the quad's lanes yields), its nibbles reordered from k0..k7 to
-    // k0 k2 k4 k6 (bits 0-15) and k1 k3 k5 k7 (bits 16-31)
+    // MFMA order: dword c of the piece is dword g of chunk 4 q + c (what the ORT layout's 4 x 4
+    // transpose across the quad's lanes yields); for the fp16 kernels its nibbles are also
+    // reordered from k0..k7 to k0 k2 k4 k6 (bits 0-15) and k1 k3 k5 k7 (bits 16-31)
     u32x4 out;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const u32x4 v = chunk(4 * q + c);
         const uint32_t d = g == 0 ? v.x : g == 1 ? v.y : g == 2 ? v.z : v.w;
-        uint32_t r = 0;
+        uint32_t r = d;
+        if (order == kStripMfmaF16) {
+            r = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            r |= ((d >> (4 * k)) & 0xFu) << ((k & 1) ? 16 + 4 * (k >> 1) : 4 * (k >> 1));
+            for (int k = 0; k < 8; ++k)
+                r |= ((d >> (4 * k)) & 0xFu) << ((k & 1) ? 16 + 4 * (k >> 1) : 4 * (k >> 1));
+        }
         out[c] = r;
     }
     dst[i] = out;
@@ -347,7 +350,8 @@ int64_t strip_pack_bytes(int64_t n, int64_t k, int64_t groups) {
 }
 
 hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
-                             hipStream_t st, int64_t groups, bool native) {
+                             hipStream_t st, int64_t groups, int order) {
+    if (order != kStripPlain && order != kStripMfmaF16 && order != kStripMfmaI8) return hipErrorInvalidValue;
     if (n < 1 || k < 32 || k % 32 || groups < 1 || reinterpret_cast<uintptr_t>(b) % 16 ||
         reinterpret_cast<uintptr_t>(dst) % 16)
         return hipErrorInvalidValue;
@@ -356,7 +360,7 @@ hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t 
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     hipLaunchKernelGGL(strip_pack, dim3((unsigned)blocks), dim3(256), 0, st,
                        reinterpret_cast<const u32x4*>(b), reinterpret_cast<u32x4*>(dst), n, k,
-                       pieces, native ? 1 : 0);
+                       pieces, order);
     return hipGetLastError();
 }
 

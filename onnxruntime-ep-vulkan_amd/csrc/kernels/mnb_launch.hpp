@@ -233,14 +233,16 @@ hipError_t launch_batch_stream(const BatchStreamGeom& g, const void* a, const ui
                                const uint8_t* b_strips = nullptr);
 // The strip-major copy of an int4 B [groups][N][K / 2] (K % 32 == 0):
 // [groups][ceil(N / 16)][ceil(K / 128)][16 columns][4 chunks] x 16 bytes, strip_pack_bytes
-// bytes, 16-byte aligned; columns past N and chunks past K zero.  native: each 16-byte piece
-// (lane (n, g)) instead holds dword g of the quad's four chunks, nibbles reordered to
-// k0 k2 k4 k6 k1 k3 k5 k7 -- the fp16 MFMA operands without a transpose (the level-0 copies
-// read by launch_batch_stream and the QMoE expert copies read by the fp16 strip GEMV; the
-// level-4 copies read by the int8 kernel keep the plain order).
+// bytes, 16-byte aligned; columns past N and chunks past K zero.  In the MFMA orders each
+// 16-byte piece (lane (n, g)) instead holds dword g of the quad's four chunks -- the operand
+// dwords the kernels otherwise form with a 4 x 4 transpose across lanes -- and for the fp16
+// kernels (the level-0 copies read by launch_batch_stream, the QMoE expert copies read by the
+// fp16 strip GEMV) each dword's nibbles reordered to k0 k2 k4 k6 k1 k3 k5 k7; the int8 kernel
+// (the level-4 copies, launch_acc4) unpacks the natural nibble order.
+enum StripOrder : int { kStripPlain = 0, kStripMfmaF16 = 1, kStripMfmaI8 = 2 };
 int64_t strip_pack_bytes(int64_t n, int64_t k, int64_t groups = 1);
 hipError_t launch_strip_pack(const uint8_t* b, uint8_t* dst, int64_t n, int64_t k,
-                             hipStream_t stream, int64_t groups = 1, bool native = false);
+                             hipStream_t stream, int64_t groups = 1, int order = kStripPlain);
 hipError_t launch_acc4(const void* a, bool a_f16, const uint8_t* b, const void* s,
                        const uint8_t* z, void* y, int64_t m, int64_t n, int64_t k, int bits,
                        int bs, void* workspace, hipStream_t stream,

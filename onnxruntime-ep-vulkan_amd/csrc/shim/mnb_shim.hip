@@ -1272,9 +1272,10 @@ int mnb_weights_prepack(mnb_weights* w, int64_t* bytes) {
         if (e != hipSuccess)
             return fail(MNB_ERR_NOMEM, "hipMalloc(%lld) for the strip-major copy: %s",
                         (long long)nb, hipGetErrorString(e));
-        // level 0: the batched kernel's MFMA-native order; level 4: the plain strip order the
-        // int8 kernel reads
-        e = mnb::launch_strip_pack(w->b, d, p.n, p.k, w->s->stream, 1, p.accuracy_level != 4);
+        // the MFMA order of the kernel that reads the copy: the batched fp16 kernel (level 0)
+        // or the int8 kernel (level 4)
+        e = mnb::launch_strip_pack(w->b, d, p.n, p.k, w->s->stream, 1,
+                                   p.accuracy_level == 4 ? mnb::kStripMfmaI8 : mnb::kStripMfmaF16);
         if (e == hipSuccess) e = hipStreamSynchronize(w->s->stream);
         if (e != hipSuccess) {
             (void)hipFree(d);
@@ -1381,7 +1382,7 @@ int mnb_qmoe_weights_prepack(mnb_qmoe_weights* w, int64_t* bytes) {
                         (long long)nb, f + 1, hipGetErrorString(e));
         // the MFMA-native order the fused QMoE's fp16 strip GEMV reads
         e = mnb::launch_strip_pack(static_cast<const uint8_t*>(w->buf[3 * f]), d, n[f], kk[f],
-                                   w->s->stream, p.num_experts, true);
+                                   w->s->stream, p.num_experts, mnb::kStripMfmaF16);
         if (e == hipSuccess) e = hipStreamSynchronize(w->s->stream);
         if (e != hipSuccess) {
             (void)hipFree(d);
