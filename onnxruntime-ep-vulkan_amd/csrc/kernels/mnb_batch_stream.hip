@@ -171,7 +171,9 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
             uint32_t v0 = bw[t][j].x, v1 = bw[t][j].y, v2 = bw[t][j].z, v3 = bw[t][j].w;
             if constexpr (!NATIVE) transpose_rows(v0, v1, v2, v3);
             const uint32_t wt[4] = {v0, v1, v2, v3};
-            f32x4 dot = {0.f, 0.f, 0.f, 0.f};
+            // one accumulator per block of the quad, scaled after all of the quad's MFMAs: the
+            // next block's MFMA does not wait for this block's scaled adds to read its result
+            f32x4 dot[BPQ];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const int bi = j * BPQ + c / CPB;        // block within the wavefront's range
@@ -190,13 +192,14 @@ batch_stream(const f16* __restrict__ A, const uint8_t* __restrict__ B, const f16
                     bq.s45 = nib_pair<2>(wt[c], zo);
                     bq.s67 = nib_pair<3>(wt[c], zo);
                 }
-                dot = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j][c], bq, dot, 0, 0, 0);
-                if ((c + 1) % CPB == 0) {                // block end: scale it
-                    const float sb = (float)__builtin_bit_cast(f16, sv[t][bi]);
+                dot[c / CPB] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    av[j][c], bq, c % CPB == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dot[c / CPB], 0, 0, 0);
+            }
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[t][q] = __builtin_fmaf(dot[q], sb, acc[t][q]);
-                    dot = f32x4{0.f, 0.f, 0.f, 0.f};
-                }
+            for (int b = 0; b < BPQ; ++b) {              // each block's partial, scaled once
+                const float sb = (float)__builtin_bit_cast(f16, sv[t][j * BPQ + b]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[t][q] = __builtin_fmaf(dot[b][q], sb, acc[t][q]);
             }
         }
     }
