@@ -315,7 +315,8 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
             if constexpr (!NATIVE) transpose_rows(v0, v1, v2, v3);
             const uint32_t wt[4] = {v0, v1, v2, v3};
             if constexpr (!I8) {
-                f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                // one accumulator per block of the quad, scaled after the quad's MFMAs
+                f32x4 d[BPQ];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const int c = 4 * (q_lo + j) + t;
@@ -333,13 +334,15 @@ strip_gemv(const void* __restrict__ Av, const float* __restrict__ a_scale,
                         bop.s45 = nib_pair<2>(wt[t], zo);
                         bop.s67 = nib_pair<3>(wt[t], zo);
                     }
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[j][t], bop, d, 0, 0, 0);
-                    if ((t + 1) % CPB == 0) {            // block end: scale its partial once
-                        const float sc = (float)ls[blk];
+                    d[t / CPB] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        af[j][t], bop, t % CPB == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : d[t / CPB], 0, 0, 0);
+                }
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(d[q], sc, acc[q]);
-                        d = f32x4{0.f, 0.f, 0.f, 0.f};
-                    }
+                for (int b = 0; b < BPQ; ++b) {          // each block's partial, scaled once
+                    const int blk = min((32 * (4 * (q_lo + j) + CPB * b)) / BS, bpc - 1);
+                    const float sc = (float)ls[blk];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(d[b][q], sc, acc[q]);
                 }
             } else {
                 i32x4 dot = {0, 0, 0, 0};
