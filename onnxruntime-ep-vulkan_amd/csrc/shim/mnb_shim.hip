@@ -369,14 +369,13 @@ static int matmul_impl(const mnb_problem* p, const void* a, const uint8_t* b,
          kern == MNB_KERNEL_STRIP_MFMA || kern == MNB_KERNEL_BATCH_STREAM) &&
         (!aligned(a, 16) || !aligned(b, 16)))
         kern = MNB_KERNEL_GENERIC;
-    // A node with the strip-major copy: at 3 rows (when the batched kernel takes several strips
-    // per workgroup) and at 4 rows the batched kernel reading the copy beats the streaming GEMV
-    // (Phi-3.5 set, same box: qkv / gate_up at 3 rows 7.16 / 9.34 us against 7.54 / 9.92,
-    // down at 4 rows 7.10 against 8.14; o and down at 3 rows stay on the streaming GEMV).
+    // A node with the MFMA-native strip copy: from 3 rows on the batched kernel reading it beats
+    // the streaming GEMV on ORT's layout (Phi-3.5 set, same box, session calls: 3 rows qkv / o /
+    // gate_up / down 6.82 / 4.44 / 9.00 / 6.41 us against 7.67 / 4.84 / 9.76 / 6.71; at 2 rows
+    // the streaming GEMV stays ahead, 6.18 / 4.12 / 8.15 / 5.80 against 6.87 / 4.36 / 8.98 / 6.47).
     if (b_strips && kern == MNB_KERNEL_GEMV_STREAM && p->m >= 3 && forced_kernel() == 0) {
         mnb::BatchStreamGeom bg{};
-        if (mnb::batch_stream_geometry(p->m, p->n, p->k, p->block_size, &bg) &&
-            (p->m >= 4 || bg.s >= 2))
+        if (mnb::batch_stream_geometry(p->m, p->n, p->k, p->block_size, &bg))
             kern = MNB_KERNEL_BATCH_STREAM;
     }
     // The batched decode loads scales as 8-byte and zero points as 2-byte runs.
