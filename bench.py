@@ -510,7 +510,7 @@ def main() -> int:
                                            for bp in bprobs})})
 
     # The same batched decode through the session layer, as the EP runs it with
-    # ep.strip_major_weights=1: each node's weights uploaded once (mnb_weights_upload) with their
+    # the EP's default (ep.strip_major_weights): each node's weights uploaded once (mnb_weights_upload) with their
     # strip-major copy (mnb_weights_prepack), then mnb_session_run_device on the session's own
     # stream; a graph of launches per node on that stream, weights rotated over the same 32
     # layer copies as the raw launches above.
@@ -739,7 +739,7 @@ def main() -> int:
                          "frac": round(a_bytes / (a_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
 
     # The same calls through the session layer with each copy's strip-major weights
-    # (mnb_weights_prepack, as the EP keeps them with ep.strip_major_weights=1).
+    # (mnb_weights_prepack, as the EP keeps them by default).
     asess = C.c_void_p()
     mnb.check(lib.mnb_session_create(0, C.byref(asess)))
     astream = torch.cuda.ExternalStream(int(lib.mnb_session_stream(asess)))
@@ -944,7 +944,7 @@ def main() -> int:
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(q_bytes / (q_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}}
 
-    # The same layer through the session layer as the EP runs it with ep.strip_major_weights=1:
+    # The same layer through the session layer as the EP runs it by default (ep.strip_major_weights):
     # both weight copies uploaded (mnb_qmoe_weights_upload) with their strip-major expert
     # weights (mnb_qmoe_weights_prepack); an async session, so device-resident calls return
     # once enqueued and can be recorded into a graph on the session's stream.
@@ -1093,7 +1093,7 @@ def main() -> int:
         "per_kernel": per_kernel,
         "batched_decode": batched,
         "batched_decode_session": {
-            "path": "EP session layer with ep.strip_major_weights=1: mnb_weights_upload + "
+            "path": "EP session layer as the EP runs by default (ep.strip_major_weights): mnb_weights_upload + "
                     "mnb_weights_prepack (strip-major copy), mnb_session_run_device; every "
                     "node at 4-16 rows runs the batched kernel on the strip-major copy",
             "rows": batched_session},

@@ -448,7 +448,7 @@ struct Ep {
     bool keep_constant_initializers = false;
     bool claim_enabled = true;
     bool qmoe_unfused_as_interleaved = false;   // ep.qmoe_unfused_as_interleaved
-    bool strip_major_weights = false;           // ep.strip_major_weights: mnb_weights_prepack
+    bool strip_major_weights = true;            // ep.strip_major_weights: mnb_weights_prepack
     // Device-memory mode: the HBM memory device ORT places this EP's tensors on (owned by the
     // factory's memory info), else null.
     const OrtMemoryDevice* memory_device = nullptr;
@@ -1440,11 +1440,11 @@ OrtStatus* ORT_API_CALL f_create_ep(OrtEpFactory* self, const OrtHardwareDevice*
             ep->keep_constant_initializers = opt == "1" || opt == "true";
         if (session_option(api, so, "ep.qmoe_unfused_as_interleaved", &opt))
             ep->qmoe_unfused_as_interleaved = opt == "1" || opt == "true";
-        // ep.strip_major_weights: each MatMulNBits node the batched decode kernels can run, and
-        // each QMoE node, also keeps a strip-major copy of its weights (twice the node's weight
-        // memory)
+        // ep.strip_major_weights (on unless "0" / "false"): each MatMulNBits node the batched
+        // decode kernels can run, and each QMoE node, also keeps a copy of its weights in the
+        // MFMA-native strip order (twice the node's weight memory: a few GB of the 288 GB)
         if (session_option(api, so, "ep.strip_major_weights", &opt))
-            ep->strip_major_weights = opt == "1" || opt == "true";
+            ep->strip_major_weights = !(opt == "0" || opt == "false");
         // ep.max_claim_ops: comma-separated allowlist (reference: rust/src/ep.rs:39-160);
         // claiming is on only when MatMulNBits is listed.
         if (session_option(api, so, "ep.max_claim_ops", &opt))

@@ -182,8 +182,8 @@ def test_ep_qmoe_matches_oracle(gpu_host, lead, H, I, E, k, per_channel, fusion)
 
 @pytest.mark.gpu
 def test_ep_qmoe_strip_major_weights_option(gpu_host):
-    """ep.strip_major_weights=1: Compile also keeps strip-major copies of the expert weights
-    (mnb_qmoe_weights_prepack); Compute's output is bit-identical to an EP without the option."""
+    """ep.strip_major_weights (on by default): Compile also keeps strip-major copies of the expert weights
+    (mnb_qmoe_weights_prepack); Compute's output is bit-identical to an EP with the option off."""
     print("[gpu] ep qmoe strip-major option T=64 H=I=2880 E=32 k=4", flush=True)
     T, H, I, E, k = 64, 2880, 2880, 32, 4
     inp = oq.make_qmoe_inputs(T, H, I, E, per_channel=True, seed=4321)

@@ -300,9 +300,9 @@ def test_stream_aware_chain_matches_oracle(dm_host):
 @pytest.mark.parametrize("M,N,K,bs,zp", [(16, 3072, 3072, 32, True), (8, 3000, 8192, 128, False),
                                          (1, 3072, 3072, 32, True)])
 def test_strip_major_weights_option(host, M, N, K, bs, zp):
-    """ep.strip_major_weights=1: Compile also keeps each node's strip-major copy of B
+    """ep.strip_major_weights (on by default): Compile also keeps each node's strip-major copy of B
     (mnb_weights_prepack), which Compute reads when the plan is the batched decode kernel; the
-    output is bit-identical to the same node on an EP without the option, and within the bar of
+    output is bit-identical to the same node on an EP with the option off, and within the bar of
     the oracle."""
     print(f"[gpu] ep strip-major M={M} N={N} K={K} bs={bs} zp={zp}", flush=True)
     inp = orc.make_inputs(M, N, K, bits=4, block_size=bs, with_zp=zp, seed=7 * M + N)
