@@ -274,36 +274,81 @@ hipError_t batch_go(const BatchStreamGeom& g, const void* a, const uint8_t* b, c
 
 }  // namespace
 
+namespace {
+
+// Wavefronts per SIMD that the instantiations reach, [S - 1][R - 1] (their VGPR counts, 36-126
+// for S R <= 8 as the compiler reports them for block 32 with zero points, in 8-register
+// granules out of 512); 0 where S R > 8 is not built.
+constexpr int kBatchWavesPerSimd[4][4] = {{8, 8, 6, 4}, {8, 7, 4, 4}, {8, 5, 0, 0}, {8, 4, 0, 0}};
+constexpr int64_t kBatchCUs = 256;
+constexpr int64_t kBatchLdsPerCU = 160 * 1024;
+// Activation bytes per CU (every workgroup reads all M rows of A) above which a geometry is
+// taken only when nothing else is left, and the per-workgroup size above which fewer, longer
+// wavefronts are preferred.
+constexpr int64_t kBatchActPerCU = 128 * 1024;
+constexpr int64_t kBatchActLongWaves = 64 * 1024;
+
+}  // namespace
+
 bool batch_stream_geometry(int64_t m, int64_t n, int64_t k, int bs, BatchStreamGeom* out) {
     if (m < 1 || m > 16 || n < 1 || k < 128 || k % 128 || (bs != 32 && bs != 64 && bs != 128))
         return false;
     if ((k / bs) % 4) return false;                      // whole 4-block groups of scales
     const int64_t quads = k / 128;
     const int64_t strips = (n + 15) / 16;
-    BatchStreamGeom g{};
-    // S strips per workgroup (each wavefront's activation registers serve all S, so the
-    // activation rows are read once per S strips): the fewest that keep the launch within one
-    // workgroup per CU, at most 4.  R quads per wavefront (16 R activation VGPRs, 4 S R weight
-    // VGPRs: S R <= 8 keeps the instantiations within 128): the largest of 4..1 that divides the
-    // quads into at most 16 wavefronts.  Measured on MI355X (same-run sweep of S 1-4 x R 1-4):
-    // qkv (576 strips) S = 3, R = 2 at 8 / 16 rows 9.7 / 11.5 us against 11.5 / 14.8 at S = 1,
-    // R = 3; o (192 strips) R = 4 5.4 / 6.4 us against 5.7 / 6.8 at R = 3; gate_up (1024
-    // strips) S = 4, R = 2 14.3 us at 16 rows against 15.2 at S = 2.
-    // (Fewer strips where no R fits: long K needs R = 4 to stay within 16 wavefronts.)
-    g.r = 0;
-    for (g.s = (int)std::min<int64_t>(4, (strips + 255) / 256); g.s >= 1 && g.r == 0; --g.s) {
-        for (int r : {4, 3, 2, 1}) {
-            if (quads % r || quads / r > kBatchMaxWaves || g.s * r > 8) continue;
-            g.r = r;
-            break;
+    const int64_t act = 2 * m * k;                       // A bytes each workgroup reads
+    // S strips per workgroup (each wavefront's activation registers serve all S) and R quads
+    // per wavefront (K / (128 R) <= 16 wavefronts; S R <= 8 keeps an instantiation within 128
+    // VGPRs), chosen in this order of preference:
+    //   1. at most 128 KB of activation reads per CU (the busiest CU's workgroups each read A),
+    //      else the fewest;
+    //   2. the fewest strips on the busiest CU (ceil(workgroups / 256) workgroups of S strips);
+    //   3. all of a CU's workgroups resident at once (by LDS and by the VGPR occupancy above);
+    //   4. below 64 KB of A per workgroup the most resident wavefronts per CU, above it the
+    //      fewest, longest wavefronts (larger R);
+    //   5. the most CUs with work, then the smaller R.
+    // Same-run sweep of every S and R on MI355X (Phi-3.5 layer, 3 / 4 / 8 / 16 rows, session
+    // calls on the MFMA-native copy; ORT's layout agrees): qkv (576 strips) S = 1, R = 3 at 3-4
+    // rows 6.43 us against 7.03 with S = 3, R = 2, which stays best at 8 and 16 rows (6.88 /
+    // 7.18 against 7.11 / 9.50); o (192 strips) R = 2 at 3-8 rows 4.01-4.04 us against
+    // 4.23-4.33 with R = 4, which stays best at 16 rows (4.36 against 4.55); gate_up (1024
+    // strips) S = 2, R = 2 at 3-8 rows 8.00-8.14 us against 8.77-9.01 with S = 4, R = 2, which
+    // the activation budget takes at 16 rows (9.36 us; S = 2 measured 9.20); down (K = 8192)
+    // S = 1, R = 4 throughout.
+    BatchStreamGeom best{};
+    int64_t bkey[6] = {0, 0, 0, 0, 0, 0};
+    bool have = false;
+    for (int s = 1; s <= 4; ++s) {
+        for (int r = 1; r <= 4; ++r) {
+            if (quads % r || quads / r > kBatchMaxWaves || s * r > 8) continue;
+            const int64_t waves = quads / r;
+            const int64_t gx = (strips + s - 1) / s;
+            const int64_t per_cu = (gx + kBatchCUs - 1) / kBatchCUs;
+            const int64_t lds = waves * (1024 * s + 16 * kBatchSlotRow);
+            const int64_t occ = std::min<int64_t>(kBatchLdsPerCU / lds,
+                                                  4 * kBatchWavesPerSimd[s - 1][r - 1] / waves);
+            const int64_t key[6] = {per_cu * act > kBatchActPerCU ? per_cu * act : 0, per_cu * s,
+                                    per_cu > occ ? 1 : 0,
+                                    act > kBatchActLongWaves ? -r : -std::min(per_cu, occ) * waves,
+                                    -std::min(gx, kBatchCUs), r};
+            bool better = !have;
+            for (int i = 0; i < 6 && !better; ++i) {
+                if (key[i] != bkey[i]) {
+                    better = key[i] < bkey[i];
+                    break;
+                }
+            }
+            if (!better) continue;
+            have = true;
+            std::copy(key, key + 6, bkey);
+            best.s = s;
+            best.r = r;
+            best.waves = (int)waves;
+            best.gx = gx;
         }
-        if (g.r) break;
     }
-    if (g.r == 0) return false;
-    g.waves = (int)(quads / g.r);
-    g.gx = (strips + g.s - 1) / g.s;
-    if (g.gx > 0x7fffffff) return false;
-    *out = g;
+    if (!have || best.gx > 0x7fffffff) return false;
+    *out = best;
     return true;
 }
 

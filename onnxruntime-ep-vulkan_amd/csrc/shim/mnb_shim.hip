@@ -63,7 +63,8 @@ int hip_fail(hipError_t e, const char* what) {
 // Rows above which the prefill GEMM replaces the 16-row MFMA GEMV.
 constexpr int64_t kGemmMinRows = 64;
 // Rows from which the batched decode kernel is planned (below: the streaming GEMV), and at four
-// rows where it still is: with several strips per workgroup, or under this many weight bytes.
+// rows where it still is: above 256 strips of 16 columns (what once meant several strips per
+// workgroup), or under this many weight bytes.
 // Measured on the Phi-3.5 decode shapes at four rows (cold weights): the batched kernel ahead on
 // qkv (3 strips per workgroup: 9.3 vs 10.0 us), gate_up (4: 11.7 vs 12.6) and o (4.7 MB of
 // weights: 5.1 vs 6.0 us), the streaming GEMV on down (one strip per workgroup, 12.6 MB: 8.7 vs
@@ -218,7 +219,7 @@ static int plan_search(const mnb_problem* p, mnb_plan_info* out) {
     const bool batch = f16 && p->bits == 4 &&
                        mnb::batch_stream_geometry(p->m, p->n, p->k, p->block_size, &bg);
     const bool batch_rows = p->m >= kBatchMinRows ||
-                            (p->m == 4 && (bg.s >= 2 || b_bytes_of(p) < kBatchFourRowsBelow)) ||
+                            (p->m == 4 && ((p->n + 15) / 16 > 256 || b_bytes_of(p) < kBatchFourRowsBelow)) ||
                             !stream;
     if (batch && p->m >= 4 && batch_rows) kern = MNB_KERNEL_BATCH_STREAM;
     if (stream && !(batch && batch_rows)) kern = MNB_KERNEL_GEMV_STREAM;

@@ -151,18 +151,18 @@ SHAPES = [
     (4, 48, 16384, 4, 32, True),       # four one-row tiles
     (5, 64, 512, 8, 16, False),
     (5, 9216, 3072, 4, 32, True),      # qkv at five rows: the batched decode kernel
-    (4, 9216, 3072, 4, 32, True),      # qkv at four rows: batched, three strips per workgroup
-    (4, 16400, 1024, 4, 32, False),    # four rows, four strips per workgroup, last workgroup one strip
+    (4, 9216, 3072, 4, 32, True),      # qkv at four rows: batched, one strip per workgroup
+    (4, 16400, 1024, 4, 32, False),    # four rows, 1025 workgroups, last strip whole
     (7, 40, 1024, 4, 64, True),
     (12, 33, 2048, 4, 128, False),     # partial strip
     (16, 3072, 8192, 4, 32, True),     # sixteen wavefronts of four quads
-    (6, 8200, 1024, 4, 64, True),      # two strips per workgroup, last strip partial
-    (9, 16400, 512, 4, 32, False),     # four strips per workgroup, last workgroup short
-    (7, 8320, 1024, 4, 64, False),     # three strips per workgroup, last workgroup one strip
-    (8, 768, 768, 4, 32, True),        # batched: three quads per wavefront (R = 3)
-    (16, 3072, 2304, 4, 32, True),     # batched R = 3 at Gemma-2's hidden size
-    (8, 2000, 768, 4, 64, True),       # batched R = 3, block 64: six scales, three zp bytes
-    (8, 20000, 1920, 4, 32, False),    # batched R = 1 with four strips, 15 wavefronts
+    (6, 8200, 1024, 4, 64, True),      # last strip partial
+    (9, 16400, 512, 4, 32, False),
+    (7, 8320, 1024, 4, 64, False),
+    (8, 768, 768, 4, 32, True),        # batched, one quad per wavefront
+    (16, 3072, 2304, 4, 32, True),     # batched, three quads per wavefront (Gemma-2's hidden size)
+    (8, 2000, 768, 4, 64, True),       # block 64: six scales, three zp bytes per wavefront
+    (8, 20000, 1920, 4, 32, False),    # two strips of three quads per wavefront
     (7, 32, 256, 8, 64, True),
     (8, 160, 1024, 8, 128, False),
     (9, 64, 4096, 4, 32, True),
@@ -182,6 +182,39 @@ def test_random_parity_f16(cuda, M, N, K, bits, bs, zp, kernel):
     y = _run(inp, N, K, bits, bs, cuda, kernel)
     ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
     _check_f16(y, ref, f"{kernel} M={M} N={N} K={K} b{bits} bs{bs} zp={zp}")
+
+
+# Every (strips per workgroup S, quads per wavefront R) the batched decode kernel is built for
+# (S R <= 8), as its planner chooses them, with whole and short last workgroups, partial strips,
+# blocks 32 / 64 and with and without zero points: (M, N, K, bits, bs, zp, S, R).
+BATCH_GEOMETRY = [
+    (8, 768, 768, 4, 32, True, 1, 1),
+    (4, 16400, 1024, 4, 32, False, 1, 2),
+    (16, 3072, 2304, 4, 32, True, 1, 3),
+    (16, 3072, 8192, 4, 32, True, 1, 4),
+    (4, 65000, 256, 4, 32, True, 2, 1),       # last workgroup one strip, partial strip
+    (4, 24008, 2048, 4, 32, True, 2, 2),      # partial strip
+    (8, 20000, 1920, 4, 32, False, 2, 3),
+    (4, 4100, 8192, 4, 32, True, 2, 4),       # last workgroup one partial strip
+    (12, 8320, 1920, 4, 32, True, 3, 1),      # last workgroup one strip
+    (4, 33000, 1024, 4, 64, False, 3, 2),     # last workgroup two strips, the second partial
+    (4, 65000, 512, 4, 32, True, 4, 1),       # last workgroup three strips, the third partial
+    (4, 65000, 1024, 4, 64, False, 4, 2),
+]
+
+
+@pytest.mark.parametrize("M,N,K,bits,bs,zp,S,R", BATCH_GEOMETRY)
+def test_batch_geometry_parity(cuda, M, N, K, bits, bs, zp, S, R):
+    import mnb
+    info = mnb.plan(mnb.problem(M, N, K, bits, bs, zp))
+    assert info.kernel == mnb.KERNEL_BATCH_STREAM
+    assert (info.tile_n // 16, (K // 128) // info.waves_per_group) == (S, R)
+    assert info.grid_x == -(-(-(-N // 16)) // S)
+    inp = orc.make_inputs(M, N, K, bits=bits, block_size=bs, with_zp=zp, seed=7 * M + N + K)
+    print(f"[gpu] batch geometry M={M} N={N} K={K} bs={bs} zp={zp} S={S} R={R}", flush=True)
+    y = _run(inp, N, K, bits, bs, cuda)
+    ref = orc.matmul_nbits(inp["A"], inp["B"], inp["scales"], inp["zp"], N, K, bits, bs)
+    _check_f16(y, ref, f"batch S={S} R={R} M={M} N={N} K={K}")
 
 
 # The first four run the generic kernel's forms (and the fp32 streaming GEMV at M <= 4); the rest

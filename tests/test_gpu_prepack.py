@@ -37,7 +37,7 @@ def _upload(lib, mnb, s, inp, N, K, bs, zp):
     (16, 9216, 3072, 32, True),     # qkv_proj: three strips per workgroup
     (8, 3000, 8192, 128, True),     # N past the last whole strip, K = 8192 (16 wavefronts)
     (4, 1000, 2048, 64, False),     # implied zero point, partial last strip
-    (12, 768, 768, 32, False),      # three quads per wavefront
+    (12, 768, 768, 32, False),      # one quad per wavefront, six wavefronts
     (1, 3072, 3072, 32, True),      # one row: the streaming GEMV, ORT's layout
 ])
 def test_prepacked_matches_ort_layout(cuda, M, N, K, bs, zp):

@@ -170,29 +170,47 @@ def test_fp32_decode_routing():
     assert mnb.plan(mnb.problem(65, 64, 48, 4, 16, True, f32)).kernel == mnb.KERNEL_GENERIC
 
 
-# (M, N, K, bs, zp) -> (quads per wavefront R, wavefronts per workgroup) of the batched decode
-# kernel; the GPU parity shapes of tests/test_gpu_matmul.py run these same plans, so every
-# instantiation family (R = 1..4, the unaligned scale/zero-point loads of R = 3) stays covered.
+# (M, N, K, bs, zp) -> (strips per workgroup S, quads per wavefront R) of the batched decode
+# kernel.  The first twelve are the GPU parity shapes of tests/test_gpu_matmul.py
+# (BATCH_GEOMETRY), one per instantiated (S, R) with S R <= 8; the rest are the Phi-3.5 decode
+# nodes at 4 / 8 / 16 rows, at the geometries measured fastest on MI355X.
 BATCH_PLANS = {
-    (8, 768, 768, 32, True): (3, 2),
-    (16, 3072, 2304, 32, True): (3, 6),
-    (8, 2000, 768, 64, True): (3, 2),
-    (8, 20000, 1920, 32, False): (1, 15),
-    (16, 3072, 8192, 32, True): (4, 16),
-    (5, 9216, 3072, 32, True): (2, 12),
+    (8, 768, 768, 32, True): (1, 1),
+    (4, 16400, 1024, 32, False): (1, 2),
+    (16, 3072, 2304, 32, True): (1, 3),
+    (16, 3072, 8192, 32, True): (1, 4),
+    (4, 65000, 256, 32, True): (2, 1),
+    (4, 24008, 2048, 32, True): (2, 2),
+    (8, 20000, 1920, 32, False): (2, 3),
+    (4, 4100, 8192, 32, True): (2, 4),
+    (12, 8320, 1920, 32, True): (3, 1),
+    (4, 33000, 1024, 64, False): (3, 2),
+    (4, 65000, 512, 32, True): (4, 1),
+    (4, 65000, 1024, 64, False): (4, 2),
+    (4, 9216, 3072, 32, True): (1, 3),       # qkv
+    (8, 9216, 3072, 32, True): (3, 2),
+    (16, 9216, 3072, 32, True): (3, 2),
+    (4, 3072, 3072, 32, True): (1, 2),       # o_proj
+    (8, 3072, 3072, 32, True): (1, 2),
+    (16, 3072, 3072, 32, True): (1, 4),
+    (4, 16384, 3072, 32, True): (2, 2),      # gate_up
+    (8, 16384, 3072, 32, True): (2, 2),
+    (16, 16384, 3072, 32, True): (4, 2),
+    (8, 3072, 8192, 32, True): (1, 4),       # down_proj
 }
 
 
-def test_batched_decode_geometry_of_parity_shapes():
-    """The planner's batched-decode geometry for the parity shapes that cover each quads-per-
-    wavefront instantiation: R = (K / 128) / waves_per_group."""
+def test_batched_decode_geometry():
+    """The planner's batched-decode geometry: S = tile_n / 16, R = (K / 128) / waves_per_group,
+    and one workgroup per S strips."""
     import mnb
 
-    for (m, n, k, bs, zp), (r, waves) in BATCH_PLANS.items():
+    for (m, n, k, bs, zp), (s, r) in BATCH_PLANS.items():
         info = mnb.plan(mnb.problem(m, n, k, 4, bs, zp))
         assert info.kernel == mnb.KERNEL_BATCH_STREAM, (m, n, k)
-        assert info.waves_per_group == waves, (m, n, k, info.waves_per_group)
-        assert (k // 128) // info.waves_per_group == r, (m, n, k)
+        assert (info.tile_n // 16, (k // 128) // info.waves_per_group) == (s, r), (m, n, k)
+        assert info.grid_x == -(-((n + 15) // 16) // s), (m, n, k)
+        assert (k // 128) % r == 0 and info.waves_per_group <= 16 and s * r <= 8
 
 
 def test_level4_stream_kernel_k_limit():
