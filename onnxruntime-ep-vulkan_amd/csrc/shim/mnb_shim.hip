@@ -62,16 +62,13 @@ int hip_fail(hipError_t e, const char* what) {
 
 // Rows above which the prefill GEMM replaces the 16-row MFMA GEMV.
 constexpr int64_t kGemmMinRows = 64;
-// Rows from which the batched decode kernel is planned (below: the streaming GEMV), and at four
-// rows where it still is: above 256 strips of 16 columns (what once meant several strips per
-// workgroup), or under this many weight bytes.
-// Measured on the Phi-3.5 decode shapes at four rows (cold weights): the batched kernel ahead on
-// qkv (3 strips per workgroup: 9.3 vs 10.0 us), gate_up (4: 11.7 vs 12.6) and o (4.7 MB of
-// weights: 5.1 vs 6.0 us), the streaming GEMV on down (one strip per workgroup, 12.6 MB: 8.7 vs
-// 9.5); at 2-3 rows the streaming GEMV on every node, at 5 and more it cannot stream the weights
-// once.
-constexpr int64_t kBatchMinRows = 5;
-constexpr int64_t kBatchFourRowsBelow = 8 << 20;
+// Rows from which the batched decode kernel is planned (below: the streaming GEMV).  Measured on
+// the Phi-3.5 decode shapes at four rows on ORT's layout (cold weights, the batched kernel at its
+// planned geometry): qkv 7.83 against 9.51-9.65 us on the streaming GEMV, o 4.26 against 5.32,
+// gate_up 9.10-9.16 against 11.88-11.95, down 8.00 against 8.22-8.32; at 2-3 rows the streaming
+// GEMV on every node (a node with the MFMA-native copy moves to the batched kernel at 3 rows,
+// in matmul_impl).
+constexpr int64_t kBatchMinRows = 4;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
@@ -218,9 +215,7 @@ static int plan_search(const mnb_problem* p, mnb_plan_info* out) {
     mnb::BatchStreamGeom bg{};
     const bool batch = f16 && p->bits == 4 &&
                        mnb::batch_stream_geometry(p->m, p->n, p->k, p->block_size, &bg);
-    const bool batch_rows = p->m >= kBatchMinRows ||
-                            (p->m == 4 && ((p->n + 15) / 16 > 256 || b_bytes_of(p) < kBatchFourRowsBelow)) ||
-                            !stream;
+    const bool batch_rows = p->m >= kBatchMinRows || !stream;
     if (batch && p->m >= 4 && batch_rows) kern = MNB_KERNEL_BATCH_STREAM;
     if (stream && !(batch && batch_rows)) kern = MNB_KERNEL_GEMV_STREAM;
     // fp32 activations, M <= 4: the fp32 streaming GEMV (same launch shape as the fp16 one)
